@@ -1,0 +1,148 @@
+/*
+ * m2r.h - C ABI of libm2r_hip.so, the MI355X (gfx950) state codec and FP4
+ * weight decode of mamba2-recall.
+ *
+ * Conventions for every entry point:
+ *   - all pointers are device pointers to contiguous buffers, binary16 data
+ *     is passed as `const void*` / `void*` (IEEE binary16 bit patterns);
+ *   - work is enqueued on `stream` (a hipStream_t) and never synchronizes,
+ *     never allocates device memory;
+ *   - the return value is 0 on success; nonzero means the call was rejected
+ *     or the launch failed, and m2r_last_error() (per host thread) describes
+ *     why.  Shape/dtype validation beyond what is stated here is the host
+ *     wrapper's job (the Python package raises the reference's ValueError /
+ *     RuntimeError / FloatingPointError types).
+ *
+ * Shapes: batch B, tokens L, heads H, head dim P, groups G (H % G == 0),
+ * state coordinates 128.  Rows are r = (b*H + h)*P + p.
+ */
+#ifndef M2R_H
+#define M2R_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Library identity and error text of the last failing call on this thread. */
+int m2r_abi_version(void);
+const char* m2r_last_error(void);
+
+/*
+ * Ridge-latent 52-byte state step: decode packed rows, run L selective-state
+ * tokens (decay, dt*B x update, C readout with the latent and static ridge
+ * predictor terms, D skip), requantize after every token, write y [B,L,H,P]
+ * FP16 and the packed rows back in place.
+ * Replaces scripts/fp4_zero_predictor_codec_v1.py:184-236 (scan, including the
+ * einsum correction :221-225) and its Triton kernel _latent_scan :76-181.
+ *   x f16[B,L,H,P]; dt f16[B,L,H]; A f32[H]; B,C f16[B,L,G,128];
+ *   D, dt_bias f16 or f32 [H] (flag 1 = f32); perm u8[G,128];
+ *   basis f16[G,nz,2]; lscale f16[G,2] (> 0); pred f16[G,n8+n4+2,nz];
+ *   lo,hi u8[rows,n8/2]; q4 u8[rows,n4/2]; latent e4m3[rows,2];
+ *   s8,s4 f16[rows]; (n8,n4,nz) one of the seven published layouts.
+ */
+int m2r_state_step_ridge(const void* x, const void* dt, const float* A, const void* B, const void* C,
+                         const void* D, int d_is_f32, const void* dt_bias, int db_is_f32, const uint8_t* perm,
+                         const void* basis, const void* lscale, const void* pred, uint8_t* lo, uint8_t* hi,
+                         uint8_t* q4, uint8_t* latent, void* s8, void* s4, void* y, int64_t batch, int64_t L,
+                         int64_t H, int64_t P, int64_t G, int n8, int n4, int nz, hipStream_t stream);
+
+/*
+ * Stored-scale tier step (INT8/INT4/zero-carry), same row format without the
+ * latent.  Replaces scripts/state_ppl_codec_v10.py:157-192 (scan, _tier_scan
+ * :78-154), scripts/w4_state_repair_codec_v2.py:103-137 (scan) and the
+ * stored_scale path of scripts/state_ppl_codec_v6.py:198-254.
+ */
+int m2r_state_step_tier(const void* x, const void* dt, const float* A, const void* B, const void* C,
+                        const void* D, int d_is_f32, const void* dt_bias, int db_is_f32, const uint8_t* perm,
+                        uint8_t* lo, uint8_t* hi, uint8_t* q4, void* s8, void* s4, void* y, int64_t batch,
+                        int64_t L, int64_t H, int64_t P, int64_t G, int n8, int n4, int nz, hipStream_t stream);
+
+/*
+ * Legacy sq3p25 step (16/64/48, binary32-denominator quantization).
+ * Replaces mamba2_recall/state_codec.py:203-262 (scan, sq3p25 branch) and its
+ * Triton kernel _sq_scan :105-176.
+ */
+int m2r_state_step_legacy(const void* x, const void* dt, const float* A, const void* B, const void* C,
+                          const void* D, int d_is_f32, const void* dt_bias, int db_is_f32, const uint8_t* perm,
+                          uint8_t* lo, uint8_t* hi, uint8_t* q4, void* s8, void* s4, void* y, int64_t batch,
+                          int64_t L, int64_t H, int64_t P, int64_t G, hipStream_t stream);
+
+/*
+ * Dense 3-bit step: codes u8[rows,3,16] (bit planes), scales f16[rows,2];
+ * table u8[G,128] permutation (table_is_equalizer = 0) or i8[G,128] power-of-two
+ * exponents in [-8, 8] (1).  Replaces mamba2_recall/state_codec_dense3.py:151-186
+ * (scan) and its Triton kernel _scan :82-148.
+ */
+int m2r_state_step_dense3(const void* x, const void* dt, const float* A, const void* B, const void* C,
+                          const void* D, int d_is_f32, const void* dt_bias, int db_is_f32, const void* table,
+                          int table_is_equalizer, uint8_t* codes, void* scales, void* y, int64_t batch, int64_t L,
+                          int64_t H, int64_t P, int64_t G, hipStream_t stream);
+
+/*
+ * FP16-carry control step: state f16[B,H,P,128] in original coordinates;
+ * stats (may be NULL) f32[B,H,ceil(P/16),128] receives sum over tokens and the
+ * 16 rows of each P tile of |FP16 carry|.  Replaces
+ * mamba2_recall/state_codec.py:203-262 (scan, s16 branch) and _s16_scan :65-102.
+ */
+int m2r_state_step_s16(const void* x, const void* dt, const float* A, const void* B, const void* C, const void* D,
+                       int d_is_f32, const void* dt_bias, int db_is_f32, void* state, void* y, float* stats,
+                       int64_t batch, int64_t L, int64_t H, int64_t P, int64_t G, hipStream_t stream);
+
+/*
+ * Diagnostic decode of packed rows to f32 [rows,128] in packed lane order.
+ * kind 0: INT8/INT4 tiers (lo, hi, q4, s8, s4; the zero tier decodes to 0);
+ * kind 1: dense 3-bit (codes in `lo`, f16[rows,2] scales in `s8`).
+ * Replaces the torch bodies of mamba2_recall/state_codec.py:269-296,
+ * state_codec_dense3.py:189-212 and w4_state_repair_codec_v2.py:141-162
+ * (before their permutation scatter).  `latent`, `extra`, `flags`: reserved.
+ */
+int m2r_state_decode(int kind, int n8, int n4, int nz, const uint8_t* lo, const uint8_t* hi, const uint8_t* q4,
+                     const uint8_t* latent, const void* s8, const void* s4, const void* extra, float* out,
+                     int64_t batch, int64_t H, int64_t P, int64_t flags, hipStream_t stream);
+
+/*
+ * Diagnostic legacy encode of f32 [rows,128] packed-order values into sq3p25
+ * rows (binary32 denominators, sign(z)*floor(|z|+0.5) codes).  Replaces the
+ * torch body of mamba2_recall/state_codec.py:299-331 (encode_state_).
+ */
+int m2r_state_encode_legacy(const float* v, uint8_t* lo, uint8_t* hi, uint8_t* q4, void* s8, void* s4, int64_t rows,
+                            hipStream_t stream);
+
+/*
+ * FP4 E2M1 G16 decode: packed u8[rows, ceil(cols/16)*8], e4m3_scales
+ * u8[rows, ceil(cols/16)] (E4M3FN bytes), global_scale f32[1] (device),
+ * out f16[rows, cols].  err_flag (may be NULL) is a device u32 that receives
+ * the OR of: 1 nonfinite scale, 2 negative scale, 4 nonzero code in a zero
+ * group, 8 nonfinite decoded value, 16 nonzero padding, 32 bad global scale.
+ * Replaces mamba2_recall/fp4.py:225-250 (decode_packet, G16 branch) with the
+ * op chain :100-103, :125-130, :151-154.
+ */
+int m2r_fp4_decode_g16(const uint8_t* packed, const uint8_t* e4m3_scales, const float* global_scale, void* out_f16,
+                       int64_t rows, int64_t cols, uint32_t* err_flag, hipStream_t stream);
+
+/* FP4 E2M1 G64 decode with f16 scales u16[rows, ceil(cols/64)]; same error bits
+ * (32 unused).  Replaces mamba2_recall/fp4.py:225-250, G64 branch. */
+int m2r_fp4_decode_g64(const uint8_t* packed, const void* f16_scales, void* out_f16, int64_t rows, int64_t cols,
+                       uint32_t* err_flag, hipStream_t stream);
+
+/*
+ * Probes of the exact arithmetic primitives, for known-answer testing.
+ * m2r_probe_stored_quantize replaces scripts/state_ppl_codec_v6.py:72-80
+ * (quantize_stored_probe): q = s > 0 ? clamp(roundf(RN(v/s)), +-limit) : 0,
+ * limit 7 or 127.  m2r_probe_unary applies primitive `op` (0 f32->f16 bits,
+ * 1 f16->f32, 2 f32->e4m3, 3 e4m3->f32, 4 roundf, 5 exp, 6 log, 7 dt
+ * softplus) to u32 words; m2r_probe_div computes RN(a/d) in the kernels'
+ * reciprocal form.  These three have no counterpart besides the first.
+ */
+int m2r_probe_stored_quantize(const float* v, const void* s_f16, int32_t* q, int64_t n, int limit, hipStream_t stream);
+int m2r_probe_unary(const uint32_t* in, uint32_t* out, int64_t n, int op, hipStream_t stream);
+int m2r_probe_div(const float* a, const float* d, float* q, int64_t n, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* M2R_H */

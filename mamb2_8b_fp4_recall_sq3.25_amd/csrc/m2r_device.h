@@ -1,0 +1,169 @@
+// Device-side arithmetic primitives for the MI355X (gfx950) state codec and
+// FP4 weight decode.  Every function here is exact in the sense stated in its
+// comment: it returns bit-for-bit the value the reference semantics define
+// (IEEE-754 binary32 round-to-nearest-even operations, C `roundf`, binary16
+// and E4M3FN round-to-nearest-even conversions), using cheaper gfx950
+// instruction sequences where a proof of equality exists.
+//
+// Build requirement: the translation units including this header are compiled
+// with -ffp-contract=off, so `a * b + c` is two rounded operations.  Fused
+// multiply-adds are only ever written explicitly (__builtin_fmaf), and only in
+// places where the fusion is part of an exactness argument or where the value
+// only feeds the tolerance-checked readout y.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace m2r {
+
+// ---------------------------------------------------------------------------
+// binary16 <-> binary32.  v_cvt_f16_f32 rounds to nearest even (MODE default)
+// and keeps binary16 subnormals; v_cvt_f32_f16 is exact.
+__device__ __forceinline__ float h2f(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ uint16_t f2h(float x) {
+  return __builtin_bit_cast(uint16_t, (_Float16)x);
+}
+// float(half(x)): the stored-scale rounding of a float denominator.
+__device__ __forceinline__ float round_to_half(float x) {
+  return (float)(_Float16)x;
+}
+
+// ---------------------------------------------------------------------------
+// E4M3FN (OCP FP8, bias 7, no infinities, 0x7F/0xFF NaN).
+__device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
+  uint32_t sign = (b & 0x80u) << 24;
+  uint32_t e = (b >> 3) & 15u, m = b & 7u;
+  float mag;
+  if (e == 0) {
+    mag = (float)m * 0x1p-9f;                       // subnormal: m * 2^-9 (exact)
+  } else {
+    mag = __builtin_bit_cast(float, ((e + 120u) << 23) | (m << 20));
+  }
+  if ((b & 0x7Fu) == 0x7Fu) mag = __builtin_nanf("");
+  return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, mag) | sign);
+}
+
+// Round-to-nearest-even binary32 -> E4M3FN for |x| <= 448 (callers clamp
+// first, as the reference does).  NaN maps to 0x7F with the input's sign.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
+  uint32_t u = __builtin_bit_cast(uint32_t, x);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return sign | 0x7Fu;
+  uint32_t code;
+  if (a < 0x3C800000u) {
+    // below 2^-6: multiples of 2^-9; scaling by 512 is exact, rint is RNE.
+    float q = __builtin_rintf(__builtin_bit_cast(float, a) * 512.0f);
+    code = (uint32_t)q;                              // 8 carries into 0x08 = 2^-6
+  } else {
+    uint32_t r = a + 0x7FFFFu + ((a >> 20) & 1u);    // RNE at 3 mantissa bits
+    r &= ~0xFFFFFu;
+    code = (((r >> 23) - 120u) << 3) | ((r >> 20) & 7u);
+  }
+  return sign | code;
+}
+
+// ---------------------------------------------------------------------------
+// C roundf (half away from zero) for every binary32 input:
+// trunc(x + copysign(pred(0.5), x)).  The exhaustive CPU check of this
+// identity lives with the parity tests.
+__device__ __forceinline__ float round_half_away(float x) {
+  return __builtin_truncf(x + __builtin_copysignf(0x1.fffffep-2f, x));
+}
+
+// Correctly rounded a/d given y = RN(1/d) (Markstein's theorem: y within half
+// an ulp of 1/d and q0 within one ulp of a/d => RN(q0 + RN(a - d*q0)*y) is
+// RN(a/d)).  The residual fma is exact.  y == 0 with d == 1 yields 0, which
+// the stored-scale quantizer uses for the zero-scale case.
+__device__ __forceinline__ float div_by_recip(float a, float d, float y) {
+  float q0 = a * y;
+  float r = __builtin_fmaf(-q0, d, a);
+  return __builtin_fmaf(r, y, q0);
+}
+
+// clamp(roundf(RN(v/d)), -lim, lim) as an integer, with y = RN(1/d).
+__device__ __forceinline__ int quantize_code(float v, float d, float y, float lim) {
+  float q = round_half_away(div_by_recip(v, d, y));
+  q = __builtin_fminf(__builtin_fmaxf(q, -lim), lim);
+  return (int)q;
+}
+
+// ---------------------------------------------------------------------------
+// Transcendentals.  The codec defines exp/log of a binary32 argument as the
+// binary32 rounding of a fixed binary64 evaluation that uses only IEEE
+// add/sub/mul/fma/div, so the host oracle and the device compute identical
+// bits.  Range reduction: x = k*ln2 + r, |r| <= ln2/2, exp(r) by a degree-13
+// Taylor polynomial (relative truncation error < 2^-58).  Log: x = m*2^e with
+// m in [sqrt(1/2), sqrt(2)), log(m) = 2*atanh(s), s = (m-1)/(m+1), series to
+// s^23.  Constants are the binary64 roundings of the named values.
+__device__ __forceinline__ double xexp_d(double x) {
+  if (x > 100.0) return __builtin_inf();
+  if (x < -110.0) return 0.0;
+  const double inv_ln2 = 1.4426950408889634;           // 1/ln2
+  const double ln2_hi = 6.93147180369123816490e-01;    // high 32 bits of ln2
+  const double ln2_lo = 1.90821492927058770002e-10;    // ln2 - ln2_hi
+  const double magic = 6755399441055744.0;             // 1.5 * 2^52
+  double kd = (x * inv_ln2 + magic) - magic;           // rint(x/ln2)
+  double r = (x - kd * ln2_hi) - kd * ln2_lo;
+  double p = 1.0 / 6227020800.0;                       // 1/13!
+  p = __builtin_fma(p, r, 1.0 / 479001600.0);
+  p = __builtin_fma(p, r, 1.0 / 39916800.0);
+  p = __builtin_fma(p, r, 1.0 / 3628800.0);
+  p = __builtin_fma(p, r, 1.0 / 362880.0);
+  p = __builtin_fma(p, r, 1.0 / 40320.0);
+  p = __builtin_fma(p, r, 1.0 / 5040.0);
+  p = __builtin_fma(p, r, 1.0 / 720.0);
+  p = __builtin_fma(p, r, 1.0 / 120.0);
+  p = __builtin_fma(p, r, 1.0 / 24.0);
+  p = __builtin_fma(p, r, 1.0 / 6.0);
+  p = __builtin_fma(p, r, 0.5);
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
+  int64_t k = (int64_t)kd;
+  double scale = __builtin_bit_cast(double, (uint64_t)(k + 1023) << 52);
+  return p * scale;
+}
+
+__device__ __forceinline__ double xlog_d(double x) {
+  // Domain used by the codec: finite x >= 1 (softplus argument exp(d)+1).
+  uint64_t u = __builtin_bit_cast(uint64_t, x);
+  int64_t e = (int64_t)((u >> 52) & 0x7FF) - 1023;
+  double m = __builtin_bit_cast(double, (u & 0x000FFFFFFFFFFFFFull) | 0x3FF0000000000000ull);
+  if (m > 1.4142135623730951) { m = m * 0.5; e += 1; }
+  double s = (m - 1.0) / (m + 1.0);
+  double s2 = s * s;
+  double p = 1.0 / 23.0;
+  p = __builtin_fma(p, s2, 1.0 / 21.0);
+  p = __builtin_fma(p, s2, 1.0 / 19.0);
+  p = __builtin_fma(p, s2, 1.0 / 17.0);
+  p = __builtin_fma(p, s2, 1.0 / 15.0);
+  p = __builtin_fma(p, s2, 1.0 / 13.0);
+  p = __builtin_fma(p, s2, 1.0 / 11.0);
+  p = __builtin_fma(p, s2, 1.0 / 9.0);
+  p = __builtin_fma(p, s2, 1.0 / 7.0);
+  p = __builtin_fma(p, s2, 1.0 / 5.0);
+  p = __builtin_fma(p, s2, 1.0 / 3.0);
+  p = __builtin_fma(p, s2, 1.0);
+  double logm = 2.0 * s * p;
+  double ed = (double)e;
+  const double ln2_hi = 6.93147180369123816490e-01;
+  const double ln2_lo = 1.90821492927058770002e-10;
+  return (ed * ln2_hi + logm) + ed * ln2_lo;
+}
+
+__device__ __forceinline__ float xexpf(float x) { return (float)xexp_d((double)x); }
+__device__ __forceinline__ float xlogf(float x) { return (float)xlog_d((double)x); }
+
+// Mamba-2 dt activation of the codec kernels: v = dt + dt_bias;
+// v <= 20 ? log(exp(v) + 1) : v, with the inner +1 rounded in binary32.
+__device__ __forceinline__ float softplus_dt(float v) {
+  if (v <= 20.0f) {
+    float e = xexpf(v);
+    return xlogf(e + 1.0f);
+  }
+  return v;
+}
+
+}  // namespace m2r

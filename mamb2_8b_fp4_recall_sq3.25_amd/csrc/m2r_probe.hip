@@ -1,0 +1,99 @@
+// Library identity, error reporting, and probe kernels that expose the exact
+// arithmetic primitives of the codec for exhaustive known-answer testing.
+#include <stdio.h>
+#include <string.h>
+#include "m2r_device.h"
+#include "m2r_abi_util.h"
+
+static thread_local char g_err[512];
+
+int m2r_fail(const char* msg) {
+  snprintf(g_err, sizeof(g_err), "%s", msg);
+  return 1;
+}
+
+int m2r_check(hipError_t e, const char* what) {
+  if (e == hipSuccess) return 0;
+  snprintf(g_err, sizeof(g_err), "%s: %s", what, hipGetErrorString(e));
+  return 2;
+}
+
+extern "C" const char* m2r_last_error(void) { return g_err; }
+extern "C" int m2r_abi_version(void) { return 1; }
+
+namespace m2r {
+
+// scripts/state_ppl_codec_v6.py:52-69 (_stored_quantize / _stored_probe):
+// q = scale > 0 ? clamp(roundf(RN(value / scale)), -limit, limit) : 0
+__global__ void k_probe_stored_quantize(const float* v, const uint16_t* s, int32_t* q, int64_t n, float lim) {
+  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  float sc = h2f(s[i]);
+  bool z = !(sc > 0.f) || sc == __builtin_inff();
+  float d = z ? 1.f : sc, r = z ? 0.f : 1.0f / sc;
+  q[i] = quantize_code(v[i], d, r, lim);
+}
+
+// Elementwise primitives, selected by `op`:
+//  0: f32 -> f16 bits (RNE)            out u32
+//  1: f16 bits -> f32                  out f32 bits
+//  2: f32 -> e4m3 byte (RNE, |x|<=448) out u32
+//  3: e4m3 byte -> f32                 out f32 bits
+//  4: roundf                           out f32 bits
+//  5: exp recipe                       out f32 bits
+//  6: log recipe                       out f32 bits
+//  7: softplus_dt                      out f32 bits
+__global__ void k_probe_unary(const uint32_t* in, uint32_t* out, int64_t n, int op) {
+  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  uint32_t u = in[i];
+  float f = __builtin_bit_cast(float, u);
+  uint32_t r = 0;
+  switch (op) {
+    case 0: r = f2h(f); break;
+    case 1: r = __builtin_bit_cast(uint32_t, h2f((uint16_t)u)); break;
+    case 2: r = f32_to_e4m3(f); break;
+    case 3: r = __builtin_bit_cast(uint32_t, e4m3_to_f32(u & 0xFFu)); break;
+    case 4: r = __builtin_bit_cast(uint32_t, round_half_away(f)); break;
+    case 5: r = __builtin_bit_cast(uint32_t, xexpf(f)); break;
+    case 6: r = __builtin_bit_cast(uint32_t, xlogf(f)); break;
+    case 7: r = __builtin_bit_cast(uint32_t, softplus_dt(f)); break;
+    default: r = 0; break;
+  }
+  out[i] = r;
+}
+
+// Correctly rounded a / d through the reciprocal form used by the kernels.
+__global__ void k_probe_div(const float* a, const float* d, float* q, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  float dd = d[i];
+  q[i] = div_by_recip(a[i], dd, 1.0f / dd);
+}
+
+}  // namespace m2r
+
+using namespace m2r;
+
+extern "C" int m2r_probe_stored_quantize(const float* v, const void* s_f16, int32_t* q, int64_t n, int limit,
+                                         hipStream_t stream) {
+  if (n < 0 || (limit != 7 && limit != 127)) return m2r_fail("probe: limit must be 7 or 127");
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(k_probe_stored_quantize, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, v,
+                     (const uint16_t*)s_f16, q, n, (float)limit);
+  return m2r_check(hipGetLastError(), "probe stored quantize");
+}
+
+extern "C" int m2r_probe_unary(const uint32_t* in, uint32_t* out, int64_t n, int op, hipStream_t stream) {
+  if (n < 0 || op < 0 || op > 7) return m2r_fail("probe: bad op");
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(k_probe_unary, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, in, out, n, op);
+  return m2r_check(hipGetLastError(), "probe unary");
+}
+
+extern "C" int m2r_probe_div(const float* a, const float* d, float* q, int64_t n, hipStream_t stream) {
+  if (n < 0) return m2r_fail("probe: bad n");
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(k_probe_div, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a, d, q, n);
+  return m2r_check(hipGetLastError(), "probe div");
+}

@@ -1,0 +1,470 @@
+// Fused Mamba-2 selective-state step + per-token requantization of the packed
+// 52-byte recurrent-state rows, for gfx950.
+//
+// One kernel template covers the three same-byte row formats of the
+// reference:
+//   MODE_LEGACY  sq3p25 16/64/48, quantized with the binary32 denominator
+//                (mamba2_recall/state_codec.py:105-176, _sq_scan)
+//   MODE_STORED  stored-scale INT8/INT4/zero tiers
+//                (scripts/state_ppl_codec_v10.py:78-154, _tier_scan;
+//                 scripts/state_ppl_codec_v6.py:83-195 stored_scale path)
+//   MODE_RIDGE   INT8/INT4 tiers + two E4M3 latent coefficients + the static
+//                zero-tier ridge predictor
+//                (scripts/fp4_zero_predictor_codec_v1.py:76-236, _latent_scan
+//                 and the einsum correction of scan())
+//
+// Mapping: one lane owns one state row r = (b, h, p); a wave owns 64
+// consecutive p of one head; a workgroup owns WPB heads of the same B/C
+// group.  The row's live coordinates (N8 + N4, compile-time) stay in VGPRs
+// for all L tokens.  Packed SoA rows are staged through LDS so that every
+// global access is a contiguous wave-wide transfer.  Per-token values shared
+// by the group (permuted B/C, dt activation, B*dt, ridge correction, dead-tier
+// dot products) are computed once per workgroup into LDS and read back as
+// wave-uniform broadcasts.
+#include "m2r_device.h"
+#include "m2r_abi_util.h"
+#include "m2r_tile.h"
+
+namespace m2r {
+
+enum { MODE_LEGACY = 0, MODE_STORED = 1, MODE_RIDGE = 2 };
+
+struct StepArgs {
+  const uint16_t* x;       // f16 [B, L, H, P]
+  const uint16_t* dt;      // f16 [B, L, H]
+  const float* A;          // f32 [H]
+  const uint16_t* Bm;      // f16 [B, L, G, 128]
+  const uint16_t* Cm;      // f16 [B, L, G, 128]
+  const void* D;           // f16 or f32 [H]
+  const void* dt_bias;     // f16 or f32 [H]
+  const uint8_t* perm;     // u8 [G, 128]: packed lane n holds coordinate perm[g, n]
+  const uint16_t* basis;   // f16 [G, NZ, 2]   (ridge)
+  const uint16_t* lscale;  // f16 [G, 2]       (ridge)
+  const uint16_t* pred;    // f16 [G, F, NZ]   (ridge), F = N8 + N4 + 2
+  uint8_t* lo;             // u8 [rows, N8/2]  low nibbles of the INT8 tier
+  uint8_t* hi;             // u8 [rows, N8/2]  high nibbles of the INT8 tier
+  uint8_t* q4;             // u8 [rows, N4/2]  INT4 tier
+  uint8_t* latent;         // e4m3 [rows, 2]   (ridge)
+  uint16_t* s8;            // f16 [rows]
+  uint16_t* s4;            // f16 [rows]
+  uint16_t* y;             // f16 [B, L, H, P]
+  int B, L, H, P, G;
+  int d_f32, db_f32;
+};
+
+template <int N8, int N4, int NZ, int MODE, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
+  constexpr int W8 = N8 / 2;          // bytes per row of lo and of hi
+  constexpr int W4 = N4 / 2;          // bytes per row of q4
+  constexpr int NL = N8 + N4;         // carried coordinates
+  constexpr int F = NL + 2;           // ridge predictor features
+  constexpr int RZ = next_pow2(NZ);
+  constexpr int NT = 64 * WPB;
+  constexpr int TILE = 64 * (2 * W8 + W4) + 16;
+  constexpr int C8 = N8 / 4, C4 = N4 / 4;   // carried code words (4 biased bytes each)
+  static_assert(N8 % 4 == 0 && N4 % 4 == 0, "tier widths must be multiples of 4");
+
+  __shared__ __align__(16) uint8_t s_tile[WPB][TILE];
+  __shared__ __align__(16) float s_b[128];
+  __shared__ __align__(16) float s_c[128];
+  __shared__ __align__(16) float s_bdt[WPB][NL > 0 ? NL : 4];
+  __shared__ float s_dtv[WPB], s_decay[WPB], s_dead[WPB];
+  __shared__ __align__(16) float s_corr[MODE == MODE_RIDGE ? F + 2 : 4];
+  __shared__ uint16_t s_pred[MODE == MODE_RIDGE ? F * NZ : 1];
+  __shared__ float s_basis[MODE == MODE_RIDGE ? 2 * NZ : 1];
+  __shared__ float s_dots[8];
+  __shared__ uint8_t s_perm[128];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int b = blockIdx.z;
+  const int h0 = blockIdx.y * WPB;
+  const int h = h0 + wave;
+  const int H = a.H, P = a.P, G = a.G, L = a.L;
+  const int g = h0 / (H / G);
+  const int pbase = blockIdx.x * 64;
+  const int nvalid = min(64, P - pbase);
+  const bool valid = lane < nvalid;
+  const int row0 = (b * H + h) * P + pbase;
+  const int row = row0 + lane;
+
+  // ---- statics of the group ------------------------------------------------
+  for (int n = tid; n < 128; n += NT) s_perm[n] = a.perm[g * 128 + n];
+  float ls0 = 0.f, ls1 = 0.f;
+  if constexpr (MODE == MODE_RIDGE) {
+    for (int i = tid; i < F * NZ; i += NT) s_pred[i] = a.pred[(size_t)g * F * NZ + i];
+    for (int i = tid; i < NZ; i += NT) {
+      s_basis[i] = h2f(a.basis[(g * NZ + i) * 2]);
+      s_basis[NZ + i] = h2f(a.basis[(g * NZ + i) * 2 + 1]);
+    }
+    ls0 = h2f(a.lscale[g * 2]);
+    ls1 = h2f(a.lscale[g * 2 + 1]);
+  }
+  const float Dh = load_param(a.D, a.d_f32, h);
+
+  // ---- load the incoming packed rows -----------------------------------------
+  uint8_t* tile = s_tile[wave];
+  if constexpr (W8 > 0) {
+    wave_copy_in<W8>(tile, a.lo, row0, nvalid, lane);
+    wave_copy_in<W8>(tile + 64 * W8, a.hi, row0, nvalid, lane);
+  }
+  if constexpr (W4 > 0) wave_copy_in<W4>(tile + 128 * W8, a.q4, row0, nvalid, lane);
+  float sc8 = 0.f, sc4 = 0.f;
+  uint32_t lat = 0;
+  if (valid) {
+    sc8 = h2f(a.s8[row]);
+    sc4 = h2f(a.s4[row]);
+    if constexpr (MODE == MODE_RIDGE) lat = ((const uint16_t*)a.latent)[row];
+  }
+  __syncthreads();
+
+  // Carried codes: byte k of c8[i] is q8[4i+k] + 128, of c4[i] is q4[4i+k] + 8.
+  uint32_t c8[C8 > 0 ? C8 : 1], c4[C4 > 0 ? C4 : 1];
+  {
+    if constexpr (W8 > 0) {
+      uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4];
+      lds_read_row<W8>(tile, lane * W8, wl);
+      lds_read_row<W8>(tile + 64 * W8, lane * W8, wh);
+      // lo/hi nibble planes -> bytes: lane 2j uses the low nibbles of byte j,
+      // lane 2j+1 the high nibbles.
+#pragma unroll
+      for (int i = 0; i < C8; ++i) {
+        uint32_t l = wl[i >> 1] >> (16 * (i & 1)), hh = wh[i >> 1] >> (16 * (i & 1));
+        // l holds lanes 4i..4i+3 in nibbles 0..3 (low 16 bits)
+        uint32_t bytes = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          uint32_t v8 = ((l >> (4 * k)) & 15u) | (((hh >> (4 * k)) & 15u) << 4);
+          bytes |= v8 << (8 * k);
+        }
+        c8[i] = bytes ^ 0x80808080u;
+      }
+    }
+    if constexpr (W4 > 0) {
+      uint32_t wq[(W4 + 3) / 4];
+      lds_read_row<W4>(tile + 128 * W8, lane * W4, wq);
+#pragma unroll
+      for (int i = 0; i < C4; ++i) {
+        uint32_t l = wq[i >> 1] >> (16 * (i & 1));
+        uint32_t bytes = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) bytes |= ((l >> (4 * k)) & 15u) << (8 * k);
+        c4[i] = bytes ^ 0x08080808u;
+      }
+    }
+    if (!valid) {
+#pragma unroll
+      for (int i = 0; i < C8; ++i) c8[i] = 0x80808080u;
+#pragma unroll
+      for (int i = 0; i < C4; ++i) c4[i] = 0x08080808u;
+    }
+  }
+  float z0 = 0.f, z1 = 0.f;
+  if constexpr (MODE == MODE_RIDGE) {
+    z0 = e4m3_to_f32(lat & 0xFFu) * ls0;
+    z1 = e4m3_to_f32(lat >> 8) * ls1;
+  }
+  uint32_t qz = lat;
+
+  const float y127 = 1.0f / 127.0f;   // RN(1/127)
+  const float y7 = 1.0f / 7.0f;       // RN(1/7)
+
+  for (int t = 0; t < L; ++t) {
+    const int bt = b * L + t;
+    // ---- per-token group setup ---------------------------------------------
+    for (int n = tid; n < 128; n += NT) {
+      int pos = s_perm[n] & 127;   // in-bounds even for a malformed table
+      s_b[n] = h2f(a.Bm[((size_t)bt * G + g) * 128 + pos]);
+      s_c[n] = h2f(a.Cm[((size_t)bt * G + g) * 128 + pos]);
+    }
+    if (tid < WPB) {
+      int hh = h0 + tid;
+      float v = h2f(a.dt[(size_t)bt * H + hh]) + load_param(a.dt_bias, a.db_f32, hh);
+      float dtv = softplus_dt(v);
+      s_dtv[tid] = dtv;
+      s_decay[tid] = xexpf(a.A[hh] * dtv);
+    }
+    __syncthreads();
+    for (int i = tid; i < WPB * NL; i += NT) {
+      int w = i / NL, n = i - w * NL;
+      s_bdt[w][n] = s_b[n] * s_dtv[w];
+    }
+    if constexpr (MODE == MODE_RIDGE) {
+      for (int f = tid; f < F; f += NT) {
+        float acc = 0.f;
+        for (int d = 0; d < NZ; ++d) acc = __builtin_fmaf(s_c[NL + d], h2f(s_pred[f * NZ + d]), acc);
+        s_corr[f] = acc;
+      }
+      if (wave == 0) {
+        float pb0[2], pb1[2], pc0[2], pc1[2], pbc[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          int d0 = (RZ == 128) ? 2 * lane + j : lane;
+          bool in = (RZ == 128 || j == 0) && d0 < NZ;
+          int d = in ? d0 : 0;
+          float bb = in ? s_b[NL + d] : 0.f, cc = in ? s_c[NL + d] : 0.f;
+          float e0 = in ? s_basis[d] : 0.f, e1 = in ? s_basis[NZ + d] : 0.f;
+          pbc[j] = in ? bb * cc : 0.f;
+          pc0[j] = in ? e0 * cc : 0.f;
+          pc1[j] = in ? e1 * cc : 0.f;
+          pb0[j] = in ? e0 * bb : 0.f;
+          pb1[j] = in ? e1 * bb : 0.f;
+        }
+        float dbc = wave_pair_tree<RZ>(pbc[0], pbc[1]);
+        float dc0 = wave_pair_tree<RZ>(pc0[0], pc0[1]);
+        float dc1 = wave_pair_tree<RZ>(pc1[0], pc1[1]);
+        float db0 = wave_pair_tree<RZ>(pb0[0], pb0[1]);
+        float db1 = wave_pair_tree<RZ>(pb1[0], pb1[1]);
+        if (lane == 0) {
+          s_dots[0] = dbc; s_dots[1] = dc0; s_dots[2] = dc1; s_dots[3] = db0; s_dots[4] = db1;
+        }
+      }
+    } else {
+      // dead tier contribution to the readout: sum_d (b_d * dt) * c_d per head
+      float part = 0.f;
+      for (int d = lane; d < NZ; d += 64) part = __builtin_fmaf(s_b[NL + d] * s_dtv[wave], s_c[NL + d], part);
+      for (int k = 1; k < 64; k <<= 1) part += __shfl_xor(part, k, 64);
+      if (lane == 0) s_dead[wave] = part;
+    }
+    __syncthreads();
+
+    // ---- per-row update and readout --------------------------------------------
+    const float decay = s_decay[wave];
+    const float dtv = s_dtv[wave];
+    const float x = valid ? h2f(a.x[((size_t)bt * H + h) * P + pbase + lane]) : 0.f;
+    const float nb8 = -128.0f * sc8, nb4 = -8.0f * sc4;   // exact
+    float acc = 0.f, accp = 0.f, amax8 = 0.f, amax4 = 0.f;
+    float v[NL];
+    const f32x4* bdt4 = (const f32x4*)s_bdt[wave];
+    const f32x4* c4v = (const f32x4*)s_c;
+    const f32x4* p4v = (const f32x4*)s_corr;
+#pragma unroll
+    for (int i0 = 0; i0 < NL; i0 += 4) {
+      const f32x4 cb = bdt4[i0 / 4], cc = c4v[i0 / 4];
+      f32x4 cp = {};
+      if constexpr (MODE == MODE_RIDGE) cp = p4v[i0 / 4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = i0 + j;
+        // prior = q * s exactly: (q + bias) * s - bias * s, all exact
+        float prior = (i < N8) ? __builtin_fmaf(ubyte_f(c8[i / 4], j), sc8, nb8)
+                               : __builtin_fmaf(ubyte_f(c4[(i - N8) / 4], j), sc4, nb4);
+        if constexpr (MODE == MODE_RIDGE) accp = __builtin_fmaf(prior, cp[j], accp);
+        float u = prior * decay + cb[j] * x;
+        v[i] = u;
+        acc = __builtin_fmaf(u, cc[j], acc);
+        if (i < N8) amax8 = __builtin_fmaxf(amax8, __builtin_fabsf(u));
+        else amax4 = __builtin_fmaxf(amax4, __builtin_fabsf(u));
+      }
+    }
+    // Materialize the readout accumulators here: otherwise the compiler sinks
+    // the whole fma chain into the predicated y store, which keeps every
+    // carried value and every LDS operand live at once.
+    asm volatile("" : "+v"(acc), "+v"(accp));
+    float out;
+    if constexpr (MODE == MODE_RIDGE) {
+      const float dbc = s_dots[0], dc0 = s_dots[1], dc1 = s_dots[2], db0 = s_dots[3], db1 = s_dots[4];
+      const float xdt = x * dtv;
+      out = acc + decay * (z0 * dc0 + z1 * dc1) + xdt * dbc + x * Dh
+          + decay * (accp + z0 * s_corr[NL] + z1 * s_corr[NL + 1]);
+      z0 = z0 * decay + xdt * db0;
+      z1 = z1 * decay + xdt * db1;
+      // IEEE division here (not the reciprocal form): the sign of a zero or
+      // subnormal quotient decides between latent bytes 0x00 and 0x80.
+      float q0 = __builtin_fminf(__builtin_fmaxf(z0 / ls0, -448.f), 448.f);
+      float q1 = __builtin_fminf(__builtin_fmaxf(z1 / ls1, -448.f), 448.f);
+      uint32_t e0 = f32_to_e4m3(q0), e1 = f32_to_e4m3(q1);
+      qz = e0 | (e1 << 8);
+      z0 = e4m3_to_f32(e0) * ls0;
+      z1 = e4m3_to_f32(e1) * ls1;
+    } else {
+      out = acc + x * s_dead[wave] + x * Dh;
+    }
+    if (valid) a.y[((size_t)bt * H + h) * P + pbase + lane] = f2h(out);
+
+    // ---- requantization: den = max(RN(amax / lim), 1e-8), stored = half(den) --
+    float den8 = __builtin_fmaxf(div_by_recip(amax8, 127.0f, y127), 1e-8f);
+    float den4 = __builtin_fmaxf(div_by_recip(amax4, 7.0f, y7), 1e-8f);
+    sc8 = round_to_half(den8);
+    sc4 = round_to_half(den4);
+    float d8, r8, d4, r4;
+    if constexpr (MODE == MODE_LEGACY) {
+      d8 = den8; r8 = 1.0f / den8;
+      d4 = den4; r4 = 1.0f / den4;
+    } else {
+      // zero (underflowed) or infinite stored scale: the reference's quotient
+      // is 0 and so is the code
+      bool z8 = !(sc8 > 0.f) || sc8 == __builtin_inff();
+      bool z4 = !(sc4 > 0.f) || sc4 == __builtin_inff();
+      d8 = z8 ? 1.f : sc8; r8 = z8 ? 0.f : 1.0f / sc8;
+      d4 = z4 ? 1.f : sc4; r4 = z4 ? 0.f : 1.0f / sc4;
+    }
+#pragma unroll
+    for (int i = 0; i < C8; ++i) {
+      int q0 = quantize_code(v[4 * i], d8, r8, 127.0f);
+      int q1 = quantize_code(v[4 * i + 1], d8, r8, 127.0f);
+      int q2 = quantize_code(v[4 * i + 2], d8, r8, 127.0f);
+      int q3 = quantize_code(v[4 * i + 3], d8, r8, 127.0f);
+      c8[i] = pack4(q0, q1, q2, q3) ^ 0x80808080u;
+    }
+#pragma unroll
+    for (int i = 0; i < C4; ++i) {
+      int q0 = quantize_code(v[N8 + 4 * i], d4, r4, 7.0f);
+      int q1 = quantize_code(v[N8 + 4 * i + 1], d4, r4, 7.0f);
+      int q2 = quantize_code(v[N8 + 4 * i + 2], d4, r4, 7.0f);
+      int q3 = quantize_code(v[N8 + 4 * i + 3], d4, r4, 7.0f);
+      c4[i] = (pack4(q0, q1, q2, q3) & 0x0F0F0F0Fu) ^ 0x08080808u;
+    }
+    __syncthreads();
+  }
+
+  // ---- repack to the nibble planes and store ------------------------------------
+  if (valid) {
+    if constexpr (W8 > 0) {
+      uint32_t wl[(W8 + 3) / 4] = {}, wh[(W8 + 3) / 4] = {};
+#pragma unroll
+      for (int i = 0; i < C8; ++i) {
+        uint32_t q = c8[i] ^ 0x80808080u;   // two's complement code bytes
+        uint32_t l = 0, hh = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          l |= ((q >> (8 * k)) & 15u) << (4 * k);
+          hh |= ((q >> (8 * k + 4)) & 15u) << (4 * k);
+        }
+        wl[i >> 1] |= l << (16 * (i & 1));
+        wh[i >> 1] |= hh << (16 * (i & 1));
+      }
+      lds_write_row<W8>(tile, lane * W8, wl);
+      lds_write_row<W8>(tile + 64 * W8, lane * W8, wh);
+    }
+    if constexpr (W4 > 0) {
+      uint32_t wq[(W4 + 3) / 4] = {};
+#pragma unroll
+      for (int i = 0; i < C4; ++i) {
+        uint32_t q = c4[i] ^ 0x08080808u;   // code nibbles in the low half of each byte
+        uint32_t l = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) l |= ((q >> (8 * k)) & 15u) << (4 * k);
+        wq[i >> 1] |= l << (16 * (i & 1));
+      }
+      lds_write_row<W4>(tile + 128 * W8, lane * W4, wq);
+    }
+  }
+  __syncthreads();
+  if constexpr (W8 > 0) {
+    wave_copy_out<W8>(a.lo, tile, row0, nvalid, lane);
+    wave_copy_out<W8>(a.hi, tile + 64 * W8, row0, nvalid, lane);
+  }
+  if constexpr (W4 > 0) wave_copy_out<W4>(a.q4, tile + 128 * W8, row0, nvalid, lane);
+  if (valid) {
+    a.s8[row] = f2h(sc8);
+    a.s4[row] = f2h(sc4);
+    if constexpr (MODE == MODE_RIDGE) ((uint16_t*)a.latent)[row] = (uint16_t)qz;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch over the supported tier layouts.
+template <int N8, int N4, int NZ, int MODE>
+static hipError_t launch_layout(const StepArgs& a, hipStream_t stream) {
+  int pblocks = (a.P + 63) / 64;
+  int hpg = a.H / a.G;
+  long long waves = (long long)a.B * a.H * pblocks;
+  if (hpg % 4 == 0 && waves >= 4LL * 1024) {
+    dim3 grid(pblocks, a.H / 4, a.B);
+    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 4>), grid, dim3(256), 0, stream, a);
+  } else {
+    dim3 grid(pblocks, a.H, a.B);
+    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 1>), grid, dim3(64), 0, stream, a);
+  }
+  return hipGetLastError();
+}
+
+#define M2R_LAYOUT(n8, n4, nz, mode)                                   \
+  if (a.n8_ == n8 && a.n4_ == n4 && a.nz_ == nz) return launch_layout<n8, n4, nz, mode>(a.args, stream);
+
+struct Dispatch { StepArgs args; int n8_, n4_, nz_; };
+
+static hipError_t dispatch_ridge(const Dispatch& a, hipStream_t stream) {
+  // scripts/fp4_zero_predictor_codec_v1.py:28-36 applied to the seven
+  // published layouts of scripts/w4_state_repair_codec_v2.py:27-28.
+  M2R_LAYOUT(36, 20, 72, MODE_RIDGE)
+  M2R_LAYOUT(16, 60, 52, MODE_RIDGE)
+  M2R_LAYOUT(32, 28, 68, MODE_RIDGE)
+  M2R_LAYOUT(40, 12, 76, MODE_RIDGE)
+  M2R_LAYOUT(24, 44, 60, MODE_RIDGE)
+  M2R_LAYOUT(8, 76, 44, MODE_RIDGE)
+  M2R_LAYOUT(44, 4, 80, MODE_RIDGE)
+  return hipErrorInvalidValue;
+}
+
+static hipError_t dispatch_tier(const Dispatch& a, hipStream_t stream) {
+  // scripts/state_ppl_codec_v10.py:24-26 and w4_state_repair_codec_v2.py:27-28
+  M2R_LAYOUT(16, 64, 48, MODE_STORED)
+  M2R_LAYOUT(8, 80, 40, MODE_STORED)
+  M2R_LAYOUT(24, 48, 56, MODE_STORED)
+  M2R_LAYOUT(32, 32, 64, MODE_STORED)
+  M2R_LAYOUT(36, 24, 68, MODE_STORED)
+  M2R_LAYOUT(40, 16, 72, MODE_STORED)
+  M2R_LAYOUT(44, 8, 76, MODE_STORED)
+  return hipErrorInvalidValue;
+}
+
+}  // namespace m2r
+
+using namespace m2r;
+
+static int check_geometry(int64_t batch, int64_t L, int64_t H, int64_t P, int64_t G) {
+  if (batch <= 0 || L <= 0 || H <= 0 || P <= 0 || G <= 0) return m2r_fail("state step: non-positive geometry");
+  if (H % G) return m2r_fail("state step: heads must be divisible by groups");
+  if (batch > 65535 || H > 65535 * 4) return m2r_fail("state step: grid limits exceeded");
+  if ((double)batch * L * H * P >= 2147483647.0) return m2r_fail("state step: B*L*H*P must fit int32");
+  return 0;
+}
+
+extern "C" int m2r_state_step_ridge(const void* x, const void* dt, const float* A, const void* B, const void* C,
+                                    const void* D, int d_is_f32, const void* dt_bias, int db_is_f32,
+                                    const uint8_t* perm, const void* basis, const void* lscale, const void* pred,
+                                    uint8_t* lo, uint8_t* hi, uint8_t* q4, uint8_t* latent, void* s8, void* s4,
+                                    void* y, int64_t batch, int64_t L, int64_t H, int64_t P, int64_t G, int n8,
+                                    int n4, int nz, hipStream_t stream) {
+  if (int e = check_geometry(batch, L, H, P, G)) return e;
+  Dispatch d{};
+  d.args = StepArgs{(const uint16_t*)x, (const uint16_t*)dt, A, (const uint16_t*)B, (const uint16_t*)C, D, dt_bias,
+                    perm, (const uint16_t*)basis, (const uint16_t*)lscale, (const uint16_t*)pred, lo, hi, q4, latent,
+                    (uint16_t*)s8, (uint16_t*)s4, (uint16_t*)y, (int)batch, (int)L, (int)H, (int)P, (int)G,
+                    d_is_f32, db_is_f32};
+  d.n8_ = n8; d.n4_ = n4; d.nz_ = nz;
+  hipError_t e = dispatch_ridge(d, stream);
+  if (e == hipErrorInvalidValue) return m2r_fail("ridge step: unsupported tier layout");
+  return m2r_check(e, "ridge step launch");
+}
+
+extern "C" int m2r_state_step_tier(const void* x, const void* dt, const float* A, const void* B, const void* C,
+                                   const void* D, int d_is_f32, const void* dt_bias, int db_is_f32,
+                                   const uint8_t* perm, uint8_t* lo, uint8_t* hi, uint8_t* q4, void* s8, void* s4,
+                                   void* y, int64_t batch, int64_t L, int64_t H, int64_t P, int64_t G, int n8,
+                                   int n4, int nz, hipStream_t stream) {
+  if (int e = check_geometry(batch, L, H, P, G)) return e;
+  Dispatch d{};
+  d.args = StepArgs{(const uint16_t*)x, (const uint16_t*)dt, A, (const uint16_t*)B, (const uint16_t*)C, D, dt_bias,
+                    perm, nullptr, nullptr, nullptr, lo, hi, q4, nullptr, (uint16_t*)s8, (uint16_t*)s4,
+                    (uint16_t*)y, (int)batch, (int)L, (int)H, (int)P, (int)G, d_is_f32, db_is_f32};
+  d.n8_ = n8; d.n4_ = n4; d.nz_ = nz;
+  hipError_t e = dispatch_tier(d, stream);
+  if (e == hipErrorInvalidValue) return m2r_fail("tier step: unsupported tier layout");
+  return m2r_check(e, "tier step launch");
+}
+
+extern "C" int m2r_state_step_legacy(const void* x, const void* dt, const float* A, const void* B, const void* C,
+                                     const void* D, int d_is_f32, const void* dt_bias, int db_is_f32,
+                                     const uint8_t* perm, uint8_t* lo, uint8_t* hi, uint8_t* q4, void* s8,
+                                     void* s4, void* y, int64_t batch, int64_t L, int64_t H, int64_t P, int64_t G,
+                                     hipStream_t stream) {
+  if (int e = check_geometry(batch, L, H, P, G)) return e;
+  StepArgs args{(const uint16_t*)x, (const uint16_t*)dt, A, (const uint16_t*)B, (const uint16_t*)C, D, dt_bias,
+                perm, nullptr, nullptr, nullptr, lo, hi, q4, nullptr, (uint16_t*)s8, (uint16_t*)s4,
+                (uint16_t*)y, (int)batch, (int)L, (int)H, (int)P, (int)G, d_is_f32, db_is_f32};
+  return m2r_check(launch_layout<16, 64, 48, MODE_LEGACY>(args, stream), "legacy step launch");
+}

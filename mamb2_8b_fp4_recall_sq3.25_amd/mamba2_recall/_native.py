@@ -1,0 +1,89 @@
+"""Loader for the gfx950 HIP library (`lib/libm2r_hip.so`) and thin helpers
+for calling its C-ABI with torch device tensors.
+
+The library must be present: every codec entry point in this package calls
+into it and raises if it is missing.  There is no CPU or Triton fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+PKG_ROOT = Path(__file__).resolve().parents[1]
+LIB_PATH = PKG_ROOT / "lib" / "libm2r_hip.so"
+
+_lib = None
+
+P, I, I64, U32P = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
+
+_SIGNATURES = {
+    "m2r_abi_version": ([], I),
+    "m2r_last_error": ([], ctypes.c_char_p),
+    "m2r_state_step_ridge": ([P] * 5 + [P, I, P, I] + [P] * 4 + [P] * 7 + [I64] * 5 + [I] * 3 + [P], I),
+    "m2r_state_step_tier": ([P] * 5 + [P, I, P, I] + [P] + [P] * 6 + [I64] * 5 + [I] * 3 + [P], I),
+    "m2r_state_step_legacy": ([P] * 5 + [P, I, P, I] + [P] + [P] * 6 + [I64] * 5 + [P], I),
+    "m2r_state_step_dense3": ([P] * 5 + [P, I, P, I] + [P, I] + [P] * 3 + [I64] * 5 + [P], I),
+    "m2r_state_step_s16": ([P] * 5 + [P, I, P, I] + [P] * 3 + [I64] * 5 + [P], I),
+    "m2r_state_decode": ([I, I, I, I] + [P] * 7 + [P] + [I64] * 4 + [P], I),
+    "m2r_state_encode_legacy": ([P] * 6 + [I64, P], I),
+    "m2r_fp4_decode_g16": ([P, P, P, P, I64, I64, P, P], I),
+    "m2r_fp4_decode_g64": ([P, P, P, I64, I64, P, P], I),
+    "m2r_probe_stored_quantize": ([P, P, P, I64, I, P], I),
+    "m2r_probe_unary": ([P, P, I64, I, P], I),
+    "m2r_probe_div": ([P, P, P, I64, P], I),
+}
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+def lib():
+    """The loaded HIP library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise NativeLibraryMissing(
+                f"HIP library {LIB_PATH} is missing; run __graft_entry__.build() "
+                "(or python build_lib.py in the package directory) first")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (args, res) in _SIGNATURES.items():
+            fn = getattr(handle, name, None)
+            if fn is None:
+                continue
+            fn.argtypes = args
+            fn.restype = res
+        _lib = handle
+    return _lib
+
+
+def exported_symbols():
+    return [name for name in _SIGNATURES if hasattr(lib(), name)]
+
+
+def call(name: str, *args):
+    """Invoke a C-ABI entry point; nonzero status raises RuntimeError."""
+    fn = getattr(lib(), name)
+    rc = fn(*args)
+    if rc != 0:
+        msg = lib().m2r_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed ({rc}): {msg}")
+
+
+def ptr(t):
+    """Device pointer of a tensor (None -> NULL)."""
+    if t is None:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    """The current HIP stream of `t`'s device, as the C-ABI expects it."""
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def require_device(t: torch.Tensor, what: str = "tensor"):
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise ValueError(f"{what} must be a CUDA (HIP) tensor")

@@ -1,0 +1,130 @@
+"""Published group-ridge latent state codec (52-byte rows, 3.25 bit/coord).
+
+Drop-in for the reference's scripts/fp4_zero_predictor_codec_v1.py: INT8 and
+INT4 tiers with stored FP16 scales, two E4M3 latent coefficients per row for
+the zero-carry tier, and a static per-group ridge predictor whose transient
+readout correction is contracted inside the kernel (no FP32 temporary, no
+host synchronization).  The scan runs the HIP kernel m2r_state_step_ridge.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _packed, tier_codec
+from .state_codec import PackedState
+
+RP = 16
+CACHE_BYTES = 28499968
+TABLE_BYTES = 57344
+
+
+def layout_descriptor(layout):
+    """fp4_zero_predictor_codec_v1.py:28-36: parent 'A_B_C' -> (A, B-4, C+4)."""
+    old = tier_codec.layout_descriptor(layout)
+    n8, n4, nzero = old["n8"], old["n4"] - 4, old["nzero"] + 4
+    if n4 < 4 or n8 + n4 + nzero != 128 or n8 + n4 // 2 + 2 + 4 != 52:
+        raise ValueError("Latent tier layout violates same-byte geometry")
+    return dict(layout=layout, n8=n8, n4=n4, nzero=nzero, payload_bytes=48, scale_bytes=4, row_bytes=52,
+                latent_coefficients=2, latent_dtype="torch.float8_e4m3fn",
+                tensor_widths=dict(lo=n8 // 2, hi=n8 // 2, q4=n4 // 2, latent=2))
+
+
+def allocate_state(batch, heads, dim, dstate, device, *, layout):
+    """fp4_zero_predictor_codec_v1.py:39-49."""
+    spec = layout_descriptor(layout)
+    if dstate != 128 or any(type(v) is not int or v <= 0 for v in (batch, heads, dim)):
+        raise ValueError("Positive state geometry and dstate=128 required")
+    base = (batch, heads, dim)
+    tensors = {name: torch.zeros((*base, width), device=device,
+                                 dtype=torch.float8_e4m3fn if name == "latent" else torch.uint8)
+               for name, width in spec["tensor_widths"].items()}
+    tensors.update({name: torch.zeros(base, device=device, dtype=torch.float16) for name in ("s8", "s4")})
+    return PackedState("latent_fp8_" + layout, tensors, (*base, 128))
+
+
+def validate_state(state, device, layout):
+    """fp4_zero_predictor_codec_v1.py:52-73."""
+    spec = layout_descriptor(layout)
+    if (state.mode != "latent_fp8_" + layout or len(state.shape) != 4 or state.shape[-1] != 128
+            or set(state.tensors) != {"lo", "hi", "q4", "latent", "s8", "s4"}):
+        raise ValueError("Latent packed state mode/inventory differs")
+    base = tuple(state.shape[:3])
+    if min(base) <= 0:
+        raise ValueError("Invalid latent state geometry")
+    storages = set()
+    for name, value in state.tensors.items():
+        shape = base + ((spec["tensor_widths"][name],) if name in spec["tensor_widths"] else ())
+        dtype = (torch.float16 if name in ("s8", "s4") else
+                 torch.float8_e4m3fn if name == "latent" else torch.uint8)
+        if (tuple(value.shape) != shape or value.dtype != dtype or value.device != torch.device(device)
+                or not value.is_contiguous() or value.storage_offset() != 0
+                or value.untyped_storage().nbytes() != value.numel() * value.element_size()):
+            raise ValueError("Latent packed state backing allocation differs: " + name)
+        storages.add(value.untyped_storage().data_ptr())
+    if len(storages) != 6 or state.nbytes != base[0] * base[1] * base[2] * 52:
+        raise ValueError("Latent state aliases or exceeds 52-byte row")
+    return True
+
+
+def validate_statics(permutation, basis, latent_scale, predictor, *, groups, layout, device):
+    """The static-table checks of scan() (fp4_zero_predictor_codec_v1.py:203-217);
+    these synchronize with the device, so controllers run them once."""
+    spec = layout_descriptor(layout)
+    if (permutation.dtype != torch.uint8 or tuple(permutation.shape) != (groups, 128)
+            or permutation.device != device
+            or basis.dtype != torch.float16 or tuple(basis.shape) != (groups, spec["nzero"], 2)
+            or basis.device != device
+            or latent_scale.dtype != torch.float16 or tuple(latent_scale.shape) != (groups, 2)
+            or latent_scale.device != device or not bool(torch.isfinite(basis).all())
+            or not bool(torch.isfinite(latent_scale).all())
+            or not bool((latent_scale > 0).all())):
+        raise ValueError("Latent static basis/scales differ")
+    features = spec["n8"] + spec["n4"] + 2
+    if (predictor.dtype != torch.float16 or tuple(predictor.shape) != (groups, features, spec["nzero"])
+            or predictor.device != device or not predictor.is_contiguous()
+            or not bool(torch.isfinite(predictor).all())):
+        raise ValueError("Static zero-tier predictor differs")
+
+
+@torch.no_grad()
+def scan(x, dt, A, B, C, D, dt_bias, state, permutation, basis, latent_scale, predictor, *, layout,
+         validate=True):
+    """Return (FP16 readout, None), mutating the packed carry after every token.
+
+    Same contract as fp4_zero_predictor_codec_v1.scan (:184-236).  The ridge
+    correction corr[b,t,g,f] = sum_d C[b,t,g,perm[g,n8+n4+d]] * pred[g,f,d]
+    is computed inside the kernel.  With validate=True the static tables and
+    the finiteness of the correction are checked here exactly as the
+    reference does (five device synchronizations); validate=False skips
+    those checks, for callers that validated the statics once.
+    """
+    spec = layout_descriptor(layout)
+    if not isinstance(x, torch.Tensor) or x.ndim != 4 or x.dtype != torch.float16 or not x.is_cuda:
+        raise ValueError("x must be CUDA FP16 [batch,tokens,heads,dim]")
+    batch, length, heads, dim = x.shape
+    if length < 1 or dim % RP or state.shape != (batch, heads, dim, 128):
+        raise ValueError("Positive sequence and matching latent state required")
+    validate_state(state, x.device, layout)
+    groups = B.shape[2] if B.ndim == 4 else 0
+    expected = ((dt, (batch, length, heads)), (A, (heads,)), (B, (batch, length, groups, 128)),
+                (C, (batch, length, groups, 128)), (D, (heads,)), (dt_bias, (heads,)))
+    for value, shape in expected:
+        if tuple(value.shape) != shape or value.device != x.device:
+            raise ValueError("Latent scan input geometry/device differs")
+    if (groups < 1 or heads % groups or A.dtype != torch.float32
+            or any(v.dtype != torch.float16 for v in (dt, B, C))
+            or any(v.dtype not in (torch.float16, torch.float32) for v in (D, dt_bias))):
+        raise ValueError("Latent scan dtype/grouping differs")
+    if validate:
+        validate_statics(permutation, basis, latent_scale, predictor, groups=groups, layout=layout,
+                         device=x.device)
+        # |C| <= 65504, |pred| <= 65504 and nzero <= 124 keep every finite
+        # correction below 6e11, so it is finite iff the gathered C entries are.
+        dead_ix = permutation[:, spec["n8"] + spec["n4"]:].long()
+        dead_c = C.gather(3, dead_ix[None, None, :, :].expand(batch, length, -1, -1))
+        if not bool(torch.isfinite(dead_c).all()):
+            raise FloatingPointError("Nonfinite transient predictor readout")
+    y = _packed.launch_packed("ridge", x, dt, A, B, C, D, dt_bias, permutation, state.tensors,
+                              n8=spec["n8"], n4=spec["n4"], nz=spec["nzero"], basis=basis,
+                              lscale=latent_scale, pred=predictor)
+    return y, None

@@ -1,0 +1,123 @@
+"""GPU parity of the FP4 decode kernels against the CPU oracle: FP16 bits
+bit-exact, and the reference's ValueError conditions raised in its order."""
+import numpy as np
+import pytest
+import torch
+
+import cases
+
+pytestmark = pytest.mark.gpu
+
+
+def g16_packet(rng, rows, cols, device, *, global_scale=None):
+    """Random nibbles; block scales per the BASELINE recipe: s ~ lognormal(-3,
+    0.5), global = max(s)/448, block byte = E4M3(clamp(s/global, 0, 448))."""
+    groups = (cols + 15) // 16
+    packed = rng.integers(0, 256, size=(rows, groups * 8), dtype=np.uint16).astype(np.uint8)
+    if cols % 16:
+        # zero the padding nibbles of the final group
+        codes = np.stack((packed & 15, packed >> 4), -1).reshape(rows, -1)
+        codes[:, cols:] = 0
+        packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
+    s = np.exp(rng.normal(-3.0, 0.5, size=(rows, groups))).astype(np.float32)
+    g = np.float32(s.max() / 448.0) if global_scale is None else np.float32(global_scale)
+    sb = torch.from_numpy(np.clip(s / g, 0, 448)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    return packed, sb, g
+
+
+def decode_dev(packed, scales_u8, g, rows, cols, device, group=16):
+    from mamba2_recall import fp4
+    pk = torch.from_numpy(packed).to(device)
+    if group == 16:
+        sc = torch.from_numpy(scales_u8).to(device).view(torch.float8_e4m3fn)
+        packet = dict(format="fp4_g16_e4m3", shape=[rows, cols], group_size=16, packed=pk, scales=sc,
+                      global_scale=torch.tensor(g, dtype=torch.float32))
+    else:
+        sc = torch.from_numpy(scales_u8.view(np.float16)).to(device)
+        packet = dict(format="fp4_g64_f16", shape=[rows, cols], group_size=64, packed=pk, scales=sc,
+                      global_scale=None)
+    return fp4.decode_packet(packet)
+
+
+@pytest.mark.parametrize("rows,cols", [(512, 4096), (37, 8192), (3, 48), (5, 40)])
+def test_g16_random_bit_exact(oracle, device, rows, cols):
+    rng = np.random.default_rng(rows * 7 + cols)
+    packed, sb, g = g16_packet(rng, rows, cols, device)
+    print(f"[fp4 g16] rows={rows} cols={cols}", flush=True)
+    want, err = oracle.fp4_decode(16, packed, sb, g, rows, cols)
+    assert err == 0
+    got = decode_dev(packed, sb, g, rows, cols, device).cpu().numpy().view(np.uint16)
+    assert int((got != want).sum()) == 0
+
+
+def test_g16_every_code_every_scale_byte(oracle, device):
+    """All 16 codes x all 254 finite non-negative-or-zero scale bytes x a set
+    of globals, including ones that overflow FP16 (must raise)."""
+    scale_bytes = np.array([b for b in range(256) if (b & 0x7F) != 0x7F and (b < 0x80 or b == 0x80)], np.uint8)
+    codes = np.arange(16, dtype=np.uint8)
+    for g in (1.0, 2.0 ** -20, 0.3, 1.7e-3, 100.0, 2.0 ** 24):
+        rows = scale_bytes.size
+        cols = 16 * 16
+        code_mat = np.tile(np.repeat(codes, 16), (rows, 1))              # group j holds code j
+        sb = np.repeat(scale_bytes[:, None], 16, axis=1)                  # [rows, 16 groups]
+        # zero scale bytes may only hold codes 0/8: keep those rows' other groups at code 0
+        zero_rows = (scale_bytes & 0x7F) == 0
+        code_mat[zero_rows] = np.where(np.isin(code_mat[zero_rows], (0, 8)), code_mat[zero_rows], 0)
+        packed = (code_mat[:, 0::2] | (code_mat[:, 1::2] << 4)).astype(np.uint8)
+        want, err = oracle.fp4_decode(16, packed, sb, g, rows, cols)
+        print(f"[fp4 g16 KAT] global={g} err={err}", flush=True)
+        if err:
+            assert err == 8, err
+            with pytest.raises(ValueError, match="Nonfinite decoded FP16 weights"):
+                decode_dev(packed, sb, g, rows, cols, device)
+            continue
+        got = decode_dev(packed, sb, g, rows, cols, device).cpu().numpy().view(np.uint16)
+        assert int((got != want).sum()) == 0
+        # closed form: FP16(FP32(FP32(lev*sign*block)*global)) via numpy float32
+        lev = np.array([0, .5, 1, 1.5, 2, 3, 4, 6], np.float32)
+        blk = torch.from_numpy(sb).view(torch.float8_e4m3fn).float().numpy()
+        c = code_mat.reshape(rows, 16, 16)
+        val = (lev[c & 7] * np.where(c & 8, np.float32(-1), np.float32(1))).astype(np.float32)
+        val = (val * blk[:, :, None]).astype(np.float32) * np.float32(g)
+        closed = val.astype(np.float32).astype(np.float16).view(np.uint16).reshape(rows, cols)
+        assert int((closed != got).sum()) == 0
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 4096), (7, 192), (3, 100)])
+def test_g64_random_bit_exact(oracle, device, rows, cols):
+    rng = np.random.default_rng(rows + cols)
+    groups = (cols + 63) // 64
+    codes = rng.integers(0, 16, size=(rows, groups * 64)).astype(np.uint8)
+    codes[:, cols:] = 0
+    packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
+    sc = np.exp(rng.normal(-3.0, 0.5, size=(rows, groups))).astype(np.float16).view(np.uint16)
+    print(f"[fp4 g64] rows={rows} cols={cols}", flush=True)
+    want, err = oracle.fp4_decode(64, packed, sc, 1.0, rows, cols)
+    assert err == 0
+    got = decode_dev(packed, sc, None, rows, cols, device, group=64).cpu().numpy().view(np.uint16)
+    assert int((got != want).sum()) == 0
+
+
+def test_decode_errors_follow_reference_order(device):
+    rng = np.random.default_rng(5)
+    rows, cols = 4, 64
+    packed, sb, g = g16_packet(rng, rows, cols, device)
+    bad = sb.copy(); bad[1, 2] = 0x7F                        # NaN block scale
+    with pytest.raises(ValueError, match="Invalid stored scale"):
+        decode_dev(packed, bad, g, rows, cols, device)
+    bad = sb.copy(); bad[0, 0] = 0xB8                        # negative block scale
+    with pytest.raises(ValueError, match="Invalid stored scale"):
+        decode_dev(packed, bad, g, rows, cols, device)
+    with pytest.raises(ValueError, match="Global scale must be finite and positive"):
+        decode_dev(packed, sb, 0.0, rows, cols, device)
+    bad = sb.copy(); bad[2, 1] = 0x00                        # zero block with nonzero codes
+    pk = packed.copy(); pk[2, 8:16] = 0x31
+    with pytest.raises(ValueError, match="Nonzero code in a zero-scale group"):
+        decode_dev(pk, bad, g, rows, cols, device)
+    pk = packed.copy(); pk[2, 8:16] = 0x88                   # codes 8 (= -0) are allowed
+    out = decode_dev(pk, bad, g, rows, cols, device).cpu().numpy().view(np.uint16)
+    assert (out[2, 16:32] == 0x8000).all()
+    p2, s2, g2 = g16_packet(rng, 2, 40, device)
+    p2[:, -1] |= 0x30                                         # padding nibble (column 41) nonzero
+    with pytest.raises(ValueError, match="Nonzero final-group padding"):
+        decode_dev(p2, s2, g2, 2, 40, device)

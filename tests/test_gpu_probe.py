@@ -1,0 +1,89 @@
+"""The device's exact arithmetic primitives against the oracle, exhaustively
+where the domain allows (all binary16 and E4M3 patterns, every stored-scale
+boundary)."""
+import numpy as np
+import pytest
+import torch
+
+from mamba2_recall import _native
+
+pytestmark = pytest.mark.gpu
+
+
+def dev_unary(values, op, device):
+    v = torch.from_numpy(np.ascontiguousarray(values, np.uint32).view(np.int32)).to(device)
+    out = torch.empty_like(v)
+    _native.call("m2r_probe_unary", _native.ptr(v), _native.ptr(out), v.numel(), op, _native.stream_of(v))
+    return out.cpu().numpy().view(np.uint32)
+
+
+def floats_sample(rng, n):
+    u = rng.integers(0, 2 ** 32, size=n, dtype=np.uint64).astype(np.uint32)
+    return u
+
+
+def same_float_bits(a, b):
+    """Bit equality, with every NaN equal to every NaN (payloads are outside
+    the codec's contract: scales and states are finite)."""
+    fa, fb = a.view(np.float32), b.view(np.float32)
+    return (a == b) | (np.isnan(fa) & np.isnan(fb))
+
+
+def test_f16_conversions(oracle, device):
+    every16 = np.arange(65536, dtype=np.uint32)
+    assert same_float_bits(dev_unary(every16, 1, device), oracle.unary(every16, 1)).all()
+    # every binary16 value, its neighbours in binary32 and all midpoints
+    f = every16.astype(np.uint16).view(np.float16).astype(np.float32)
+    f = f[np.isfinite(f)]
+    mids = ((f[:-1].astype(np.float64) + f[1:]) / 2).astype(np.float32)
+    vals = np.concatenate([f, mids, np.nextafter(mids, np.inf), np.nextafter(mids, -np.inf)]).view(np.uint32)
+    vals = np.concatenate([vals, floats_sample(np.random.default_rng(1), 1 << 20)])
+    assert (dev_unary(vals, 0, device) == oracle.unary(vals, 0)).all()
+
+
+def test_e4m3_conversions(oracle, device):
+    every8 = np.arange(256, dtype=np.uint32)
+    assert same_float_bits(dev_unary(every8, 3, device), oracle.unary(every8, 3)).all()
+    fin = every8[(every8 & 0x7F) != 0x7F]
+    f = oracle.unary(fin, 3).view(np.float32)
+    f = np.sort(np.unique(f[np.isfinite(f)]))
+    mids = ((f[:-1].astype(np.float64) + f[1:]) / 2).astype(np.float32)
+    vals = np.concatenate([f, mids, np.nextafter(mids, np.inf), np.nextafter(mids, -np.inf)])
+    rnd = np.random.default_rng(2).uniform(-448, 448, size=1 << 20).astype(np.float32)
+    tiny = np.random.default_rng(3).uniform(-0.02, 0.02, size=1 << 18).astype(np.float32)
+    vals = np.concatenate([vals, rnd, tiny, [0.0, -0.0]]).astype(np.float32).view(np.uint32)
+    assert (dev_unary(vals, 2, device) == oracle.unary(vals, 2)).all()
+
+
+def test_round_and_transcendentals(oracle, device):
+    rng = np.random.default_rng(4)
+    vals = np.concatenate([floats_sample(rng, 1 << 20),
+                           (np.arange(-600, 600) / 2).astype(np.float32).view(np.uint32)])
+    assert (dev_unary(vals, 4, device) == oracle.unary(vals, 4)).all()
+    args = np.concatenate([rng.uniform(-120, 30, size=1 << 20), rng.normal(0, 3, size=1 << 18)]).astype(np.float32)
+    assert (dev_unary(args.view(np.uint32), 5, device) == oracle.unary(args.view(np.uint32), 5)).all()
+    logs = np.concatenate([rng.uniform(1, 5e8, size=1 << 19), 1 + rng.uniform(0, 1, size=1 << 19)]).astype(np.float32)
+    assert (dev_unary(logs.view(np.uint32), 6, device) == oracle.unary(logs.view(np.uint32), 6)).all()
+    sp = np.concatenate([rng.normal(0, 4, size=1 << 20), [20.0, 20.000002, 19.999998, -30, 0]]).astype(np.float32)
+    assert (dev_unary(sp.view(np.uint32), 7, device) == oracle.unary(sp.view(np.uint32), 7)).all()
+
+
+@pytest.mark.parametrize("limit", [7, 127])
+def test_stored_quantize_every_scale_boundary(oracle, device, limit):
+    """Every positive FP16 scale (plus zero and the largest), values at every
+    half-integer boundary k+1/2 (and +-1 ulp) and random values."""
+    s_bits = np.arange(0, 0x7C00, 3, dtype=np.uint16)
+    s = s_bits.view(np.float16).astype(np.float32)
+    ks = np.arange(0, limit + 2, dtype=np.float32) + 0.5
+    v = (s[:, None] * ks[None, :]).astype(np.float32)
+    vals = np.concatenate([v.ravel(), np.nextafter(v, np.inf).ravel(), np.nextafter(v, -np.inf).ravel()])
+    scales = np.tile(np.repeat(s_bits, ks.size), 3)
+    vals = np.concatenate([vals, -vals])
+    scales = np.concatenate([scales, scales])
+    want = oracle.stored_quantize(vals, scales, limit)
+    vd = torch.from_numpy(vals).to(device)
+    sd = torch.from_numpy(scales.view(np.int16)).to(device)
+    q = torch.empty(vals.size, dtype=torch.int32, device=device)
+    _native.call("m2r_probe_stored_quantize", _native.ptr(vd), _native.ptr(sd), _native.ptr(q), vals.size, limit,
+                 _native.stream_of(vd))
+    assert (q.cpu().numpy() == want).all()

@@ -1,0 +1,238 @@
+"""GPU parity of the fused state step against the CPU oracle.
+
+Bar: packed codes, stored scales and latent bytes bit-exact; the FP16
+readout y within 1e-3 relative L2 (north_star tolerance, FP32 accumulate).
+Every case prints its identity before the device call.
+"""
+import numpy as np
+import pytest
+import torch
+
+import cases
+from cases import RIDGE_LAYOUTS, TIER_LAYOUTS, ridge_counts, tier_counts
+
+pytestmark = pytest.mark.gpu
+
+Y_TOL = 1e-3
+
+
+def dev16(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.float16)).to(device)
+
+
+def devp(a, device):
+    """f16 params come as uint16 bits, f32 ones as float32."""
+    if a.dtype == np.uint16:
+        return dev16(a, device)
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def to_state(np_state, state, device):
+    for k, v in np_state.items():
+        t = state.tensors[k]
+        src = torch.from_numpy(np.ascontiguousarray(v))
+        t.view(torch.uint8).copy_(src.view(torch.uint8).reshape(t.view(torch.uint8).shape).to(device))
+
+
+def from_state(state):
+    out = {}
+    for k, t in state.tensors.items():
+        u8 = t.view(torch.uint8).cpu().numpy()
+        out[k] = u8.view(np.uint16).reshape(t.shape) if t.element_size() == 2 else u8.reshape(t.shape)
+    return out
+
+
+def assert_state_equal(got, want, what):
+    for k in want:
+        g, w = got[k], want[k]
+        assert g.shape == w.shape, (what, k, g.shape, w.shape)
+        bad = int((g.reshape(-1) != w.reshape(-1)).sum())
+        assert bad == 0, f"{what}: {bad} mismatched {k} elements of {w.size}"
+
+
+def assert_y_close(y_dev, y_ref, what):
+    got = cases.f16_to_f32(y_dev.cpu().numpy().view(np.uint16))
+    want = cases.f16_to_f32(y_ref)
+    assert np.isfinite(got).all(), what
+    err = cases.rel_l2(got, want)
+    assert err <= Y_TOL, f"{what}: y rel L2 {err:.3e} > {Y_TOL}"
+    return err
+
+
+def run_ridge(oracle, device, layout, batch, L, H, P, G, seed, *, random_state=True, d_f32=False, db_f32=False,
+              dt_bias_zero=True):
+    from mamba2_recall import ridge_codec
+    n8, n4, nz = ridge_counts(layout)
+    rng = np.random.default_rng(seed)
+    inp = cases.step_inputs(rng, batch, L, H, P, G, d_f32=d_f32, db_f32=db_f32, dt_bias_zero=dt_bias_zero)
+    sta = cases.ridge_statics(rng, G, n8, n4, nz)
+    st0 = (cases.random_packed_state(rng, batch, H, P, n8, n4, latent=True) if random_state
+           else cases.zero_packed_state(batch, H, P, n8, n4, latent=True))
+    print(f"[ridge] layout={layout} B={batch} L={L} H={H} P={P} G={G} seed={seed}", flush=True)
+    ref_state = cases.copy_state(st0)
+    y_ref = oracle.state_step(oracle.MODE_RIDGE, n8, n4, nz, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"],
+                              inp["D"], inp["dt_bias"], inp["perm"], sta["basis"], sta["lscale"], sta["pred"],
+                              ref_state)
+    state = ridge_codec.allocate_state(batch, H, P, 128, device, layout=layout)
+    to_state(st0, state, device)
+    t = {k: devp(v, device) for k, v in inp.items() if k != "perm"}
+    perm = torch.from_numpy(inp["perm"]).to(device)
+    basis, ls, pred = (dev16(sta[k], device) for k in ("basis", "lscale", "pred"))
+    y, _ = ridge_codec.scan(t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["dt_bias"], state, perm, basis, ls,
+                            pred, layout=layout)
+    torch.cuda.synchronize()
+    assert_state_equal(from_state(state), ref_state, f"ridge {layout}")
+    return assert_y_close(y, y_ref, f"ridge {layout}")
+
+
+def run_tier(oracle, device, kind, layout, batch, L, H, P, G, seed, *, random_state=True, d_f32=False,
+             db_f32=False, dt_bias_zero=True):
+    from mamba2_recall import state_codec, tier_codec
+    n8, n4, nz = tier_counts(layout)
+    rng = np.random.default_rng(seed)
+    inp = cases.step_inputs(rng, batch, L, H, P, G, d_f32=d_f32, db_f32=db_f32, dt_bias_zero=dt_bias_zero)
+    st0 = (cases.random_packed_state(rng, batch, H, P, n8, n4) if random_state
+           else cases.zero_packed_state(batch, H, P, n8, n4))
+    print(f"[{kind}] layout={layout} B={batch} L={L} H={H} P={P} G={G} seed={seed}", flush=True)
+    ref_state = cases.copy_state(st0)
+    mode = oracle.MODE_LEGACY if kind == "legacy" else oracle.MODE_STORED
+    y_ref = oracle.state_step(mode, n8, n4, nz, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"],
+                              inp["dt_bias"], inp["perm"], None, None, None, ref_state)
+    t = {k: devp(v, device) for k, v in inp.items() if k != "perm"}
+    perm = torch.from_numpy(inp["perm"]).to(device)
+    if kind == "legacy":
+        state = state_codec.allocate_state(batch, H, P, 128, "sq3p25", device)
+        to_state(st0, state, device)
+        y, _ = state_codec.scan(t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["dt_bias"], state, perm)
+    else:
+        state = tier_codec.allocate_state(batch, H, P, 128, device, layout=layout)
+        to_state(st0, state, device)
+        y, _ = tier_codec.scan(t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["dt_bias"], state, perm,
+                               layout=layout)
+    torch.cuda.synchronize()
+    assert_state_equal(from_state(state), ref_state, f"{kind} {layout}")
+    return assert_y_close(y, y_ref, f"{kind} {layout}")
+
+
+@pytest.mark.parametrize("layout", RIDGE_LAYOUTS)
+def test_ridge_one_token_model_geometry(oracle, device, layout):
+    run_ridge(oracle, device, layout, batch=2, L=1, H=128, P=64, G=8, seed=11)
+
+
+@pytest.mark.parametrize("layout", RIDGE_LAYOUTS)
+def test_ridge_multi_token(oracle, device, layout):
+    run_ridge(oracle, device, layout, batch=1, L=5, H=128, P=64, G=8, seed=12)
+
+
+@pytest.mark.parametrize("L", [1, 17, 65])
+def test_ridge_reference_fixture_geometry(oracle, device, L):
+    # scripts/check_state_ridge_training_v3.py:28 uses b,h,p,g = 1,8,16,2
+    for layout in RIDGE_LAYOUTS:
+        run_ridge(oracle, device, layout, batch=1, L=L, H=8, P=16, G=2, seed=13 + L, random_state=False)
+
+
+def test_ridge_zero_state_and_f32_params(oracle, device):
+    run_ridge(oracle, device, "32_32_64", batch=3, L=2, H=128, P=64, G=8, seed=14, random_state=False,
+              d_f32=True, db_f32=True, dt_bias_zero=False)
+
+
+def test_ridge_wide_batch_four_wave_blocks(oracle, device):
+    # batch * heads * p-blocks >= 4096 selects the 4-wave workgroups
+    run_ridge(oracle, device, "24_48_56", batch=32, L=1, H=128, P=64, G=8, seed=15)
+
+
+def test_ridge_ragged_p(oracle, device):
+    run_ridge(oracle, device, "36_24_68", batch=2, L=2, H=16, P=80, G=2, seed=16)
+
+
+@pytest.mark.parametrize("layout", TIER_LAYOUTS)
+def test_tier_one_token(oracle, device, layout):
+    run_tier(oracle, device, "tier", layout, batch=2, L=1, H=128, P=64, G=8, seed=21)
+
+
+@pytest.mark.parametrize("layout", TIER_LAYOUTS)
+def test_tier_multi_token_small(oracle, device, layout):
+    run_tier(oracle, device, "tier", layout, batch=1, L=17, H=8, P=16, G=2, seed=22, random_state=False)
+
+
+def test_tier_wide_batch(oracle, device):
+    run_tier(oracle, device, "tier", "8_80_40", batch=32, L=1, H=128, P=64, G=8, seed=23)
+
+
+def test_legacy_one_and_multi_token(oracle, device):
+    run_tier(oracle, device, "legacy", "16_64_48", batch=2, L=1, H=128, P=64, G=8, seed=31)
+    run_tier(oracle, device, "legacy", "16_64_48", batch=1, L=9, H=128, P=64, G=8, seed=32, random_state=False,
+             d_f32=True, dt_bias_zero=False)
+
+
+def test_sequential_tokens_equal_one_call(oracle, device):
+    """L tokens in one call == L calls of one token (the carry between tokens
+    is exactly the dequantized codes)."""
+    from mamba2_recall import ridge_codec
+    layout = "40_16_72"
+    n8, n4, nz = ridge_counts(layout)
+    rng = np.random.default_rng(41)
+    batch, L, H, P, G = 2, 6, 128, 64, 8
+    inp = cases.step_inputs(rng, batch, L, H, P, G)
+    sta = cases.ridge_statics(rng, G, n8, n4, nz)
+    st0 = cases.random_packed_state(rng, batch, H, P, n8, n4, latent=True)
+    t = {k: devp(v, device) for k, v in inp.items() if k != "perm"}
+    perm = torch.from_numpy(inp["perm"]).to(device)
+    basis, ls, pred = (dev16(sta[k], device) for k in ("basis", "lscale", "pred"))
+    s_all = ridge_codec.allocate_state(batch, H, P, 128, device, layout=layout)
+    s_seq = ridge_codec.allocate_state(batch, H, P, 128, device, layout=layout)
+    to_state(st0, s_all, device)
+    to_state(st0, s_seq, device)
+    y_all, _ = ridge_codec.scan(t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["dt_bias"], s_all, perm, basis,
+                                ls, pred, layout=layout)
+    ys = []
+    for i in range(L):
+        sl = slice(i, i + 1)
+        y1, _ = ridge_codec.scan(t["x"][:, sl], t["dt"][:, sl], t["A"], t["B"][:, sl], t["C"][:, sl], t["D"],
+                                 t["dt_bias"], s_seq, perm, basis, ls, pred, layout=layout, validate=False)
+        ys.append(y1)
+    torch.cuda.synchronize()
+    assert_state_equal(from_state(s_seq), from_state(s_all), "sequential vs one call")
+    assert torch.equal(torch.cat(ys, 1), y_all)
+
+
+def run_dense3(oracle, device, kind, batch, L, H, P, G, seed, *, random_state=True):
+    from mamba2_recall import state_codec_dense3 as d3
+    rng = np.random.default_rng(seed)
+    inp = cases.step_inputs(rng, batch, L, H, P, G)
+    if kind == "equalizer":
+        table = rng.integers(-8, 9, size=(G, 128)).astype(np.int8)
+    else:
+        table = inp["perm"]
+    rows = (batch, H, P)
+    if random_state:
+        st0 = dict(codes=rng.integers(0, 256, size=rows + (3, 16), dtype=np.uint16).astype(np.uint8),
+                   scales=cases.f16(np.exp(rng.normal(-2.0, 0.5, size=rows + (2,)))))
+    else:
+        st0 = dict(codes=np.zeros(rows + (3, 16), np.uint8), scales=np.zeros(rows + (2,), np.uint16))
+    print(f"[dense3 {kind}] B={batch} L={L} H={H} P={P} G={G} seed={seed}", flush=True)
+    ref = cases.copy_state(st0)
+    y_ref = oracle.dense3_step(1 if kind == "equalizer" else 0, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"],
+                               inp["D"], inp["dt_bias"], np.ascontiguousarray(table), ref)
+    state = d3.allocate_state(batch, H, P, 128, device)
+    to_state(st0, state, device)
+    t = {k: devp(v, device) for k, v in inp.items() if k != "perm"}
+    y = d3.scan(t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["dt_bias"], state,
+                torch.from_numpy(np.ascontiguousarray(table)).to(device), kind)
+    torch.cuda.synchronize()
+    assert_state_equal(from_state(state), ref, f"dense3 {kind}")
+    return assert_y_close(y, y_ref, f"dense3 {kind}")
+
+
+@pytest.mark.parametrize("kind", ["permutation", "equalizer"])
+def test_dense3_one_token(oracle, device, kind):
+    run_dense3(oracle, device, kind, batch=2, L=1, H=128, P=64, G=8, seed=51)
+
+
+@pytest.mark.parametrize("kind", ["permutation", "equalizer"])
+def test_dense3_multi_token_small(oracle, device, kind):
+    run_dense3(oracle, device, kind, batch=1, L=9, H=8, P=16, G=2, seed=52, random_state=False)
+
+
+def test_dense3_wide_batch(oracle, device):
+    run_dense3(oracle, device, "permutation", batch=32, L=1, H=128, P=64, G=8, seed=53)

@@ -1,0 +1,321 @@
+"""Pins of the CPU oracle: every golden vector and known-answer check the
+reference holds for this path, library routines (numpy binary16, torch
+float8_e4m3fn), closed forms and invariants.  Each check is chosen so that a
+plausible restatement mistake fails it."""
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import cases
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+# ---------------------------------------------------------------- formats
+
+def test_f16_decode_every_pattern_matches_numpy(oracle):
+    every = np.arange(65536, dtype=np.uint32)
+    got = oracle.unary(every, 1).view(np.float32)
+    want = every.astype(np.uint16).view(np.float16).astype(np.float32)
+    same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+    assert same.all()
+
+
+def test_f16_encode_matches_numpy_rne(oracle):
+    rng = np.random.default_rng(0)
+    f = np.arange(65536, dtype=np.uint16).view(np.float16).astype(np.float32)
+    f = np.sort(f[np.isfinite(f)])
+    mids = ((f[:-1].astype(np.float64) + f[1:]) / 2).astype(np.float32)   # ties: exactly representable
+    vals = np.concatenate([f, mids, np.nextafter(mids, np.inf), np.nextafter(mids, -np.inf),
+                           rng.standard_normal(1 << 18).astype(np.float32) * 1e4,
+                           np.float32([65519.99, 65520.0, 7e4, 1e-8, 2.98e-8, 3e-8, -0.0])])
+    got = oracle.unary(vals.view(np.uint32), 0).astype(np.uint16)
+    with np.errstate(over="ignore"):
+        want = vals.astype(np.float16).view(np.uint16)
+    assert (got == want).all()
+
+
+def test_e4m3_reference_kat(oracle):
+    """docs/evidence/fp_state_diagnostics/v13/cpu_reference.json: 254 finite
+    E4M3FN bit patterns with 253 unique values (+0 and -0)."""
+    kat = json.loads((GOLDEN / "v13_cpu_reference_checks.json").read_text())
+    vals = oracle.unary(np.arange(256, dtype=np.uint32), 3).view(np.float32)
+    finite = np.isfinite(vals)
+    assert int(finite.sum()) == kat["fp8_finite_bit_patterns"] == 254
+    assert len(set(vals[finite].tolist())) == kat["fp8_unique_values"] == 253
+
+
+def test_e4m3_matches_torch_float8(oracle):
+    every = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(every).view(torch.float8_e4m3fn).float().numpy()
+    got = oracle.unary(every.astype(np.uint32), 3).view(np.float32)
+    assert ((got == want) | (np.isnan(got) & np.isnan(want))).all()
+    assert (np.signbit(got[every != 0x7F]) == np.signbit(want[every != 0x7F])).all()
+    # encode: every representable value, every midpoint and its neighbours,
+    # random values in the clamp range
+    f = np.sort(np.unique(want[np.isfinite(want)]))
+    mids = ((f[:-1].astype(np.float64) + f[1:]) / 2).astype(np.float32)
+    rng = np.random.default_rng(1)
+    vals = np.concatenate([f, mids, np.nextafter(mids, np.inf), np.nextafter(mids, -np.inf),
+                           rng.uniform(-448, 448, 1 << 18).astype(np.float32),
+                           rng.uniform(-0.03, 0.03, 1 << 16).astype(np.float32), np.float32([-0.0, 0.0])])
+    got = oracle.unary(vals.view(np.uint32), 2).astype(np.uint8)
+    want = torch.from_numpy(vals).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert (got == want).all()
+
+
+def test_fp4_tie_kat_reference_encoder_rule():
+    """v13/cpu_reference.json: E2M1 ties [.25,.75,1.25,1.75,2.5,3.5,5] go to the
+    even codes [0,2,2,4,4,6,6]; the decode table is the reference's
+    E2M1_MAGNITUDES.  (Pins the magnitude table the decoder uses.)"""
+    kat = json.loads((GOLDEN / "v13_cpu_reference_checks.json").read_text())
+    lev = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+    for tie, code in zip(kat["fp4_ties"], kat["fp4_even_codes"]):
+        lo = max(i for i, v in enumerate(lev) if v < tie)
+        assert tie == (lev[lo] + lev[lo + 1]) / 2 and code in (lo, lo + 1) and code % 2 == 0
+
+
+# --------------------------------------------------------- rounding identities
+
+def test_round_half_away_identity_exhaustive(oracle):
+    """trunc(x + copysign(pred(0.5), x)) == roundf(x) for every binary32 with
+    |x| < 2^25 (both signs): the device quantizer's rounding."""
+    assert oracle.check_round_identity(0, 0x4C000000) == 0
+
+
+def test_reciprocal_quantizer_equals_ieee_division(oracle):
+    codes_bad, div_bad = oracle.check_markstein(20260901, 50_000_000, 3000)
+    assert codes_bad == 0 and div_bad == 0
+
+
+def test_stored_quantize_kat(oracle):
+    """state_ppl_codec_v6.py:54-61: exact half ties go away from zero, a zero
+    or underflowed scale gives 0, codes clamp at +-limit."""
+    s = cases.f16([0.5, 0.5, 0.5, 0.5, 1.0, 1e-8, 0.0, 2.0 ** -24, 0.25])
+    v = np.float32([1.75, -1.75, 1.25, 100.0, 3.5, 5.0, 3.0, 127.5 * 2.0 ** -24, -0.125])
+    q = oracle.stored_quantize(v, s, 7)
+    assert q.tolist() == [4, -4, 3, 7, 4, 0, 0, 7, -1]   # 3.5 -> 4, -3.5 -> -4, 2.5 -> 3
+    q = oracle.stored_quantize(np.float32([127.5 * 2.0 ** -24, -126.5 * 0.5]), cases.f16([2.0 ** -24, 0.5]), 127)
+    assert q.tolist() == [127, -127]
+
+
+# ------------------------------------------------------------ transcendentals
+
+def test_exp_log_recipe_matches_correctly_rounded_libm(oracle):
+    """The codec's exp/log recipe equals binary32 rounding of libm's
+    binary64 results (which are within 1 ulp of exact) on a dense sample."""
+    rng = np.random.default_rng(2)
+    x = np.concatenate([rng.uniform(-110, 88, 200000), rng.normal(0, 2, 200000)]).astype(np.float32)
+    got = oracle.unary(x.view(np.uint32), 5).view(np.float32)
+    want = np.exp(x.astype(np.float64)).astype(np.float32)
+    assert int((got.view(np.uint32) != want.view(np.uint32)).sum()) == 0
+    y = np.concatenate([rng.uniform(1, 5e8, 200000), 1 + rng.uniform(0, 4, 200000)]).astype(np.float32)
+    got = oracle.unary(y.view(np.uint32), 6).view(np.float32)
+    want = np.log(y.astype(np.float64)).astype(np.float32)
+    assert int((got.view(np.uint32) != want.view(np.uint32)).sum()) == 0
+
+
+def test_softplus_closed_form(oracle):
+    v = np.float32([-30.0, -1.0, 0.0, 1.0, 19.5, 20.0, 20.5, 80.0])
+    got = oracle.unary(v.view(np.uint32), 7).view(np.float32)
+    e = np.exp(v.astype(np.float64)).astype(np.float32)
+    want = np.where(v <= 20, np.log((e + np.float32(1)).astype(np.float64)).astype(np.float32), v)
+    assert (got == want).all()
+    assert got[-1] == 80.0 and got[-2] == 20.5    # identity above 20
+
+
+# ------------------------------------------------------------- FP4 decode
+
+def test_fp4_decode_closed_form_all_codes_all_scales(oracle):
+    lev = np.float32([0, .5, 1, 1.5, 2, 3, 4, 6])
+    scale_bytes = np.array([b for b in range(128) if b != 0x7F] + [0x80], np.uint8)
+    rows = scale_bytes.size
+    code_mat = np.tile(np.repeat(np.arange(16, dtype=np.uint8), 16), (rows, 1))
+    zero = (scale_bytes & 0x7F) == 0
+    code_mat[zero] = np.where(np.isin(code_mat[zero], (0, 8)), code_mat[zero], 0)
+    packed = (code_mat[:, 0::2] | (code_mat[:, 1::2] << 4)).astype(np.uint8)
+    sb = np.repeat(scale_bytes[:, None], 16, 1)
+    blk = torch.from_numpy(sb).view(torch.float8_e4m3fn).float().numpy()
+    for g in (1.0, 0.37, 2.0 ** -20):
+        out, err = oracle.fp4_decode(16, packed, sb, g, rows, 256)
+        assert err == 0
+        c = code_mat.reshape(rows, 16, 16)
+        val = lev[c & 7] * np.where(c & 8, np.float32(-1), np.float32(1))
+        val = (val * blk[:, :, None]).astype(np.float32) * np.float32(g)
+        want = val.astype(np.float32).astype(np.float16).view(np.uint16).reshape(rows, 256)
+        assert (out == want).all()
+    # code 8 decodes to -0.0 (0x8000) and code 0 to +0, except under the -0
+    # block scale (byte 0x80), where IEEE sign rules flip both
+    pos = scale_bytes < 0x80
+    assert (out[pos, 16 * 8:16 * 9] == 0x8000).all() and (out[pos, :16] == 0).all()
+    assert (out[~pos, 16 * 8:16 * 9] == 0).all() and (out[~pos, :16] == 0x8000).all()
+
+
+def test_fp4_decode_error_bits(oracle):
+    packed = np.full((1, 8), 0x11, np.uint8)
+    out, err = oracle.fp4_decode(16, packed, np.uint8([[0x7F]]), 1.0, 1, 16)
+    assert err & 1
+    out, err = oracle.fp4_decode(16, packed, np.uint8([[0x00]]), 1.0, 1, 16)
+    assert err & 4
+    out, err = oracle.fp4_decode(16, packed, np.uint8([[0x40]]), 1e30, 1, 16)
+    assert err & 8
+    out, err = oracle.fp4_decode(16, packed, np.uint8([[0x40]]), 0.0, 1, 16)
+    assert err & 32
+    out, err = oracle.fp4_decode(16, packed, np.uint8([[0xC0]]), 1.0, 1, 16)
+    assert err & 2
+    out, err = oracle.fp4_decode(16, packed, np.uint8([[0x40]]), 1.0, 1, 14)
+    assert err & 16
+
+
+# ------------------------------------------------------ state-step invariants
+
+def _ridge(oracle, layout, inp, sta, st):
+    n8, n4, nz = cases.ridge_counts(layout)
+    return oracle.state_step(oracle.MODE_RIDGE, n8, n4, nz, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"],
+                             inp["D"], inp["dt_bias"], inp["perm"], sta["basis"], sta["lscale"], sta["pred"], st)
+
+
+def test_zero_state_zero_input_stays_zero(oracle):
+    rng = np.random.default_rng(3)
+    for layout in cases.RIDGE_LAYOUTS:
+        n8, n4, nz = cases.ridge_counts(layout)
+        inp = cases.step_inputs(rng, 1, 3, 8, 16, 2)
+        inp["x"][:] = 0
+        st = cases.zero_packed_state(1, 8, 16, n8, n4, latent=True)
+        y = _ridge(oracle, layout, inp, cases.ridge_statics(rng, 2, n8, n4, nz), st)
+        assert not y.any()
+        assert not st["lo"].any() and not st["hi"].any() and not st["q4"].any() and not st["latent"].any()
+        # den floors at 1e-8, whose binary16 rounding underflows to 0
+        assert not st["s8"].any() and not st["s4"].any()
+
+
+def test_d_skip_passthrough(oracle):
+    """B = C = 0, zero predictor: y = half(x * D) exactly and the carry only decays."""
+    rng = np.random.default_rng(4)
+    layout = "32_32_64"
+    n8, n4, nz = cases.ridge_counts(layout)
+    inp = cases.step_inputs(rng, 2, 1, 8, 16, 2)
+    inp["B"][:] = 0
+    inp["C"][:] = 0
+    sta = cases.ridge_statics(rng, 2, n8, n4, nz)
+    st = cases.random_packed_state(rng, 2, 8, 16, n8, n4, latent=True)
+    y = _ridge(oracle, layout, inp, sta, st)
+    x = cases.f16_to_f32(inp["x"])
+    D = cases.f16_to_f32(inp["D"])
+    want = (x * D[None, None, :, None]).astype(np.float32).astype(np.float16).view(np.uint16)
+    assert (y == want).all()
+
+
+def test_identity_step_is_idempotent(oracle):
+    """A = 0 (decay 1) and B = 0: requantizing a dequantized row whose largest
+    INT8 code is +-127 (and INT4 +-7) returns the same codes and scales."""
+    rng = np.random.default_rng(5)
+    for layout in cases.TIER_LAYOUTS:
+        n8, n4, nz = cases.tier_counts(layout)
+        inp = cases.step_inputs(rng, 1, 1, 8, 16, 2)
+        inp["A"][:] = 0
+        inp["B"][:] = 0
+        st = cases.random_packed_state(rng, 1, 8, 16, n8, n4)
+        # valid carries never hold -128: move such codes to -127 (lo nibble 0 -> 1)
+        lo, hi = st["lo"], st["hi"]
+        for sh in (0, 4):
+            m = (((lo >> sh) & 15) == 0) & (((hi >> sh) & 15) == 8)
+            lo[m] |= np.uint8(1 << sh)
+        # force one +127 INT8 code and one -7 INT4 code per row (lane 0)
+        st["lo"][..., 0] = (st["lo"][..., 0] & 0xF0) | 0xF
+        st["hi"][..., 0] = (st["hi"][..., 0] & 0xF0) | 0x7
+        q = st["q4"].copy()
+        codes = np.stack((q & 15, q >> 4), -1).reshape(q.shape[:-1] + (n4,))
+        codes = np.where(codes == 8, 9, codes)          # no -8 (outside +-7)
+        codes[..., 0] = 9                               # -7
+        st["q4"] = (codes[..., 0::2] | (codes[..., 1::2] << 4)).astype(np.uint8)
+        # scales that are exact binary16 values representable as den*127 / den*7
+        before = cases.copy_state(st)
+        oracle.state_step(oracle.MODE_STORED, n8, n4, nz, inp["x"] * 0, inp["dt"], inp["A"], inp["B"], inp["C"],
+                          inp["D"], inp["dt_bias"], inp["perm"], None, None, None, st)
+        for k in ("lo", "hi", "q4", "s8", "s4"):
+            assert (st[k] == before[k]).all(), (layout, k)
+
+
+def test_multi_token_equals_sequential_single_tokens(oracle):
+    rng = np.random.default_rng(6)
+    layout = "24_48_56"
+    n8, n4, nz = cases.ridge_counts(layout)
+    inp = cases.step_inputs(rng, 2, 4, 8, 16, 2)
+    sta = cases.ridge_statics(rng, 2, n8, n4, nz)
+    st0 = cases.random_packed_state(rng, 2, 8, 16, n8, n4, latent=True)
+    a = cases.copy_state(st0)
+    y_all = _ridge(oracle, layout, inp, sta, a)
+    b = cases.copy_state(st0)
+    ys = []
+    for t in range(4):
+        one = {k: (np.ascontiguousarray(v[:, t:t + 1]) if k in ("x", "dt", "B", "C") else v) for k, v in inp.items()}
+        ys.append(_ridge(oracle, layout, one, sta, b))
+    assert all((a[k] == b[k]).all() for k in a)
+    assert (np.concatenate(ys, 1) == y_all).all()
+
+
+def test_ridge_reduces_to_tiers_without_latent_terms(oracle):
+    """Zero basis, zero predictor and zero latent: the ridge row's INT8/INT4
+    codes equal a tier step over the same carried lanes."""
+    rng = np.random.default_rng(7)
+    layout = "36_24_68"
+    n8, n4, nz = cases.ridge_counts(layout)
+    inp = cases.step_inputs(rng, 1, 2, 8, 16, 2)
+    sta = dict(basis=np.zeros((2, nz, 2), np.uint16), lscale=cases.f16(np.full((2, 2), 1e-3)),
+               pred=np.zeros((2, n8 + n4 + 2, nz), np.uint16))
+    st = cases.random_packed_state(rng, 1, 8, 16, n8, n4, latent=True)
+    st["latent"][:] = 0
+    tier = {k: st[k].copy() for k in ("lo", "hi", "q4", "s8", "s4")}
+    y_r = _ridge(oracle, layout, inp, sta, st)
+    y_t = oracle.state_step(oracle.MODE_STORED, n8, n4, nz, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"],
+                            inp["D"], inp["dt_bias"], inp["perm"], None, None, None, tier)
+    for k in tier:
+        assert (tier[k] == st[k]).all(), k
+    assert not st["latent"].any()
+    assert cases.rel_l2(cases.f16_to_f32(y_r), cases.f16_to_f32(y_t)) < 1e-3
+
+
+def test_readout_matches_float64_restatement(oracle):
+    """y against a float64 evaluation of the readout formula from the decoded
+    pre-step carry (catches a dropped/transposed readout term)."""
+    rng = np.random.default_rng(8)
+    layout = "16_64_48"
+    n8, n4, nz = cases.ridge_counts(layout)
+    H, P, G = 8, 16, 2
+    inp = cases.step_inputs(rng, 1, 1, H, P, G, dt_bias_zero=False)
+    sta = cases.ridge_statics(rng, G, n8, n4, nz)
+    st = cases.random_packed_state(rng, 1, H, P, n8, n4, latent=True)
+    pre = cases.copy_state(st)
+    y = cases.f16_to_f32(_ridge(oracle, layout, inp, sta, st))
+    f = cases.f16_to_f32
+    lo, hi, q4 = pre["lo"].astype(np.int32), pre["hi"].astype(np.int32), pre["q4"].astype(np.int32)
+    l8 = np.stack((lo & 15, lo >> 4), -1).reshape(lo.shape[:-1] + (n8,))
+    h8 = np.stack((hi & 15, hi >> 4), -1).reshape(hi.shape[:-1] + (n8,))
+    q8 = ((h8 << 4) | l8).astype(np.int32); q8 -= 256 * (q8 > 127)
+    n4c = np.stack((q4 & 15, q4 >> 4), -1).reshape(q4.shape[:-1] + (n4,)); n4c -= 16 * (n4c > 7)
+    prior = np.concatenate([q8 * f(pre["s8"])[..., None], n4c * f(pre["s4"])[..., None]], -1).astype(np.float64)
+    ls = f(sta["lscale"]).astype(np.float64)
+    lat = torch.from_numpy(pre["latent"]).view(torch.float8_e4m3fn).double().numpy()
+    for h in range(H):
+        g = h // (H // G)
+        perm = inp["perm"][g].astype(np.int64)
+        bv = f(inp["B"][0, 0, g])[perm].astype(np.float64)
+        cv = f(inp["C"][0, 0, g])[perm].astype(np.float64)
+        dtv = math.log1p(math.exp(float(f(inp["dt"][0, 0, h])) + float(f(inp["dt_bias"])[h])))
+        decay = math.exp(float(inp["A"][h]) * dtv)
+        x = f(inp["x"][0, 0, h]).astype(np.float64)
+        L8 = n8 + n4
+        basis = f(sta["basis"][g]).astype(np.float64)
+        pred = f(sta["pred"][g]).astype(np.float64)
+        corr = pred @ cv[L8:]
+        for p in range(P):
+            z = lat[0, h, p] * ls[g]
+            state = prior[0, h, p] * decay + bv[:L8] * dtv * x[p]
+            out = state @ cv[:L8] + decay * (z @ (basis.T @ cv[L8:])) + x[p] * dtv * (bv[L8:] @ cv[L8:])
+            out += x[p] * float(f(inp["D"])[h]) + decay * (prior[0, h, p] @ corr[:L8] + z @ corr[L8:])
+            assert abs(y[0, 0, h, p] - out) <= 2e-3 * max(1.0, abs(out)), (h, p, y[0, 0, h, p], out)
