@@ -1,0 +1,305 @@
+"""Benchmark of the MI355X state codec and FP4 weight decode.
+
+Headline (`value`): algorithmic GB/s of one 56-layer token step of the
+published ridge-latent state codec (fused selective-state step +
+per-token requantization) at batch 64, BASELINE config 4, with the published
+per-layer layouts.  One step = 56 per-layer kernel launches replayed as a
+HIP graph; inputs and packed states are resident in HBM.  Also reported:
+the same step at batch 1 (µs/token, graph of 56 launches), the full 8B FP4
+G16 decode, the measured device-to-device copy
+bandwidth, a live roofline for the dominant kernel, and the CPU oracle
+timed on a bounded sample as a baseline.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-fp4] [--skip-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "mamb2_8b_fp4_recall_sq3.25_amd"))
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+METRIC = "state codec GB/s (frac HBM peak); 56-layer per-token requant µs, batch 1/64"
+HBM_PEAK_GBS = 8000.0
+# evaluation/wt2_test_v1/comparison.json state_provenance.layouts (per layer)
+PUBLISHED_LAYOUTS = (
+    "36_24_68", "16_64_48", "32_32_64", "40_16_72", "16_64_48", "16_64_48", "24_48_56", "32_32_64", "32_32_64",
+    "32_32_64", "32_32_64", "36_24_68", "40_16_72", "24_48_56", "8_80_40", "32_32_64", "32_32_64", "32_32_64",
+    "32_32_64", "24_48_56", "16_64_48", "16_64_48", "24_48_56", "16_64_48", "32_32_64", "24_48_56", "24_48_56",
+    "8_80_40", "40_16_72", "32_32_64", "24_48_56", "24_48_56", "40_16_72", "36_24_68", "16_64_48", "8_80_40",
+    "16_64_48", "24_48_56", "44_8_76", "36_24_68", "24_48_56", "24_48_56", "16_64_48", "32_32_64", "8_80_40",
+    "32_32_64", "8_80_40", "8_80_40", "24_48_56", "8_80_40", "16_64_48", "44_8_76", "44_8_76", "8_80_40",
+    "24_48_56", "32_32_64")
+H, P, G, NSTATE = 128, 64, 8, 128
+
+
+def ridge_counts(layout):
+    a, b, c = map(int, layout.split("_"))
+    return a, b - 4, c + 4
+
+
+def step_bytes(batch, layouts):
+    """Algorithmic HBM bytes of one 56-layer step: per layer
+    889,088*B (packed state in+out 2*52*8192, x and y 2*16384, B and C 4096,
+    dt 256) plus statics perm 1024 + basis 32*nz + lscale 32 +
+    predictor 16*F*nz + A/D/dt_bias 1024."""
+    total = 0
+    for layout in layouts:
+        n8, n4, nz = ridge_counts(layout)
+        F = n8 + n4 + 2
+        total += 889_088 * batch + 1024 + 32 * nz + 32 + 16 * F * nz + 1024
+    return total
+
+
+class RidgeStack:
+    """56 layers of resident inputs, statics and packed states."""
+
+    def __init__(self, batch, device, seed=2026):
+        from mamba2_recall import _native, ridge_codec
+        self.native = _native
+        self.batch = batch
+        self.device = device
+        gen = torch.Generator(device=device).manual_seed(seed)
+        f16 = torch.float16
+        self.layers = []
+        for i, layout in enumerate(PUBLISHED_LAYOUTS):
+            n8, n4, nz = ridge_counts(layout)
+            F = n8 + n4 + 2
+            d = dict(layout=layout, n8=n8, n4=n4, nz=nz)
+            d["x"] = torch.randn((batch, 1, H, P), generator=gen, device=device).to(f16)
+            d["dt"] = torch.randn((batch, 1, H), generator=gen, device=device).to(f16)
+            u = torch.rand(H, generator=gen, device=device) * float(np.log(16.0))
+            d["A"] = (-torch.exp(u)).float().contiguous()
+            d["B"] = torch.randn((batch, 1, G, NSTATE), generator=gen, device=device).to(f16)
+            d["C"] = torch.randn((batch, 1, G, NSTATE), generator=gen, device=device).to(f16)
+            d["D"] = torch.randn(H, generator=gen, device=device).to(f16)
+            d["dt_bias"] = torch.zeros(H, device=device, dtype=f16)
+            d["perm"] = torch.stack([torch.randperm(NSTATE, generator=gen, device=device)
+                                     for _ in range(G)]).to(torch.uint8).contiguous()
+            d["basis"] = (torch.randn((G, nz, 2), generator=gen, device=device) * 0.03).to(f16)
+            d["lscale"] = torch.full((G, 2), 0.001, device=device, dtype=f16)
+            d["pred"] = (torch.randn((G, F, nz), generator=gen, device=device) * 0.05).to(f16)
+            d["state"] = ridge_codec.allocate_state(batch, H, P, NSTATE, device, layout=layout)
+            d["y"] = torch.empty_like(d["x"])
+            self.layers.append(d)
+        # warm the carry from zero with 16 tokens per layer
+        for d in self.layers:
+            xs = d["x"].expand(batch, 16, H, P).contiguous()
+            dts = d["dt"].expand(batch, 16, H).contiguous()
+            Bs = d["B"].expand(batch, 16, G, NSTATE).contiguous()
+            Cs = d["C"].expand(batch, 16, G, NSTATE).contiguous()
+            ridge_codec.scan(xs, dts, d["A"], Bs, Cs, d["D"], d["dt_bias"], d["state"], d["perm"], d["basis"],
+                             d["lscale"], d["pred"], layout=d["layout"])
+        torch.cuda.synchronize()
+
+    def launch_all(self, stream_handle):
+        p = self.native.ptr
+        for d in self.layers:
+            t = d["state"].tensors
+            self.native.call("m2r_state_step_ridge", p(d["x"]), p(d["dt"]), p(d["A"]), p(d["B"]), p(d["C"]),
+                             p(d["D"]), 0, p(d["dt_bias"]), 0, p(d["perm"]), p(d["basis"]), p(d["lscale"]),
+                             p(d["pred"]), p(t["lo"]), p(t["hi"]), p(t["q4"]), p(t["latent"]), p(t["s8"]),
+                             p(t["s4"]), p(d["y"]), self.batch, 1, H, P, G, d["n8"], d["n4"], d["nz"],
+                             stream_handle)
+
+    def graph(self):
+        import ctypes
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            self.launch_all(ctypes.c_void_p(s.cuda_stream))   # untimed warm-up on the side stream
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            self.launch_all(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        return g
+
+
+def time_graph(g, steps, warmup):
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(steps):
+        g.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return ev0.elapsed_time(ev1) / steps, wall * 1e3 / steps
+
+
+def kernel_average_us(stack, reps):
+    """Average duration of the per-layer step kernel, from HIP events on the
+    launch stream over `reps` back-to-back eager 56-launch sweeps."""
+    import ctypes
+    h = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    stack.launch_all(h)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(reps):
+        stack.launch_all(h)
+    ev1.record()
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) * 1e3 / (reps * len(PUBLISHED_LAYOUTS))
+
+
+def copy_bandwidth(device):
+    a = torch.empty(1 << 30, dtype=torch.uint8, device=device)
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(10):
+        b.copy_(a)
+    ev1.record()
+    torch.cuda.synchronize()
+    gbs = 2 * a.numel() * 10 / (ev0.elapsed_time(ev1) * 1e-3) / 1e9
+    del a, b
+    torch.cuda.empty_cache()
+    return gbs
+
+
+def fp4_full_decode(device, steps=3):
+    """56 x in_proj [18560,4096] + 56 x out_proj [4096,8192]
+    + embedding and lm_head [256000,4096]; random nibbles, lognormal(-3,0.5)
+    block scales in the reference G16 format (E4M3 of s/global, global =
+    max(s)/448)."""
+    from mamba2_recall import fp4
+    shapes = [(18560, 4096)] * 56 + [(4096, 8192)] * 56 + [(256000, 4096)] * 2
+    gen = torch.Generator(device=device).manual_seed(7)
+    mats = []
+    for rows, cols in shapes:
+        packed = torch.randint(0, 256, (rows, cols // 2), generator=gen, device=device, dtype=torch.uint8)
+        s = torch.exp(torch.randn((rows, cols // 16), generator=gen, device=device) * 0.5 - 3.0)
+        g = (s.max() / 448.0).float().reshape(1)
+        sb = (s / g).clamp(0, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+        out = torch.empty((rows, cols), dtype=torch.float16, device=device)
+        mats.append((packed, sb, g, out, rows, cols))
+    nbytes = sum(r * c // 2 + r * c // 16 + 4 + r * c * 2 for r, c in shapes)
+    assert nbytes == 21_098_136_008
+
+    def run():
+        for packed, sb, g, out, rows, cols in mats:
+            fp4.decode_into(packed, sb, g, out, rows=rows, columns=cols, group=16)
+    run()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        run()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    del mats
+    torch.cuda.empty_cache()
+    return ms, nbytes / (ms * 1e-3) / 1e9
+
+
+def cpu_baseline(budget_s=12.0):
+    """The C oracle (OpenMP over rows) on a bounded sample of the batch-64
+    workload: consecutive published layers at batch 8 until the budget is
+    spent; throughput in algorithmic GB/s."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import cases
+    from oracle import oracle
+    oracle.build()
+    rng = np.random.default_rng(1)
+    batch = 8
+    done_bytes, elapsed, layers = 0, 0.0, 0
+    for layout in PUBLISHED_LAYOUTS:
+        n8, n4, nz = ridge_counts(layout)
+        inp = cases.step_inputs(rng, batch, 1, H, P, G)
+        sta = cases.ridge_statics(rng, G, n8, n4, nz)
+        st = cases.random_packed_state(rng, batch, H, P, n8, n4, latent=True)
+        t0 = time.perf_counter()
+        oracle.state_step(oracle.MODE_RIDGE, n8, n4, nz, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"],
+                          inp["D"], inp["dt_bias"], inp["perm"], sta["basis"], sta["lscale"], sta["pred"], st)
+        elapsed += time.perf_counter() - t0
+        done_bytes += step_bytes(batch, (layout,))
+        layers += 1
+        if elapsed >= budget_s:
+            break
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return dict(value=round(done_bytes / elapsed / 1e9, 4), unit="GB/s", cores=cores, kind="port",
+                sample=f"C oracle (OpenMP over rows), {layers} consecutive published ridge layers at batch {batch}, "
+                       f"1 token each, {elapsed:.1f} s")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--skip-fp4", action="store_true")
+    ap.add_argument("--skip-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the state codec and FP4 decode shard with no communication "
+              "(rows by sequence or B/C group; weights by matrix rows), so multi-GPU runs are not part of "
+              "this build. Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    device = torch.device("cuda:0")
+    from mamba2_recall import _native
+    _native.lib()
+
+    stack = RidgeStack(args.batch, device)
+    g = stack.graph()
+    ms, wall_ms = time_graph(g, args.steps, args.warmup)
+    nbytes = step_bytes(args.batch, PUBLISHED_LAYOUTS)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    kern_us = kernel_average_us(stack, max(2, args.steps // 5))
+    per_launch = nbytes / len(PUBLISHED_LAYOUTS)
+    achieved = per_launch / (kern_us * 1e-6) / 1e9
+    del g, stack
+    torch.cuda.empty_cache()
+
+    stack1 = RidgeStack(1, device, seed=2027)
+    g1 = stack1.graph()
+    ms1, _ = time_graph(g1, max(args.steps, 50), args.warmup)
+    del g1, stack1
+    torch.cuda.empty_cache()
+
+    copy_gbs = copy_bandwidth(device)
+    extra = dict(batch1_us_per_token=round(ms1 * 1e3, 2), batch1_gbs=round(step_bytes(1, PUBLISHED_LAYOUTS) / (ms1 * 1e-3) / 1e9, 1),
+                 batch64_us_per_token=round(ms * 1e3, 2), wall_ms_per_step=round(wall_ms, 4),
+                 d2d_copy_gbs=round(copy_gbs, 1), hbm_frac_of_copy=round(gbs / copy_gbs, 4))
+    if not args.skip_fp4:
+        fp4_ms, fp4_gbs = fp4_full_decode(device)
+        extra.update(fp4_g16_full_decode_ms=round(fp4_ms, 3), fp4_g16_full_decode_gbs=round(fp4_gbs, 1),
+                     fp4_g16_full_decode_frac=round(fp4_gbs / HBM_PEAK_GBS, 4))
+    line = dict(
+        metric=METRIC, value=round(gbs, 2), unit="GB/s", n_gpus=1, steps=args.steps, warmup=args.warmup,
+        ms_per_step=round(ms, 5), higher_is_better=True, scaling="weak", vs_baseline=None, dtype="f32",
+        data="synthetic",
+        config=dict(workload="56-layer ridge-latent state step + per-token requant (BASELINE config 4, one token)",
+                    batch=args.batch, layers=56, heads=H, headdim=P, d_state=NSTATE, groups=G,
+                    layouts="published per-layer (wt2_test_v1)", launch="HIP graph of 56 per-layer kernels",
+                    algorithmic_bytes_per_step=nbytes),
+        roofline=dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                      frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
+                      kernel="k_state_step (ridge)", avg_launch_us=round(kern_us, 3),
+                      algorithmic_bytes_per_launch=round(per_launch)),
+        extra=extra)
+    if not args.skip_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

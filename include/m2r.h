@@ -140,6 +140,10 @@ int m2r_fp4_decode_g64(const uint8_t* packed, const void* f16_scales, void* out_
 int m2r_probe_stored_quantize(const float* v, const void* s_f16, int32_t* q, int64_t n, int limit, hipStream_t stream);
 int m2r_probe_unary(const uint32_t* in, uint32_t* out, int64_t n, int op, hipStream_t stream);
 int m2r_probe_div(const float* a, const float* d, float* q, int64_t n, hipStream_t stream);
+/* One wave (in: 192 floats, out: 386 floats): out[64*l + lane] is the
+ * level-l butterfly pair sum of in[lane] (l = 0..5); out[384] / out[385] are
+ * the canonical adjacent-pair tree sums of in[64..191] / in[0..63]. */
+int m2r_probe_butterfly(const float* in, float* out, hipStream_t stream);
 
 #ifdef __cplusplus
 }

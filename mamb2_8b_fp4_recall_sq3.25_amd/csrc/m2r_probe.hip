@@ -4,6 +4,7 @@
 #include <string.h>
 #include "m2r_device.h"
 #include "m2r_abi_util.h"
+#include "m2r_tile.h"
 
 static thread_local char g_err[512];
 
@@ -71,9 +72,31 @@ __global__ void k_probe_div(const float* a, const float* d, float* q, int64_t n)
   q[i] = div_by_recip(a[i], dd, 1.0f / dd);
 }
 
+// One wave: out[level * 64 + lane] = butterfly_add<level>(in[lane]) for the
+// six butterfly levels, and out[384 + w] = wave_pair_tree<128> of the 128
+// values in[64 + 2*lane], in[64 + 2*lane + 1] (w = 0) / <64> of in[lane] (w = 1).
+__global__ __launch_bounds__(64) void k_probe_butterfly(const float* in, float* out) {
+  const int lane = threadIdx.x;
+  const float v = in[lane];
+  out[0 * 64 + lane] = butterfly_add<0>(v);
+  out[1 * 64 + lane] = butterfly_add<1>(v);
+  out[2 * 64 + lane] = butterfly_add<2>(v);
+  out[3 * 64 + lane] = butterfly_add<3>(v);
+  out[4 * 64 + lane] = butterfly_add<4>(v);
+  out[5 * 64 + lane] = butterfly_add<5>(v);
+  const float t128 = wave_pair_tree<128>(in[64 + 2 * lane], in[65 + 2 * lane]);
+  const float t64 = wave_pair_tree<64>(v, 0.f);
+  if (lane == 0) { out[384] = t128; out[385] = t64; }
+}
+
 }  // namespace m2r
 
 using namespace m2r;
+
+extern "C" int m2r_probe_butterfly(const float* in, float* out, hipStream_t stream) {
+  hipLaunchKernelGGL(k_probe_butterfly, dim3(1), dim3(64), 0, stream, in, out);
+  return m2r_check(hipGetLastError(), "probe butterfly");
+}
 
 extern "C" int m2r_probe_stored_quantize(const float* v, const void* s_f16, int32_t* q, int64_t n, int limit,
                                          hipStream_t stream) {

@@ -52,27 +52,107 @@ struct StepArgs {
   int d_f32, db_f32;
 };
 
+// Per-token values shared by the workgroup (one B/C group, WPB heads): the
+// permuted B and C, dt activation and decay per head, B*dt per head, the
+// ridge correction and dead-tier dot products.  Loads are issued first and
+// the binary64 dt activation runs while they are in flight.
+template <int N8, int N4, int NZ, int MODE, int WPB>
+struct TokenShared {
+  static constexpr int NL = N8 + N4;
+  static constexpr int F = NL + 2;
+  float b[128], c[128];
+  float bdt[WPB][NL];
+  float dtv[WPB], decay[WPB], dead[WPB];
+  float corr[MODE == MODE_RIDGE ? F + 2 : 4];
+  float dots[8];
+};
+
+template <int N8, int N4, int NZ, int MODE, int WPB>
+__device__ __forceinline__ void token_setup(const StepArgs& a, TokenShared<N8, N4, NZ, MODE, WPB>& sh,
+                                            const uint8_t* s_perm, const float* s_basis, int bt, int g, int h0,
+                                            int tid, int lane, int wave) {
+  constexpr int NL = N8 + N4, F = NL + 2, NT = 64 * WPB;
+  constexpr int RZ = next_pow2(NZ);
+  const int H = a.H, G = a.G;
+  // gather B and C at the permuted positions: one value per thread-slot
+  float gv[256 / NT];
+#pragma unroll
+  for (int k = 0; k < 256 / NT; ++k) {
+    const int i = k * NT + tid, n = i & 127;
+    const uint16_t* src = (i < 128) ? a.Bm : a.Cm;
+    gv[k] = h2f(src[((size_t)bt * G + g) * 128 + (s_perm[n] & 127)]);
+  }
+  if (tid < WPB) {
+    const int hh = h0 + tid;
+    float v = h2f(a.dt[(size_t)bt * H + hh]) + load_param(a.dt_bias, a.db_f32, hh);
+    float dtv = softplus_dt(v);
+    sh.dtv[tid] = dtv;
+    sh.decay[tid] = xexpf(a.A[hh] * dtv);
+  }
+#pragma unroll
+  for (int k = 0; k < 256 / NT; ++k) {
+    const int i = k * NT + tid;
+    if (i < 128) sh.b[i] = gv[k]; else sh.c[i - 128] = gv[k];
+  }
+  __syncthreads();
+  for (int i = tid; i < WPB * NL; i += NT) {
+    const int w = i / NL, n = i - w * NL;
+    sh.bdt[w][n] = sh.b[n] * sh.dtv[w];
+  }
+  if constexpr (MODE == MODE_RIDGE) {
+    // corr[f] = sum_d C[dead d] * pred[g, f, d]: four threads per output,
+    // interleaved d, combined inside the quad (readout-only value)
+    const uint16_t* pg = a.pred + (size_t)g * F * NZ;
+    for (int idx = tid; idx < 4 * F; idx += NT) {
+      const int f = idx >> 2, part = idx & 3;
+      float acc = 0.f;
+#pragma unroll 4
+      for (int d = part; d < NZ; d += 4) acc = __builtin_fmaf(sh.c[NL + d], h2f(pg[f * NZ + d]), acc);
+      acc = butterfly_add<0>(acc);
+      acc = butterfly_add<1>(acc);
+      if (part == 0) sh.corr[f] = acc;
+    }
+    // dead-tier dot products: canonical adjacent-pair trees, one per wave
+#pragma unroll
+    for (int k = 0; k < 5; ++k) {
+      if (wave != k % WPB) continue;
+      float v[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int d0 = (RZ == 128) ? 2 * lane + j : lane;
+        const bool in = (RZ == 128 || j == 0) && d0 < NZ;
+        const int d = in ? d0 : 0;
+        const float bb = sh.b[NL + d], cc = sh.c[NL + d], e0 = s_basis[d], e1 = s_basis[NZ + d];
+        float pr = k == 0 ? bb * cc : k == 1 ? e0 * cc : k == 2 ? e1 * cc : k == 3 ? e0 * bb : e1 * bb;
+        v[j] = in ? pr : 0.f;
+      }
+      const float t = wave_pair_tree<RZ>(v[0], v[1]);
+      if (lane == 0) sh.dots[k] = t;
+    }
+  } else {
+    // dead tier contribution to the readout: sum_d (b_d * dt) * c_d per head
+    float part = 0.f;
+    for (int d = lane; d < NZ; d += 64) part = __builtin_fmaf(sh.b[NL + d] * sh.dtv[wave], sh.c[NL + d], part);
+    part = wave_sum(part);
+    if (lane == 0) sh.dead[wave] = part;
+  }
+  __syncthreads();
+}
+
 template <int N8, int N4, int NZ, int MODE, int WPB>
 __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
   constexpr int W8 = N8 / 2;          // bytes per row of lo and of hi
   constexpr int W4 = N4 / 2;          // bytes per row of q4
   constexpr int NL = N8 + N4;         // carried coordinates
   constexpr int F = NL + 2;           // ridge predictor features
-  constexpr int RZ = next_pow2(NZ);
   constexpr int NT = 64 * WPB;
   constexpr int TILE = 64 * (2 * W8 + W4) + 16;
   constexpr int C8 = N8 / 4, C4 = N4 / 4;   // carried code words (4 biased bytes each)
-  static_assert(N8 % 4 == 0 && N4 % 4 == 0, "tier widths must be multiples of 4");
+  static_assert(N8 % 4 == 0 && N4 % 4 == 0 && NL % 4 == 0, "tier widths must be multiples of 4");
 
   __shared__ __align__(16) uint8_t s_tile[WPB][TILE];
-  __shared__ __align__(16) float s_b[128];
-  __shared__ __align__(16) float s_c[128];
-  __shared__ __align__(16) float s_bdt[WPB][NL > 0 ? NL : 4];
-  __shared__ float s_dtv[WPB], s_decay[WPB], s_dead[WPB];
-  __shared__ __align__(16) float s_corr[MODE == MODE_RIDGE ? F + 2 : 4];
-  __shared__ uint16_t s_pred[MODE == MODE_RIDGE ? F * NZ : 1];
+  __shared__ __align__(16) TokenShared<N8, N4, NZ, MODE, WPB> sh;
   __shared__ float s_basis[MODE == MODE_RIDGE ? 2 * NZ : 1];
-  __shared__ float s_dots[8];
   __shared__ uint8_t s_perm[128];
 
   const int tid = threadIdx.x;
@@ -88,12 +168,26 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
   const bool valid = lane < nvalid;
   const int row0 = (b * H + h) * P + pbase;
   const int row = row0 + lane;
+  uint8_t* tile = s_tile[wave];
+  const bool dword_tiles = (((row0 | nvalid) & 1) == 0);   // row0*W and nvalid*W are dword multiples
 
-  // ---- statics of the group ------------------------------------------------
+  // ---- issue the packed-row and per-row loads --------------------------------
+  TileRegs<W8> tlo, thi;
+  TileRegs<W4> tq4;
+  if (dword_tiles) {
+    if constexpr (W8 > 0) { tile_load<W8>(tlo, a.lo, row0, nvalid, lane); tile_load<W8>(thi, a.hi, row0, nvalid, lane); }
+    if constexpr (W4 > 0) tile_load<W4>(tq4, a.q4, row0, nvalid, lane);
+  }
+  float sc8 = 0.f, sc4 = 0.f;
+  uint32_t lat = 0;
+  if (valid) {
+    sc8 = h2f(a.s8[row]);
+    sc4 = h2f(a.s4[row]);
+    if constexpr (MODE == MODE_RIDGE) lat = ((const uint16_t*)a.latent)[row];
+  }
   for (int n = tid; n < 128; n += NT) s_perm[n] = a.perm[g * 128 + n];
   float ls0 = 0.f, ls1 = 0.f;
   if constexpr (MODE == MODE_RIDGE) {
-    for (int i = tid; i < F * NZ; i += NT) s_pred[i] = a.pred[(size_t)g * F * NZ + i];
     for (int i = tid; i < NZ; i += NT) {
       s_basis[i] = h2f(a.basis[(g * NZ + i) * 2]);
       s_basis[NZ + i] = h2f(a.basis[(g * NZ + i) * 2 + 1]);
@@ -102,20 +196,15 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
     ls1 = h2f(a.lscale[g * 2 + 1]);
   }
   const float Dh = load_param(a.D, a.d_f32, h);
-
-  // ---- load the incoming packed rows -----------------------------------------
-  uint8_t* tile = s_tile[wave];
-  if constexpr (W8 > 0) {
-    wave_copy_in<W8>(tile, a.lo, row0, nvalid, lane);
-    wave_copy_in<W8>(tile + 64 * W8, a.hi, row0, nvalid, lane);
-  }
-  if constexpr (W4 > 0) wave_copy_in<W4>(tile + 128 * W8, a.q4, row0, nvalid, lane);
-  float sc8 = 0.f, sc4 = 0.f;
-  uint32_t lat = 0;
-  if (valid) {
-    sc8 = h2f(a.s8[row]);
-    sc4 = h2f(a.s4[row]);
-    if constexpr (MODE == MODE_RIDGE) lat = ((const uint16_t*)a.latent)[row];
+  if (dword_tiles) {
+    if constexpr (W8 > 0) { tile_store_lds<W8>(tlo, tile, nvalid, lane); tile_store_lds<W8>(thi, tile + 64 * W8, nvalid, lane); }
+    if constexpr (W4 > 0) tile_store_lds<W4>(tq4, tile + 128 * W8, nvalid, lane);
+  } else {
+    if constexpr (W8 > 0) {
+      wave_copy_in<W8>(tile, a.lo, row0, nvalid, lane);
+      wave_copy_in<W8>(tile + 64 * W8, a.hi, row0, nvalid, lane);
+    }
+    if constexpr (W4 > 0) wave_copy_in<W4>(tile + 128 * W8, a.q4, row0, nvalid, lane);
   }
   __syncthreads();
 
@@ -131,7 +220,6 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
 #pragma unroll
       for (int i = 0; i < C8; ++i) {
         uint32_t l = wl[i >> 1] >> (16 * (i & 1)), hh = wh[i >> 1] >> (16 * (i & 1));
-        // l holds lanes 4i..4i+3 in nibbles 0..3 (low 16 bits)
         uint32_t bytes = 0;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -172,73 +260,18 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
 
   for (int t = 0; t < L; ++t) {
     const int bt = b * L + t;
-    // ---- per-token group setup ---------------------------------------------
-    for (int n = tid; n < 128; n += NT) {
-      int pos = s_perm[n] & 127;   // in-bounds even for a malformed table
-      s_b[n] = h2f(a.Bm[((size_t)bt * G + g) * 128 + pos]);
-      s_c[n] = h2f(a.Cm[((size_t)bt * G + g) * 128 + pos]);
-    }
-    if (tid < WPB) {
-      int hh = h0 + tid;
-      float v = h2f(a.dt[(size_t)bt * H + hh]) + load_param(a.dt_bias, a.db_f32, hh);
-      float dtv = softplus_dt(v);
-      s_dtv[tid] = dtv;
-      s_decay[tid] = xexpf(a.A[hh] * dtv);
-    }
-    __syncthreads();
-    for (int i = tid; i < WPB * NL; i += NT) {
-      int w = i / NL, n = i - w * NL;
-      s_bdt[w][n] = s_b[n] * s_dtv[w];
-    }
-    if constexpr (MODE == MODE_RIDGE) {
-      for (int f = tid; f < F; f += NT) {
-        float acc = 0.f;
-        for (int d = 0; d < NZ; ++d) acc = __builtin_fmaf(s_c[NL + d], h2f(s_pred[f * NZ + d]), acc);
-        s_corr[f] = acc;
-      }
-      if (wave == 0) {
-        float pb0[2], pb1[2], pc0[2], pc1[2], pbc[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          int d0 = (RZ == 128) ? 2 * lane + j : lane;
-          bool in = (RZ == 128 || j == 0) && d0 < NZ;
-          int d = in ? d0 : 0;
-          float bb = in ? s_b[NL + d] : 0.f, cc = in ? s_c[NL + d] : 0.f;
-          float e0 = in ? s_basis[d] : 0.f, e1 = in ? s_basis[NZ + d] : 0.f;
-          pbc[j] = in ? bb * cc : 0.f;
-          pc0[j] = in ? e0 * cc : 0.f;
-          pc1[j] = in ? e1 * cc : 0.f;
-          pb0[j] = in ? e0 * bb : 0.f;
-          pb1[j] = in ? e1 * bb : 0.f;
-        }
-        float dbc = wave_pair_tree<RZ>(pbc[0], pbc[1]);
-        float dc0 = wave_pair_tree<RZ>(pc0[0], pc0[1]);
-        float dc1 = wave_pair_tree<RZ>(pc1[0], pc1[1]);
-        float db0 = wave_pair_tree<RZ>(pb0[0], pb0[1]);
-        float db1 = wave_pair_tree<RZ>(pb1[0], pb1[1]);
-        if (lane == 0) {
-          s_dots[0] = dbc; s_dots[1] = dc0; s_dots[2] = dc1; s_dots[3] = db0; s_dots[4] = db1;
-        }
-      }
-    } else {
-      // dead tier contribution to the readout: sum_d (b_d * dt) * c_d per head
-      float part = 0.f;
-      for (int d = lane; d < NZ; d += 64) part = __builtin_fmaf(s_b[NL + d] * s_dtv[wave], s_c[NL + d], part);
-      for (int k = 1; k < 64; k <<= 1) part += __shfl_xor(part, k, 64);
-      if (lane == 0) s_dead[wave] = part;
-    }
-    __syncthreads();
+    const float x = valid ? h2f(a.x[((size_t)bt * H + h) * P + pbase + lane]) : 0.f;
+    token_setup<N8, N4, NZ, MODE, WPB>(a, sh, s_perm, s_basis, bt, g, h0, tid, lane, wave);
 
     // ---- per-row update and readout --------------------------------------------
-    const float decay = s_decay[wave];
-    const float dtv = s_dtv[wave];
-    const float x = valid ? h2f(a.x[((size_t)bt * H + h) * P + pbase + lane]) : 0.f;
+    const float decay = sh.decay[wave];
+    const float dtv = sh.dtv[wave];
     const float nb8 = -128.0f * sc8, nb4 = -8.0f * sc4;   // exact
     float acc = 0.f, accp = 0.f, amax8 = 0.f, amax4 = 0.f;
     float v[NL];
-    const f32x4* bdt4 = (const f32x4*)s_bdt[wave];
-    const f32x4* c4v = (const f32x4*)s_c;
-    const f32x4* p4v = (const f32x4*)s_corr;
+    const f32x4* bdt4 = (const f32x4*)sh.bdt[wave];
+    const f32x4* c4v = (const f32x4*)sh.c;
+    const f32x4* p4v = (const f32x4*)sh.corr;
 #pragma unroll
     for (int i0 = 0; i0 < NL; i0 += 4) {
       const f32x4 cb = bdt4[i0 / 4], cc = c4v[i0 / 4];
@@ -257,6 +290,7 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
         if (i < N8) amax8 = __builtin_fmaxf(amax8, __builtin_fabsf(u));
         else amax4 = __builtin_fmaxf(amax4, __builtin_fabsf(u));
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
     // Materialize the readout accumulators here: otherwise the compiler sinks
     // the whole fma chain into the predicated y store, which keeps every
@@ -264,10 +298,10 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
     asm volatile("" : "+v"(acc), "+v"(accp));
     float out;
     if constexpr (MODE == MODE_RIDGE) {
-      const float dbc = s_dots[0], dc0 = s_dots[1], dc1 = s_dots[2], db0 = s_dots[3], db1 = s_dots[4];
+      const float dbc = sh.dots[0], dc0 = sh.dots[1], dc1 = sh.dots[2], db0 = sh.dots[3], db1 = sh.dots[4];
       const float xdt = x * dtv;
       out = acc + decay * (z0 * dc0 + z1 * dc1) + xdt * dbc + x * Dh
-          + decay * (accp + z0 * s_corr[NL] + z1 * s_corr[NL + 1]);
+          + decay * (accp + z0 * sh.corr[NL] + z1 * sh.corr[NL + 1]);
       z0 = z0 * decay + xdt * db0;
       z1 = z1 * decay + xdt * db1;
       // IEEE division here (not the reciprocal form): the sign of a zero or
@@ -279,7 +313,7 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
       z0 = e4m3_to_f32(e0) * ls0;
       z1 = e4m3_to_f32(e1) * ls1;
     } else {
-      out = acc + x * s_dead[wave] + x * Dh;
+      out = acc + x * sh.dead[wave] + x * Dh;
     }
     if (valid) a.y[((size_t)bt * H + h) * P + pbase + lane] = f2h(out);
 
@@ -307,6 +341,7 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
       int q2 = quantize_code(v[4 * i + 2], d8, r8, 127.0f);
       int q3 = quantize_code(v[4 * i + 3], d8, r8, 127.0f);
       c8[i] = pack4(q0, q1, q2, q3) ^ 0x80808080u;
+      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int i = 0; i < C4; ++i) {
@@ -315,8 +350,8 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
       int q2 = quantize_code(v[N8 + 4 * i + 2], d4, r4, 7.0f);
       int q3 = quantize_code(v[N8 + 4 * i + 3], d4, r4, 7.0f);
       c4[i] = (pack4(q0, q1, q2, q3) & 0x0F0F0F0Fu) ^ 0x08080808u;
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();
   }
 
   // ---- repack to the nibble planes and store ------------------------------------

@@ -14,19 +14,71 @@ __device__ __forceinline__ float load_param(const void* p, int f32, int i) {
   return f32 ? ((const float*)p)[i] : h2f(((const uint16_t*)p)[i]);
 }
 
+// Sum of `v` with the value held by lane ^ (1 << level), for the butterfly
+// levels 0..5 of a 64-lane wave.  Levels 0-1 use quad_perm DPP; levels 2-3
+// use half-row / row mirrors, which pair each lane with a lane of the other
+// aligned half-block (equal to the xor partner's value once every lane of a
+// block holds the block sum); levels 4-5 use ds_bpermute lane exchanges.
+// IEEE addition is commutative, so all lanes of a pair obtain identical bits.
+template <int LEVEL>
+__device__ __forceinline__ float butterfly_add(float v) {
+  const int iv = __builtin_bit_cast(int, v);
+  if constexpr (LEVEL == 0) return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, false));
+  if constexpr (LEVEL == 1) return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, false));
+  if constexpr (LEVEL == 2) return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x141, 0xF, 0xF, false));
+  if constexpr (LEVEL == 3) return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x140, 0xF, 0xF, false));
+  if constexpr (LEVEL == 4) return v + __shfl_xor(v, 16, 64);
+  if constexpr (LEVEL == 5) return v + __shfl_xor(v, 32, 64);
+  return v;
+}
+
 // Adjacent-pair binary tree over RZ = next_pow2(NZ) products, zero padded:
-// level k adds elements (2i, 2i+1) of level k-1.  An XOR butterfly computes
-// exactly this tree because IEEE addition is commutative.  Every lane
-// receives the total.  `v0`/`v1` are the products at 2*lane and 2*lane+1
-// when RZ == 128, else `v0` is the product at `lane`.
+// level k adds elements (2i, 2i+1) of level k-1.  The butterfly computes
+// exactly this tree.  Every lane receives the total.  `v0`/`v1` are the
+// products at 2*lane and 2*lane+1 when RZ == 128, else `v0` is the product
+// at `lane`.
 template <int RZ>
 __device__ __forceinline__ float wave_pair_tree(float v0, float v1) {
-  float s;
-  int levels;
-  if constexpr (RZ == 128) { s = v0 + v1; levels = 6; }
-  else { s = v0; levels = (RZ >= 64) ? 6 : (RZ >= 32 ? 5 : (RZ >= 16 ? 4 : (RZ >= 8 ? 3 : (RZ >= 4 ? 2 : (RZ >= 2 ? 1 : 0))))); }
-  for (int k = 0; k < levels; ++k) s = s + __shfl_xor(s, 1 << k, 64);
+  float s = (RZ == 128) ? v0 + v1 : v0;
+  constexpr int levels = (RZ >= 64) ? 6 : (RZ >= 32 ? 5 : (RZ >= 16 ? 4 : (RZ >= 8 ? 3 : (RZ >= 4 ? 2 : (RZ >= 2 ? 1 : 0)))));
+  if constexpr (levels > 0) s = butterfly_add<0>(s);
+  if constexpr (levels > 1) s = butterfly_add<1>(s);
+  if constexpr (levels > 2) s = butterfly_add<2>(s);
+  if constexpr (levels > 3) s = butterfly_add<3>(s);
+  if constexpr (levels > 4) s = butterfly_add<4>(s);
+  if constexpr (levels > 5) s = butterfly_add<5>(s);
   return s;
+}
+
+// Wave sum in any order (readout-only quantities).
+__device__ __forceinline__ float wave_sum(float v) { return wave_pair_tree<64>(v, 0.f); }
+
+// Dword-granular tile transfers split into a load phase (registers) and a
+// store phase, so that all of a wave's global loads can be in flight before
+// the first wait.  KW = dwords per lane = ceil(16 * W / 64).
+template <int W>
+struct TileRegs { uint32_t r[(16 * W + 63) / 64]; };
+
+template <int W>
+__device__ __forceinline__ void tile_load(TileRegs<W>& t, const uint8_t* g, int row0, int nvalid, int lane) {
+  const uint32_t* src = (const uint32_t*)(g + (size_t)row0 * W);
+  const int ndw = nvalid * W / 4;
+#pragma unroll
+  for (int k = 0; k < (16 * W + 63) / 64; ++k) {
+    int i = k * 64 + lane;
+    t.r[k] = (i < ndw) ? src[i] : 0u;
+  }
+}
+
+template <int W>
+__device__ __forceinline__ void tile_store_lds(const TileRegs<W>& t, uint8_t* lds, int nvalid, int lane) {
+  uint32_t* dst = (uint32_t*)lds;
+  const int ndw = nvalid * W / 4;
+#pragma unroll
+  for (int k = 0; k < (16 * W + 63) / 64; ++k) {
+    int i = k * 64 + lane;
+    if (i < ndw) dst[i] = t.r[k];
+  }
 }
 
 // Reads W (even) bytes at lds[off .. off+W) (off even) as little-endian

@@ -87,3 +87,30 @@ def test_stored_quantize_every_scale_boundary(oracle, device, limit):
     _native.call("m2r_probe_stored_quantize", _native.ptr(vd), _native.ptr(sd), _native.ptr(q), vals.size, limit,
                  _native.stream_of(vd))
     assert (q.cpu().numpy() == want).all()
+
+
+def test_butterfly_levels_and_pair_tree(device):
+    """Each butterfly level adds the xor partner's value, and the wave tree
+    equals the canonical adjacent-pair tree (bit-exact)."""
+    lanes = np.arange(64, dtype=np.float32)
+    vals = np.random.default_rng(9).standard_normal(128).astype(np.float32)
+    inp = torch.from_numpy(np.concatenate([lanes, vals])).to(device)
+    out = torch.empty(386, dtype=torch.float32, device=device)
+    _native.call("m2r_probe_butterfly", _native.ptr(inp), _native.ptr(out), _native.stream_of(inp))
+    o = out.cpu().numpy()
+    ln = np.arange(64)
+    # levels 2 and 3 are mirrors inside the (half-)row: the partner lies in the
+    # other aligned half-block, which is all the tree needs
+    expect = {0: ln ^ 1, 1: ln ^ 2, 2: (ln & ~7) | (7 - (ln & 7)), 3: (ln & ~15) | (15 - (ln & 15)),
+              4: ln ^ 16, 5: ln ^ 32}
+    got = {lv: (o[lv * 64:(lv + 1) * 64] - lanes).astype(np.int64) for lv in range(6)}
+    for level in range(6):
+        assert (got[level] == expect[level]).all(), (level, got[level].tolist())
+
+    def tree(v):
+        v = v.copy()
+        while v.size > 1:
+            v = (v[0::2] + v[1::2]).astype(np.float32)
+        return v[0]
+    assert o[384].view(np.uint32) == tree(vals).view(np.uint32)
+    assert o[385].view(np.uint32) == tree(lanes).view(np.uint32)
