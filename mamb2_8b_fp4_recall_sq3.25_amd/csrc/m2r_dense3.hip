@@ -106,9 +106,9 @@ __global__ __launch_bounds__(64 * WPB) void k_dense3_step(Dense3Args a) {
     if (tid < WPB) {
       int hh = h0 + tid;
       float v = h2f(a.dt[(size_t)bt * H + hh]) + load_param(a.dt_bias, a.db_f32, hh);
-      float dtv = softplus_dt(v);
-      s_dtv[tid] = dtv;
-      s_decay[tid] = xexpf(a.A[hh] * dtv);
+      const float2 act = dt_activation(v, a.A[hh]);
+      s_dtv[tid] = act.x;
+      s_decay[tid] = act.y;
     }
     __syncthreads();
     for (int i = tid; i < WPB * 128; i += NT) {
@@ -151,10 +151,10 @@ __global__ __launch_bounds__(64 * WPB) void k_dense3_step(Dense3Args a) {
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
       const float d = (i < 16) ? den0 : den1, r = (i < 16) ? r0 : r1;
-      int q0 = quantize_code(v[4 * i], d, r, 3.0f);
-      int q1 = quantize_code(v[4 * i + 1], d, r, 3.0f);
-      int q2 = quantize_code(v[4 * i + 2], d, r, 3.0f);
-      int q3 = quantize_code(v[4 * i + 3], d, r, 3.0f);
+      int q0 = quantize_code(v[4 * i], d, r, QTOP3);
+      int q1 = quantize_code(v[4 * i + 1], d, r, QTOP3);
+      int q2 = quantize_code(v[4 * i + 2], d, r, QTOP3);
+      int q3 = quantize_code(v[4 * i + 3], d, r, QTOP3);
       c[i] = (pack4(q0, q1, q2, q3) & 0x07070707u) ^ 0x04040404u;   // (q & 7) ^ 4 == q + 4
     }
     __syncthreads();
@@ -212,8 +212,8 @@ __global__ __launch_bounds__(64) void k_s16_step(S16Args a) {
       s_c[n] = h2f(a.Cm[((size_t)bt * G + g) * 128 + n]);
     }
     __syncthreads();
-    float dtv = softplus_dt(h2f(a.dt[(size_t)bt * H + h]) + bias);
-    float decay = xexpf(av * dtv);
+    const float2 act = dt_activation(h2f(a.dt[(size_t)bt * H + h]) + bias, av);
+    const float dtv = act.x, decay = act.y;
     float x = valid ? h2f(a.x[((size_t)bt * H + h) * P + pbase + lane]) : 0.f;
     float acc = 0.f;
 #pragma unroll

@@ -47,22 +47,34 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
 
 // Round-to-nearest-even binary32 -> E4M3FN for |x| <= 448 (callers clamp
 // first, as the reference does).  NaN maps to 0x7F with the input's sign.
+// Both magnitude paths are computed and selected (no divergent branches).
 __device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
-  uint32_t u = __builtin_bit_cast(uint32_t, x);
-  uint32_t sign = (u >> 24) & 0x80u;
-  uint32_t a = u & 0x7FFFFFFFu;
-  if (a > 0x7F800000u) return sign | 0x7Fu;
-  uint32_t code;
-  if (a < 0x3C800000u) {
-    // below 2^-6: multiples of 2^-9; scaling by 512 is exact, rint is RNE.
-    float q = __builtin_rintf(__builtin_bit_cast(float, a) * 512.0f);
-    code = (uint32_t)q;                              // 8 carries into 0x08 = 2^-6
-  } else {
-    uint32_t r = a + 0x7FFFFu + ((a >> 20) & 1u);    // RNE at 3 mantissa bits
-    r &= ~0xFFFFFu;
-    code = (((r >> 23) - 120u) << 3) | ((r >> 20) & 7u);
-  }
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7FFFFFFFu;
+  // below 2^-6: multiples of 2^-9; scaling by 512 is exact, rint is RNE, and
+  // a carry to 8 is exactly the code of 2^-6
+  const float sub = __builtin_rintf(__builtin_fminf(__builtin_bit_cast(float, a), 0x1p-6f) * 512.0f);
+  const uint32_t cs = (uint32_t)sub;
+  const uint32_t r = (a + 0x7FFFFu + ((a >> 20) & 1u)) & ~0xFFFFFu;   // RNE at 3 mantissa bits
+  const uint32_t cn = (((r >> 23) - 120u) << 3) | ((r >> 20) & 7u);
+  uint32_t code = (a < 0x3C800000u) ? cs : cn;
+  code = (a > 0x7F800000u) ? 0x7Fu : code;
   return sign | code;
+}
+
+// z / ls for the latent byte, in reciprocal form (y = RN(1/ls)).  z is first
+// clamped to +-464*ls (exact: 464 has 5 significant bits, ls 11), beyond which
+// both this and IEEE division clamp to +-448 downstream; the sign of z is then
+// restored so signed zeros and underflowed quotients keep the IEEE sign.  The
+// E4M3 byte of clamp(result, +-448) equals that of IEEE z / ls for every
+// finite z and binary16 ls > 0 (exhaustive over ls in the CPU checks).
+__device__ __forceinline__ float latent_quotient(float z, float ls, float y) {
+  const float top = 464.0f * ls;
+  const float c = __builtin_fminf(__builtin_fmaxf(z, -top), top);
+  const float q0 = c * y;
+  const float r = __builtin_fmaf(-q0, ls, c);
+  return __builtin_copysignf(__builtin_fmaf(r, y, q0), z);
 }
 
 // ---------------------------------------------------------------------------
@@ -83,12 +95,18 @@ __device__ __forceinline__ float div_by_recip(float a, float d, float y) {
   return __builtin_fmaf(r, y, q0);
 }
 
-// clamp(roundf(RN(v/d)), -lim, lim) as an integer, with y = RN(1/d).
-__device__ __forceinline__ int quantize_code(float v, float d, float y, float lim) {
-  float q = round_half_away(div_by_recip(v, d, y));
-  q = __builtin_fminf(__builtin_fmaxf(q, -lim), lim);
-  return (int)q;
+// clamp(roundf(RN(v/d)), -lim, lim) as an integer, with y = RN(1/d) and
+// top = the largest binary32 below lim + 1.  roundf(q) is trunc(q + copysign(
+// pred(0.5), q)); clamping that sum to +-top before the truncating integer
+// conversion equals clamping the rounded value to +-lim.
+__device__ __forceinline__ int quantize_code(float v, float d, float y, float top) {
+  const float q = div_by_recip(v, d, y);
+  const float t = q + __builtin_copysignf(0x1.fffffep-2f, q);
+  return (int)__builtin_fminf(__builtin_fmaxf(t, -top), top);
 }
+constexpr float QTOP127 = 0x1.fffffep+6f;   // below 128
+constexpr float QTOP7 = 0x1.fffffep+2f;     // below 8
+constexpr float QTOP3 = 0x1.fffffep+1f;     // below 4
 
 // ---------------------------------------------------------------------------
 // Transcendentals.  The codec defines exp/log of a binary32 argument as the
@@ -164,6 +182,14 @@ __device__ __forceinline__ float softplus_dt(float v) {
     return xlogf(e + 1.0f);
   }
   return v;
+}
+
+// dt activation and decay for one head, out of line: the binary64
+// polynomial constants then live only inside the call instead of being
+// hoisted into VGPRs for the whole token loop of the calling kernel.
+__device__ __attribute__((noinline)) inline float2 dt_activation(float dt_plus_bias, float A) {
+  const float dtv = softplus_dt(dt_plus_bias);
+  return make_float2(dtv, xexpf(A * dtv));
 }
 
 }  // namespace m2r

@@ -32,7 +32,7 @@ __global__ void k_probe_stored_quantize(const float* v, const uint16_t* s, int32
   float sc = h2f(s[i]);
   bool z = !(sc > 0.f) || sc == __builtin_inff();
   float d = z ? 1.f : sc, r = z ? 0.f : 1.0f / sc;
-  q[i] = quantize_code(v[i], d, r, lim);
+  q[i] = quantize_code(v[i], d, r, lim == 7.0f ? QTOP7 : QTOP127);
 }
 
 // Elementwise primitives, selected by `op`:

@@ -52,47 +52,131 @@ struct StepArgs {
   int d_f32, db_f32;
 };
 
+// Carried coordinates are held in an internal lane order that makes the
+// conversion between the nibble planes and code bytes two bitfield inserts
+// per four coordinates: within each tier, every full group of 8 packed lanes
+// is ordered (0,2,4,6,1,3,5,7) and a final group of 4 is ordered (0,2,1,3).
+// packed_lane<N8,N4>(j) is the packed lane of internal position j (< N8+N4);
+// the zero tier keeps its natural order.
+constexpr int tier_packed_of(int j, int T) {
+  const int g = j / 8, k = j % 8;
+  if (g * 8 + 8 <= T) return g * 8 + (k < 4 ? 2 * k : 2 * (k - 4) + 1);
+  return g * 8 + (k < 2 ? 2 * k : 2 * (k - 2) + 1);
+}
+template <int N8, int N4>
+__device__ __forceinline__ int packed_lane(int j) {
+  return j < N8 ? tier_packed_of(j, N8) : (j < N8 + N4 ? N8 + tier_packed_of(j - N8, N4) : j);
+}
+
+// nibble-plane words -> carried code-byte words for one tier.
+// INT8: lo/hi plane words (8 lanes per word); byte = (q + 128) = code ^ 0x80.
+template <int N>
+__device__ __forceinline__ void planes_to_bytes8(const uint32_t* wl, const uint32_t* wh, uint32_t* c) {
+#pragma unroll
+  for (int g = 0; g < (N + 7) / 8; ++g) {
+    const uint32_t hb = wh[g] ^ 0x88888888u;                                   // bias via the high nibble
+    const uint32_t e = (wl[g] & 0x0F0F0F0Fu) | ((hb << 4) & 0xF0F0F0F0u);
+    const uint32_t o = ((wl[g] >> 4) & 0x0F0F0F0Fu) | (hb & 0xF0F0F0F0u);
+    if (g * 8 + 8 <= N) { c[2 * g] = e; c[2 * g + 1] = o; }
+    else c[2 * g] = (e & 0xFFFFu) | (o << 16);
+  }
+}
+// INT4: q4 plane words; byte = (q + 8) = nibble ^ 8.
+template <int N>
+__device__ __forceinline__ void plane_to_bytes4(const uint32_t* wq, uint32_t* c) {
+#pragma unroll
+  for (int g = 0; g < (N + 7) / 8; ++g) {
+    const uint32_t q = wq[g] ^ 0x88888888u;
+    const uint32_t e = q & 0x0F0F0F0Fu, o = (q >> 4) & 0x0F0F0F0Fu;
+    if (g * 8 + 8 <= N) { c[2 * g] = e; c[2 * g + 1] = o; }
+    else c[2 * g] = (e & 0xFFFFu) | (o << 16);
+  }
+}
+// carried bytes -> nibble-plane words (inverse of the two above)
+template <int N>
+__device__ __forceinline__ void bytes_to_planes8(const uint32_t* c, uint32_t* wl, uint32_t* wh) {
+#pragma unroll
+  for (int g = 0; g < (N + 7) / 8; ++g) {
+    uint32_t e, o;
+    if (g * 8 + 8 <= N) { e = c[2 * g]; o = c[2 * g + 1]; }
+    else { e = c[2 * g] & 0xFFFFu; o = c[2 * g] >> 16; }
+    wl[g] = (e & 0x0F0F0F0Fu) | ((o << 4) & 0xF0F0F0F0u);
+    wh[g] = (((e >> 4) & 0x0F0F0F0Fu) | (o & 0xF0F0F0F0u)) ^ 0x88888888u;
+  }
+}
+template <int N>
+__device__ __forceinline__ void bytes_to_plane4(const uint32_t* c, uint32_t* wq) {
+#pragma unroll
+  for (int g = 0; g < (N + 7) / 8; ++g) {
+    uint32_t e, o;
+    if (g * 8 + 8 <= N) { e = c[2 * g]; o = c[2 * g + 1]; }
+    else { e = c[2 * g] & 0xFFFFu; o = c[2 * g] >> 16; }
+    wq[g] = ((e & 0x0F0F0F0Fu) | ((o << 4) & 0xF0F0F0F0u)) ^ 0x88888888u;
+  }
+}
+
 // Per-token values shared by the workgroup (one B/C group, WPB heads): the
 // permuted B and C, dt activation and decay per head, B*dt per head, the
-// ridge correction and dead-tier dot products.  Loads are issued first and
-// the binary64 dt activation runs while they are in flight.
+// ridge correction and dead-tier dot products.
 template <int N8, int N4, int NZ, int MODE, int WPB>
 struct TokenShared {
   static constexpr int NL = N8 + N4;
   static constexpr int F = NL + 2;
-  float b[128], c[128];
+  uint16_t raw[256];                 // B row then C row of the group, original order
+  float b[128], c[128];              // permuted (packed lane order)
   float bdt[WPB][NL];
   float dtv[WPB], decay[WPB], dead[WPB];
   float corr[MODE == MODE_RIDGE ? F + 2 : 4];
   float dots[8];
 };
 
-template <int N8, int N4, int NZ, int MODE, int WPB>
-__device__ __forceinline__ void token_setup(const StepArgs& a, TokenShared<N8, N4, NZ, MODE, WPB>& sh,
-                                            const uint8_t* s_perm, const float* s_basis, int bt, int g, int h0,
-                                            int tid, int lane, int wave) {
-  constexpr int NL = N8 + N4, F = NL + 2, NT = 64 * WPB;
-  constexpr int RZ = next_pow2(NZ);
-  const int H = a.H, G = a.G;
-  // gather B and C at the permuted positions: one value per thread-slot
-  float gv[256 / NT];
-#pragma unroll
-  for (int k = 0; k < 256 / NT; ++k) {
-    const int i = k * NT + tid, n = i & 127;
-    const uint16_t* src = (i < 128) ? a.Bm : a.Cm;
-    gv[k] = h2f(src[((size_t)bt * G + g) * 128 + (s_perm[n] & 127)]);
-  }
-  if (tid < WPB) {
-    const int hh = h0 + tid;
-    float v = h2f(a.dt[(size_t)bt * H + hh]) + load_param(a.dt_bias, a.db_f32, hh);
-    float dtv = softplus_dt(v);
-    sh.dtv[tid] = dtv;
-    sh.decay[tid] = xexpf(a.A[hh] * dtv);
-  }
+// Raw per-token inputs a thread loads: its share of the group's B and C rows
+// (contiguous, independent of the permutation) and, for the first WPB
+// threads, one head's dt.
+template <int WPB>
+struct TokenRaw {
+  uint16_t bc[256 / (64 * WPB)];
+  float dtb;
+};
+
+template <int WPB>
+__device__ __forceinline__ void token_load(const StepArgs& a, TokenRaw<WPB>& r, int bt, int g, int h0, int tid) {
+  constexpr int NT = 64 * WPB;
 #pragma unroll
   for (int k = 0; k < 256 / NT; ++k) {
     const int i = k * NT + tid;
-    if (i < 128) sh.b[i] = gv[k]; else sh.c[i - 128] = gv[k];
+    const uint16_t* src = (i < 128) ? a.Bm : a.Cm;
+    r.bc[k] = src[((size_t)bt * a.G + g) * 128 + (i & 127)];
+  }
+  r.dtb = 0.f;
+  if (tid < WPB) r.dtb = h2f(a.dt[(size_t)bt * a.H + h0 + tid]) + load_param(a.dt_bias, a.db_f32, h0 + tid);
+}
+
+template <int N8, int N4, int NZ, int MODE, int WPB>
+__device__ __forceinline__ void token_store(const StepArgs& a, TokenShared<N8, N4, NZ, MODE, WPB>& sh,
+                                            const TokenRaw<WPB>& r, int h0, int tid) {
+  constexpr int NT = 64 * WPB;
+#pragma unroll
+  for (int k = 0; k < 256 / NT; ++k) sh.raw[k * NT + tid] = r.bc[k];
+  if (tid < WPB) {
+    const float2 act = dt_activation(r.dtb, a.A[h0 + tid]);
+    sh.dtv[tid] = act.x;
+    sh.decay[tid] = act.y;
+  }
+}
+
+// After token_store and a barrier: gather through the permutation, B*dt per
+// head, ridge correction and dead-tier dot products; ends with a barrier.
+template <int N8, int N4, int NZ, int MODE, int WPB>
+__device__ __forceinline__ void token_build(TokenShared<N8, N4, NZ, MODE, WPB>& sh, const uint8_t* s_perm,
+                                            const float* s_basis, const uint16_t* s_pred, int tid, int lane,
+                                            int wave) {
+  constexpr int NL = N8 + N4, F = NL + 2, NT = 64 * WPB;
+  constexpr int RZ = next_pow2(NZ);
+  for (int i = tid; i < 256; i += NT) {
+    const int n = i & 127;   // internal position
+    const float v = h2f(sh.raw[(i & 128) + (s_perm[packed_lane<N8, N4>(n)] & 127)]);
+    if (i < 128) sh.b[n] = v; else sh.c[n] = v;
   }
   __syncthreads();
   for (int i = tid; i < WPB * NL; i += NT) {
@@ -102,17 +186,17 @@ __device__ __forceinline__ void token_setup(const StepArgs& a, TokenShared<N8, N
   if constexpr (MODE == MODE_RIDGE) {
     // corr[f] = sum_d C[dead d] * pred[g, f, d]: four threads per output,
     // interleaved d, combined inside the quad (readout-only value)
-    const uint16_t* pg = a.pred + (size_t)g * F * NZ;
     for (int idx = tid; idx < 4 * F; idx += NT) {
-      const int f = idx >> 2, part = idx & 3;
+      const int j = idx >> 2, part = idx & 3;     // internal feature position
+      const int f = packed_lane<N8, N4>(j);       // predictor row (packed lane; latent rows last)
       float acc = 0.f;
 #pragma unroll 4
-      for (int d = part; d < NZ; d += 4) acc = __builtin_fmaf(sh.c[NL + d], h2f(pg[f * NZ + d]), acc);
+      for (int d = part; d < NZ; d += 4) acc = __builtin_fmaf(sh.c[NL + d], h2f(s_pred[f * NZ + d]), acc);
       acc = butterfly_add<0>(acc);
       acc = butterfly_add<1>(acc);
-      if (part == 0) sh.corr[f] = acc;
+      if (part == 0) sh.corr[j] = acc;
     }
-    // dead-tier dot products: canonical adjacent-pair trees, one per wave
+    // dead-tier dot products: canonical adjacent-pair trees, spread over waves
 #pragma unroll
     for (int k = 0; k < 5; ++k) {
       if (wave != k % WPB) continue;
@@ -148,10 +232,13 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
   constexpr int NT = 64 * WPB;
   constexpr int TILE = 64 * (2 * W8 + W4) + 16;
   constexpr int C8 = N8 / 4, C4 = N4 / 4;   // carried code words (4 biased bytes each)
+  constexpr int PRED_DW = (MODE == MODE_RIDGE) ? F * NZ / 2 : 1;   // F*NZ is even for every layout
   static_assert(N8 % 4 == 0 && N4 % 4 == 0 && NL % 4 == 0, "tier widths must be multiples of 4");
+  static_assert(MODE != MODE_RIDGE || (F * NZ) % 2 == 0, "predictor staged as dwords");
 
   __shared__ __align__(16) uint8_t s_tile[WPB][TILE];
   __shared__ __align__(16) TokenShared<N8, N4, NZ, MODE, WPB> sh;
+  __shared__ __align__(16) uint32_t s_pred32[PRED_DW];
   __shared__ float s_basis[MODE == MODE_RIDGE ? 2 * NZ : 1];
   __shared__ uint8_t s_perm[128];
 
@@ -169,31 +256,40 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
   const int row0 = (b * H + h) * P + pbase;
   const int row = row0 + lane;
   uint8_t* tile = s_tile[wave];
+  const uint16_t* s_pred = (const uint16_t*)s_pred32;
   const bool dword_tiles = (((row0 | nvalid) & 1) == 0);   // row0*W and nvalid*W are dword multiples
 
-  // ---- issue the packed-row and per-row loads --------------------------------
+  // ---- issue every independent load of the first token -------------------------
   TileRegs<W8> tlo, thi;
   TileRegs<W4> tq4;
   if (dword_tiles) {
     if constexpr (W8 > 0) { tile_load<W8>(tlo, a.lo, row0, nvalid, lane); tile_load<W8>(thi, a.hi, row0, nvalid, lane); }
     if constexpr (W4 > 0) tile_load<W4>(tq4, a.q4, row0, nvalid, lane);
   }
-  float sc8 = 0.f, sc4 = 0.f;
+  TokenRaw<WPB> raw;
+  token_load<WPB>(a, raw, b * L, g, h0, tid);
+  float sc8 = 0.f, sc4 = 0.f, x = 0.f;
   uint32_t lat = 0;
   if (valid) {
     sc8 = h2f(a.s8[row]);
     sc4 = h2f(a.s4[row]);
     if constexpr (MODE == MODE_RIDGE) lat = ((const uint16_t*)a.latent)[row];
+    x = h2f(a.x[((size_t)(b * L) * H + h) * P + pbase + lane]);
   }
   for (int n = tid; n < 128; n += NT) s_perm[n] = a.perm[g * 128 + n];
-  float ls0 = 0.f, ls1 = 0.f;
+  float ls0 = 0.f, ls1 = 0.f, rls0 = 0.f, rls1 = 0.f;
   if constexpr (MODE == MODE_RIDGE) {
+    const uint32_t* pg = (const uint32_t*)(a.pred + (size_t)g * F * NZ);
+    for (int i = tid; i < PRED_DW; i += NT) s_pred32[i] = pg[i];
     for (int i = tid; i < NZ; i += NT) {
-      s_basis[i] = h2f(a.basis[(g * NZ + i) * 2]);
-      s_basis[NZ + i] = h2f(a.basis[(g * NZ + i) * 2 + 1]);
+      const uint32_t e = ((const uint32_t*)a.basis)[g * NZ + i];
+      s_basis[i] = h2f((uint16_t)(e & 0xFFFFu));
+      s_basis[NZ + i] = h2f((uint16_t)(e >> 16));
     }
     ls0 = h2f(a.lscale[g * 2]);
     ls1 = h2f(a.lscale[g * 2 + 1]);
+    rls0 = 1.0f / ls0;   // correctly rounded reciprocals
+    rls1 = 1.0f / ls1;
   }
   const float Dh = load_param(a.D, a.d_f32, h);
   if (dword_tiles) {
@@ -206,40 +302,23 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
     }
     if constexpr (W4 > 0) wave_copy_in<W4>(tile + 128 * W8, a.q4, row0, nvalid, lane);
   }
+  token_store<N8, N4, NZ, MODE, WPB>(a, sh, raw, h0, tid);
   __syncthreads();
 
-  // Carried codes: byte k of c8[i] is q8[4i+k] + 128, of c4[i] is q4[4i+k] + 8.
+  // Carried codes, internal lane order: byte k of c8[i] is q8 + 128 of
+  // internal coordinate 4i+k, of c4[i] q4 + 8.
   uint32_t c8[C8 > 0 ? C8 : 1], c4[C4 > 0 ? C4 : 1];
   {
     if constexpr (W8 > 0) {
       uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4];
       lds_read_row<W8>(tile, lane * W8, wl);
       lds_read_row<W8>(tile + 64 * W8, lane * W8, wh);
-      // lo/hi nibble planes -> bytes: lane 2j uses the low nibbles of byte j,
-      // lane 2j+1 the high nibbles.
-#pragma unroll
-      for (int i = 0; i < C8; ++i) {
-        uint32_t l = wl[i >> 1] >> (16 * (i & 1)), hh = wh[i >> 1] >> (16 * (i & 1));
-        uint32_t bytes = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          uint32_t v8 = ((l >> (4 * k)) & 15u) | (((hh >> (4 * k)) & 15u) << 4);
-          bytes |= v8 << (8 * k);
-        }
-        c8[i] = bytes ^ 0x80808080u;
-      }
+      planes_to_bytes8<N8>(wl, wh, c8);
     }
     if constexpr (W4 > 0) {
       uint32_t wq[(W4 + 3) / 4];
       lds_read_row<W4>(tile + 128 * W8, lane * W4, wq);
-#pragma unroll
-      for (int i = 0; i < C4; ++i) {
-        uint32_t l = wq[i >> 1] >> (16 * (i & 1));
-        uint32_t bytes = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) bytes |= ((l >> (4 * k)) & 15u) << (8 * k);
-        c4[i] = bytes ^ 0x08080808u;
-      }
+      plane_to_bytes4<N4>(wq, c4);
     }
     if (!valid) {
 #pragma unroll
@@ -260,8 +339,16 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
 
   for (int t = 0; t < L; ++t) {
     const int bt = b * L + t;
-    const float x = valid ? h2f(a.x[((size_t)bt * H + h) * P + pbase + lane]) : 0.f;
-    token_setup<N8, N4, NZ, MODE, WPB>(a, sh, s_perm, s_basis, bt, g, h0, tid, lane, wave);
+    if (t > 0) {
+      token_store<N8, N4, NZ, MODE, WPB>(a, sh, raw, h0, tid);
+      __syncthreads();
+    }
+    float xn = 0.f;
+    if (t + 1 < L) {   // prefetch the next token's raw inputs
+      token_load<WPB>(a, raw, bt + 1, g, h0, tid);
+      if (valid) xn = h2f(a.x[((size_t)(bt + 1) * H + h) * P + pbase + lane]);
+    }
+    token_build<N8, N4, NZ, MODE, WPB>(sh, s_perm, s_basis, s_pred, tid, lane, wave);
 
     // ---- per-row update and readout --------------------------------------------
     const float decay = sh.decay[wave];
@@ -304,10 +391,8 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
           + decay * (accp + z0 * sh.corr[NL] + z1 * sh.corr[NL + 1]);
       z0 = z0 * decay + xdt * db0;
       z1 = z1 * decay + xdt * db1;
-      // IEEE division here (not the reciprocal form): the sign of a zero or
-      // subnormal quotient decides between latent bytes 0x00 and 0x80.
-      float q0 = __builtin_fminf(__builtin_fmaxf(z0 / ls0, -448.f), 448.f);
-      float q1 = __builtin_fminf(__builtin_fmaxf(z1 / ls1, -448.f), 448.f);
+      float q0 = __builtin_fminf(__builtin_fmaxf(latent_quotient(z0, ls0, rls0), -448.f), 448.f);
+      float q1 = __builtin_fminf(__builtin_fmaxf(latent_quotient(z1, ls1, rls1), -448.f), 448.f);
       uint32_t e0 = f32_to_e4m3(q0), e1 = f32_to_e4m3(q1);
       qz = e0 | (e1 << 8);
       z0 = e4m3_to_f32(e0) * ls0;
@@ -336,53 +421,37 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < C8; ++i) {
-      int q0 = quantize_code(v[4 * i], d8, r8, 127.0f);
-      int q1 = quantize_code(v[4 * i + 1], d8, r8, 127.0f);
-      int q2 = quantize_code(v[4 * i + 2], d8, r8, 127.0f);
-      int q3 = quantize_code(v[4 * i + 3], d8, r8, 127.0f);
+      int q0 = quantize_code(v[4 * i], d8, r8, QTOP127);
+      int q1 = quantize_code(v[4 * i + 1], d8, r8, QTOP127);
+      int q2 = quantize_code(v[4 * i + 2], d8, r8, QTOP127);
+      int q3 = quantize_code(v[4 * i + 3], d8, r8, QTOP127);
       c8[i] = pack4(q0, q1, q2, q3) ^ 0x80808080u;
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int i = 0; i < C4; ++i) {
-      int q0 = quantize_code(v[N8 + 4 * i], d4, r4, 7.0f);
-      int q1 = quantize_code(v[N8 + 4 * i + 1], d4, r4, 7.0f);
-      int q2 = quantize_code(v[N8 + 4 * i + 2], d4, r4, 7.0f);
-      int q3 = quantize_code(v[N8 + 4 * i + 3], d4, r4, 7.0f);
+      int q0 = quantize_code(v[N8 + 4 * i], d4, r4, QTOP7);
+      int q1 = quantize_code(v[N8 + 4 * i + 1], d4, r4, QTOP7);
+      int q2 = quantize_code(v[N8 + 4 * i + 2], d4, r4, QTOP7);
+      int q3 = quantize_code(v[N8 + 4 * i + 3], d4, r4, QTOP7);
       c4[i] = (pack4(q0, q1, q2, q3) & 0x0F0F0F0Fu) ^ 0x08080808u;
       __builtin_amdgcn_sched_barrier(0);
     }
+    x = xn;
+    if (t + 1 < L) __syncthreads();   // shared token values are rebuilt next iteration
   }
 
   // ---- repack to the nibble planes and store ------------------------------------
   if (valid) {
     if constexpr (W8 > 0) {
-      uint32_t wl[(W8 + 3) / 4] = {}, wh[(W8 + 3) / 4] = {};
-#pragma unroll
-      for (int i = 0; i < C8; ++i) {
-        uint32_t q = c8[i] ^ 0x80808080u;   // two's complement code bytes
-        uint32_t l = 0, hh = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          l |= ((q >> (8 * k)) & 15u) << (4 * k);
-          hh |= ((q >> (8 * k + 4)) & 15u) << (4 * k);
-        }
-        wl[i >> 1] |= l << (16 * (i & 1));
-        wh[i >> 1] |= hh << (16 * (i & 1));
-      }
+      uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4];
+      bytes_to_planes8<N8>(c8, wl, wh);
       lds_write_row<W8>(tile, lane * W8, wl);
       lds_write_row<W8>(tile + 64 * W8, lane * W8, wh);
     }
     if constexpr (W4 > 0) {
-      uint32_t wq[(W4 + 3) / 4] = {};
-#pragma unroll
-      for (int i = 0; i < C4; ++i) {
-        uint32_t q = c4[i] ^ 0x08080808u;   // code nibbles in the low half of each byte
-        uint32_t l = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) l |= ((q >> (8 * k)) & 15u) << (4 * k);
-        wq[i >> 1] |= l << (16 * (i & 1));
-      }
+      uint32_t wq[(W4 + 3) / 4];
+      bytes_to_plane4<N4>(c4, wq);
       lds_write_row<W4>(tile + 128 * W8, lane * W4, wq);
     }
   }

@@ -527,13 +527,15 @@ int64_t orc_check_markstein(uint64_t seed, int64_t n_random, int n_boundary_scal
     }
     if (!isfinite(a) || !isfinite(d) || d == 0.0f) continue;
     if (z & 2) a = -a;
-    float lim = (z & 4) ? 127.0f : 7.0f;
+    float lim = (z & 4) ? 127.0f : ((z & 8) ? 7.0f : 3.0f);
     float y = 1.0f / d;
     float q0 = a * y;
     float r = fmaf(-q0, d, a);
     float q = fmaf(r, y, q0);
     if (a != 0.0f && fabsf(a) >= 0x1p-100f && f_bits(q) != f_bits(a / d)) ++dbad;
-    int c1 = (int)fminf(fmaxf(truncf(q + copysignf(0x1.fffffep-2f, q)), -lim), lim);
+    /* device form: clamp below +-(lim+1) and let the int conversion truncate */
+    const float top = nextafterf(lim + 1.0f, 0.0f);
+    int c1 = (int)fminf(fmaxf(q + copysignf(0x1.fffffep-2f, q), -top), top);
     int c2 = (int)fminf(fmaxf(roundf(a / d), -lim), lim);
     if (c1 != c2) ++bad;
   }
@@ -551,7 +553,7 @@ int64_t orc_check_markstein(uint64_t seed, int64_t n_random, int n_boundary_scal
           float r = fmaf(-q0, d, aa);
           float q = fmaf(r, y, q0);
           if (fabsf(aa) >= 0x1p-100f && f_bits(q) != f_bits(aa / d)) ++dbad;
-          int c1 = (int)fminf(fmaxf(truncf(q + copysignf(0x1.fffffep-2f, q)), -127.0f), 127.0f);
+          int c1 = (int)fminf(fmaxf(q + copysignf(0x1.fffffep-2f, q), -0x1.fffffep+6f), 0x1.fffffep+6f);
           int c2 = (int)fminf(fmaxf(roundf(aa / d), -127.0f), 127.0f);
           if (c1 != c2) ++bad;
         }
@@ -559,5 +561,57 @@ int64_t orc_check_markstein(uint64_t seed, int64_t n_random, int n_boundary_scal
     }
   }
   if (div_bad) *div_bad = dbad;
+  return bad;
+}
+
+/* The latent quotient z / ls is taken on the device as
+ * copysign(fma(fma(-z*y, ls, z), y, z*y), z) with y = RN(1/ls); the E4M3 byte
+ * of clamp(quotient, +-448) must equal the one from IEEE division.  Checks
+ * every binary16 ls in [2^-24, 65504] against dense z: all E4M3 values times
+ * ls and their midpoints (+-2 ulps), zeros of both signs, subnormal z, and
+ * pseudo-random z.  Returns the number of differing bytes. */
+int64_t orc_check_latent_division(uint64_t seed, int n_random_per_scale) {
+  int64_t bad = 0;
+#pragma omp parallel for reduction(+ : bad) schedule(dynamic, 64)
+  for (int sb = 1; sb < 0x7C00; ++sb) {
+    const float ls = orc_f16_to_f32((uint16_t)sb);
+    const float y = 1.0f / ls;
+    uint64_t z = seed ^ ((uint64_t)sb * 0x9E3779B97F4A7C15ull);
+    for (int i = -n_random_per_scale - 520; i < n_random_per_scale; ++i) {
+      float zv;
+      if (i < -n_random_per_scale) {
+        int k = i + n_random_per_scale + 520;        /* 0..519 structured cases */
+        if (k < 256) {
+          float e = orc_e4m3_to_f32((uint8_t)(k & 0x7F));
+          zv = bits_f(f_bits(e * ls) + (k >> 7) * 2 - 1);
+        } else if (k < 512) {
+          int kk = k - 256;
+          float e0 = orc_e4m3_to_f32((uint8_t)(kk & 0x7E)), e1 = orc_e4m3_to_f32((uint8_t)((kk & 0x7E) + 1));
+          zv = ((e0 + e1) * 0.5f) * ls;                /* near every rounding midpoint */
+          zv = bits_f(f_bits(zv) + (kk & 1 ? 1 : -1));
+        } else if (k == 512) zv = 0.0f;
+        else if (k == 513) zv = -0.0f;
+        else zv = bits_f((uint32_t)(k * 977));          /* subnormals */
+        if (!isfinite(zv)) continue;                     /* NaN is outside the contract */
+      } else {
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        z ^= z >> 31;
+        zv = bits_f((uint32_t)(z & 0x7FFFFFFFu));
+        if (!isfinite(zv)) continue;
+      }
+      const float top = 464.0f * ls;   /* exact; beyond it both quotients clamp to 448 */
+      for (int sgn = 0; sgn < 2; ++sgn) {
+        const float a = sgn ? -zv : zv;
+        const float ac = fminf(fmaxf(a, -top), top);
+        float q0 = ac * y;
+        float r = fmaf(-q0, ls, ac);
+        float q = copysignf(fmaf(r, y, q0), a);
+        uint8_t b1 = orc_f32_to_e4m3(fminf(fmaxf(q, -448.0f), 448.0f));
+        uint8_t b2 = orc_f32_to_e4m3(fminf(fmaxf(a / ls, -448.0f), 448.0f));
+        if (b1 != b2) ++bad;
+      }
+    }
+  }
   return bad;
 }

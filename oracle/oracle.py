@@ -48,6 +48,8 @@ def lib():
         _lib.orc_check_round_identity.restype = I64
         _lib.orc_check_markstein.argtypes = [ctypes.c_uint64, I64, I, P]
         _lib.orc_check_markstein.restype = I64
+        _lib.orc_check_latent_division.argtypes = [ctypes.c_uint64, I]
+        _lib.orc_check_latent_division.restype = I64
     return _lib
 
 
@@ -132,3 +134,7 @@ def check_markstein(seed: int, n_random: int, n_boundary_scales: int):
 
 def threads():
     return int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+
+
+def check_latent_division(seed: int, n_random_per_scale: int) -> int:
+    return int(lib().orc_check_latent_division(seed, n_random_per_scale))

@@ -92,6 +92,13 @@ def test_reciprocal_quantizer_equals_ieee_division(oracle):
     assert codes_bad == 0 and div_bad == 0
 
 
+def test_latent_reciprocal_division_gives_ieee_e4m3_bytes(oracle):
+    """Every binary16 latent scale: copysign(reciprocal-form quotient, z)
+    yields the same E4M3 byte as IEEE z / ls, signed zeros and subnormals
+    included."""
+    assert oracle.check_latent_division(77, 400) == 0
+
+
 def test_stored_quantize_kat(oracle):
     """state_ppl_codec_v6.py:54-61: exact half ties go away from zero, a zero
     or underflowed scale gives 0, codes clamp at +-limit."""
