@@ -71,6 +71,16 @@ int m2r_state_step_legacy(const void* x, const void* dt, const float* A, const v
                           int64_t L, int64_t H, int64_t P, int64_t G, hipStream_t stream);
 
 /*
+ * Test and tuning hook for the three steps above: force the workgroup shape
+ * (waves per workgroup, 64-row head slots per wave) to one of (1,1), (4,1),
+ * (4,2), (4,4); (0,0) restores the automatic choice.  A forced shape whose
+ * head count does not divide the heads per group falls back to the automatic
+ * choice.  Process-wide; results do not depend on the shape.  No counterpart
+ * in the reference (its Triton launch grid is fixed per call).
+ */
+int m2r_set_step_shape(int waves_per_block, int heads_per_wave);
+
+/*
  * Dense 3-bit step: codes u8[rows,3,16] (bit planes), scales f16[rows,2];
  * table u8[G,128] permutation (table_is_equalizer = 0) or i8[G,128] power-of-two
  * exponents in [-8, 8] (1).  Replaces mamba2_recall/state_codec_dense3.py:151-186

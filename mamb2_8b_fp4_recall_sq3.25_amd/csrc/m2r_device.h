@@ -33,15 +33,13 @@ __device__ __forceinline__ float round_to_half(float x) {
 // ---------------------------------------------------------------------------
 // E4M3FN (OCP FP8, bias 7, no infinities, 0x7F/0xFF NaN).
 __device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
-  uint32_t sign = (b & 0x80u) << 24;
-  uint32_t e = (b >> 3) & 15u, m = b & 7u;
-  float mag;
-  if (e == 0) {
-    mag = (float)m * 0x1p-9f;                       // subnormal: m * 2^-9 (exact)
-  } else {
-    mag = __builtin_bit_cast(float, ((e + 120u) << 23) | (m << 20));
-  }
-  if ((b & 0x7Fu) == 0x7Fu) mag = __builtin_nanf("");
+  const uint32_t sign = (b & 0x80u) << 24;
+  const uint32_t e = (b >> 3) & 15u, m = b & 7u;
+  // both forms computed and selected: subnormal m * 2^-9 (exact) or normal
+  const float sub = (float)m * 0x1p-9f;
+  const float nrm = __builtin_bit_cast(float, ((e + 120u) << 23) | (m << 20));
+  float mag = (e == 0) ? sub : nrm;
+  mag = ((b & 0x7Fu) == 0x7Fu) ? __builtin_nanf("") : mag;
   return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, mag) | sign);
 }
 

@@ -25,6 +25,8 @@
 #include "m2r_abi_util.h"
 #include "m2r_tile.h"
 
+#include <atomic>
+
 namespace m2r {
 
 enum { MODE_LEGACY = 0, MODE_STORED = 1, MODE_RIDGE = 2 };
@@ -115,63 +117,82 @@ __device__ __forceinline__ void bytes_to_plane4(const uint32_t* c, uint32_t* wq)
   }
 }
 
-// Per-token values shared by the workgroup (one B/C group, WPB heads): the
-// permuted B and C, dt activation and decay per head, B*dt per head, the
-// ridge correction and dead-tier dot products.
-template <int N8, int N4, int NZ, int MODE, int WPB>
+// Per-token values shared by the workgroup (one B/C group, NH heads): the raw
+// B/C rows and x, the permuted B and C, dt activation and decay per head, B*dt
+// per head, the readout weights and the latent dot products.
+template <int N8, int N4, int NZ, int MODE, int NH>
 struct TokenShared {
   static constexpr int NL = N8 + N4;
-  static constexpr int F = NL + 2;
-  uint16_t raw[256];                 // B row then C row of the group, original order
-  float b[128], c[128];              // permuted (packed lane order)
-  float bdt[WPB][NL];
-  float dtv[WPB], decay[WPB], dead[WPB];
-  float corr[MODE == MODE_RIDGE ? F + 2 : 4];
+  uint16_t raw[256];                                   // B row then C row of the group, original order
+  uint16_t xr[NH * 64];                                // x of the NH heads, this P block
+  alignas(16) float b[128];                            // internal order
+  alignas(16) float c[128];
+  alignas(16) float cp[MODE == MODE_RIDGE ? NL : 4];   // c + ridge correction of the live coordinates
+  alignas(16) float bdt[NH][NL];                       // RN(b * dt) per head
+  float dtv[NH], decay[NH];
+  // 0: sum of b*c over all 128 coordinates (readout); 1, 2: dead-tier e0.c,
+  // e1.c (readout); 3, 4: dead-tier e0.b, e1.b (canonical trees, exact);
+  // 5, 6: ridge correction of the two latent coefficients (readout)
   float dots[8];
 };
 
-// Raw per-token inputs a thread loads: its share of the group's B and C rows
-// (contiguous, independent of the permutation) and, for the first WPB
-// threads, one head's dt.
-template <int WPB>
+// Raw per-token inputs a thread loads one token ahead: its share of the
+// group's B and C rows, x of the rows it owns in each of its HPW head slots,
+// and, for the first NH threads, one head's dt + dt_bias.
+template <int WPB, int HPW>
 struct TokenRaw {
-  uint16_t bc[256 / (64 * WPB)];
+  static constexpr int NT = 64 * WPB;
+  static constexpr int NBC = (256 + NT - 1) / NT;
+  uint16_t bc[NBC];
+  uint16_t xv[HPW];
   float dtb;
 };
 
-template <int WPB>
-__device__ __forceinline__ void token_load(const StepArgs& a, TokenRaw<WPB>& r, int bt, int g, int h0, int tid) {
-  constexpr int NT = 64 * WPB;
+template <int WPB, int HPW>
+__device__ __forceinline__ void token_load(const StepArgs& a, TokenRaw<WPB, HPW>& r, int bt, int g, int h0,
+                                           int pbase, int tid, int lane, int wave) {
+  using R = TokenRaw<WPB, HPW>;
 #pragma unroll
-  for (int k = 0; k < 256 / NT; ++k) {
-    const int i = k * NT + tid;
+  for (int k = 0; k < R::NBC; ++k) {
+    const int i = k * R::NT + tid;
     const uint16_t* src = (i < 128) ? a.Bm : a.Cm;
-    r.bc[k] = src[((size_t)bt * a.G + g) * 128 + (i & 127)];
+    r.bc[k] = (i < 256) ? src[((size_t)bt * a.G + g) * 128 + (i & 127)] : (uint16_t)0;
+  }
+  const int p = pbase + lane;
+#pragma unroll
+  for (int k = 0; k < HPW; ++k) {
+    const int hh = k * WPB + wave;
+    r.xv[k] = (p < a.P) ? a.x[((size_t)bt * a.H + h0 + hh) * a.P + p] : (uint16_t)0;
   }
   r.dtb = 0.f;
-  if (tid < WPB) r.dtb = h2f(a.dt[(size_t)bt * a.H + h0 + tid]) + load_param(a.dt_bias, a.db_f32, h0 + tid);
+  if (tid < WPB * HPW) r.dtb = h2f(a.dt[(size_t)bt * a.H + h0 + tid]) + load_param(a.dt_bias, a.db_f32, h0 + tid);
 }
 
-template <int N8, int N4, int NZ, int MODE, int WPB>
-__device__ __forceinline__ void token_store(const StepArgs& a, TokenShared<N8, N4, NZ, MODE, WPB>& sh,
-                                            const TokenRaw<WPB>& r, int h0, int tid) {
-  constexpr int NT = 64 * WPB;
+template <int N8, int N4, int NZ, int MODE, int WPB, int HPW>
+__device__ __forceinline__ void token_store(TokenShared<N8, N4, NZ, MODE, WPB * HPW>& sh,
+                                            const TokenRaw<WPB, HPW>& r, float Ah, int tid, int lane, int wave) {
+  using R = TokenRaw<WPB, HPW>;
 #pragma unroll
-  for (int k = 0; k < 256 / NT; ++k) sh.raw[k * NT + tid] = r.bc[k];
-  if (tid < WPB) {
-    const float2 act = dt_activation(r.dtb, a.A[h0 + tid]);
+  for (int k = 0; k < R::NBC; ++k) {
+    const int i = k * R::NT + tid;
+    if (i < 256) sh.raw[i] = r.bc[k];
+  }
+#pragma unroll
+  for (int k = 0; k < HPW; ++k) sh.xr[(k * WPB + wave) * 64 + lane] = r.xv[k];
+  if (tid < WPB * HPW) {
+    const float2 act = dt_activation(r.dtb, Ah);
     sh.dtv[tid] = act.x;
     sh.decay[tid] = act.y;
   }
 }
 
 // After token_store and a barrier: gather through the permutation, B*dt per
-// head, ridge correction and dead-tier dot products; ends with a barrier.
-template <int N8, int N4, int NZ, int MODE, int WPB>
-__device__ __forceinline__ void token_build(TokenShared<N8, N4, NZ, MODE, WPB>& sh, const uint8_t* s_perm,
+// head, readout weights and latent dot products; ends with a barrier.
+template <int N8, int N4, int NZ, int MODE, int WPB, int HPW>
+__device__ __forceinline__ void token_build(TokenShared<N8, N4, NZ, MODE, WPB * HPW>& sh, const uint8_t* s_perm,
                                             const float* s_basis, const uint16_t* s_pred, int tid, int lane,
                                             int wave) {
-  constexpr int NL = N8 + N4, F = NL + 2, NT = 64 * WPB;
+  constexpr int NL = N8 + N4, F = NL + 2, NT = 64 * WPB, NH = WPB * HPW;
   constexpr int RZ = next_pow2(NZ);
   for (int i = tid; i < 256; i += NT) {
     const int n = i & 127;   // internal position
@@ -179,13 +200,14 @@ __device__ __forceinline__ void token_build(TokenShared<N8, N4, NZ, MODE, WPB>& 
     if (i < 128) sh.b[n] = v; else sh.c[n] = v;
   }
   __syncthreads();
-  for (int i = tid; i < WPB * NL; i += NT) {
+  for (int i = tid; i < NH * NL; i += NT) {
     const int w = i / NL, n = i - w * NL;
     sh.bdt[w][n] = sh.b[n] * sh.dtv[w];
   }
   if constexpr (MODE == MODE_RIDGE) {
     // corr[f] = sum_d C[dead d] * pred[g, f, d]: four threads per output,
-    // interleaved d, combined inside the quad (readout-only value)
+    // interleaved d, combined inside the quad; live rows are folded into the
+    // readout weight c + corr, latent rows kept apart (readout-only values)
     for (int idx = tid; idx < 4 * F; idx += NT) {
       const int j = idx >> 2, part = idx & 3;     // internal feature position
       const int f = packed_lane<N8, N4>(j);       // predictor row (packed lane; latent rows last)
@@ -194,91 +216,151 @@ __device__ __forceinline__ void token_build(TokenShared<N8, N4, NZ, MODE, WPB>& 
       for (int d = part; d < NZ; d += 4) acc = __builtin_fmaf(sh.c[NL + d], h2f(s_pred[f * NZ + d]), acc);
       acc = butterfly_add<0>(acc);
       acc = butterfly_add<1>(acc);
-      if (part == 0) sh.corr[j] = acc;
+      if (part == 0) {
+        if (j < NL) sh.cp[j] = sh.c[j] + acc;
+        else sh.dots[5 + (j - NL)] = acc;
+      }
     }
-    // dead-tier dot products: canonical adjacent-pair trees, spread over waves
 #pragma unroll
     for (int k = 0; k < 5; ++k) {
       if (wave != k % WPB) continue;
-      float v[2];
+      float t;
+      if (k == 0) {
+        t = wave_sum(sh.b[lane] * sh.c[lane] + sh.b[lane + 64] * sh.c[lane + 64]);
+      } else {
+        // dead-tier dot products: canonical adjacent-pair trees
+        float v[2];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int d0 = (RZ == 128) ? 2 * lane + j : lane;
-        const bool in = (RZ == 128 || j == 0) && d0 < NZ;
-        const int d = in ? d0 : 0;
-        const float bb = sh.b[NL + d], cc = sh.c[NL + d], e0 = s_basis[d], e1 = s_basis[NZ + d];
-        float pr = k == 0 ? bb * cc : k == 1 ? e0 * cc : k == 2 ? e1 * cc : k == 3 ? e0 * bb : e1 * bb;
-        v[j] = in ? pr : 0.f;
+        for (int j = 0; j < 2; ++j) {
+          const int d0 = (RZ == 128) ? 2 * lane + j : lane;
+          const bool in = (RZ == 128 || j == 0) && d0 < NZ;
+          const int d = in ? d0 : 0;
+          const float bb = sh.b[NL + d], cc = sh.c[NL + d], e0 = s_basis[d], e1 = s_basis[NZ + d];
+          const float pr = k == 1 ? e0 * cc : k == 2 ? e1 * cc : k == 3 ? e0 * bb : e1 * bb;
+          v[j] = in ? pr : 0.f;
+        }
+        t = wave_pair_tree<RZ>(v[0], v[1]);
       }
-      const float t = wave_pair_tree<RZ>(v[0], v[1]);
       if (lane == 0) sh.dots[k] = t;
     }
   } else {
-    // dead tier contribution to the readout: sum_d (b_d * dt) * c_d per head
-    float part = 0.f;
-    for (int d = lane; d < NZ; d += 64) part = __builtin_fmaf(sh.b[NL + d] * sh.dtv[wave], sh.c[NL + d], part);
-    part = wave_sum(part);
-    if (lane == 0) sh.dead[wave] = part;
+    if (wave == 0) {
+      const float t = wave_sum(sh.b[lane] * sh.c[lane] + sh.b[lane + 64] * sh.c[lane + 64]);
+      if (lane == 0) sh.dots[0] = t;
+    }
   }
   __syncthreads();
 }
 
-template <int N8, int N4, int NZ, int MODE, int WPB>
+// Orders a wave's LDS accesses across its lanes (the wave's own staging
+// tiles need no workgroup barrier).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// One workgroup = WPB waves, each owning HPW head slots of 64 rows (the same
+// P block of NH = WPB * HPW consecutive heads of one B/C group and batch
+// row).  The packed rows of every slot stay in LDS, in the reference's SoA
+// field layout, for all L tokens; a slot is unpacked into VGPRs, stepped and
+// repacked in one pass per token.  The first token streams the slots in:
+// the next slot's rows are loaded into VGPRs while the current one computes.
+// Per-token shared values are built once per workgroup for all NH heads.
+template <int N8, int N4, int NZ, int MODE, int WPB, int HPW>
 __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
   constexpr int W8 = N8 / 2;          // bytes per row of lo and of hi
   constexpr int W4 = N4 / 2;          // bytes per row of q4
   constexpr int NL = N8 + N4;         // carried coordinates
   constexpr int F = NL + 2;           // ridge predictor features
   constexpr int NT = 64 * WPB;
-  constexpr int TILE = 64 * (2 * W8 + W4) + 16;
+  constexpr int NH = WPB * HPW;
+  constexpr bool RIDGE = MODE == MODE_RIDGE;
+  constexpr int O_LO = 0, O_HI = 64 * W8, O_Q4 = 128 * W8, O_S8 = O_Q4 + 64 * W4, O_S4 = O_S8 + 128;
+  constexpr int O_LAT = O_S4 + 128;
+  constexpr int TILE = O_LAT + (RIDGE ? 128 : 0) + 16;   // 16 bytes of slack for row reads
   constexpr int C8 = N8 / 4, C4 = N4 / 4;   // carried code words (4 biased bytes each)
-  constexpr int PRED_DW = (MODE == MODE_RIDGE) ? F * NZ / 2 : 1;   // F*NZ is even for every layout
-  static_assert(N8 % 4 == 0 && N4 % 4 == 0 && NL % 4 == 0, "tier widths must be multiples of 4");
-  static_assert(MODE != MODE_RIDGE || (F * NZ) % 2 == 0, "predictor staged as dwords");
+  constexpr int PRED_DW = RIDGE ? F * NZ / 2 : 1;   // F*NZ is even for every layout
+  static_assert(N8 % 4 == 0 && N4 % 4 == 0 && N8 > 0 && N4 > 0, "tier widths must be positive multiples of 4");
+  static_assert(!RIDGE || (F * NZ) % 2 == 0, "predictor staged as dwords");
+  static_assert(TILE % 16 == 0, "tiles stay 16-byte aligned");
 
-  __shared__ __align__(16) uint8_t s_tile[WPB][TILE];
-  __shared__ __align__(16) TokenShared<N8, N4, NZ, MODE, WPB> sh;
-  __shared__ __align__(16) uint32_t s_pred32[PRED_DW];
-  __shared__ float s_basis[MODE == MODE_RIDGE ? 2 * NZ : 1];
+  // small, often-read arrays first: their LDS offsets fit instruction immediates
+  __shared__ __align__(16) TokenShared<N8, N4, NZ, MODE, NH> sh;
+  __shared__ float s_D[NH];
   __shared__ uint8_t s_perm[128];
+  __shared__ float s_basis[RIDGE ? 2 * NZ : 1];
+  __shared__ __align__(16) uint32_t s_pred32[PRED_DW];
+  __shared__ __align__(16) uint8_t s_tile[NH][TILE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int b = blockIdx.z;
-  const int h0 = blockIdx.y * WPB;
-  const int h = h0 + wave;
-  const int H = a.H, P = a.P, G = a.G, L = a.L;
-  const int g = h0 / (H / G);
+  const int h0 = blockIdx.y * NH;
+  const int H = a.H, P = a.P, L = a.L;
+  const int g = h0 / (H / a.G);
   const int pbase = blockIdx.x * 64;
   const int nvalid = min(64, P - pbase);
   const bool valid = lane < nvalid;
-  const int row0 = (b * H + h) * P + pbase;
-  const int row = row0 + lane;
-  uint8_t* tile = s_tile[wave];
+  const bool dword_tiles = (P & 1) == 0;   // every slot's row0 * W and nvalid * W are dword multiples
   const uint16_t* s_pred = (const uint16_t*)s_pred32;
-  const bool dword_tiles = (((row0 | nvalid) & 1) == 0);   // row0*W and nvalid*W are dword multiples
 
-  // ---- issue every independent load of the first token -------------------------
-  TileRegs<W8> tlo, thi;
-  TileRegs<W4> tq4;
-  if (dword_tiles) {
-    if constexpr (W8 > 0) { tile_load<W8>(tlo, a.lo, row0, nvalid, lane); tile_load<W8>(thi, a.hi, row0, nvalid, lane); }
-    if constexpr (W4 > 0) tile_load<W4>(tq4, a.q4, row0, nvalid, lane);
-  }
-  TokenRaw<WPB> raw;
-  token_load<WPB>(a, raw, b * L, g, h0, tid);
-  float sc8 = 0.f, sc4 = 0.f, x = 0.f;
-  uint32_t lat = 0;
-  if (valid) {
-    sc8 = h2f(a.s8[row]);
-    sc4 = h2f(a.s4[row]);
-    if constexpr (MODE == MODE_RIDGE) lat = ((const uint16_t*)a.latent)[row];
-    x = h2f(a.x[((size_t)(b * L) * H + h) * P + pbase + lane]);
-  }
+  struct SlotRegs {
+    TileRegs<W8> lo, hi;
+    TileRegs<W4> q4;
+    TileRegs<2> s8, s4, lat;
+  };
+  auto slot_row0 = [&](int hh) { return (b * H + h0 + hh) * P + pbase; };
+  auto slot_load = [&](SlotRegs& r, int hh) {
+    const int row0 = slot_row0(hh);
+    tile_load<W8>(r.lo, a.lo, row0, nvalid, lane);
+    tile_load<W8>(r.hi, a.hi, row0, nvalid, lane);
+    tile_load<W4>(r.q4, a.q4, row0, nvalid, lane);
+    tile_load<2>(r.s8, (const uint8_t*)a.s8, row0, nvalid, lane);
+    tile_load<2>(r.s4, (const uint8_t*)a.s4, row0, nvalid, lane);
+    if constexpr (RIDGE) tile_load<2>(r.lat, a.latent, row0, nvalid, lane);
+  };
+  auto slot_store = [&](const SlotRegs& r, int hh) {
+    uint8_t* t = s_tile[hh];
+    tile_store_lds<W8>(r.lo, t + O_LO, nvalid, lane);
+    tile_store_lds<W8>(r.hi, t + O_HI, nvalid, lane);
+    tile_store_lds<W4>(r.q4, t + O_Q4, nvalid, lane);
+    tile_store_lds<2>(r.s8, t + O_S8, nvalid, lane);
+    tile_store_lds<2>(r.s4, t + O_S4, nvalid, lane);
+    if constexpr (RIDGE) tile_store_lds<2>(r.lat, t + O_LAT, nvalid, lane);
+  };
+  auto slot_copy_in = [&](int hh) {   // odd P: 16-bit transfers
+    const int row0 = slot_row0(hh);
+    uint8_t* t = s_tile[hh];
+    wave_copy_in<W8>(t + O_LO, a.lo, row0, nvalid, lane);
+    wave_copy_in<W8>(t + O_HI, a.hi, row0, nvalid, lane);
+    wave_copy_in<W4>(t + O_Q4, a.q4, row0, nvalid, lane);
+    wave_copy_in<2>(t + O_S8, (const uint8_t*)a.s8, row0, nvalid, lane);
+    wave_copy_in<2>(t + O_S4, (const uint8_t*)a.s4, row0, nvalid, lane);
+    if constexpr (RIDGE) wave_copy_in<2>(t + O_LAT, a.latent, row0, nvalid, lane);
+  };
+  auto slot_copy_out = [&](int hh) {
+    const int row0 = slot_row0(hh);
+    const uint8_t* t = s_tile[hh];
+    wave_copy_out<W8>(a.lo, t + O_LO, row0, nvalid, lane);
+    wave_copy_out<W8>(a.hi, t + O_HI, row0, nvalid, lane);
+    wave_copy_out<W4>(a.q4, t + O_Q4, row0, nvalid, lane);
+    wave_copy_out<2>((uint8_t*)a.s8, t + O_S8, row0, nvalid, lane);
+    wave_copy_out<2>((uint8_t*)a.s4, t + O_S4, row0, nvalid, lane);
+    if constexpr (RIDGE) wave_copy_out<2>(a.latent, t + O_LAT, row0, nvalid, lane);
+  };
+
+  // ---- issue every independent load of the first token and first slot -----------
+  SlotRegs nxt;
+  if (dword_tiles) slot_load(nxt, wave);
+  TokenRaw<WPB, HPW> raw;
+  token_load<WPB, HPW>(a, raw, b * L, g, h0, pbase, tid, lane, wave);
+  const float Ah = (tid < NH) ? a.A[h0 + tid] : 0.f;
+  if (tid < NH) s_D[tid] = load_param(a.D, a.d_f32, h0 + tid);
   for (int n = tid; n < 128; n += NT) s_perm[n] = a.perm[g * 128 + n];
   float ls0 = 0.f, ls1 = 0.f, rls0 = 0.f, rls1 = 0.f;
-  if constexpr (MODE == MODE_RIDGE) {
+  if constexpr (RIDGE) {
     const uint32_t* pg = (const uint32_t*)(a.pred + (size_t)g * F * NZ);
     for (int i = tid; i < PRED_DW; i += NT) s_pred32[i] = pg[i];
     for (int i = tid; i < NZ; i += NT) {
@@ -291,48 +373,9 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
     rls0 = 1.0f / ls0;   // correctly rounded reciprocals
     rls1 = 1.0f / ls1;
   }
-  const float Dh = load_param(a.D, a.d_f32, h);
-  if (dword_tiles) {
-    if constexpr (W8 > 0) { tile_store_lds<W8>(tlo, tile, nvalid, lane); tile_store_lds<W8>(thi, tile + 64 * W8, nvalid, lane); }
-    if constexpr (W4 > 0) tile_store_lds<W4>(tq4, tile + 128 * W8, nvalid, lane);
-  } else {
-    if constexpr (W8 > 0) {
-      wave_copy_in<W8>(tile, a.lo, row0, nvalid, lane);
-      wave_copy_in<W8>(tile + 64 * W8, a.hi, row0, nvalid, lane);
-    }
-    if constexpr (W4 > 0) wave_copy_in<W4>(tile + 128 * W8, a.q4, row0, nvalid, lane);
-  }
-  token_store<N8, N4, NZ, MODE, WPB>(a, sh, raw, h0, tid);
+  if (dword_tiles) slot_store(nxt, wave); else slot_copy_in(wave);
+  token_store<N8, N4, NZ, MODE, WPB, HPW>(sh, raw, Ah, tid, lane, wave);
   __syncthreads();
-
-  // Carried codes, internal lane order: byte k of c8[i] is q8 + 128 of
-  // internal coordinate 4i+k, of c4[i] q4 + 8.
-  uint32_t c8[C8 > 0 ? C8 : 1], c4[C4 > 0 ? C4 : 1];
-  {
-    if constexpr (W8 > 0) {
-      uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4];
-      lds_read_row<W8>(tile, lane * W8, wl);
-      lds_read_row<W8>(tile + 64 * W8, lane * W8, wh);
-      planes_to_bytes8<N8>(wl, wh, c8);
-    }
-    if constexpr (W4 > 0) {
-      uint32_t wq[(W4 + 3) / 4];
-      lds_read_row<W4>(tile + 128 * W8, lane * W4, wq);
-      plane_to_bytes4<N4>(wq, c4);
-    }
-    if (!valid) {
-#pragma unroll
-      for (int i = 0; i < C8; ++i) c8[i] = 0x80808080u;
-#pragma unroll
-      for (int i = 0; i < C4; ++i) c4[i] = 0x08080808u;
-    }
-  }
-  float z0 = 0.f, z1 = 0.f;
-  if constexpr (MODE == MODE_RIDGE) {
-    z0 = e4m3_to_f32(lat & 0xFFu) * ls0;
-    z1 = e4m3_to_f32(lat >> 8) * ls1;
-  }
-  uint32_t qz = lat;
 
   const float y127 = 1.0f / 127.0f;   // RN(1/127)
   const float y7 = 1.0f / 7.0f;       // RN(1/7)
@@ -340,147 +383,200 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
   for (int t = 0; t < L; ++t) {
     const int bt = b * L + t;
     if (t > 0) {
-      token_store<N8, N4, NZ, MODE, WPB>(a, sh, raw, h0, tid);
+      token_store<N8, N4, NZ, MODE, WPB, HPW>(sh, raw, Ah, tid, lane, wave);
       __syncthreads();
     }
-    float xn = 0.f;
-    if (t + 1 < L) {   // prefetch the next token's raw inputs
-      token_load<WPB>(a, raw, bt + 1, g, h0, tid);
-      if (valid) xn = h2f(a.x[((size_t)(bt + 1) * H + h) * P + pbase + lane]);
-    }
-    token_build<N8, N4, NZ, MODE, WPB>(sh, s_perm, s_basis, s_pred, tid, lane, wave);
+    if (t + 1 < L) token_load<WPB, HPW>(a, raw, bt + 1, g, h0, pbase, tid, lane, wave);   // prefetch
+    token_build<N8, N4, NZ, MODE, WPB, HPW>(sh, s_perm, s_basis, s_pred, tid, lane, wave);
 
-    // ---- per-row update and readout --------------------------------------------
-    const float decay = sh.decay[wave];
-    const float dtv = sh.dtv[wave];
-    const float nb8 = -128.0f * sc8, nb4 = -8.0f * sc4;   // exact
-    float acc = 0.f, accp = 0.f, amax8 = 0.f, amax4 = 0.f;
-    float v[NL];
-    const f32x4* bdt4 = (const f32x4*)sh.bdt[wave];
-    const f32x4* c4v = (const f32x4*)sh.c;
-    const f32x4* p4v = (const f32x4*)sh.corr;
-#pragma unroll
-    for (int i0 = 0; i0 < NL; i0 += 4) {
-      const f32x4 cb = bdt4[i0 / 4], cc = c4v[i0 / 4];
-      f32x4 cp = {};
-      if constexpr (MODE == MODE_RIDGE) cp = p4v[i0 / 4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int i = i0 + j;
-        // prior = q * s exactly: (q + bias) * s - bias * s, all exact
-        float prior = (i < N8) ? __builtin_fmaf(ubyte_f(c8[i / 4], j), sc8, nb8)
-                               : __builtin_fmaf(ubyte_f(c4[(i - N8) / 4], j), sc4, nb4);
-        if constexpr (MODE == MODE_RIDGE) accp = __builtin_fmaf(prior, cp[j], accp);
-        float u = prior * decay + cb[j] * x;
-        v[i] = u;
-        acc = __builtin_fmaf(u, cc[j], acc);
-        if (i < N8) amax8 = __builtin_fmaxf(amax8, __builtin_fabsf(u));
-        else amax4 = __builtin_fmaxf(amax4, __builtin_fabsf(u));
+    for (int k = 0; k < HPW; ++k) {
+      const int hh = k * WPB + wave;
+      const int h = h0 + hh;
+      const bool stream_next = (t == 0) && (k + 1 < HPW);
+      if (stream_next) {
+        if (dword_tiles) slot_load(nxt, hh + WPB); else slot_copy_in(hh + WPB);
       }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // Materialize the readout accumulators here: otherwise the compiler sinks
-    // the whole fma chain into the predicated y store, which keeps every
-    // carried value and every LDS operand live at once.
-    asm volatile("" : "+v"(acc), "+v"(accp));
-    float out;
-    if constexpr (MODE == MODE_RIDGE) {
-      const float dbc = sh.dots[0], dc0 = sh.dots[1], dc1 = sh.dots[2], db0 = sh.dots[3], db1 = sh.dots[4];
-      const float xdt = x * dtv;
-      out = acc + decay * (z0 * dc0 + z1 * dc1) + xdt * dbc + x * Dh
-          + decay * (accp + z0 * sh.corr[NL] + z1 * sh.corr[NL + 1]);
-      z0 = z0 * decay + xdt * db0;
-      z1 = z1 * decay + xdt * db1;
-      float q0 = __builtin_fminf(__builtin_fmaxf(latent_quotient(z0, ls0, rls0), -448.f), 448.f);
-      float q1 = __builtin_fminf(__builtin_fmaxf(latent_quotient(z1, ls1, rls1), -448.f), 448.f);
-      uint32_t e0 = f32_to_e4m3(q0), e1 = f32_to_e4m3(q1);
-      qz = e0 | (e1 << 8);
-      z0 = e4m3_to_f32(e0) * ls0;
-      z1 = e4m3_to_f32(e1) * ls1;
-    } else {
-      out = acc + x * sh.dead[wave] + x * Dh;
-    }
-    if (valid) a.y[((size_t)bt * H + h) * P + pbase + lane] = f2h(out);
+      uint8_t* tile = s_tile[hh];
+      uint16_t* t16 = (uint16_t*)tile;
 
-    // ---- requantization: den = max(RN(amax / lim), 1e-8), stored = half(den) --
-    float den8 = __builtin_fmaxf(div_by_recip(amax8, 127.0f, y127), 1e-8f);
-    float den4 = __builtin_fmaxf(div_by_recip(amax4, 7.0f, y7), 1e-8f);
-    sc8 = round_to_half(den8);
-    sc4 = round_to_half(den4);
-    float d8, r8, d4, r4;
-    if constexpr (MODE == MODE_LEGACY) {
-      d8 = den8; r8 = 1.0f / den8;
-      d4 = den4; r4 = 1.0f / den4;
-    } else {
-      // zero (underflowed) or infinite stored scale: the reference's quotient
-      // is 0 and so is the code
-      bool z8 = !(sc8 > 0.f) || sc8 == __builtin_inff();
-      bool z4 = !(sc4 > 0.f) || sc4 == __builtin_inff();
-      d8 = z8 ? 1.f : sc8; r8 = z8 ? 0.f : 1.0f / sc8;
-      d4 = z4 ? 1.f : sc4; r4 = z4 ? 0.f : 1.0f / sc4;
-    }
+      // ---- unpack the slot: carried codes, internal lane order ------------------
+      // byte k of c8[i] is q8 + 128 of internal coordinate 4i+k, of c4[i] q4 + 8
+      uint32_t c8[C8], c4[C4];
+      {
+        uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4], wq[(W4 + 3) / 4];
+        lds_read_row<W8>(tile + O_LO, lane * W8, wl);
+        lds_read_row<W8>(tile + O_HI, lane * W8, wh);
+        planes_to_bytes8<N8>(wl, wh, c8);
+        lds_read_row<W4>(tile + O_Q4, lane * W4, wq);
+        plane_to_bytes4<N4>(wq, c4);
+      }
+      float sc8 = h2f(t16[O_S8 / 2 + lane]);
+      float sc4 = h2f(t16[O_S4 / 2 + lane]);
+      float z0 = 0.f, z1 = 0.f;
+      if constexpr (RIDGE) {
+        const uint32_t lat = t16[O_LAT / 2 + lane];
+        z0 = e4m3_to_f32(lat & 0xFFu) * ls0;
+        z1 = e4m3_to_f32(lat >> 8) * ls1;
+      }
+      if (!valid) {   // rows past P: finite placeholders, never stored
 #pragma unroll
-    for (int i = 0; i < C8; ++i) {
-      int q0 = quantize_code(v[4 * i], d8, r8, QTOP127);
-      int q1 = quantize_code(v[4 * i + 1], d8, r8, QTOP127);
-      int q2 = quantize_code(v[4 * i + 2], d8, r8, QTOP127);
-      int q3 = quantize_code(v[4 * i + 3], d8, r8, QTOP127);
-      c8[i] = pack4(q0, q1, q2, q3) ^ 0x80808080u;
-      __builtin_amdgcn_sched_barrier(0);
-    }
+        for (int i = 0; i < C8; ++i) c8[i] = 0x80808080u;
 #pragma unroll
-    for (int i = 0; i < C4; ++i) {
-      int q0 = quantize_code(v[N8 + 4 * i], d4, r4, QTOP7);
-      int q1 = quantize_code(v[N8 + 4 * i + 1], d4, r4, QTOP7);
-      int q2 = quantize_code(v[N8 + 4 * i + 2], d4, r4, QTOP7);
-      int q3 = quantize_code(v[N8 + 4 * i + 3], d4, r4, QTOP7);
-      c4[i] = (pack4(q0, q1, q2, q3) & 0x0F0F0F0Fu) ^ 0x08080808u;
-      __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < C4; ++i) c4[i] = 0x08080808u;
+        sc8 = sc4 = z0 = z1 = 0.f;
+      }
+      const float x = h2f(sh.xr[hh * 64 + lane]);
+      const float decay = sh.decay[hh];
+      const float dtv = sh.dtv[hh];
+
+      // ---- update, readout accumulation, tier maxima -----------------------------
+      const float nb8 = -128.0f * sc8, nb4 = -8.0f * sc4;   // exact
+      float acc = 0.f, amax8 = 0.f, amax4 = 0.f;
+      float v[NL];
+      const f32x4* bdt4 = (const f32x4*)sh.bdt[hh];
+      const f32x4* cw4;
+      if constexpr (RIDGE) cw4 = (const f32x4*)sh.cp; else cw4 = (const f32x4*)sh.c;
+      // the shared operands of chunk i+1 are read while chunk i computes
+      f32x4 cb_next = bdt4[0], cw_next = cw4[0];
+#pragma unroll
+      for (int i0 = 0; i0 < NL; i0 += 4) {
+        const f32x4 cb = cb_next, cw = cw_next;
+        if (i0 + 4 < NL) {
+          cb_next = bdt4[i0 / 4 + 1];
+          cw_next = cw4[i0 / 4 + 1];
+        }
+        float au[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int i = i0 + j;
+          // prior = q * s exactly: (q + bias) * s - bias * s, all exact
+          const float prior = (i < N8) ? __builtin_fmaf(ubyte_f(c8[i / 4], j), sc8, nb8)
+                                       : __builtin_fmaf(ubyte_f(c4[(i - N8) / 4], j), sc4, nb4);
+          acc = __builtin_fmaf(prior, cw[j], acc);
+          const float u = prior * decay + cb[j] * x;
+          v[i] = u;
+          au[j] = __builtin_fabsf(u);
+        }
+        const float m = __builtin_fmaxf(__builtin_fmaxf(au[0], au[1]), __builtin_fmaxf(au[2], au[3]));
+        if (i0 < N8) amax8 = __builtin_fmaxf(amax8, m); else amax4 = __builtin_fmaxf(amax4, m);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // Materialize the accumulator and the tier maxima here: otherwise the
+      // compiler sinks their chains (and every update behind the maxima) into
+      // the predicated y store and the requantization, which keeps every
+      // prior and LDS operand live at once.
+      asm volatile("" : "+v"(acc), "+v"(amax8), "+v"(amax4));
+      // readout: sum_i u_i c_i + corrections = decay * (sum_i prior_i (c_i +
+      // corr_i) + latent terms) + x * (dt * sum_all b c + D)
+      float out;
+      uint32_t qz = 0;
+      if constexpr (RIDGE) {
+        const float kz0 = sh.dots[1] + sh.dots[5], kz1 = sh.dots[2] + sh.dots[6];
+        out = decay * (acc + z0 * kz0 + z1 * kz1) + x * (dtv * sh.dots[0] + s_D[hh]);
+        // latent step (bit-exact): z <- z * decay + (x * dt) * (e . b_dead), requantized
+        const float xdt = x * dtv;
+        const float zn0 = z0 * decay + xdt * sh.dots[3];
+        const float zn1 = z1 * decay + xdt * sh.dots[4];
+        const float q0 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn0, ls0, rls0), -448.f), 448.f);
+        const float q1 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn1, ls1, rls1), -448.f), 448.f);
+        qz = f32_to_e4m3(q0) | (f32_to_e4m3(q1) << 8);
+      } else {
+        out = decay * acc + x * (dtv * sh.dots[0] + s_D[hh]);
+      }
+      if (valid) a.y[((size_t)bt * H + h) * P + pbase + lane] = f2h(out);
+
+      // ---- requantization: den = max(RN(amax / lim), 1e-8), stored = half(den) --
+      const float den8 = __builtin_fmaxf(div_by_recip(amax8, 127.0f, y127), 1e-8f);
+      const float den4 = __builtin_fmaxf(div_by_recip(amax4, 7.0f, y7), 1e-8f);
+      sc8 = round_to_half(den8);
+      sc4 = round_to_half(den4);
+      float d8, r8, d4, r4;
+      if constexpr (MODE == MODE_LEGACY) {
+        d8 = den8; r8 = 1.0f / den8;
+        d4 = den4; r4 = 1.0f / den4;
+      } else {
+        // zero (underflowed) or infinite stored scale: the reference's quotient
+        // is 0 and so is the code
+        const bool z8 = !(sc8 > 0.f) || sc8 == __builtin_inff();
+        const bool z4 = !(sc4 > 0.f) || sc4 == __builtin_inff();
+        d8 = z8 ? 1.f : sc8; r8 = z8 ? 0.f : 1.0f / sc8;
+        d4 = z4 ? 1.f : sc4; r4 = z4 ? 0.f : 1.0f / sc4;
+      }
+#pragma unroll
+      for (int i = 0; i < C8; ++i) {
+        const int q0 = quantize_code(v[4 * i], d8, r8, QTOP127);
+        const int q1 = quantize_code(v[4 * i + 1], d8, r8, QTOP127);
+        const int q2 = quantize_code(v[4 * i + 2], d8, r8, QTOP127);
+        const int q3 = quantize_code(v[4 * i + 3], d8, r8, QTOP127);
+        c8[i] = pack4(q0, q1, q2, q3) ^ 0x80808080u;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int i = 0; i < C4; ++i) {
+        const int q0 = quantize_code(v[N8 + 4 * i], d4, r4, QTOP7);
+        const int q1 = quantize_code(v[N8 + 4 * i + 1], d4, r4, QTOP7);
+        const int q2 = quantize_code(v[N8 + 4 * i + 2], d4, r4, QTOP7);
+        const int q3 = quantize_code(v[N8 + 4 * i + 3], d4, r4, QTOP7);
+        c4[i] = (pack4(q0, q1, q2, q3) & 0x0F0F0F0Fu) ^ 0x08080808u;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+
+      // ---- repack the slot row into the tile ---------------------------------------
+      if (valid) {
+        uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4], wq[(W4 + 3) / 4];
+        bytes_to_planes8<N8>(c8, wl, wh);
+        lds_write_row<W8>(tile + O_LO, lane * W8, wl);
+        lds_write_row<W8>(tile + O_HI, lane * W8, wh);
+        bytes_to_plane4<N4>(c4, wq);
+        lds_write_row<W4>(tile + O_Q4, lane * W4, wq);
+        t16[O_S8 / 2 + lane] = f2h(sc8);
+        t16[O_S4 / 2 + lane] = f2h(sc4);
+        if constexpr (RIDGE) t16[O_LAT / 2 + lane] = (uint16_t)qz;
+      }
+      if (stream_next && dword_tiles) slot_store(nxt, hh + WPB);
+      wave_sync();
+      if (t == L - 1) slot_copy_out(hh);
     }
-    x = xn;
     if (t + 1 < L) __syncthreads();   // shared token values are rebuilt next iteration
-  }
-
-  // ---- repack to the nibble planes and store ------------------------------------
-  if (valid) {
-    if constexpr (W8 > 0) {
-      uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4];
-      bytes_to_planes8<N8>(c8, wl, wh);
-      lds_write_row<W8>(tile, lane * W8, wl);
-      lds_write_row<W8>(tile + 64 * W8, lane * W8, wh);
-    }
-    if constexpr (W4 > 0) {
-      uint32_t wq[(W4 + 3) / 4];
-      bytes_to_plane4<N4>(c4, wq);
-      lds_write_row<W4>(tile + 128 * W8, lane * W4, wq);
-    }
-  }
-  __syncthreads();
-  if constexpr (W8 > 0) {
-    wave_copy_out<W8>(a.lo, tile, row0, nvalid, lane);
-    wave_copy_out<W8>(a.hi, tile + 64 * W8, row0, nvalid, lane);
-  }
-  if constexpr (W4 > 0) wave_copy_out<W4>(a.q4, tile + 128 * W8, row0, nvalid, lane);
-  if (valid) {
-    a.s8[row] = f2h(sc8);
-    a.s4[row] = f2h(sc4);
-    if constexpr (MODE == MODE_RIDGE) ((uint16_t*)a.latent)[row] = (uint16_t)qz;
   }
 }
 
 // ---------------------------------------------------------------------------
-// Host dispatch over the supported tier layouts.
+// Host dispatch over the supported tier layouts.  Heads per workgroup grow
+// with the number of 64-row slots so that the per-token shared work is
+// amortized while the grid still spans every CU; small grids keep four waves
+// per workgroup, which splits the per-token shared work four ways.
+// Workgroup shape forced through m2r_set_step_shape (0 = automatic), encoded
+// as waves_per_block * 16 + heads_per_wave.
+static std::atomic<int> g_forced_shape{0};
+
 template <int N8, int N4, int NZ, int MODE>
 static hipError_t launch_layout(const StepArgs& a, hipStream_t stream) {
-  int pblocks = (a.P + 63) / 64;
-  int hpg = a.H / a.G;
-  long long waves = (long long)a.B * a.H * pblocks;
-  if (hpg % 4 == 0 && waves >= 4LL * 1024) {
+  const int pblocks = (a.P + 63) / 64;
+  const int hpg = a.H / a.G;
+  const long long slots = (long long)a.B * a.H * pblocks;
+  const int forced = g_forced_shape.load(std::memory_order_relaxed);
+  if (forced && hpg % ((forced >> 4) * (forced & 15)) == 0) {
+    const int wpb = forced >> 4, hpw = forced & 15;
+    dim3 grid(pblocks, a.H / (wpb * hpw), a.B);
+    if (wpb == 1) hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 1, 1>), grid, dim3(64), 0, stream, a);
+    else if (hpw == 1) hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 4, 1>), grid, dim3(256), 0, stream, a);
+    else if (hpw == 2) hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 4, 2>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 4, 4>), grid, dim3(256), 0, stream, a);
+    return hipGetLastError();
+  }
+  if (hpg % 16 == 0 && slots >= 16LL * 512) {
+    dim3 grid(pblocks, a.H / 16, a.B);
+    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 4, 4>), grid, dim3(256), 0, stream, a);
+  } else if (hpg % 8 == 0 && slots >= 8LL * 512) {
+    dim3 grid(pblocks, a.H / 8, a.B);
+    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 4, 2>), grid, dim3(256), 0, stream, a);
+  } else if (hpg % 4 == 0) {
     dim3 grid(pblocks, a.H / 4, a.B);
-    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 4>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 4, 1>), grid, dim3(256), 0, stream, a);
   } else {
     dim3 grid(pblocks, a.H, a.B);
-    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 1>), grid, dim3(64), 0, stream, a);
+    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 1, 1>), grid, dim3(64), 0, stream, a);
   }
   return hipGetLastError();
 }
@@ -559,6 +655,14 @@ extern "C" int m2r_state_step_tier(const void* x, const void* dt, const float* A
   hipError_t e = dispatch_tier(d, stream);
   if (e == hipErrorInvalidValue) return m2r_fail("tier step: unsupported tier layout");
   return m2r_check(e, "tier step launch");
+}
+
+extern "C" int m2r_set_step_shape(int waves_per_block, int heads_per_wave) {
+  const int w = waves_per_block, k = heads_per_wave;
+  const bool ok = (w == 0 && k == 0) || (w == 1 && k == 1) || (w == 4 && (k == 1 || k == 2 || k == 4));
+  if (!ok) return m2r_fail("step shape: supported (waves, heads per wave) are (1,1), (4,1), (4,2), (4,4) or (0,0)");
+  g_forced_shape.store(w * 16 + k, std::memory_order_relaxed);
+  return 0;
 }
 
 extern "C" int m2r_state_step_legacy(const void* x, const void* dt, const float* A, const void* B, const void* C,

@@ -34,6 +34,7 @@ _SIGNATURES = {
     "m2r_probe_unary": ([P, P, I64, I, P], I),
     "m2r_probe_div": ([P, P, P, I64, P], I),
     "m2r_probe_butterfly": ([P, P, P], I),
+    "m2r_set_step_shape": ([I, I], I),
 }
 
 

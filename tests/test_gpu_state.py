@@ -145,6 +145,38 @@ def test_ridge_ragged_p(oracle, device):
     run_ridge(oracle, device, "36_24_68", batch=2, L=2, H=16, P=80, G=2, seed=16)
 
 
+def test_ridge_model_batch_sixteen_head_blocks(oracle, device):
+    # the benchmark geometry (batch 64, one token) selects 16 heads per workgroup
+    run_ridge(oracle, device, "32_32_64", batch=64, L=1, H=128, P=64, G=8, seed=19)
+
+
+SHAPES = [(1, 1), (4, 1), (4, 2), (4, 4)]
+
+
+@pytest.fixture
+def forced_shape(request):
+    from mamba2_recall import _native
+    _native.call("m2r_set_step_shape", *request.param)
+    yield request.param
+    _native.call("m2r_set_step_shape", 0, 0)
+
+
+@pytest.mark.parametrize("forced_shape", SHAPES, indirect=True, ids=lambda s: f"w{s[0]}h{s[1]}")
+def test_ridge_every_workgroup_shape(oracle, device, forced_shape):
+    """Each (waves, head slots per wave) variant: multi-token, ragged P, one
+    group and several (the ridge format needs P % 16 == 0)."""
+    run_ridge(oracle, device, "32_32_64", batch=2, L=3, H=32, P=80, G=2, seed=61)
+    run_ridge(oracle, device, "8_80_40", batch=1, L=2, H=16, P=48, G=1, seed=62)
+    run_ridge(oracle, device, "44_8_76", batch=3, L=1, H=16, P=64, G=1, seed=63, random_state=False)
+
+
+@pytest.mark.parametrize("forced_shape", SHAPES, indirect=True, ids=lambda s: f"w{s[0]}h{s[1]}")
+def test_tier_and_legacy_every_workgroup_shape(oracle, device, forced_shape):
+    # odd P exercises the 16-bit row staging
+    run_tier(oracle, device, "tier", "36_24_68", batch=2, L=3, H=32, P=80, G=2, seed=64)
+    run_tier(oracle, device, "legacy", "16_64_48", batch=1, L=2, H=16, P=33, G=1, seed=65)
+
+
 @pytest.mark.parametrize("layout", TIER_LAYOUTS)
 def test_tier_one_token(oracle, device, layout):
     run_tier(oracle, device, "tier", layout, batch=2, L=1, H=128, P=64, G=8, seed=21)
