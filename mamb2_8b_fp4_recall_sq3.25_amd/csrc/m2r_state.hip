@@ -138,14 +138,15 @@ struct TokenShared {
 
 // Raw per-token inputs a thread loads one token ahead: its share of the
 // group's B and C rows, x of the rows it owns in each of its HPW head slots,
-// and, for the first NH threads, one head's dt + dt_bias.
+// and, for the first NH threads, one head's dt and dt_bias bits.  Nothing is
+// converted at load time, so no wait is needed until token_store.
 template <int WPB, int HPW>
 struct TokenRaw {
   static constexpr int NT = 64 * WPB;
   static constexpr int NBC = (256 + NT - 1) / NT;
   uint16_t bc[NBC];
   uint16_t xv[HPW];
-  float dtb;
+  uint16_t dt, db_lo, db_hi;   // dt_bias: f16 bits, or the halves of f32 bits
 };
 
 template <int WPB, int HPW>
@@ -164,13 +165,20 @@ __device__ __forceinline__ void token_load(const StepArgs& a, TokenRaw<WPB, HPW>
     const int hh = k * WPB + wave;
     r.xv[k] = (p < a.P) ? a.x[((size_t)bt * a.H + h0 + hh) * a.P + p] : (uint16_t)0;
   }
-  r.dtb = 0.f;
-  if (tid < WPB * HPW) r.dtb = h2f(a.dt[(size_t)bt * a.H + h0 + tid]) + load_param(a.dt_bias, a.db_f32, h0 + tid);
+  r.dt = r.db_lo = r.db_hi = 0;
+  if (tid < WPB * HPW) {
+    const int h = h0 + tid;
+    const uint16_t* db = (const uint16_t*)a.dt_bias;
+    r.dt = a.dt[(size_t)bt * a.H + h];
+    r.db_lo = db[a.db_f32 ? 2 * h : h];
+    r.db_hi = db[a.db_f32 ? 2 * h + 1 : h];
+  }
 }
 
 template <int N8, int N4, int NZ, int MODE, int WPB, int HPW>
 __device__ __forceinline__ void token_store(TokenShared<N8, N4, NZ, MODE, WPB * HPW>& sh,
-                                            const TokenRaw<WPB, HPW>& r, float Ah, int tid, int lane, int wave) {
+                                            const TokenRaw<WPB, HPW>& r, float Ah, int db_f32, int tid, int lane,
+                                            int wave) {
   using R = TokenRaw<WPB, HPW>;
 #pragma unroll
   for (int k = 0; k < R::NBC; ++k) {
@@ -180,7 +188,8 @@ __device__ __forceinline__ void token_store(TokenShared<N8, N4, NZ, MODE, WPB * 
 #pragma unroll
   for (int k = 0; k < HPW; ++k) sh.xr[(k * WPB + wave) * 64 + lane] = r.xv[k];
   if (tid < WPB * HPW) {
-    const float2 act = dt_activation(r.dtb, Ah);
+    const float db = db_f32 ? __builtin_bit_cast(float, (uint32_t)r.db_lo | ((uint32_t)r.db_hi << 16)) : h2f(r.db_lo);
+    const float2 act = dt_activation(h2f(r.dt) + db, Ah);
     sh.dtv[tid] = act.x;
     sh.decay[tid] = act.y;
   }
@@ -281,6 +290,9 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
   constexpr int TILE = O_LAT + (RIDGE ? 128 : 0) + 16;   // 16 bytes of slack for row reads
   constexpr int C8 = N8 / 4, C4 = N4 / 4;   // carried code words (4 biased bytes each)
   constexpr int PRED_DW = RIDGE ? F * NZ / 2 : 1;   // F*NZ is even for every layout
+  constexpr int PRED_OPS = (PRED_DW + 63) / 64;     // 64-dword transfers of the predictor
+  constexpr int PERM_PT = (128 + NT - 1) / NT;      // permutation bytes per thread
+  constexpr int BASIS_PT = (NZ + NT - 1) / NT;      // basis pairs per thread
   static_assert(N8 % 4 == 0 && N4 % 4 == 0 && N8 > 0 && N4 > 0, "tier widths must be positive multiples of 4");
   static_assert(!RIDGE || (F * NZ) % 2 == 0, "predictor staged as dwords");
   static_assert(TILE % 16 == 0, "tiles stay 16-byte aligned");
@@ -290,12 +302,12 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
   __shared__ float s_D[NH];
   __shared__ uint8_t s_perm[128];
   __shared__ float s_basis[RIDGE ? 2 * NZ : 1];
-  __shared__ __align__(16) uint32_t s_pred32[PRED_DW];
+  __shared__ __align__(16) uint32_t s_pred32[PRED_OPS * 64];
   __shared__ __align__(16) uint8_t s_tile[NH][TILE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: per-wave values in SGPRs
   const int b = blockIdx.z;
   const int h0 = blockIdx.y * NH;
   const int H = a.H, P = a.P, L = a.L;
@@ -306,29 +318,29 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
   const bool dword_tiles = (P & 1) == 0;   // every slot's row0 * W and nvalid * W are dword multiples
   const uint16_t* s_pred = (const uint16_t*)s_pred32;
 
-  struct SlotRegs {
-    TileRegs<W8> lo, hi;
-    TileRegs<W4> q4;
-    TileRegs<2> s8, s4, lat;
-  };
+  // vector memory operations per slot transfer (field_dma counts)
+  constexpr int SLOT_DMA = 2 * dma_ops(W8) + dma_ops(W4) + dma_ops(2) * (RIDGE ? 3 : 2);
+  static_assert(SLOT_DMA * (HPW - 1) <= 63, "slot transfers must fit the vmcnt range");
   auto slot_row0 = [&](int hh) { return (b * H + h0 + hh) * P + pbase; };
-  auto slot_load = [&](SlotRegs& r, int hh) {
+  auto slot_dma = [&](int hh) {   // even P: direct global -> LDS transfers
     const int row0 = slot_row0(hh);
-    tile_load<W8>(r.lo, a.lo, row0, nvalid, lane);
-    tile_load<W8>(r.hi, a.hi, row0, nvalid, lane);
-    tile_load<W4>(r.q4, a.q4, row0, nvalid, lane);
-    tile_load<2>(r.s8, (const uint8_t*)a.s8, row0, nvalid, lane);
-    tile_load<2>(r.s4, (const uint8_t*)a.s4, row0, nvalid, lane);
-    if constexpr (RIDGE) tile_load<2>(r.lat, a.latent, row0, nvalid, lane);
-  };
-  auto slot_store = [&](const SlotRegs& r, int hh) {
     uint8_t* t = s_tile[hh];
-    tile_store_lds<W8>(r.lo, t + O_LO, nvalid, lane);
-    tile_store_lds<W8>(r.hi, t + O_HI, nvalid, lane);
-    tile_store_lds<W4>(r.q4, t + O_Q4, nvalid, lane);
-    tile_store_lds<2>(r.s8, t + O_S8, nvalid, lane);
-    tile_store_lds<2>(r.s4, t + O_S4, nvalid, lane);
-    if constexpr (RIDGE) tile_store_lds<2>(r.lat, t + O_LAT, nvalid, lane);
+    field_dma<W8>(t + O_LO, a.lo, row0, nvalid, lane);
+    field_dma<W8>(t + O_HI, a.hi, row0, nvalid, lane);
+    field_dma<W4>(t + O_Q4, a.q4, row0, nvalid, lane);
+    field_dma<2>(t + O_S8, (const uint8_t*)a.s8, row0, nvalid, lane);
+    field_dma<2>(t + O_S4, (const uint8_t*)a.s4, row0, nvalid, lane);
+    if constexpr (RIDGE) field_dma<2>(t + O_LAT, a.latent, row0, nvalid, lane);
+  };
+  // at the first token, before slot k is read: its transfers have landed
+  // once at most (HPW - 1 - k) slots' transfers are outstanding (program
+  // order; later operations only make the wait longer)
+  auto slot_wait = [&](int k) {
+    const int later = HPW - 1 - k;
+    if (later >= 3) wait_vmcnt<(HPW >= 4 ? 3 * SLOT_DMA : 0)>();
+    else if (later == 2) wait_vmcnt<(HPW >= 3 ? 2 * SLOT_DMA : 0)>();
+    else if (later == 1) wait_vmcnt<(HPW >= 2 ? SLOT_DMA : 0)>();
+    else wait_vmcnt<0>();
   };
   auto slot_copy_in = [&](int hh) {   // odd P: 16-bit transfers
     const int row0 = slot_row0(hh);
@@ -343,6 +355,15 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
   auto slot_copy_out = [&](int hh) {
     const int row0 = slot_row0(hh);
     const uint8_t* t = s_tile[hh];
+    if (dword_tiles) {
+      field_store<W8>(a.lo, t + O_LO, row0, nvalid, lane);
+      field_store<W8>(a.hi, t + O_HI, row0, nvalid, lane);
+      field_store<W4>(a.q4, t + O_Q4, row0, nvalid, lane);
+      field_store<2>((uint8_t*)a.s8, t + O_S8, row0, nvalid, lane);
+      field_store<2>((uint8_t*)a.s4, t + O_S4, row0, nvalid, lane);
+      if constexpr (RIDGE) field_store<2>(a.latent, t + O_LAT, row0, nvalid, lane);
+      return;
+    }
     wave_copy_out<W8>(a.lo, t + O_LO, row0, nvalid, lane);
     wave_copy_out<W8>(a.hi, t + O_HI, row0, nvalid, lane);
     wave_copy_out<W4>(a.q4, t + O_Q4, row0, nvalid, lane);
@@ -351,30 +372,65 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
     if constexpr (RIDGE) wave_copy_out<2>(a.latent, t + O_LAT, row0, nvalid, lane);
   };
 
-  // ---- issue every independent load of the first token and first slot -----------
-  SlotRegs nxt;
-  if (dword_tiles) slot_load(nxt, wave);
+  // ---- prologue: register loads of the first token and the statics, then the
+  // LDS transfers (predictor, every slot), then the LDS stores that need the
+  // register loads (whose waits then leave the transfers in flight) ---------
   TokenRaw<WPB, HPW> raw;
   token_load<WPB, HPW>(a, raw, b * L, g, h0, pbase, tid, lane, wave);
   const float Ah = (tid < NH) ? a.A[h0 + tid] : 0.f;
-  if (tid < NH) s_D[tid] = load_param(a.D, a.d_f32, h0 + tid);
-  for (int n = tid; n < 128; n += NT) s_perm[n] = a.perm[g * 128 + n];
+  const float Dv = (tid < NH) ? load_param(a.D, a.d_f32, h0 + tid) : 0.f;
+  uint8_t permv[PERM_PT];
+#pragma unroll
+  for (int k = 0; k < PERM_PT; ++k) {
+    const int n = k * NT + tid;
+    permv[k] = (n < 128) ? a.perm[g * 128 + n] : (uint8_t)0;
+  }
+  uint32_t basisv[BASIS_PT];
   float ls0 = 0.f, ls1 = 0.f, rls0 = 0.f, rls1 = 0.f;
   if constexpr (RIDGE) {
-    const uint32_t* pg = (const uint32_t*)(a.pred + (size_t)g * F * NZ);
-    for (int i = tid; i < PRED_DW; i += NT) s_pred32[i] = pg[i];
-    for (int i = tid; i < NZ; i += NT) {
-      const uint32_t e = ((const uint32_t*)a.basis)[g * NZ + i];
-      s_basis[i] = h2f((uint16_t)(e & 0xFFFFu));
-      s_basis[NZ + i] = h2f((uint16_t)(e >> 16));
+#pragma unroll
+    for (int k = 0; k < BASIS_PT; ++k) {
+      const int i = k * NT + tid;
+      basisv[k] = (i < NZ) ? ((const uint32_t*)a.basis)[g * NZ + i] : 0u;
     }
     ls0 = h2f(a.lscale[g * 2]);
     ls1 = h2f(a.lscale[g * 2 + 1]);
     rls0 = 1.0f / ls0;   // correctly rounded reciprocals
     rls1 = 1.0f / ls1;
   }
-  if (dword_tiles) slot_store(nxt, wave); else slot_copy_in(wave);
-  token_store<N8, N4, NZ, MODE, WPB, HPW>(sh, raw, Ah, tid, lane, wave);
+  // the register loads complete before any LDS transfer is issued
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+  if constexpr (RIDGE) {   // predictor rows of the group, spread over the waves
+    const uint8_t* pg = (const uint8_t*)(a.pred + (size_t)g * F * NZ);
+    for (int j = wave; j < PRED_OPS; j += WPB) lds_dma_b32(pg + 4 * min(j * 64 + lane, PRED_DW - 1),
+                                                           lds_address(s_pred32 + 64 * j));
+  }
+  if (dword_tiles) {
+    for (int k = 0; k < HPW; ++k) slot_dma(k * WPB + wave);
+  }
+  if (tid < NH) s_D[tid] = Dv;
+#pragma unroll
+  for (int k = 0; k < PERM_PT; ++k) {
+    const int n = k * NT + tid;
+    if (n < 128) s_perm[n] = permv[k];
+  }
+  if constexpr (RIDGE) {
+#pragma unroll
+    for (int k = 0; k < BASIS_PT; ++k) {
+      const int i = k * NT + tid;
+      if (i < NZ) {
+        s_basis[i] = h2f((uint16_t)(basisv[k] & 0xFFFFu));
+        s_basis[NZ + i] = h2f((uint16_t)(basisv[k] >> 16));
+      }
+    }
+  }
+  if (!dword_tiles) {
+    for (int k = 0; k < HPW; ++k) slot_copy_in(k * WPB + wave);
+  }
+  token_store<N8, N4, NZ, MODE, WPB, HPW>(sh, raw, Ah, a.db_f32, tid, lane, wave);
+  // the predictor transfers precede every slot transfer
+  // (a smaller count than the slot transfers only waits longer)
+  if (dword_tiles) wait_vmcnt<(HPW * SLOT_DMA > 63 ? 63 : HPW * SLOT_DMA)>(); else wait_vmcnt<0>();
   __syncthreads();
 
   const float y127 = 1.0f / 127.0f;   // RN(1/127)
@@ -383,7 +439,7 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
   for (int t = 0; t < L; ++t) {
     const int bt = b * L + t;
     if (t > 0) {
-      token_store<N8, N4, NZ, MODE, WPB, HPW>(sh, raw, Ah, tid, lane, wave);
+      token_store<N8, N4, NZ, MODE, WPB, HPW>(sh, raw, Ah, a.db_f32, tid, lane, wave);
       __syncthreads();
     }
     if (t + 1 < L) token_load<WPB, HPW>(a, raw, bt + 1, g, h0, pbase, tid, lane, wave);   // prefetch
@@ -392,10 +448,7 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
     for (int k = 0; k < HPW; ++k) {
       const int hh = k * WPB + wave;
       const int h = h0 + hh;
-      const bool stream_next = (t == 0) && (k + 1 < HPW);
-      if (stream_next) {
-        if (dword_tiles) slot_load(nxt, hh + WPB); else slot_copy_in(hh + WPB);
-      }
+      if (t == 0) slot_wait(k);
       uint8_t* tile = s_tile[hh];
       uint16_t* t16 = (uint16_t*)tile;
 
@@ -533,7 +586,6 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
         t16[O_S4 / 2 + lane] = f2h(sc4);
         if constexpr (RIDGE) t16[O_LAT / 2 + lane] = (uint16_t)qz;
       }
-      if (stream_next && dword_tiles) slot_store(nxt, hh + WPB);
       wave_sync();
       if (t == L - 1) slot_copy_out(hh);
     }

@@ -81,6 +81,121 @@ __device__ __forceinline__ void tile_store_lds(const TileRegs<W>& t, uint8_t* ld
   }
 }
 
+// Direct global -> LDS transfers (LDS DMA): every lane reads SIZE bytes at
+// its own global address; they land at LDS byte address lds + SIZE * lane.
+// Issued as inline assembly on purpose: the compiler then neither counts
+// them in its own vmcnt bookkeeping nor guards later LDS stores with waits
+// for them, so the callers own the ordering.  A caller must (1) let every
+// compiler-visible global load complete before issuing transfers (otherwise
+// the compiler's wait for such a load would also wait for the transfers),
+// and (2) wait with wait_vmcnt before reading the destination.  M0, which
+// carries the LDS address (wave-uniform by contract), is saved and restored
+// around the instruction.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+__device__ __forceinline__ void lds_dma_b32(const void* g, uint32_t lds) {
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved) : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+
+// LDS DMA of one SoA field of a 64-row slot: 64 * W bytes at g + row0 * W
+// land at lds[0 .. 64 * W).  W / 4 dword transfers (64 lanes x 4 bytes)
+// plus, for W % 4 == 2, one transfer by lanes 0..31 cover the field exactly
+// (narrower transfers still advance the LDS address by 4 bytes per lane, so
+// they cannot pack 16-bit elements).  Lanes past the nvalid valid rows
+// re-read the last valid dword; their copies land in rows nobody reads.
+// Every transfer has active lanes, so a call issues exactly dma_ops(W)
+// vector memory operations.  Requires row0 * W and nvalid * W to be dword
+// multiples.
+constexpr int dma_ops(int W) { return W / 4 + (W % 4 ? 1 : 0); }
+
+// Same transfer with a wave-uniform 64-bit base in SGPRs, a per-lane 32-bit
+// offset and a compile-time instruction offset: no per-transfer VALU work.
+// The instruction offset moves the global and the LDS address alike (LDS
+// destination = M0 + IMM + 4 * lane), so M0 stays at the field base.
+template <int IMM>
+__device__ __forceinline__ void lds_dma_b32_sbase(uint32_t voff, const void* sbase, uint32_t lds) {
+  static_assert(IMM >= 0 && IMM < 4096, "instruction offset range");
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\tglobal_load_lds_dword %1, %2 offset:%4\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved) : "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds)), "n"(IMM)
+               : "memory");
+}
+
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+// full 64-row field: transfer K.. of N with offsets 256 * K
+template <int K, int N>
+struct FullFieldDma {
+  static __device__ __forceinline__ void run(uint32_t lane4, const void* base, uint32_t l0) {
+    if constexpr (K < N) {
+      lds_dma_b32_sbase<256 * K>(lane4, base, l0);
+      FullFieldDma<K + 1, N>::run(lane4, base, l0);
+    }
+  }
+};
+
+template <int W>
+__device__ __forceinline__ void field_dma(uint8_t* lds, const uint8_t* g, int row0, int nvalid, int lane) {
+  static_assert(W % 2 == 0, "even field widths");
+  const uint8_t* base = (const uint8_t*)uniform_ptr(g + (size_t)row0 * W);
+  const uint32_t l0 = lds_address(lds);
+  if (nvalid == 64) {   // every row valid: constant offsets, nothing to clamp
+    const uint32_t lane4 = 4u * (uint32_t)lane;
+    FullFieldDma<0, W / 4>::run(lane4, base, l0);
+    if constexpr (W % 4 != 0) {
+      if (lane < 32) lds_dma_b32_sbase<256 * (W / 4)>(lane4, base, l0);
+    }
+    return;
+  }
+  const int last_dw = nvalid * W / 4 - 1;
+#pragma unroll
+  for (int k = 0; k < W / 4; ++k) lds_dma_b32(base + 4 * min(k * 64 + lane, last_dw), l0 + 256 * k);
+  if constexpr (W % 4 != 0) {
+    if (lane < 32) lds_dma_b32(base + 4 * min((W / 4) * 64 + lane, last_dw), l0 + 256 * (W / 4));
+  }
+}
+
+// Raw buffer resource over `bytes` bytes at `base` (gfx9-family dword 3:
+// 32-bit raw data, no swizzle): accesses at offsets >= bytes are dropped
+// (stores) or read 0 (loads) by the hardware range check.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_buffer(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+// Stores one SoA field of a 64-row slot staged in LDS (64 * W bytes) to
+// g + row0 * W, nvalid rows: all LDS reads first, then unguarded dword
+// buffer stores whose range check drops everything past nvalid * W bytes.
+// Requires row0 * W and nvalid * W to be dword multiples.
+template <int W>
+__device__ __forceinline__ void field_store(uint8_t* g, const uint8_t* lds, int row0, int nvalid, int lane) {
+  constexpr int NW = (16 * W + 63) / 64;
+  const uint32_t* src = (const uint32_t*)lds;
+  const __amdgpu_buffer_rsrc_t rsrc = raw_buffer(g + (size_t)row0 * W, nvalid * W);
+  uint32_t v[NW];
+#pragma unroll
+  for (int k = 0; k < NW; ++k) v[k] = src[(k * 64 + 64 <= 16 * W) ? k * 64 + lane : min(k * 64 + lane, 16 * W - 1)];
+#pragma unroll
+  // the chunk offset goes into the range-checked offset (the scalar offset
+  // operand is outside the raw-buffer range check)
+  for (int k = 0; k < NW; ++k) __builtin_amdgcn_raw_buffer_store_b32(v[k], rsrc, 4 * (k * 64 + lane), 0, 0);
+}
+
+// Waits until at most N vector memory operations of this wave are
+// outstanding; also a compiler barrier for memory accesses.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // Reads W (even) bytes at lds[off .. off+W) (off even) as little-endian
 // words: aligned dword reads plus one funnel shift per word.  The tile keeps
 // 4 bytes of slack so the last dword read stays inside the allocation.
