@@ -11,6 +11,8 @@ bandwidth, a live roofline for the dominant kernel, and the CPU oracle
 timed on a bounded sample as a baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-fp4] [--skip-cpu]
+       python bench.py --only step|copy   (profiling runs: only the batch-64
+       step graph, or only a 256 MiB device copy used to calibrate counters)
 """
 from __future__ import annotations
 
@@ -91,14 +93,13 @@ class RidgeStack:
             d["state"] = ridge_codec.allocate_state(batch, H, P, NSTATE, device, layout=layout)
             d["y"] = torch.empty_like(d["x"])
             self.layers.append(d)
-        # warm the carry from zero with 16 tokens per layer
+        # warm the carry from zero with 16 tokens per layer,
+        # as 16 one-token steps (equal to one 16-token call; keeps every launch
+        # of the kernel a one-token launch, as in the timed region)
         for d in self.layers:
-            xs = d["x"].expand(batch, 16, H, P).contiguous()
-            dts = d["dt"].expand(batch, 16, H).contiguous()
-            Bs = d["B"].expand(batch, 16, G, NSTATE).contiguous()
-            Cs = d["C"].expand(batch, 16, G, NSTATE).contiguous()
-            ridge_codec.scan(xs, dts, d["A"], Bs, Cs, d["D"], d["dt_bias"], d["state"], d["perm"], d["basis"],
-                             d["lscale"], d["pred"], layout=d["layout"])
+            for t in range(16):
+                ridge_codec.scan(d["x"], d["dt"], d["A"], d["B"], d["C"], d["D"], d["dt_bias"], d["state"],
+                                 d["perm"], d["basis"], d["lscale"], d["pred"], layout=d["layout"], validate=(t == 0))
         torch.cuda.synchronize()
 
     def launch_all(self, stream_handle):
@@ -141,20 +142,19 @@ def time_graph(g, steps, warmup):
     return ev0.elapsed_time(ev1) / steps, wall * 1e3 / steps
 
 
-def kernel_average_us(stack, reps):
-    """Average duration of the per-layer step kernel, from HIP events on the
-    launch stream over `reps` back-to-back eager 56-launch sweeps."""
-    import ctypes
-    h = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    stack.launch_all(h)
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    for _ in range(reps):
-        stack.launch_all(h)
-    ev1.record()
-    torch.cuda.synchronize()
-    return ev0.elapsed_time(ev1) * 1e3 / (reps * len(PUBLISHED_LAYOUTS))
+TRAFFIC_PROFILE = ROOT / "profiles" / "state_step_b64_pmc_traffic.txt"
+
+
+def measured_traffic():
+    """HBM bytes per launch of the step kernel at batch 64, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (copy-calibrated), or None."""
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch"):
+                return int(line.split("=")[1].strip())
+    except (OSError, ValueError, IndexError):
+        return None
+    return None
 
 
 def copy_bandwidth(device):
@@ -212,8 +212,8 @@ def fp4_full_decode(device, steps=3):
 
 def cpu_baseline(budget_s=12.0):
     """The C oracle (OpenMP over rows) on a bounded sample of the batch-64
-    workload: consecutive published layers at batch 8 until the budget is
-    spent; throughput in algorithmic GB/s."""
+    workload: the published layers in order at batch 8, repeated until the
+    budget is spent; throughput in algorithmic GB/s."""
     sys.path.insert(0, str(ROOT / "tests"))
     import cases
     from oracle import oracle
@@ -221,7 +221,7 @@ def cpu_baseline(budget_s=12.0):
     rng = np.random.default_rng(1)
     batch = 8
     done_bytes, elapsed, layers = 0, 0.0, 0
-    for layout in PUBLISHED_LAYOUTS:
+    for layout in PUBLISHED_LAYOUTS * 64:
         n8, n4, nz = ridge_counts(layout)
         inp = cases.step_inputs(rng, batch, 1, H, P, G)
         sta = cases.ridge_statics(rng, G, n8, n4, nz)
@@ -236,8 +236,8 @@ def cpu_baseline(budget_s=12.0):
             break
     cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     return dict(value=round(done_bytes / elapsed / 1e9, 4), unit="GB/s", cores=cores, kind="port",
-                sample=f"C oracle (OpenMP over rows), {layers} consecutive published ridge layers at batch {batch}, "
-                       f"1 token each, {elapsed:.1f} s")
+                sample=f"C oracle (OpenMP over rows), {layers} published ridge layer steps in order at batch "
+                       f"{batch}, 1 token each, {elapsed:.1f} s")
 
 
 def main():
@@ -248,6 +248,7 @@ def main():
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--skip-fp4", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--only", choices=("step", "copy"), default=None)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the state codec and FP4 decode shard with no communication "
@@ -257,17 +258,30 @@ def main():
     device = torch.device("cuda:0")
     from mamba2_recall import _native
     _native.lib()
+    if args.only == "copy":
+        a = torch.empty(256 << 20, dtype=torch.uint8, device=device)
+        b = torch.empty_like(a)
+        for _ in range(args.steps):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps(dict(only="copy", bytes_read=a.numel(), bytes_written=a.numel(), launches=args.steps)))
+        return
 
     stack = RidgeStack(args.batch, device)
     g = stack.graph()
     ms, wall_ms = time_graph(g, args.steps, args.warmup)
     nbytes = step_bytes(args.batch, PUBLISHED_LAYOUTS)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    kern_us = kernel_average_us(stack, max(2, args.steps // 5))
+    # average launch of the step kernel: the timed graph region (HIP events on
+    # the replay stream) over its 56 launches per step
+    kern_us = ms * 1e3 / len(PUBLISHED_LAYOUTS)
     per_launch = nbytes / len(PUBLISHED_LAYOUTS)
     achieved = per_launch / (kern_us * 1e-6) / 1e9
     del g, stack
     torch.cuda.empty_cache()
+    if args.only == "step":
+        print(json.dumps(dict(only="step", batch=args.batch, ms_per_step=round(ms, 5), avg_launch_us=round(kern_us, 3))))
+        return
 
     stack1 = RidgeStack(1, device, seed=2027)
     g1 = stack1.graph()
@@ -292,7 +306,7 @@ def main():
                     layouts="published per-layer (wt2_test_v1)", launch="HIP graph of 56 per-layer kernels",
                     algorithmic_bytes_per_step=nbytes),
         roofline=dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                      frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
+                      frac=round(achieved / HBM_PEAK_GBS, 4), traffic=measured_traffic(),
                       kernel="k_state_step (ridge)", avg_launch_us=round(kern_us, 3),
                       algorithmic_bytes_per_launch=round(per_launch)),
         extra=extra)
