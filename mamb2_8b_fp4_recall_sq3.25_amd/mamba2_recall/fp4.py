@@ -147,14 +147,19 @@ def decode_packet(packet):
     flag = torch.zeros(1, dtype=torch.int32, device=packed.device)
     decode_into(packed, scales.view(torch.uint8) if group == 16 else scales, global_scale, out,
                 rows=rows, columns=columns, group=group, err_flag=flag)
-    err = int(flag.item())
+    raise_decode_errors(int(flag.item()))
+    return out
+
+
+def raise_decode_errors(err):
+    """Raises the reference's ValueError for the first condition (in the
+    reference's check order) whose bit is set in the kernels' error word."""
     if err:
         _need(not err & ERR_SCALE, "Invalid stored scale")
         _need(not err & ERR_GLOBAL, "Global scale must be finite and positive")
         _need(not err & ERR_PADDING, "Nonzero final-group padding")
         _need(not err & ERR_ZERO_SCALE, "Nonzero code in a zero-scale group")
         _need(not err & ERR_DECODED, "Nonfinite decoded FP16 weights")
-    return out
 
 
 def expected_payload_bytes(format_name):
