@@ -177,6 +177,61 @@ static float load_param(const void* p, int f32, int64_t i) {
   return f32 ? ((const float*)p)[i] : orc_f16_to_f32(((const uint16_t*)p)[i]);
 }
 
+/* ------------------------------------------------ FP16-carry control step
+ * _s16_scan (mamba2_recall/state_codec.py:65-102): per row the FP32 carry is
+ * state*decay + (b*dt)*x (three roundings), read out against C with D*x,
+ * then rounded to FP16.  Statistics (optional, may be NULL): for every
+ * (b, h, 16-row tile of P, coordinate) the sum over tokens and tile rows of
+ * |FP16 carry|, accumulated in double and rounded once.  state is
+ * [B,H,P,128] f16 bits, stats [B,H,ceil(P/16),128] f32.
+ */
+int orc_s16_step(const uint16_t* X, const uint16_t* DT, const float* A, const uint16_t* Bm, const uint16_t* Cm,
+                 const void* D, int d_f32, const void* DB, int db_f32, uint16_t* S, uint16_t* Y, float* stats,
+                 int64_t batch, int64_t L, int64_t H, int64_t P, int64_t G) {
+  if (H % G) return 1;
+  const int64_t hpg = H / G, tiles = (P + 15) / 16;
+  if (stats) memset(stats, 0, sizeof(float) * batch * H * tiles * 128);
+  #pragma omp parallel for collapse(2) schedule(static)
+  for (int64_t b = 0; b < batch; ++b)
+    for (int64_t h = 0; h < H; ++h) {
+      const int64_t g = h / hpg;
+      const float av = A[h], dv = load_param(D, d_f32, h), bias = load_param(DB, db_f32, h);
+      double* acc = stats ? (double*)calloc((size_t)tiles * 128, sizeof(double)) : NULL;
+      for (int64_t p = 0; p < P; ++p) {
+        uint16_t* st = S + ((b * H + h) * P + p) * 128;
+        float v[128];
+        for (int n = 0; n < 128; ++n) v[n] = orc_f16_to_f32(st[n]);
+        for (int64_t t = 0; t < L; ++t) {
+          const int64_t bt = b * L + t;
+          const float x = orc_f16_to_f32(X[(bt * H + h) * P + p]);
+          const float dtv = orc_softplus_dt(orc_f16_to_f32(DT[bt * H + h]) + bias);
+          const float decay = orc_expf(av * dtv);
+          const uint16_t* bv = Bm + (bt * G + g) * 128;
+          const uint16_t* cv = Cm + (bt * G + g) * 128;
+          double out = 0.0;
+          for (int n = 0; n < 128; ++n) {
+            const float db = orc_f16_to_f32(bv[n]) * dtv;
+            const float pd = v[n] * decay;
+            const float bx = db * x;
+            v[n] = pd + bx;
+            out += (double)v[n] * (double)orc_f16_to_f32(cv[n]);
+          }
+          Y[(bt * H + h) * P + p] = orc_f32_to_f16((float)out + x * dv);
+          for (int n = 0; n < 128; ++n) {
+            v[n] = orc_f16_to_f32(orc_f32_to_f16(v[n]));
+            if (acc) acc[(p / 16) * 128 + n] += fabs((double)v[n]);
+          }
+        }
+        for (int n = 0; n < 128; ++n) st[n] = orc_f32_to_f16(v[n]);
+      }
+      if (acc) {
+        for (int64_t i = 0; i < tiles * 128; ++i) stats[(b * H + h) * tiles * 128 + i] = (float)acc[i];
+        free(acc);
+      }
+    }
+  return 0;
+}
+
 /* ------------------------------------------------ packed 52-byte state step
  * mode 0: legacy sq3p25 (FP32 denominator quantize, state_codec.py:156-163)
  * mode 1: stored-scale tiers (state_ppl_codec_v10.py:110-141)

@@ -40,6 +40,8 @@ def lib():
         _lib.orc_state_step.restype = I
         _lib.orc_dense3_step.argtypes = [I] + [P] * 5 + [P, I, P, I, P, P, P, P] + [I64] * 5
         _lib.orc_dense3_step.restype = I
+        _lib.orc_s16_step.argtypes = [P] * 5 + [P, I, P, I] + [P] * 3 + [I64] * 5
+        _lib.orc_s16_step.restype = I
         _lib.orc_fp4_decode.argtypes = [I, P, P, F, P, I64, I64]
         _lib.orc_fp4_decode.restype = ctypes.c_uint32
         _lib.orc_unary.argtypes = [P, P, I64, I]
@@ -109,6 +111,21 @@ def dense3_step(table_kind, x, dt, A, B, C, D, dt_bias, table, state):
     if rc:
         raise ValueError(f"oracle dense3 step rejected the geometry (rc={rc})")
     return y
+
+
+def s16_step(x, dt, A, B, C, D, dt_bias, state, collect_stats=False):
+    """mamba2_recall/state_codec.py:65-102 on CPU; mutates `state` (uint16
+    f16 bits [B,H,P,128]) and returns (y uint16 bits, stats f32 or None)."""
+    batch, length, heads, dim = x.shape
+    groups = B.shape[2]
+    y = np.zeros_like(x)
+    stats = np.zeros((batch, heads, (dim + 15) // 16, 128), np.float32) if collect_stats else None
+    rc = lib().orc_s16_step(_p(x), _p(dt), _p(A), _p(B), _p(C), _p(D), int(D.dtype == np.float32), _p(dt_bias),
+                            int(dt_bias.dtype == np.float32), _p(state), _p(y), _p(stats), batch, length, heads,
+                            dim, groups)
+    if rc:
+        raise ValueError(f"oracle s16 step rejected the geometry (rc={rc})")
+    return y, stats
 
 
 def fp4_decode(group, packed, scales, global_scale, rows, cols):

@@ -268,3 +268,34 @@ def test_dense3_multi_token_small(oracle, device, kind):
 
 def test_dense3_wide_batch(oracle, device):
     run_dense3(oracle, device, "permutation", batch=32, L=1, H=128, P=64, G=8, seed=53)
+
+
+def run_s16(oracle, device, batch, L, H, P, G, seed, collect):
+    from mamba2_recall import state_codec
+    rng = np.random.default_rng(seed)
+    inp = cases.step_inputs(rng, batch, L, H, P, G)
+    st0 = cases.f16(rng.standard_normal((batch, H, P, 128)) * 0.5)
+    print(f"[s16] B={batch} L={L} H={H} P={P} G={G} seed={seed} stats={collect}", flush=True)
+    ref = st0.copy()
+    y_ref, s_ref = oracle.s16_step(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], inp["dt_bias"], ref,
+                                   collect_stats=collect)
+    state = state_codec.allocate_state(batch, H, P, 128, "s16", device)
+    state.tensors["state"].copy_(dev16(st0, device))
+    t = {k: devp(v, device) for k, v in inp.items() if k != "perm"}
+    y, stats = state_codec.scan(t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["dt_bias"], state,
+                                collect_stats=collect)
+    torch.cuda.synchronize()
+    got = state.tensors["state"].cpu().numpy().view(np.uint16)
+    assert int((got != ref).sum()) == 0, "s16 carry differs"
+    assert_y_close(y, y_ref, "s16")
+    if collect:
+        s = stats.cpu().numpy()
+        assert s.shape == s_ref.shape
+        assert np.allclose(s, s_ref, rtol=1e-5, atol=1e-6)
+    else:
+        assert stats is None
+
+
+def test_s16_control_step(oracle, device):
+    run_s16(oracle, device, 2, 3, 128, 64, 8, 81, collect=False)
+    run_s16(oracle, device, 1, 5, 16, 40, 2, 82, collect=True)      # ragged statistics tile

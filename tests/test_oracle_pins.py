@@ -326,3 +326,74 @@ def test_readout_matches_float64_restatement(oracle):
             out = state @ cv[:L8] + decay * (z @ (basis.T @ cv[L8:])) + x[p] * dtv * (bv[L8:] @ cv[L8:])
             out += x[p] * float(f(inp["D"])[h]) + decay * (prior[0, h, p] @ corr[:L8] + z @ corr[L8:])
             assert abs(y[0, 0, h, p] - out) <= 2e-3 * max(1.0, abs(out)), (h, p, y[0, 0, h, p], out)
+
+
+# ---------------------------------------------------------------- s16 control
+
+def _s16_inputs(rng, batch, L, H, P, G):
+    inp = cases.step_inputs(rng, batch, L, H, P, G)
+    st = cases.f16(rng.standard_normal((batch, H, P, 128)) * 0.5)
+    return inp, st
+
+
+def test_s16_unit_decay_zero_input_keeps_carry_and_reads_it_out(oracle):
+    """A = 0 (decay exp(0) = 1), B = 0: the FP16 carry is unchanged and the
+    readout is the float64 dot product with C plus x*D (closed form)."""
+    rng = np.random.default_rng(71)
+    inp, st = _s16_inputs(rng, 1, 2, 4, 32, 2)
+    inp["A"][:] = 0
+    inp["B"][:] = 0
+    st0 = st.copy()
+    y, _ = oracle.s16_step(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], inp["dt_bias"], st)
+    assert (st == st0).all()
+    v = cases.f16_to_f32(st0).astype(np.float64)                       # [1,H,P,128]
+    c = cases.f16_to_f32(inp["C"]).astype(np.float64)                  # [1,L,G,128]
+    x = cases.f16_to_f32(inp["x"]).astype(np.float64)                  # [1,L,H,P]
+    D = cases.f16_to_f32(inp["D"]).astype(np.float64)
+    g = np.arange(4) // 2
+    want = np.einsum("hpn,lhn->lhp", v[0], c[0][:, g]) + x[0] * D[None, :, None]
+    got = cases.f16_to_f32(y[0]).astype(np.float64)
+    assert np.allclose(got, want, rtol=2e-3, atol=2e-3)
+
+
+def test_s16_input_lands_on_its_coordinate(oracle):
+    """A = 0, B = e_j, x = 1: carry_j grows by exactly softplus(dt) (rounded
+    to FP16), every other coordinate is untouched."""
+    rng = np.random.default_rng(72)
+    inp, st = _s16_inputs(rng, 1, 1, 2, 16, 1)
+    inp["A"][:] = 0
+    inp["B"][:] = 0
+    j = 37
+    inp["B"][0, 0, 0, j] = cases.f16(np.array([1.0]))[0]
+    inp["x"][:] = cases.f16(np.array([1.0]))[0]
+    st0 = cases.f16_to_f32(st.copy())
+    oracle.s16_step(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], inp["dt_bias"], st)
+    after = cases.f16_to_f32(st)
+    dt = cases.f16_to_f32(inp["dt"])[0, 0]                             # [H]
+    sp = np.log1p(np.exp(dt.astype(np.float64))).astype(np.float32)
+    want_j = (st0[..., j] + sp[None, :, None]).astype(np.float16).astype(np.float32)
+    assert np.array_equal(after[..., j], want_j)
+    mask = np.ones(128, bool)
+    mask[j] = False
+    assert np.array_equal(after[..., mask], st0[..., mask])
+
+
+def test_s16_statistics_sum_stored_carry_per_tile(oracle):
+    """Statistics = sum over tokens and the 16 rows of each P tile of
+    |FP16 carry| after each token; ragged last tile."""
+    rng = np.random.default_rng(73)
+    inp, st = _s16_inputs(rng, 2, 3, 4, 40, 2)
+    want = np.zeros((2, 4, 3, 128))
+    cur = st.copy()
+    for t in range(3):
+        sl = slice(t, t + 1)
+        oracle.s16_step(inp["x"][:, sl].copy(), inp["dt"][:, sl].copy(), inp["A"], inp["B"][:, sl].copy(),
+                        inp["C"][:, sl].copy(), inp["D"], inp["dt_bias"], cur)
+        a = np.abs(cases.f16_to_f32(cur).astype(np.float64))
+        for tile in range(3):
+            want[:, :, tile] += a[:, :, 16 * tile:16 * tile + 16].sum(2)
+    st2 = st.copy()
+    _, stats = oracle.s16_step(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], inp["dt_bias"], st2,
+                               collect_stats=True)
+    assert (st2 == cur).all()                                           # one call == sequential calls
+    assert np.allclose(stats, want, rtol=1e-6)
