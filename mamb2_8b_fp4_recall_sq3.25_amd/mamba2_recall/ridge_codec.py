@@ -128,3 +128,86 @@ def scan(x, dt, A, B, C, D, dt_bias, state, permutation, basis, latent_scale, pr
                               n8=spec["n8"], n4=spec["n4"], nz=spec["nzero"], basis=basis,
                               lscale=latent_scale, pred=predictor)
     return y, None
+
+
+class PredictorState(tier_codec.StateRepairV2):
+    """Mixer controller with ridge-predicted zero-tier history
+    (fp4_zero_predictor_codec_v1.py:239-367): the stored-scale tier carry of
+    StateRepairV2 plus two E4M3 latent coefficients per row, with per-layer
+    static bases [8,nz,2], latent scales [8,2] and predictors [8,F,nz].
+
+    `validate_each_step` (default True, as the reference) repeats the scan's
+    static-table and correction-finiteness checks on every call; the statics
+    are already checked here at construction, so a caller that accepts
+    non-finite activations surfacing later (assert_finite_cache) may turn it
+    off to keep the per-token path free of host synchronizations."""
+
+    validate_each_step = True
+
+    def __init__(self, model, table, layouts, bases, scales, predictors):
+        super().__init__(model, table, layouts)
+        if len(bases) != self.LAYERS or len(scales) != self.LAYERS or len(predictors) != self.LAYERS:
+            raise ValueError("Exactly 56 static bases/scales/predictors required")
+        self.bases, self.latent_scales, self.predictors = [], [], []
+        for layer, layout in enumerate(self.layouts):
+            spec = layout_descriptor(layout)
+            basis = bases[layer].to(device=self.device, dtype=torch.float16).contiguous()
+            scale = scales[layer].to(device=self.device, dtype=torch.float16).contiguous()
+            predictor = predictors[layer].to(device=self.device, dtype=torch.float16).contiguous()
+            features = spec["n8"] + spec["n4"] + 2
+            if (tuple(basis.shape) != (self.GROUPS, spec["nzero"], 2) or tuple(scale.shape) != (self.GROUPS, 2)
+                    or tuple(predictor.shape) != (self.GROUPS, features, spec["nzero"])
+                    or not bool(torch.isfinite(basis).all()) or not bool(torch.isfinite(scale).all())
+                    or not bool(torch.isfinite(predictor).all()) or not bool((scale > 0).all())
+                    or any(v.untyped_storage().nbytes() != v.numel() * 2 for v in (basis, scale, predictor))):
+                raise ValueError("Static predictor/basis/scale allocation differs")
+            self.bases.append(basis)
+            self.latent_scales.append(scale)
+            self.predictors.append(predictor)
+
+    def _new_state(self, batch_size, index):
+        layout = self.layouts[index]
+        state = allocate_state(batch_size, self.HEADS, self.HEADDIM, self.D_STATE, self.device, layout=layout)
+        validate_state(state, self.device, layout)
+        return state
+
+    def _after_reset(self, batch_size):
+        if self.cache_breakdown()["total_bytes"] != batch_size * (CACHE_BYTES - TABLE_BYTES) + TABLE_BYTES:
+            raise RuntimeError("Latent request cache violates fixed physical budget")
+
+    def _scan_layer(self, index, mx, x, dt, aa, bm, cm, entry):
+        return scan(x, dt, aa, bm, cm, mx.D, mx.dt_bias, entry.state, self.permutations[index], self.bases[index],
+                    self.latent_scales[index], self.predictors[index], layout=self.layouts[index],
+                    validate=self.validate_each_step)
+
+    def assert_finite_cache(self):
+        """fp4_zero_predictor_codec_v1.py:306-312."""
+        values = [entry.conv for entry in self._cache]
+        values.extend(t for entry in self._cache for t in entry.state.tensors.values() if t.is_floating_point())
+        if values and not all(bool(torch.isfinite(v.float()).all()) for v in values):
+            raise FloatingPointError("Nonfinite persistent latent/scale/convolution cache")
+        return True
+
+    def storage_descriptor(self):
+        """fp4_zero_predictor_codec_v1.py:282-304."""
+        layers = []
+        for layer, (entry, layout, basis, scale, predictor) in enumerate(
+                zip(self._cache, self.layouts, self.bases, self.latent_scales, self.predictors)):
+            validate_state(entry.state, self.device, layout)
+            layers.append(dict(**layout_descriptor(layout), layer=layer, state_shape=list(entry.state.shape),
+                               state_bytes=entry.state.nbytes,
+                               tensors={k: dict(shape=list(v.shape), dtype=str(v.dtype),
+                                                storage_bytes=v.untyped_storage().nbytes())
+                                        for k, v in entry.state.tensors.items()},
+                               conv_shape=list(entry.conv.shape),
+                               conv_storage_bytes=entry.conv.untyped_storage().nbytes(),
+                               static_basis_bytes=basis.untyped_storage().nbytes(),
+                               static_scale_bytes=scale.untyped_storage().nbytes(),
+                               static_predictor_bytes=predictor.untyped_storage().nbytes()))
+        return dict(format="FP4_LATENT_STATE_STORAGE_V1", layouts=list(self.layouts), row_bytes=52, payload_bytes=48,
+                    scale_bytes=4, permutation_storage_bytes=self.permutations.untyped_storage().nbytes(),
+                    total_cache_bytes=self.cache_breakdown()["total_bytes"],
+                    static_basis_bytes=sum(x.untyped_storage().nbytes() for x in self.bases),
+                    static_scale_bytes=sum(x.untyped_storage().nbytes() for x in self.latent_scales),
+                    static_predictor_bytes=sum(x.untyped_storage().nbytes() for x in self.predictors),
+                    layers=layers)

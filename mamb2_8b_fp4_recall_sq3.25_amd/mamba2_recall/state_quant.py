@@ -1,0 +1,414 @@
+"""Per-token state controllers for a frozen Mamba-2 8B model: drop-in for the
+reference's mamba2_recall/state_quant.py (StateQuant, PackedStateRuntime,
+_LayerCache).
+
+A controller replaces every mixer's forward with: in_proj -> causal conv ->
+split -> codec scan (the gfx950 state-step kernel: readout of each token's
+FP32 update, then requantization or FP16 rounding of the carry) -> the
+mixer's gated norm *called as a module* (so external norm hooks still fire)
+-> out_proj.  It owns one request cache (convolution window + packed state
+per layer), is single-stream and non-reentrant, and one controller at a time
+may own a model.
+
+`_MixerController` holds the orchestration shared by every codec; a codec
+supplies `_new_state` (one layer's carry), `_scan_layer` (one layer's codec
+call) and its cache accounting.  StateQuant covers the s16 control and the
+legacy sq3p25 carry; state_quant_dense3, tier_codec and ridge_codec define
+the dense 3-bit, stored-scale tier and ridge-latent controllers.
+"""
+from __future__ import annotations
+
+import types
+import weakref
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from . import state_codec
+
+_OWNERS = weakref.WeakKeyDictionary()
+
+
+@dataclass
+class _LayerCache:
+    conv: torch.Tensor
+    state: object
+    tokens: int = 0
+
+
+def _native_conv_ops():
+    """mamba_ssm's fused causal-conv kernels when that package is present,
+    else (None, None) and the PyTorch arithmetic below is used."""
+    try:
+        from mamba_ssm.modules import mamba2 as native
+    except ImportError:
+        return None, None
+    return native.causal_conv1d_update, native.causal_conv1d_fn
+
+
+class _MixerController:
+    """Install / reset / request-ordering logic around one codec
+    (state_quant.py:59-281).  Geometry constants describe the Mamba-2 8B
+    mixer; the model is checked against them at construction."""
+
+    LAYERS, D_MODEL, HEADS, HEADDIM, D_STATE, GROUPS, D_CONV, D_INNER = 56, 4096, 128, 64, 128, 8, 4, 8192
+    PARAMETER_TENSORS, PARAMETER_COUNT = 507, 8_236_999_680
+    TABLE_SHAPE = (56, 8, 128)
+
+    def __init__(self, model, mode, permutations, collect_stats):
+        self.model = model
+        self.mode = mode
+        self.collect_stats = bool(collect_stats)
+        self._mixers = [layer.mixer for layer in model.backbone.layers]
+        self._validate_model()
+        self.device = self._mixers[0].in_proj.weight.device
+        if self.device.type != "cuda":
+            raise ValueError("The packed state codec requires a CUDA model")
+        self.permutations = self._validate_permutations(permutations)
+        self._cache = []
+        self._sums = [None] * len(self._mixers)
+        self._counts = [0] * len(self._mixers)
+        self._originals = []
+        self._batch_size = None
+        self._expected_layer = 0
+        self._call_length = None
+        self._failed = False
+        self._installed = False
+        self._inside_backbone = False
+
+    # ---------------------------------------------------------------- geometry
+    @property
+    def _conv_channels(self):
+        return self.D_INNER + 2 * self.GROUPS * self.D_STATE
+
+    def _validate_model(self):
+        """state_quant.py:81-119."""
+        backbone = self.model.backbone
+        if len(self._mixers) != self.LAYERS:
+            raise ValueError("This runtime requires the pure 56-layer 8B model")
+        if backbone.fused_add_norm or backbone.residual_in_fp32:
+            raise ValueError("Native unfused FP16 residual orchestration required")
+        params = dict(self.model.named_parameters())
+        if len(params) != self.PARAMETER_TENSORS or sum(p.numel() for p in params.values()) != self.PARAMETER_COUNT:
+            raise ValueError("Source must have 507 original tensors / 8,236,999,680 parameters")
+        if any(p.dtype != torch.float16 or p.requires_grad or p.grad is not None for p in params.values()):
+            raise ValueError("Load the frozen FP16 source with no gradients")
+        if len({p.device for p in params.values()}) != 1:
+            raise ValueError("The frozen model must occupy one CUDA device")
+        want = (self.D_MODEL, self.HEADS, self.HEADDIM, self.D_STATE, self.GROUPS, self.D_CONV, self.D_INNER,
+                self.D_INNER)
+        shapes = ((self.D_INNER * 2 + 2 * self.GROUPS * self.D_STATE + self.HEADS, self.D_MODEL),
+                  (self.D_MODEL, self.D_INNER), (self._conv_channels, 1, self.D_CONV))
+        for index, (layer, mx) in enumerate(zip(backbone.layers, self._mixers)):
+            if layer.fused_add_norm or layer.residual_in_fp32 or layer.mlp is not None:
+                raise ValueError(f"Unsupported block orchestration at layer {index}")
+            geometry = (mx.d_model, mx.nheads, mx.headdim, mx.d_state, mx.ngroups, mx.d_conv, mx.d_ssm, mx.d_inner)
+            if geometry != want:
+                raise ValueError(f"Unsupported mixer geometry at layer {index}: {geometry}")
+            if mx.use_mem_eff_path or not mx.rmsnorm or mx.D_has_hdim:
+                raise ValueError("Explicit gated norm and one D per head required")
+            if mx.activation not in ("silu", "swish") or mx.dt_limit != (0.0, float("inf")):
+                raise ValueError("Unsupported activation or dt clipping")
+            if mx.process_group is not None:
+                raise ValueError("Distributed tensor parallel execution is unsupported")
+            if mx.norm.group_size != self.D_INNER // self.GROUPS:
+                raise ValueError("Expected eight gated RMSNorm groups")
+            actual = tuple(tuple(v.shape) for v in (mx.in_proj.weight, mx.out_proj.weight, mx.conv1d.weight))
+            if actual != shapes:
+                raise ValueError(f"Projection/convolution shapes differ: {actual}")
+
+    def _validate_permutations(self, values):
+        """state_quant.py:121-133 (a uint8 permutation per layer and group)."""
+        if not isinstance(values, torch.Tensor) or values.dtype != torch.uint8:
+            raise ValueError("Packed state requires a uint8 tensor of permutations")
+        if tuple(values.shape) != self.TABLE_SHAPE:
+            raise ValueError("Expected permutations of shape [56,8,128]")
+        cpu = values.detach().cpu().contiguous()
+        if not torch.equal(cpu.sort(dim=-1).values, torch.arange(self.D_STATE, dtype=torch.uint8).expand_as(cpu)):
+            raise ValueError("Every state group must be a permutation of 0..127")
+        return cpu.to(device=self.device, dtype=torch.uint8).contiguous()
+
+    # ---------------------------------------------------------------- lifetime
+    def install(self):
+        """Replace every mixer's forward; state_quant.py:135-151."""
+        if self._installed:
+            raise RuntimeError("StateQuant controller is already installed")
+        owner = _OWNERS.get(self.model)
+        if owner is not None and owner() is not None:
+            raise RuntimeError("Another StateQuant controller owns this model")
+        _OWNERS[self.model] = weakref.ref(self)
+        try:
+            for index, mx in enumerate(self._mixers):
+                self._originals.append((mx, mx.forward))
+
+                def forward(module, u, seqlen=None, seq_idx=None, cu_seqlens=None, inference_params=None,
+                            _index=index):
+                    return self._forward(_index, module, u, seqlen, seq_idx, cu_seqlens, inference_params)
+
+                mx.forward = types.MethodType(forward, mx)
+            self._installed = True
+        except Exception:
+            self.close()
+            raise
+        return self
+
+    def __enter__(self):
+        return self.install()
+
+    def __exit__(self, exc_type, exc_value, traceback):
+        self.close()
+        return False
+
+    def close(self):
+        for mx, original in reversed(self._originals):
+            mx.forward = original
+        self._originals.clear()
+        self._installed = False
+        owner = _OWNERS.get(self.model)
+        if owner is not None and owner() is self:
+            del _OWNERS[self.model]
+        self.clear()
+
+    def clear(self):
+        """Release all request caches, retaining calibration totals and tables."""
+        self._cache.clear()
+        self._batch_size = None
+        self._expected_layer = 0
+        self._call_length = None
+        self._failed = False
+
+    @torch.no_grad()
+    def reset(self, batch_size=1):
+        """Allocate fresh zero caches (state_quant.py:177-193)."""
+        if not self._installed:
+            raise RuntimeError("Install the controller before resetting caches")
+        if not isinstance(batch_size, int) or isinstance(batch_size, bool) or batch_size <= 0:
+            raise ValueError("batch_size must be a positive integer")
+        self.clear()
+        for index in range(len(self._mixers)):
+            # channels-last window, as the native convolution state is strided
+            conv = torch.zeros(batch_size, self.D_CONV, self._conv_channels, device=self.device,
+                               dtype=torch.float16).transpose(1, 2)
+            self._cache.append(_LayerCache(conv=conv, state=self._new_state(batch_size, index)))
+        self._batch_size = batch_size
+        self._after_reset(batch_size)
+        return self
+
+    def _after_reset(self, batch_size):
+        pass
+
+    @torch.no_grad()
+    def backbone(self, ids, reset=False):
+        """Hidden states of model.backbone(ids), advancing this controller's
+        cache (state_quant.py:195-217)."""
+        if not self._installed:
+            raise RuntimeError("StateQuant controller is not installed")
+        if not isinstance(ids, torch.Tensor) or ids.ndim != 2 or ids.shape[1] == 0:
+            raise ValueError("Input IDs must be nonempty [batch,tokens]")
+        if ids.device != self.device or ids.dtype != torch.long:
+            raise ValueError("Input IDs must be CUDA int64 on the model device")
+        if self._inside_backbone:
+            raise RuntimeError("Concurrent/reentrant backbone invocation is unsupported")
+        if reset or not self._cache:
+            self.reset(ids.shape[0])
+        self._inside_backbone = True
+        try:
+            result = self.model.backbone(ids)
+            if self._expected_layer != 0:
+                raise RuntimeError("Backbone did not execute every state-quantized layer")
+            return result
+        except Exception:
+            self._failed = True
+            raise
+        finally:
+            self._inside_backbone = False
+
+    # ---------------------------------------------------------------- one layer
+    @torch.no_grad()
+    def _forward(self, index, mx, u, seqlen, seq_idx, cu_seqlens, inference_params):
+        """state_quant.py:219-281: guards, then the mixer step around the codec."""
+        if not self._installed or self._failed:
+            raise RuntimeError("Controller is inactive or failed; reset before reusing it")
+        if any(value is not None for value in (seqlen, seq_idx, cu_seqlens, inference_params)):
+            raise ValueError("Use controller-owned caches; native InferenceParams/varlen are unsupported")
+        if (not isinstance(u, torch.Tensor) or u.ndim != 3 or u.dtype != torch.float16
+                or u.device != self.device or u.shape[-1] != self.D_MODEL or u.shape[1] == 0):
+            raise ValueError("Mixer input must be CUDA FP16 [batch,tokens,4096]")
+        if not self._cache:
+            if index != 0:
+                raise RuntimeError("A new request must start with backbone layer zero")
+            self.reset(u.shape[0])
+        if u.shape[0] != self._batch_size or index != self._expected_layer:
+            raise RuntimeError("Batch shape or backbone layer order changed without a reset")
+        length = u.shape[1]
+        if index == 0:
+            if len({entry.tokens for entry in self._cache}) != 1:
+                raise RuntimeError("Per-layer cache positions disagree; reset the request")
+            self._call_length = length
+        elif length != self._call_length:
+            raise RuntimeError("Backbone layers received different token counts")
+        entry = self._cache[index]
+        try:
+            # a one-token continuation keeps the native rank-two GEMM / norm shapes
+            is_step = entry.tokens > 0 and length == 1
+            projected = mx.in_proj(u.squeeze(1) if is_step else u)
+            zxbcdt = projected.unsqueeze(1) if is_step else projected
+            bc = self.GROUPS * self.D_STATE
+            z, xbc, dt = torch.split(zxbcdt, (self.D_INNER, self.D_INNER + 2 * bc, self.HEADS), dim=-1)
+            xbc = self._convolution(mx, xbc, entry)
+            x, bm, cm = torch.split(xbc, (self.D_INNER, bc, bc), dim=-1)
+            batch = u.shape[0]
+            x = x.reshape(batch, length, self.HEADS, self.HEADDIM)
+            bm = bm.reshape(batch, length, self.GROUPS, self.D_STATE)
+            cm = cm.reshape(batch, length, self.GROUPS, self.D_STATE)
+            aa = -torch.exp(mx.A_log.float())
+            y, stats = self._scan_layer(index, mx, x, dt, aa, bm, cm, entry)
+            if y.dtype != torch.float16 or tuple(y.shape) != (batch, length, self.HEADS, self.HEADDIM):
+                raise RuntimeError("State codec returned unexpected readout dtype/shape")
+            if self.collect_stats:
+                self._accumulate_statistics(index, stats, batch, length)
+            # the gated norm stays a module call: external norm hooks see (y, z)
+            y = y.reshape(batch, length, self.D_INNER)
+            if is_step:
+                out = mx.out_proj(mx.norm(y[:, 0], z[:, 0])).unsqueeze(1)
+            else:
+                out = mx.out_proj(mx.norm(y, z))
+            entry.tokens += length
+            self._expected_layer = (index + 1) % len(self._mixers)
+            if self._expected_layer == 0:
+                self._call_length = None
+            return out
+        except Exception:
+            self._failed = True
+            raise
+
+    def _convolution(self, mx, xbc, entry):
+        """Causal depthwise convolution with the cached window
+        (state_quant.py:283-317): the one-token update rolls the window; a
+        prefill prepends the cached raw inputs and refreshes the window."""
+        update_op, conv_op = _native_conv_ops()
+        length = xbc.shape[1]
+        weight = mx.conv1d.weight[:, 0, :]
+        if entry.tokens > 0 and length == 1:
+            value = xbc[:, 0, :]
+            if update_op is None:
+                entry.conv.copy_(torch.roll(entry.conv, shifts=-1, dims=-1))
+                entry.conv[:, :, -1] = value
+                value = torch.sum(entry.conv * weight, dim=-1)
+                if mx.conv1d.bias is not None:
+                    value = value + mx.conv1d.bias
+                value = mx.act(value).to(dtype=xbc.dtype)
+            else:
+                value = update_op(value, entry.conv, weight, mx.conv1d.bias, mx.activation)
+            return value[:, None, :]
+        raw = xbc.transpose(1, 2)
+        prefix = 0
+        if entry.tokens > 0:
+            # only past raw projections are prepended; the causal result then
+            # covers exactly the requested continuation positions
+            raw = torch.cat((entry.conv[:, :, 1:], raw), dim=-1)
+            prefix = self.D_CONV - 1
+        entry.conv.copy_(F.pad(raw, (self.D_CONV - raw.shape[-1], 0)))
+        if conv_op is None:
+            result = mx.act(mx.conv1d(raw).transpose(1, 2)[:, :-(self.D_CONV - 1)])
+        else:
+            result = conv_op(raw, weight, bias=mx.conv1d.bias, activation=mx.activation, seq_idx=None).transpose(1, 2)
+        return result[:, prefix:prefix + length]
+
+    # ---------------------------------------------------------------- statistics
+    def _accumulate_statistics(self, index, stats, batch, length):
+        """state_quant.py:319-330: FP64 group totals of |FP16 carry|."""
+        tiles = (self.HEADDIM + 15) // 16
+        if (not isinstance(stats, torch.Tensor) or stats.dtype != torch.float32 or stats.device != self.device
+                or tuple(stats.shape) != (batch, self.HEADS, tiles, self.D_STATE)):
+            raise RuntimeError("Expected codec calibration sum [batch,128,4,128] FP32")
+        hpg = self.HEADS // self.GROUPS
+        totals = stats.reshape(batch, self.GROUPS, hpg, tiles, self.D_STATE).double().sum(dim=(0, 2, 3))
+        if self._sums[index] is None:
+            self._sums[index] = totals
+        else:
+            self._sums[index].add_(totals)
+        self._counts[index] += batch * length * hpg * self.HEADDIM
+
+    def reset_statistics(self):
+        self._sums = [None] * len(self._mixers)
+        self._counts = [0] * len(self._mixers)
+
+    def statistics(self):
+        """CPU FP64 sums/means [56,8,128] and sample counts [56]."""
+        if not self.collect_stats or any(value is None for value in self._sums):
+            raise RuntimeError("Complete S16 calibration is required before collecting statistics")
+        sums = torch.stack(self._sums).detach().cpu()
+        counts = torch.tensor(self._counts, dtype=torch.int64)
+        if bool((counts <= 0).any()):
+            raise RuntimeError("Calibration has empty layers")
+        return {"sum_abs": sums, "sample_count_per_group": counts, "mean_abs": sums / counts[:, None, None],
+                "semantics": "abs(FP16 stored carry), each token; average over batch, heads within each group, "
+                             "P and time"}
+
+    @property
+    def cache_bytes(self):
+        return self.cache_breakdown()["total_bytes"]
+
+    # ---------------------------------------------------------------- codec hooks
+    def _new_state(self, batch_size, index):
+        raise NotImplementedError
+
+    def _scan_layer(self, index, mx, x, dt, aa, bm, cm, entry):
+        raise NotImplementedError
+
+    def cache_breakdown(self):
+        raise NotImplementedError
+
+
+class StateQuant(_MixerController):
+    """Sequential s16 control or packed sq3p25 carry (state_quant.py:41-79).
+
+    ``permutations`` is uint8[56,8,128] for sq3p25 (in packed order the first
+    16 coordinates use INT8, the next 64 INT4, the last 48 carry nothing) and
+    must be None for s16.  ``collect_stats`` (s16 only) accumulates FP64
+    group totals of |FP16 carry|; they survive request resets.
+    """
+
+    def __init__(self, model, mode="s16", permutations=None, collect_stats=False):
+        if mode not in ("s16", "sq3p25"):
+            raise ValueError("State mode must be explicitly s16 or sq3p25")
+        if collect_stats and mode != "s16":
+            raise ValueError("Calibration statistics require the S16 control")
+        self._codec_mode = mode
+        super().__init__(model, mode, permutations, collect_stats)
+
+    def _validate_permutations(self, values):
+        if self._codec_mode == "s16":
+            if values is not None:
+                raise ValueError("S16 control must use original state coordinates")
+            return None
+        return super()._validate_permutations(values)
+
+    def _new_state(self, batch_size, index):
+        return state_codec.allocate_state(batch_size, self.HEADS, self.HEADDIM, self.D_STATE, self._codec_mode,
+                                          self.device)
+
+    def _scan_layer(self, index, mx, x, dt, aa, bm, cm, entry):
+        permutation = None if self.permutations is None else self.permutations[index]
+        return state_codec.scan(x, dt, aa, bm, cm, mx.D, mx.dt_bias, entry.state, permutation=permutation,
+                                collect_stats=self.collect_stats)
+
+    def cache_breakdown(self):
+        """Persistent request cache payload (state_quant.py:347-366)."""
+        conv = sum(v.conv.numel() * v.conv.element_size() for v in self._cache)
+        state = sum(int(v.state.nbytes) for v in self._cache)
+        scales = sum(t.numel() * t.element_size() for v in self._cache for k, t in v.state.tensors.items()
+                     if k in ("s4", "s8"))
+        tables = 0 if self.permutations is None else self.permutations.numel() * self.permutations.element_size()
+        statistics = sum(v.numel() * v.element_size() for v in self._sums if v is not None)
+        return {"mode": self.mode, "batch_size": self._batch_size, "allocated_layers": len(self._cache),
+                "conv_fp16_bytes": conv, "ssm_payload_bytes": state - scales, "ssm_scale_bytes": scales,
+                "ssm_total_bytes": state, "permutation_bytes": tables, "total_bytes": conv + state + tables,
+                "calibration_workspace_bytes": statistics, "tokens_per_layer": [v.tokens for v in self._cache],
+                "scope": "Actual persistent request cache plus compact permutation table; weights, activations, "
+                         "registers, allocator reserve and calibration workspace excluded from total_bytes"}
+
+
+PackedStateRuntime = StateQuant

@@ -14,6 +14,7 @@ import torch
 
 from . import _packed
 from .state_codec import PackedState, validate_permutation
+from .state_quant import _MixerController
 
 V10_LAYOUTS = ("16_64_48", "8_80_40", "24_48_56", "32_32_64")
 BASELINE = "32_32_64"
@@ -141,3 +142,82 @@ def validate_finite_result(state, output=None):
     if values and not bool(torch.stack([torch.isfinite(v).all() for v in values]).all()):
         raise FloatingPointError("Nonfinite state scale, diagnostic carry or readout")
     return True
+
+
+class StateRepairV2(_MixerController):
+    """Per-layer stored-scale tier carry with one [56,8,128] coordinate table
+    (w4_state_repair_codec_v2.py:168-260): each layer uses its own layout,
+    all rows are 52 bytes, and a batch-one request cache (convolution windows
+    + packed rows + table) is exactly 28,499,968 bytes."""
+
+    scale_mode, int4_clip, diagnostic = "stored_scale", 1.0, None
+
+    def __init__(self, model, table, layouts):
+        self._layouts = validate_layouts(layouts)
+        super().__init__(model, "sq3p25", table, False)
+        if (self.permutations.numel() != TABLE_BYTES
+                or self.permutations.untyped_storage().nbytes() != TABLE_BYTES):
+            raise ValueError("The one coordinate table must occupy exactly 57,344 bytes")
+
+    @property
+    def layouts(self):
+        return self._layouts
+
+    def _new_state(self, batch_size, index):
+        layout = self.layouts[index]
+        state = allocate_state(batch_size, self.HEADS, self.HEADDIM, self.D_STATE, self.device, layout=layout)
+        validate_state(state, self.device, layout)
+        return state
+
+    def _after_reset(self, batch_size):
+        if self.cache_breakdown()["total_bytes"] != batch_size * (CACHE_BYTES - TABLE_BYTES) + TABLE_BYTES:
+            raise RuntimeError("Per-layer repair cache exceeds the fixed physical budget")
+
+    def _scan_layer(self, index, mx, x, dt, aa, bm, cm, entry):
+        return scan(x, dt, aa, bm, cm, mx.D, mx.dt_bias, entry.state, self.permutations[index],
+                    layout=self.layouts[index])
+
+    def assert_finite_cache(self):
+        """state_ppl_codec_v6.py:362-367."""
+        values = [v.conv for v in self._cache]
+        values += [t for v in self._cache for t in v.state.tensors.values() if t.is_floating_point()]
+        if values and not bool(torch.stack([torch.isfinite(t.float()).all() for t in values]).all()):
+            raise FloatingPointError("Nonfinite persistent scale, convolution or diagnostic carry")
+        return True
+
+    def cache_breakdown(self):
+        """state_ppl_codec_v6.py:369-384 (stored-scale, no diagnostic)."""
+        conv = sum(v.conv.untyped_storage().nbytes() for v in self._cache)
+        state = sum(v.state.nbytes for v in self._cache)
+        scales = sum(v.state.tensors[k].untyped_storage().nbytes() for v in self._cache for k in ("s8", "s4"))
+        table = self.permutations.untyped_storage().nbytes()
+        return {"mode": self.mode, "scale_mode": self.scale_mode, "int4_clip": self.int4_clip,
+                "diagnostic": self.diagnostic, "is_3p25_candidate": True, "batch_size": self._batch_size,
+                "allocated_layers": len(self._cache), "conv_fp16_bytes": conv, "ssm_payload_bytes": state - scales,
+                "ssm_scale_bytes": scales, "ssm_total_bytes": state, "permutation_bytes": table,
+                "total_bytes": conv + state + table, "calibration_workspace_bytes": 0,
+                "diagnostic_dense_fp32_bytes": 0, "row_bytes": 52,
+                "tokens_per_layer": [v.tokens for v in self._cache],
+                "scope": "Actual persistent request cache and permutation table. Weights, activations, registers "
+                         "and allocator reserve excluded."}
+
+    def storage_descriptor(self):
+        """w4_state_repair_codec_v2.py:203-224."""
+        layers = []
+        for index, entry in enumerate(self._cache):
+            layout = self.layouts[index]
+            validate_state(entry.state, self.device, layout)
+            layers.append(dict(**layout_descriptor(layout), state_shape=list(entry.state.shape),
+                               state_bytes=entry.state.nbytes,
+                               tensors={k: dict(shape=list(v.shape), dtype=str(v.dtype),
+                                                storage_bytes=v.untyped_storage().nbytes())
+                                        for k, v in entry.state.tensors.items()},
+                               conv_shape=list(entry.conv.shape),
+                               conv_storage_bytes=entry.conv.untyped_storage().nbytes()))
+        return dict(format="W4_STATE_REPAIR_STORAGE_V2", layouts=list(self.layouts), row_bytes=52, payload_bytes=48,
+                    scale_bytes=4, resident_layout_metadata_bytes=0,
+                    cpu_layout_metadata=dict(kind="tuple[str,...]", entries=56,
+                                             scope="Host orchestration only; Python heap is not GPU recurrent storage"),
+                    permutation_shape=list(self.permutations.shape), permutation_dtype=str(self.permutations.dtype),
+                    permutation_storage_bytes=self.permutations.untyped_storage().nbytes(),
+                    total_cache_bytes=self.cache_breakdown()["total_bytes"], layers=layers)

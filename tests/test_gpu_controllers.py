@@ -1,0 +1,147 @@
+"""The per-token state controllers on a random-init Mamba-2 8B model (the
+real geometry: 56 layers, 507 tensors, 8,236,999,680 parameters, 16.5 GB of
+FP16 weights).  Known answer: a batch-one request cache (convolution windows
++ packed rows + one [56,8,128] table) is 28,499,968 bytes (README.md:123).
+Wiring check: the controller's layer-0 carry after a prefill equals the codec
+scan applied to the Mamba-2 definition of that layer's inputs."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import cases
+from mamba2_model import random_model
+
+pytestmark = pytest.mark.gpu
+
+LAYOUTS = ("36_24_68", "16_64_48", "32_32_64", "40_16_72", "16_64_48", "16_64_48", "24_48_56", "32_32_64") * 7
+CACHE_B1 = 28_499_968
+TABLE = 57_344
+
+
+@pytest.fixture(scope="module")
+def model(device):
+    print("[controllers] building the random 8B model", flush=True)
+    m = random_model(device)
+    torch.cuda.synchronize()
+    return m
+
+
+def tables(device, seed=3):
+    g = torch.Generator().manual_seed(seed)
+    return torch.stack([torch.randperm(128, generator=g) for _ in range(56 * 8)]).reshape(56, 8, 128).to(torch.uint8)
+
+
+def ids(device, batch, n, seed=5):
+    g = torch.Generator(device=device).manual_seed(seed)
+    return torch.randint(0, 256000, (batch, n), generator=g, device=device)
+
+
+def layer0_inputs(model, tokens):
+    """Mamba-2 definition of layer 0's codec inputs for a prefill from zero."""
+    mx = model.backbone.layers[0].mixer
+    u = model.backbone.layers[0].norm(model.backbone.embedding(tokens))
+    z, xbc, dt = torch.split(mx.in_proj(u), (8192, 8192 + 2048, 128), dim=-1)
+    xbc = F.silu(F.conv1d(xbc.transpose(1, 2), mx.conv1d.weight, mx.conv1d.bias, padding=3, groups=10240)[..., :-3])
+    xbc = xbc.transpose(1, 2)
+    b, n = tokens.shape
+    x, bm, cm = torch.split(xbc, (8192, 1024, 1024), dim=-1)
+    return (x.reshape(b, n, 128, 64), dt, -torch.exp(mx.A_log.float()), bm.reshape(b, n, 8, 128),
+            cm.reshape(b, n, 8, 128), mx.D, mx.dt_bias)
+
+
+def test_state_quant_sq3p25_cache_wiring_and_guards(model, device):
+    from mamba2_recall import state_codec
+    from mamba2_recall.state_quant import PackedStateRuntime, StateQuant
+    perms = tables(device)
+    tok = ids(device, 1, 6)
+    with StateQuant(model, mode="sq3p25", permutations=perms) as sq:
+        print("[controllers] sq3p25 prefill 4 + 2 steps", flush=True)
+        h = sq.backbone(tok[:, :4])
+        assert h.shape == (1, 4, 4096) and bool(torch.isfinite(h).all())
+        ref = state_codec.allocate_state(1, 128, 64, 128, "sq3p25", device)
+        x, dt, A, B, C, D, db = layer0_inputs(model, tok[:, :4])
+        state_codec.scan(x, dt, A, B, C, D, db, ref, permutation=perms[0].to(device))
+        for k in ref.tensors:
+            assert torch.equal(ref.tensors[k], sq._cache[0].state.tensors[k]), k
+        for t in (4, 5):
+            h = sq.backbone(tok[:, t:t + 1])
+            assert h.shape == (1, 1, 4096) and bool(torch.isfinite(h).all())
+        br = sq.cache_breakdown()
+        assert br["total_bytes"] == CACHE_B1 and sq.cache_bytes == CACHE_B1
+        assert br["tokens_per_layer"] == [6] * 56
+        with pytest.raises(RuntimeError, match="Another StateQuant controller owns this model"):
+            PackedStateRuntime(model, mode="sq3p25", permutations=perms).install()
+        with pytest.raises(RuntimeError, match="layer order changed"):
+            sq._forward(3, model.backbone.layers[3].mixer, torch.zeros(1, 1, 4096, dtype=torch.float16,
+                                                                    device=device), None, None, None, None)
+        sq.reset(2)
+        assert sq.cache_bytes == 2 * (CACHE_B1 - TABLE) + TABLE
+    assert all(isinstance(layer.mixer.forward, type(model.backbone.layers[0].mixer.forward))
+               for layer in model.backbone.layers)
+    with pytest.raises(RuntimeError, match="native Mamba-2 mixer forward"):
+        model.backbone(tok[:, :1])
+
+
+def test_state_quant_s16_statistics(model, device):
+    from mamba2_recall.state_quant import StateQuant
+    with pytest.raises(ValueError, match="require the S16 control"):
+        StateQuant(model, mode="sq3p25", permutations=tables(device), collect_stats=True)
+    with StateQuant(model, mode="s16", collect_stats=True) as sq:
+        print("[controllers] s16 prefill 3 + 1 step with statistics", flush=True)
+        sq.backbone(ids(device, 2, 3))
+        sq.backbone(ids(device, 2, 1, seed=6))
+        st = sq.statistics()
+        assert st["sum_abs"].shape == (56, 8, 128) and st["sum_abs"].dtype == torch.float64
+        assert st["sample_count_per_group"].tolist() == [2 * 4 * 16 * 64] * 56
+        assert bool(torch.isfinite(st["mean_abs"]).all())
+
+
+@pytest.mark.parametrize("kind", ["permutation", "equalizer"])
+def test_dense3_controller(model, device, kind):
+    from mamba2_recall.state_quant_dense3 import DenseStateQuant
+    if kind == "permutation":
+        table = tables(device)
+    else:
+        g = torch.Generator().manual_seed(9)
+        table = torch.randint(-8, 9, (56, 8, 128), generator=g).to(torch.int8)
+    with DenseStateQuant(model, table, table_kind=kind) as dq:
+        print(f"[controllers] dense3 {kind}", flush=True)
+        h = dq.backbone(ids(device, 1, 3))
+        h = dq.backbone(ids(device, 1, 1, seed=7))
+        assert bool(torch.isfinite(h).all())
+        assert dq.assert_finite_cache()
+        assert dq.cache_bytes == CACHE_B1
+
+
+def test_tier_and_predictor_controllers(model, device):
+    from mamba2_recall import ridge_codec
+    from mamba2_recall.tier_codec import StateRepairV2
+    perms = tables(device)
+    with StateRepairV2(model, perms, LAYOUTS) as rq:
+        print("[controllers] tier", flush=True)
+        h = rq.backbone(ids(device, 1, 3))
+        h = rq.backbone(ids(device, 1, 1, seed=8))
+        assert bool(torch.isfinite(h).all()) and rq.assert_finite_cache()
+        assert rq.cache_bytes == CACHE_B1
+        assert rq.storage_descriptor()["total_cache_bytes"] == CACHE_B1
+    rng = np.random.default_rng(11)
+    bases, scales, preds = [], [], []
+    for layout in LAYOUTS:
+        n8, n4, nz = cases.ridge_counts(layout)
+        s = cases.ridge_statics(rng, 8, n8, n4, nz)
+        bases.append(torch.from_numpy(s["basis"].view(np.float16)))
+        scales.append(torch.from_numpy(s["lscale"].view(np.float16)))
+        preds.append(torch.from_numpy(s["pred"].view(np.float16)))
+    with ridge_codec.PredictorState(model, perms, LAYOUTS, bases, scales, preds) as pq:
+        print("[controllers] ridge", flush=True)
+        h = pq.backbone(ids(device, 2, 3))
+        h = pq.backbone(ids(device, 2, 1, seed=9))
+        assert bool(torch.isfinite(h).all()) and pq.assert_finite_cache()
+        assert pq.cache_bytes == 2 * (CACHE_B1 - TABLE) + TABLE
+        d = pq.storage_descriptor()
+        assert d["static_predictor_bytes"] == sum(p.numel() * 2 for p in preds)
+    bad = list(scales)
+    bad[3] = torch.zeros_like(bad[3])
+    with pytest.raises(ValueError, match="Static predictor/basis/scale allocation differs"):
+        ridge_codec.PredictorState(model, perms, LAYOUTS, bases, bad, preds)
