@@ -114,29 +114,38 @@ constexpr float QTOP3 = 0x1.fffffep+1f;     // below 4
 // Taylor polynomial (relative truncation error < 2^-58).  Log: x = m*2^e with
 // m in [sqrt(1/2), sqrt(2)), log(m) = 2*atanh(s), s = (m-1)/(m+1), series to
 // s^23.  Constants are the binary64 roundings of the named values.
+//
+// A binary64 constant passed through an empty volatile asm: the value is
+// unchanged, but the compiler can no longer hoist its materialization out of
+// loops (keeping ~20 such constants in registers for a whole kernel).
+__device__ __forceinline__ double kconst(double v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+
 __device__ __forceinline__ double xexp_d(double x) {
-  if (x > 100.0) return __builtin_inf();
-  if (x < -110.0) return 0.0;
-  const double inv_ln2 = 1.4426950408889634;           // 1/ln2
-  const double ln2_hi = 6.93147180369123816490e-01;    // high 32 bits of ln2
-  const double ln2_lo = 1.90821492927058770002e-10;    // ln2 - ln2_hi
-  const double magic = 6755399441055744.0;             // 1.5 * 2^52
+  if (x > kconst(100.0)) return __builtin_inf();
+  if (x < -kconst(110.0)) return kconst(0.0);
+  const double inv_ln2 = kconst(1.4426950408889634);           // 1/ln2
+  const double ln2_hi = kconst(6.93147180369123816490e-01);    // high 32 bits of ln2
+  const double ln2_lo = kconst(1.90821492927058770002e-10);    // ln2 - ln2_hi
+  const double magic = kconst(6755399441055744.0);             // 1.5 * 2^52
   double kd = (x * inv_ln2 + magic) - magic;           // rint(x/ln2)
   double r = (x - kd * ln2_hi) - kd * ln2_lo;
-  double p = 1.0 / 6227020800.0;                       // 1/13!
-  p = __builtin_fma(p, r, 1.0 / 479001600.0);
-  p = __builtin_fma(p, r, 1.0 / 39916800.0);
-  p = __builtin_fma(p, r, 1.0 / 3628800.0);
-  p = __builtin_fma(p, r, 1.0 / 362880.0);
-  p = __builtin_fma(p, r, 1.0 / 40320.0);
-  p = __builtin_fma(p, r, 1.0 / 5040.0);
-  p = __builtin_fma(p, r, 1.0 / 720.0);
-  p = __builtin_fma(p, r, 1.0 / 120.0);
-  p = __builtin_fma(p, r, 1.0 / 24.0);
-  p = __builtin_fma(p, r, 1.0 / 6.0);
-  p = __builtin_fma(p, r, 0.5);
-  p = __builtin_fma(p, r, 1.0);
-  p = __builtin_fma(p, r, 1.0);
+  double p = kconst(1.0 / 6227020800.0);                       // 1/13!
+  p = __builtin_fma(p, r, kconst(1.0 / 479001600.0));
+  p = __builtin_fma(p, r, kconst(1.0 / 39916800.0));
+  p = __builtin_fma(p, r, kconst(1.0 / 3628800.0));
+  p = __builtin_fma(p, r, kconst(1.0 / 362880.0));
+  p = __builtin_fma(p, r, kconst(1.0 / 40320.0));
+  p = __builtin_fma(p, r, kconst(1.0 / 5040.0));
+  p = __builtin_fma(p, r, kconst(1.0 / 720.0));
+  p = __builtin_fma(p, r, kconst(1.0 / 120.0));
+  p = __builtin_fma(p, r, kconst(1.0 / 24.0));
+  p = __builtin_fma(p, r, kconst(1.0 / 6.0));
+  p = __builtin_fma(p, r, kconst(0.5));
+  p = __builtin_fma(p, r, kconst(1.0));
+  p = __builtin_fma(p, r, kconst(1.0));
   int64_t k = (int64_t)kd;
   double scale = __builtin_bit_cast(double, (uint64_t)(k + 1023) << 52);
   return p * scale;
@@ -147,25 +156,25 @@ __device__ __forceinline__ double xlog_d(double x) {
   uint64_t u = __builtin_bit_cast(uint64_t, x);
   int64_t e = (int64_t)((u >> 52) & 0x7FF) - 1023;
   double m = __builtin_bit_cast(double, (u & 0x000FFFFFFFFFFFFFull) | 0x3FF0000000000000ull);
-  if (m > 1.4142135623730951) { m = m * 0.5; e += 1; }
-  double s = (m - 1.0) / (m + 1.0);
+  if (m > kconst(1.4142135623730951)) { m = m * kconst(0.5); e += 1; }
+  double s = (m - kconst(1.0)) / (m + kconst(1.0));
   double s2 = s * s;
-  double p = 1.0 / 23.0;
-  p = __builtin_fma(p, s2, 1.0 / 21.0);
-  p = __builtin_fma(p, s2, 1.0 / 19.0);
-  p = __builtin_fma(p, s2, 1.0 / 17.0);
-  p = __builtin_fma(p, s2, 1.0 / 15.0);
-  p = __builtin_fma(p, s2, 1.0 / 13.0);
-  p = __builtin_fma(p, s2, 1.0 / 11.0);
-  p = __builtin_fma(p, s2, 1.0 / 9.0);
-  p = __builtin_fma(p, s2, 1.0 / 7.0);
-  p = __builtin_fma(p, s2, 1.0 / 5.0);
-  p = __builtin_fma(p, s2, 1.0 / 3.0);
-  p = __builtin_fma(p, s2, 1.0);
-  double logm = 2.0 * s * p;
+  double p = kconst(1.0 / 23.0);
+  p = __builtin_fma(p, s2, kconst(1.0 / 21.0));
+  p = __builtin_fma(p, s2, kconst(1.0 / 19.0));
+  p = __builtin_fma(p, s2, kconst(1.0 / 17.0));
+  p = __builtin_fma(p, s2, kconst(1.0 / 15.0));
+  p = __builtin_fma(p, s2, kconst(1.0 / 13.0));
+  p = __builtin_fma(p, s2, kconst(1.0 / 11.0));
+  p = __builtin_fma(p, s2, kconst(1.0 / 9.0));
+  p = __builtin_fma(p, s2, kconst(1.0 / 7.0));
+  p = __builtin_fma(p, s2, kconst(1.0 / 5.0));
+  p = __builtin_fma(p, s2, kconst(1.0 / 3.0));
+  p = __builtin_fma(p, s2, kconst(1.0));
+  double logm = kconst(2.0) * s * p;
   double ed = (double)e;
-  const double ln2_hi = 6.93147180369123816490e-01;
-  const double ln2_lo = 1.90821492927058770002e-10;
+  const double ln2_hi = kconst(6.93147180369123816490e-01);
+  const double ln2_lo = kconst(1.90821492927058770002e-10);
   return (ed * ln2_hi + logm) + ed * ln2_lo;
 }
 
@@ -182,10 +191,9 @@ __device__ __forceinline__ float softplus_dt(float v) {
   return v;
 }
 
-// dt activation and decay for one head, out of line: the binary64
-// polynomial constants then live only inside the call instead of being
-// hoisted into VGPRs for the whole token loop of the calling kernel.
-__device__ __attribute__((noinline)) inline float2 dt_activation(float dt_plus_bias, float A) {
+// dt activation and decay for one head (inline; its binary64 constants are
+// rematerialized at each use, see kconst).
+__device__ __forceinline__ float2 dt_activation(float dt_plus_bias, float A) {
   const float dtv = softplus_dt(dt_plus_bias);
   return make_float2(dtv, xexpf(A * dtv));
 }

@@ -203,31 +203,48 @@ __device__ __forceinline__ void token_build(TokenShared<N8, N4, NZ, MODE, WPB * 
                                             int wave) {
   constexpr int NL = N8 + N4, F = NL + 2, NT = 64 * WPB, NH = WPB * HPW;
   constexpr int RZ = next_pow2(NZ);
-  for (int i = tid; i < 256; i += NT) {
-    const int n = i & 127;   // internal position
-    const float v = h2f(sh.raw[(i & 128) + (s_perm[packed_lane<N8, N4>(n)] & 127)]);
-    if (i < 128) sh.b[n] = v; else sh.c[n] = v;
+#pragma unroll
+  for (int k = 0; k < (256 + NT - 1) / NT; ++k) {
+    const int i = k * NT + tid;
+    if (i < 256) {
+      const int n = i & 127;   // internal position
+      const float v = h2f(sh.raw[(i & 128) + (s_perm[packed_lane<N8, N4>(n)] & 127)]);
+      if (i < 128) sh.b[n] = v; else sh.c[n] = v;
+    }
   }
   __syncthreads();
-  for (int i = tid; i < NH * NL; i += NT) {
-    const int w = i / NL, n = i - w * NL;
-    sh.bdt[w][n] = sh.b[n] * sh.dtv[w];
+  // compile-time trip counts: every LDS read of a loop is issued before the
+  // first use, so each loop costs about one LDS latency
+#pragma unroll
+  for (int k = 0; k < (NH * NL + NT - 1) / NT; ++k) {
+    const int i = k * NT + tid;
+    if (i < NH * NL) {
+      const int w = i / NL, n = i - w * NL;
+      sh.bdt[w][n] = sh.b[n] * sh.dtv[w];
+    }
   }
   if constexpr (MODE == MODE_RIDGE) {
     // corr[f] = sum_d C[dead d] * pred[g, f, d]: four threads per output,
     // interleaved d, combined inside the quad; live rows are folded into the
     // readout weight c + corr, latent rows kept apart (readout-only values)
-    for (int idx = tid; idx < 4 * F; idx += NT) {
-      const int j = idx >> 2, part = idx & 3;     // internal feature position
-      const int f = packed_lane<N8, N4>(j);       // predictor row (packed lane; latent rows last)
-      float acc = 0.f;
-#pragma unroll 4
-      for (int d = part; d < NZ; d += 4) acc = __builtin_fmaf(sh.c[NL + d], h2f(s_pred[f * NZ + d]), acc);
-      acc = butterfly_add<0>(acc);
-      acc = butterfly_add<1>(acc);
-      if (part == 0) {
-        if (j < NL) sh.cp[j] = sh.c[j] + acc;
-        else sh.dots[5 + (j - NL)] = acc;
+#pragma unroll
+    for (int k = 0; k < (4 * F + NT - 1) / NT; ++k) {
+      const int idx = k * NT + tid;
+      if (idx < 4 * F) {                            // whole quads take this branch together
+        const int j = idx >> 2, part = idx & 3;     // internal feature position
+        const int f = packed_lane<N8, N4>(j);       // predictor row (packed lane; latent rows last)
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < (NZ + 3) / 4; ++i) {
+          const int d = part + 4 * i;
+          if (d < NZ) acc = __builtin_fmaf(sh.c[NL + d], h2f(s_pred[f * NZ + d]), acc);
+        }
+        acc = butterfly_add<0>(acc);
+        acc = butterfly_add<1>(acc);
+        if (part == 0) {
+          if (j < NL) sh.cp[j] = sh.c[j] + acc;
+          else sh.dots[5 + (j - NL)] = acc;
+        }
       }
     }
 #pragma unroll
@@ -261,6 +278,77 @@ __device__ __forceinline__ void token_build(TokenShared<N8, N4, NZ, MODE, WPB * 
   __syncthreads();
 }
 
+// One tier of a row: update its N carried coordinates (biased code bytes in
+// c[0 .. N/4)), accumulate the readout (prior * readout weight), then
+// requantize with den = max(RN(amax / lim), 1e-8) and the stored (binary16)
+// scale, writing the new codes back into c.  Returns the new stored scale.
+// INT8: byte = q + 128, lim 127; INT4: byte = q + 8, lim 7.  Legacy mode
+// quantizes with the binary32 denominator.
+template <int N, bool INT8, int MODE>
+__device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, float x, const f32x4* bdt4,
+                                           const f32x4* cw4, float& acc) {
+  constexpr float BIAS = INT8 ? 128.0f : 8.0f;
+  constexpr float LIM = INT8 ? 127.0f : 7.0f;
+  constexpr float TOP = INT8 ? QTOP127 : QTOP7;
+  const float nb = -BIAS * sc;   // exact
+  float v[N];
+  float amax = 0.f;
+  // the shared operands of chunk i+1 are read while chunk i computes
+  f32x4 cb_next = bdt4[0], cw_next = cw4[0];
+#pragma unroll
+  for (int i0 = 0; i0 < N; i0 += 4) {
+    const f32x4 cb = cb_next, cw = cw_next;
+    if (i0 + 4 < N) {
+      cb_next = bdt4[i0 / 4 + 1];
+      cw_next = cw4[i0 / 4 + 1];
+    }
+    float au[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // prior = q * s exactly: (q + bias) * s - bias * s, all exact
+      const float prior = __builtin_fmaf(ubyte_f(c[i0 / 4], j), sc, nb);
+      acc = __builtin_fmaf(prior, cw[j], acc);
+      float u = prior * decay + cb[j] * x;
+      // ordered pin: chunk by chunk, each prior dies as soon as it is used
+      asm volatile("" : "+v"(u));
+      v[i0 + j] = u;
+      au[j] = __builtin_fabsf(u);
+    }
+    amax = __builtin_fmaxf(amax, __builtin_fmaxf(__builtin_fmaxf(au[0], au[1]), __builtin_fmaxf(au[2], au[3])));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // Materialize the accumulator and the maximum here: otherwise the compiler
+  // sinks their chains (and every update behind the maximum) into the
+  // requantization, which keeps every prior and LDS operand live at once.
+  asm volatile("" : "+v"(acc), "+v"(amax));
+  const float den = __builtin_fmaxf(div_by_recip(amax, LIM, 1.0f / LIM), 1e-8f);
+  const float stored = round_to_half(den);
+  float d, r;
+  if constexpr (MODE == MODE_LEGACY) {
+    d = den;
+    r = 1.0f / den;
+  } else {
+    // zero (underflowed) or infinite stored scale: the reference's quotient
+    // is 0 and so is the code
+    const bool zero = !(stored > 0.f) || stored == __builtin_inff();
+    d = zero ? 1.f : stored;
+    r = zero ? 0.f : 1.0f / stored;
+  }
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i) {
+    const int q0 = quantize_code(v[4 * i], d, r, TOP);
+    const int q1 = quantize_code(v[4 * i + 1], d, r, TOP);
+    const int q2 = quantize_code(v[4 * i + 2], d, r, TOP);
+    const int q3 = quantize_code(v[4 * i + 3], d, r, TOP);
+    uint32_t packed = pack4(q0, q1, q2, q3);
+    packed = INT8 ? (packed ^ 0x80808080u) : ((packed & 0x0F0F0F0Fu) ^ 0x08080808u);
+    asm volatile("" : "+v"(packed));
+    c[i] = packed;
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  return stored;
+}
+
 // Orders a wave's LDS accesses across its lanes (the wave's own staging
 // tiles need no workgroup barrier).
 __device__ __forceinline__ void wave_sync() {
@@ -277,7 +365,8 @@ __device__ __forceinline__ void wave_sync() {
 // the next slot's rows are loaded into VGPRs while the current one computes.
 // Per-token shared values are built once per workgroup for all NH heads.
 template <int N8, int N4, int NZ, int MODE, int WPB, int HPW>
-__global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
+__global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(WPB == 8 ? 4 : 1, 8)))
+void k_state_step(StepArgs a) {
   constexpr int W8 = N8 / 2;          // bytes per row of lo and of hi
   constexpr int W4 = N4 / 2;          // bytes per row of q4
   constexpr int NL = N8 + N4;         // carried coordinates
@@ -320,7 +409,7 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
 
   // vector memory operations per slot transfer (field_dma counts)
   constexpr int SLOT_DMA = 2 * dma_ops(W8) + dma_ops(W4) + dma_ops(2) * (RIDGE ? 3 : 2);
-  static_assert(SLOT_DMA * (HPW - 1) <= 63, "slot transfers must fit the vmcnt range");
+  static_assert(SLOT_DMA <= 63, "a slot's transfers must fit the vmcnt range");
   auto slot_row0 = [&](int hh) { return (b * H + h0 + hh) * P + pbase; };
   auto slot_dma = [&](int hh) {   // even P: direct global -> LDS transfers
     const int row0 = slot_row0(hh);
@@ -332,15 +421,17 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
     field_dma<2>(t + O_S4, (const uint8_t*)a.s4, row0, nvalid, lane);
     if constexpr (RIDGE) field_dma<2>(t + O_LAT, a.latent, row0, nvalid, lane);
   };
-  // at the first token, before slot k is read: its transfers have landed
-  // once at most (HPW - 1 - k) slots' transfers are outstanding (program
-  // order; later operations only make the wait longer)
-  auto slot_wait = [&](int k) {
-    const int later = HPW - 1 - k;
-    if (later >= 3) wait_vmcnt<(HPW >= 4 ? 3 * SLOT_DMA : 0)>();
-    else if (later == 2) wait_vmcnt<(HPW >= 3 ? 2 * SLOT_DMA : 0)>();
-    else if (later == 1) wait_vmcnt<(HPW >= 2 ? SLOT_DMA : 0)>();
-    else wait_vmcnt<0>();
+  // at the first token, before slot k is read: issue slot k+1's transfers,
+  // then wait until only those are outstanding (vector memory operations
+  // complete in program order, so slot k's transfers and everything issued
+  // before them have landed)
+  auto slot_fetch_next_and_wait = [&](int k) {
+    if (dword_tiles && k + 1 < HPW) {
+      slot_dma((k + 1) * WPB + wave);
+      wait_vmcnt<SLOT_DMA>();
+    } else {
+      wait_vmcnt<0>();
+    }
   };
   auto slot_copy_in = [&](int hh) {   // odd P: 16-bit transfers
     const int row0 = slot_row0(hh);
@@ -372,9 +463,15 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
     if constexpr (RIDGE) wave_copy_out<2>(a.latent, t + O_LAT, row0, nvalid, lane);
   };
 
-  // ---- prologue: register loads of the first token and the statics, then the
-  // LDS transfers (predictor, every slot), then the LDS stores that need the
-  // register loads (whose waits then leave the transfers in flight) ---------
+  // ---- prologue: the predictor's LDS transfer, then the register loads of the
+  // first token and the statics (one wait covers both), then the LDS transfer
+  // of the wave's first slot, which lands during the token build; each later
+  // slot is fetched while the previous one computes -----------------------------
+  if constexpr (RIDGE) {   // predictor rows of the group, spread over the waves
+    const uint8_t* pg = (const uint8_t*)(a.pred + (size_t)g * F * NZ);
+    for (int j = wave; j < PRED_OPS; j += WPB) lds_dma_b32(pg + 4 * min(j * 64 + lane, PRED_DW - 1),
+                                                           lds_address(s_pred32 + 64 * j));
+  }
   TokenRaw<WPB, HPW> raw;
   token_load<WPB, HPW>(a, raw, b * L, g, h0, pbase, tid, lane, wave);
   const float Ah = (tid < NH) ? a.A[h0 + tid] : 0.f;
@@ -398,16 +495,11 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
     rls0 = 1.0f / ls0;   // correctly rounded reciprocals
     rls1 = 1.0f / ls1;
   }
-  // the register loads complete before any LDS transfer is issued
+  // the predictor transfer and the register loads complete before any slot
+  // transfer is issued (the compiler's own waits for the register loads then
+  // never cover a slot transfer)
   __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-  if constexpr (RIDGE) {   // predictor rows of the group, spread over the waves
-    const uint8_t* pg = (const uint8_t*)(a.pred + (size_t)g * F * NZ);
-    for (int j = wave; j < PRED_OPS; j += WPB) lds_dma_b32(pg + 4 * min(j * 64 + lane, PRED_DW - 1),
-                                                           lds_address(s_pred32 + 64 * j));
-  }
-  if (dword_tiles) {
-    for (int k = 0; k < HPW; ++k) slot_dma(k * WPB + wave);
-  }
+  if (dword_tiles) slot_dma(wave);
   if (tid < NH) s_D[tid] = Dv;
 #pragma unroll
   for (int k = 0; k < PERM_PT; ++k) {
@@ -428,13 +520,7 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
     for (int k = 0; k < HPW; ++k) slot_copy_in(k * WPB + wave);
   }
   token_store<N8, N4, NZ, MODE, WPB, HPW>(sh, raw, Ah, a.db_f32, tid, lane, wave);
-  // the predictor transfers precede every slot transfer
-  // (a smaller count than the slot transfers only waits longer)
-  if (dword_tiles) wait_vmcnt<(HPW * SLOT_DMA > 63 ? 63 : HPW * SLOT_DMA)>(); else wait_vmcnt<0>();
   __syncthreads();
-
-  const float y127 = 1.0f / 127.0f;   // RN(1/127)
-  const float y7 = 1.0f / 7.0f;       // RN(1/7)
 
   for (int t = 0; t < L; ++t) {
     const int bt = b * L + t;
@@ -448,7 +534,7 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
     for (int k = 0; k < HPW; ++k) {
       const int hh = k * WPB + wave;
       const int h = h0 + hh;
-      if (t == 0) slot_wait(k);
+      if (t == 0) slot_fetch_next_and_wait(k);
       uint8_t* tile = s_tile[hh];
       uint16_t* t16 = (uint16_t*)tile;
 
@@ -482,43 +568,17 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
       const float decay = sh.decay[hh];
       const float dtv = sh.dtv[hh];
 
-      // ---- update, readout accumulation, tier maxima -----------------------------
-      const float nb8 = -128.0f * sc8, nb4 = -8.0f * sc4;   // exact
-      float acc = 0.f, amax8 = 0.f, amax4 = 0.f;
-      float v[NL];
+      // ---- per tier: update, readout accumulation, requantization ---------------
+      // (each tier is requantized before the next is updated, so only one
+      // tier's updated values are live at a time)
       const f32x4* bdt4 = (const f32x4*)sh.bdt[hh];
       const f32x4* cw4;
       if constexpr (RIDGE) cw4 = (const f32x4*)sh.cp; else cw4 = (const f32x4*)sh.c;
-      // the shared operands of chunk i+1 are read while chunk i computes
-      f32x4 cb_next = bdt4[0], cw_next = cw4[0];
-#pragma unroll
-      for (int i0 = 0; i0 < NL; i0 += 4) {
-        const f32x4 cb = cb_next, cw = cw_next;
-        if (i0 + 4 < NL) {
-          cb_next = bdt4[i0 / 4 + 1];
-          cw_next = cw4[i0 / 4 + 1];
-        }
-        float au[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int i = i0 + j;
-          // prior = q * s exactly: (q + bias) * s - bias * s, all exact
-          const float prior = (i < N8) ? __builtin_fmaf(ubyte_f(c8[i / 4], j), sc8, nb8)
-                                       : __builtin_fmaf(ubyte_f(c4[(i - N8) / 4], j), sc4, nb4);
-          acc = __builtin_fmaf(prior, cw[j], acc);
-          const float u = prior * decay + cb[j] * x;
-          v[i] = u;
-          au[j] = __builtin_fabsf(u);
-        }
-        const float m = __builtin_fmaxf(__builtin_fmaxf(au[0], au[1]), __builtin_fmaxf(au[2], au[3]));
-        if (i0 < N8) amax8 = __builtin_fmaxf(amax8, m); else amax4 = __builtin_fmaxf(amax4, m);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      // Materialize the accumulator and the tier maxima here: otherwise the
-      // compiler sinks their chains (and every update behind the maxima) into
-      // the predicated y store and the requantization, which keeps every
-      // prior and LDS operand live at once.
-      asm volatile("" : "+v"(acc), "+v"(amax8), "+v"(amax4));
+      float acc = 0.f;
+      sc8 = tier_step<N8, true, MODE>(c8, sc8, decay, x, bdt4, cw4, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      sc4 = tier_step<N4, false, MODE>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc);
+      __builtin_amdgcn_sched_barrier(0);
       // readout: sum_i u_i c_i + corrections = decay * (sum_i prior_i (c_i +
       // corr_i) + latent terms) + x * (dt * sum_all b c + D)
       float out;
@@ -537,42 +597,6 @@ __global__ __launch_bounds__(64 * WPB) void k_state_step(StepArgs a) {
         out = decay * acc + x * (dtv * sh.dots[0] + s_D[hh]);
       }
       if (valid) a.y[((size_t)bt * H + h) * P + pbase + lane] = f2h(out);
-
-      // ---- requantization: den = max(RN(amax / lim), 1e-8), stored = half(den) --
-      const float den8 = __builtin_fmaxf(div_by_recip(amax8, 127.0f, y127), 1e-8f);
-      const float den4 = __builtin_fmaxf(div_by_recip(amax4, 7.0f, y7), 1e-8f);
-      sc8 = round_to_half(den8);
-      sc4 = round_to_half(den4);
-      float d8, r8, d4, r4;
-      if constexpr (MODE == MODE_LEGACY) {
-        d8 = den8; r8 = 1.0f / den8;
-        d4 = den4; r4 = 1.0f / den4;
-      } else {
-        // zero (underflowed) or infinite stored scale: the reference's quotient
-        // is 0 and so is the code
-        const bool z8 = !(sc8 > 0.f) || sc8 == __builtin_inff();
-        const bool z4 = !(sc4 > 0.f) || sc4 == __builtin_inff();
-        d8 = z8 ? 1.f : sc8; r8 = z8 ? 0.f : 1.0f / sc8;
-        d4 = z4 ? 1.f : sc4; r4 = z4 ? 0.f : 1.0f / sc4;
-      }
-#pragma unroll
-      for (int i = 0; i < C8; ++i) {
-        const int q0 = quantize_code(v[4 * i], d8, r8, QTOP127);
-        const int q1 = quantize_code(v[4 * i + 1], d8, r8, QTOP127);
-        const int q2 = quantize_code(v[4 * i + 2], d8, r8, QTOP127);
-        const int q3 = quantize_code(v[4 * i + 3], d8, r8, QTOP127);
-        c8[i] = pack4(q0, q1, q2, q3) ^ 0x80808080u;
-        __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (int i = 0; i < C4; ++i) {
-        const int q0 = quantize_code(v[N8 + 4 * i], d4, r4, QTOP7);
-        const int q1 = quantize_code(v[N8 + 4 * i + 1], d4, r4, QTOP7);
-        const int q2 = quantize_code(v[N8 + 4 * i + 2], d4, r4, QTOP7);
-        const int q3 = quantize_code(v[N8 + 4 * i + 3], d4, r4, QTOP7);
-        c4[i] = (pack4(q0, q1, q2, q3) & 0x0F0F0F0Fu) ^ 0x08080808u;
-        __builtin_amdgcn_sched_barrier(0);
-      }
 
       // ---- repack the slot row into the tile ---------------------------------------
       if (valid) {
@@ -613,6 +637,7 @@ static hipError_t launch_layout(const StepArgs& a, hipStream_t stream) {
     dim3 grid(pblocks, a.H / (wpb * hpw), a.B);
     if (wpb == 1) hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 1, 1>), grid, dim3(64), 0, stream, a);
     else if (hpw == 1) hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 4, 1>), grid, dim3(256), 0, stream, a);
+    else if (wpb == 8) hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 8, 2>), grid, dim3(512), 0, stream, a);
     else if (hpw == 2) hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 4, 2>), grid, dim3(256), 0, stream, a);
     else hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 4, 4>), grid, dim3(256), 0, stream, a);
     return hipGetLastError();
@@ -711,8 +736,10 @@ extern "C" int m2r_state_step_tier(const void* x, const void* dt, const float* A
 
 extern "C" int m2r_set_step_shape(int waves_per_block, int heads_per_wave) {
   const int w = waves_per_block, k = heads_per_wave;
-  const bool ok = (w == 0 && k == 0) || (w == 1 && k == 1) || (w == 4 && (k == 1 || k == 2 || k == 4));
-  if (!ok) return m2r_fail("step shape: supported (waves, heads per wave) are (1,1), (4,1), (4,2), (4,4) or (0,0)");
+  const bool ok = (w == 0 && k == 0) || (w == 1 && k == 1) || (w == 4 && (k == 1 || k == 2 || k == 4)) ||
+                  (w == 8 && k == 2);
+  if (!ok)
+    return m2r_fail("step shape: supported (waves, heads per wave) are (1,1), (4,1), (4,2), (4,4), (8,2) or (0,0)");
   g_forced_shape.store(w * 16 + k, std::memory_order_relaxed);
   return 0;
 }

@@ -150,7 +150,7 @@ def test_ridge_model_batch_sixteen_head_blocks(oracle, device):
     run_ridge(oracle, device, "32_32_64", batch=64, L=1, H=128, P=64, G=8, seed=19)
 
 
-SHAPES = [(1, 1), (4, 1), (4, 2), (4, 4)]
+SHAPES = [(1, 1), (4, 1), (4, 2), (4, 4), (8, 2)]
 
 
 @pytest.fixture
