@@ -26,6 +26,7 @@
 #include "m2r_tile.h"
 
 #include <atomic>
+#include <initializer_list>
 
 namespace m2r {
 
@@ -52,6 +53,7 @@ struct StepArgs {
   uint16_t* y;             // f16 [B, L, H, P]
   int B, L, H, P, G;
   int d_f32, db_f32;
+  int dma_tiles;           // P % 8 == 0 and 16-byte aligned state fields: 16-byte LDS transfers
 };
 
 // Carried coordinates are held in an internal lane order that makes the
@@ -117,165 +119,202 @@ __device__ __forceinline__ void bytes_to_plane4(const uint32_t* c, uint32_t* wq)
   }
 }
 
-// Per-token values shared by the workgroup (one B/C group, NH heads): the raw
-// B/C rows and x, the permuted B and C, dt activation and decay per head, B*dt
-// per head, the readout weights and the latent dot products.
-template <int N8, int N4, int NZ, int MODE, int NH>
-struct TokenShared {
+// Per-token values of one wave, in the wave's own LDS region.  Only the
+// wave's own lanes read them, so building them needs no workgroup barrier:
+// the raw B/C rows, the permuted b and c, B*dt per head slot, the readout
+// weights of the carried coordinates, x of the wave's rows and per-slot and
+// per-token scalars.
+template <int N8, int N4, int HPW>
+struct WaveToken {
   static constexpr int NL = N8 + N4;
-  uint16_t raw[256];                                   // B row then C row of the group, original order
-  uint16_t xr[NH * 64];                                // x of the NH heads, this P block
-  alignas(16) float b[128];                            // internal order
+  uint32_t raw[128];                 // B row (dwords 0..63) then C row (64..127): f16 pairs, original order
+  alignas(16) float b[128];          // internal order
   alignas(16) float c[128];
-  alignas(16) float cp[MODE == MODE_RIDGE ? NL : 4];   // c + ridge correction of the live coordinates
-  alignas(16) float bdt[NH][NL];                       // RN(b * dt) per head
-  float dtv[NH], decay[NH];
+  alignas(16) float cw[NL];          // readout weights of the carried coordinates: c (+ ridge correction)
+  alignas(16) float bdt[HPW][NL];    // RN(b * dt) per head slot
+  uint16_t x[HPW][64];               // x of the wave's rows, per head slot
+  float dtv[HPW], decay[HPW], D[HPW];
+  // per head slot: 1 when B*dt and the decay are bounded (|.| < 2^100), so
+  // that the state update of finite operands is finite
+  uint32_t bounded[HPW];
   // 0: sum of b*c over all 128 coordinates (readout); 1, 2: dead-tier e0.c,
-  // e1.c (readout); 3, 4: dead-tier e0.b, e1.b (canonical trees, exact);
-  // 5, 6: ridge correction of the two latent coefficients (readout)
-  float dots[8];
+  // e1.c plus the ridge correction of the latent coefficients (readout);
+  // 3, 4: dead-tier e0.b, e1.b (canonical trees, exact)
+  float dots[5];
 };
 
-// Raw per-token inputs a thread loads one token ahead: its share of the
-// group's B and C rows, x of the rows it owns in each of its HPW head slots,
-// and, for the first NH threads, one head's dt and dt_bias bits.  Nothing is
-// converted at load time, so no wait is needed until token_store.
-template <int WPB, int HPW>
-struct TokenRaw {
-  static constexpr int NT = 64 * WPB;
-  static constexpr int NBC = (256 + NT - 1) / NT;
-  uint16_t bc[NBC];
+// Inputs of one token that a wave loads one token ahead: its lane's two f16
+// of the group's B and of its C row, x of its rows in every head slot, and
+// for lanes < HPW the dt and dt_bias bits of head slot `lane`.  Nothing is
+// converted at load time, so no wait is needed until the token is built.
+template <int HPW>
+struct WaveRaw {
+  uint16_t bc[4];              // B[2 lane], B[2 lane + 1], C[2 lane], C[2 lane + 1]
   uint16_t xv[HPW];
   uint16_t dt, db_lo, db_hi;   // dt_bias: f16 bits, or the halves of f32 bits
 };
 
+// The dt inputs are loaded first: the dt activation of the first token
+// starts as soon as they land, while the other loads are still in flight.
+// Every load here is unconditional, with clamped indices (a conditional load
+// makes the compiler wait for it at the end of its branch).
 template <int WPB, int HPW>
-__device__ __forceinline__ void token_load(const StepArgs& a, TokenRaw<WPB, HPW>& r, int bt, int g, int h0,
-                                           int pbase, int tid, int lane, int wave) {
-  using R = TokenRaw<WPB, HPW>;
-#pragma unroll
-  for (int k = 0; k < R::NBC; ++k) {
-    const int i = k * R::NT + tid;
-    const uint16_t* src = (i < 128) ? a.Bm : a.Cm;
-    r.bc[k] = (i < 256) ? src[((size_t)bt * a.G + g) * 128 + (i & 127)] : (uint16_t)0;
-  }
-  const int p = pbase + lane;
+__device__ __forceinline__ void wave_load_dt(const StepArgs& a, WaveRaw<HPW>& r, int bt, int h0, int lane,
+                                             int wave) {
+  const int h = h0 + min(lane, HPW - 1) * WPB + wave;   // lanes >= HPW repeat the last slot
+  const uint16_t* db = (const uint16_t*)a.dt_bias;
+  r.dt = a.dt[(size_t)bt * a.H + h];
+  r.db_lo = db[a.db_f32 ? 2 * h : h];
+  r.db_hi = db[a.db_f32 ? 2 * h + 1 : h];
+}
+template <int WPB, int HPW>
+__device__ __forceinline__ void wave_load_rest(const StepArgs& a, WaveRaw<HPW>& r, int bt, int g, int h0,
+                                               int pbase, int lane, int wave) {
+  const size_t row = ((size_t)bt * a.G + g) * 128 + 2 * lane;
+  r.bc[0] = a.Bm[row];
+  r.bc[1] = a.Bm[row + 1];
+  r.bc[2] = a.Cm[row];
+  r.bc[3] = a.Cm[row + 1];
+  const int p = min(pbase + lane, a.P - 1);   // rows past P read row P-1 (never stored)
 #pragma unroll
   for (int k = 0; k < HPW; ++k) {
-    const int hh = k * WPB + wave;
-    r.xv[k] = (p < a.P) ? a.x[((size_t)bt * a.H + h0 + hh) * a.P + p] : (uint16_t)0;
-  }
-  r.dt = r.db_lo = r.db_hi = 0;
-  if (tid < WPB * HPW) {
-    const int h = h0 + tid;
-    const uint16_t* db = (const uint16_t*)a.dt_bias;
-    r.dt = a.dt[(size_t)bt * a.H + h];
-    r.db_lo = db[a.db_f32 ? 2 * h : h];
-    r.db_hi = db[a.db_f32 ? 2 * h + 1 : h];
+    const int h = h0 + k * WPB + wave;
+    r.xv[k] = a.x[((size_t)bt * a.H + h) * a.P + p];
   }
 }
 
-template <int N8, int N4, int NZ, int MODE, int WPB, int HPW>
-__device__ __forceinline__ void token_store(TokenShared<N8, N4, NZ, MODE, WPB * HPW>& sh,
-                                            const TokenRaw<WPB, HPW>& r, float Ah, int db_f32, int tid, int lane,
-                                            int wave) {
-  using R = TokenRaw<WPB, HPW>;
-#pragma unroll
-  for (int k = 0; k < R::NBC; ++k) {
-    const int i = k * R::NT + tid;
-    if (i < 256) sh.raw[i] = r.bc[k];
-  }
-#pragma unroll
-  for (int k = 0; k < HPW; ++k) sh.xr[(k * WPB + wave) * 64 + lane] = r.xv[k];
-  if (tid < WPB * HPW) {
-    const float db = db_f32 ? __builtin_bit_cast(float, (uint32_t)r.db_lo | ((uint32_t)r.db_hi << 16)) : h2f(r.db_lo);
-    const float2 act = dt_activation(h2f(r.dt) + db, Ah);
-    sh.dtv[tid] = act.x;
-    sh.decay[tid] = act.y;
-  }
+// dt activation of head slot `lane` (lanes < HPW; the others compute a copy
+// of the last slot's, unused).
+template <int HPW>
+__device__ __forceinline__ float2 wave_dt_activation(const WaveRaw<HPW>& r, float Ah, int db_f32) {
+  const float db = db_f32 ? __builtin_bit_cast(float, (uint32_t)r.db_lo | ((uint32_t)r.db_hi << 16)) : h2f(r.db_lo);
+  return dt_activation(h2f(r.dt) + db, Ah);
 }
 
-// After token_store and a barrier: gather through the permutation, B*dt per
-// head, readout weights and latent dot products; ends with a barrier.
-template <int N8, int N4, int NZ, int MODE, int WPB, int HPW>
-__device__ __forceinline__ void token_build(TokenShared<N8, N4, NZ, MODE, WPB * HPW>& sh, const uint8_t* s_perm,
-                                            const float* s_basis, const uint16_t* s_pred, int tid, int lane,
-                                            int wave) {
-  constexpr int NL = N8 + N4, F = NL + 2, NT = 64 * WPB, NH = WPB * HPW;
-  constexpr int RZ = next_pow2(NZ);
+// Orders a wave's LDS accesses across its lanes (the wave's own regions
+// need no workgroup barrier).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// Builds the wave's token values from its landed raw inputs and the dt
+// activation `act` of head slot `lane` (lanes < HPW): raw rows and x, dt and
+// decay per head slot, b and c gathered through
+// the permutation (lane holds internal positions lane and lane + 64, whose
+// raw indices are pv0 and pv1), B*dt, sum b.c, the readout weights and, for
+// the ridge codec, the correction of the readout weights by the static
+// predictor and the dead-tier dot products.  `first`: the first token, whose
+// ridge correction waits for the workgroup's predictor transfer.
+template <int N8, int N4, int NZ, int MODE, int HPW>
+__device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, const WaveRaw<HPW>& r, float2 act,
+                                                 int pv0, int pv1, const float (&e0v)[2],
+                                                 const float (&e1v)[2], const uint16_t* s_pred, bool first,
+                                                 int lane) {
+  constexpr int NL = N8 + N4, F = NL + 2, RZ = next_pow2(NZ);
+  wt.raw[lane] = (uint32_t)r.bc[0] | ((uint32_t)r.bc[1] << 16);
+  wt.raw[64 + lane] = (uint32_t)r.bc[2] | ((uint32_t)r.bc[3] << 16);
 #pragma unroll
-  for (int k = 0; k < (256 + NT - 1) / NT; ++k) {
-    const int i = k * NT + tid;
-    if (i < 256) {
-      const int n = i & 127;   // internal position
-      const float v = h2f(sh.raw[(i & 128) + (s_perm[packed_lane<N8, N4>(n)] & 127)]);
-      if (i < 128) sh.b[n] = v; else sh.c[n] = v;
-    }
+  for (int k = 0; k < HPW; ++k) wt.x[k][lane] = r.xv[k];
+  const float dtv = act.x;
+  wave_sync();
+  const uint16_t* raw16 = (const uint16_t*)wt.raw;
+  const float b0 = h2f(raw16[pv0]), b1 = h2f(raw16[pv1]);
+  const float c0 = h2f(raw16[128 + pv0]), c1 = h2f(raw16[128 + pv1]);
+  // the carried coordinates' b are finite binary16 values (|b| <= 65504)
+  const bool b_lane_ok = (lane >= NL || __builtin_fabsf(b0) <= 65504.f) &&
+                         (64 + lane >= NL || __builtin_fabsf(b1) <= 65504.f);
+  const bool b_ok = __builtin_amdgcn_ballot_w64(!b_lane_ok) == 0;
+  if (lane < HPW) {
+    wt.dtv[lane] = act.x;
+    wt.decay[lane] = act.y;
+    wt.bounded[lane] = (b_ok && 65504.f * __builtin_fabsf(act.x) < 0x1p100f && __builtin_fabsf(act.y) < 0x1p100f);
   }
-  __syncthreads();
-  // compile-time trip counts: every LDS read of a loop is issued before the
-  // first use, so each loop costs about one LDS latency
+  wt.b[lane] = b0;
+  wt.b[64 + lane] = b1;
+  wt.c[lane] = c0;
+  wt.c[64 + lane] = c1;
 #pragma unroll
-  for (int k = 0; k < (NH * NL + NT - 1) / NT; ++k) {
-    const int i = k * NT + tid;
-    if (i < NH * NL) {
-      const int w = i / NL, n = i - w * NL;
-      sh.bdt[w][n] = sh.b[n] * sh.dtv[w];
-    }
+  for (int k = 0; k < HPW; ++k) {
+    const float dk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, dtv), k));
+    if (lane < NL) wt.bdt[k][lane] = b0 * dk;
+    if (64 + lane < NL) wt.bdt[k][64 + lane] = b1 * dk;
   }
-  if constexpr (MODE == MODE_RIDGE) {
-    // corr[f] = sum_d C[dead d] * pred[g, f, d]: four threads per output,
-    // interleaved d, combined inside the quad; live rows are folded into the
-    // readout weight c + corr, latent rows kept apart (readout-only values)
-#pragma unroll
-    for (int k = 0; k < (4 * F + NT - 1) / NT; ++k) {
-      const int idx = k * NT + tid;
-      if (idx < 4 * F) {                            // whole quads take this branch together
-        const int j = idx >> 2, part = idx & 3;     // internal feature position
-        const int f = packed_lane<N8, N4>(j);       // predictor row (packed lane; latent rows last)
-        float acc = 0.f;
-#pragma unroll
-        for (int i = 0; i < (NZ + 3) / 4; ++i) {
-          const int d = part + 4 * i;
-          if (d < NZ) acc = __builtin_fmaf(sh.c[NL + d], h2f(s_pred[f * NZ + d]), acc);
-        }
-        acc = butterfly_add<0>(acc);
-        acc = butterfly_add<1>(acc);
-        if (part == 0) {
-          if (j < NL) sh.cp[j] = sh.c[j] + acc;
-          else sh.dots[5 + (j - NL)] = acc;
-        }
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < 5; ++k) {
-      if (wave != k % WPB) continue;
-      float t;
-      if (k == 0) {
-        t = wave_sum(sh.b[lane] * sh.c[lane] + sh.b[lane + 64] * sh.c[lane + 64]);
-      } else {
-        // dead-tier dot products: canonical adjacent-pair trees
-        float v[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int d0 = (RZ == 128) ? 2 * lane + j : lane;
-          const bool in = (RZ == 128 || j == 0) && d0 < NZ;
-          const int d = in ? d0 : 0;
-          const float bb = sh.b[NL + d], cc = sh.c[NL + d], e0 = s_basis[d], e1 = s_basis[NZ + d];
-          const float pr = k == 1 ? e0 * cc : k == 2 ? e1 * cc : k == 3 ? e0 * bb : e1 * bb;
-          v[j] = in ? pr : 0.f;
-        }
-        t = wave_pair_tree<RZ>(v[0], v[1]);
-      }
-      if (lane == 0) sh.dots[k] = t;
-    }
+  const float sbc = wave_sum(b0 * c0 + b1 * c1);
+  if (lane == 0) wt.dots[0] = sbc;
+  if constexpr (MODE != MODE_RIDGE) {
+    if (lane < NL) wt.cw[lane] = c0;
+    if (64 + lane < NL) wt.cw[64 + lane] = c1;
   } else {
-    if (wave == 0) {
-      const float t = wave_sum(sh.b[lane] * sh.c[lane] + sh.b[lane + 64] * sh.c[lane + 64]);
-      if (lane == 0) sh.dots[0] = t;
+    wave_sync();                 // the dead-tier c and b are read across lanes below
+    if (first) __syncthreads();  // every wave's share of the predictor transfer has landed
+    // corr[j] = sum_d C[dead d] * pred[g, row(j), d] for output j = lane and
+    // lane + 64 (rows past F recompute row F-1, unused); the dead-tier C is a
+    // wave-uniform operand, the predictor row a per-lane one
+    const int f0 = packed_lane<N8, N4>(min(lane, F - 1));
+    const int f1 = packed_lane<N8, N4>(min(64 + lane, F - 1));
+    const uint16_t* p0 = s_pred + f0 * NZ;
+    const uint16_t* p1 = s_pred + f1 * NZ;
+    float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+    for (int d = 0; d < NZ; d += 4) {
+      const f32x4 cv = *(const f32x4*)(wt.c + NL + d);
+      const uint2 w0 = *(const uint2*)(p0 + d);
+      acc0 = __builtin_fmaf(cv.x, h2f((uint16_t)w0.x), acc0);
+      acc0 = __builtin_fmaf(cv.y, h2f((uint16_t)(w0.x >> 16)), acc0);
+      acc0 = __builtin_fmaf(cv.z, h2f((uint16_t)w0.y), acc0);
+      acc0 = __builtin_fmaf(cv.w, h2f((uint16_t)(w0.y >> 16)), acc0);
+      if constexpr (F > 64) {
+        const uint2 w1 = *(const uint2*)(p1 + d);
+        acc1 = __builtin_fmaf(cv.x, h2f((uint16_t)w1.x), acc1);
+        acc1 = __builtin_fmaf(cv.y, h2f((uint16_t)(w1.x >> 16)), acc1);
+        acc1 = __builtin_fmaf(cv.z, h2f((uint16_t)w1.y), acc1);
+        acc1 = __builtin_fmaf(cv.w, h2f((uint16_t)(w1.y >> 16)), acc1);
+      }
+    }
+    if (lane < NL) wt.cw[lane] = c0 + acc0;
+    if (64 + lane < NL) wt.cw[64 + lane] = c1 + acc1;
+    // correction of the latent coefficients: outputs NL and NL + 1
+    const float lc0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                    __builtin_bit_cast(int, NL < 64 ? acc0 : acc1), NL % 64));
+    const float lc1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                    __builtin_bit_cast(int, NL + 1 < 64 ? acc0 : acc1), (NL + 1) % 64));
+    // dead-tier dot products: canonical adjacent-pair trees (products at
+    // 2 lane + j when RZ == 128, else at lane)
+    float v[4][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int d0 = (RZ == 128) ? 2 * lane + j : lane;
+      const bool in = (RZ == 128 || j == 0) && d0 < NZ;
+      const int d = in ? d0 : 0;
+      const float bb = wt.b[NL + d], cc = wt.c[NL + d];
+      v[0][j] = in ? e0v[j] * cc : 0.f;
+      v[1][j] = in ? e1v[j] * cc : 0.f;
+      v[2][j] = in ? e0v[j] * bb : 0.f;
+      v[3][j] = in ? e1v[j] * bb : 0.f;
+    }
+    const float ec0 = wave_pair_tree<RZ>(v[0][0], v[0][1]);
+    const float ec1 = wave_pair_tree<RZ>(v[1][0], v[1][1]);
+    const float eb0 = wave_pair_tree<RZ>(v[2][0], v[2][1]);
+    const float eb1 = wave_pair_tree<RZ>(v[3][0], v[3][1]);
+    if (lane == 0) {
+      wt.dots[1] = ec0 + lc0;
+      wt.dots[2] = ec1 + lc1;
+      wt.dots[3] = eb0;
+      wt.dots[4] = eb1;
     }
   }
-  __syncthreads();
+  wave_sync();
+}
+
+// max(m, |a|, |b|) as one v_max3_f32 (IEEE maxNum: a quiet NaN operand is
+// ignored, as fmaxf does).  Written out because the compiler otherwise
+// canonicalizes each pinned operand first.
+__device__ __forceinline__ float max3_abs(float m, float a, float b) {
+  float r;
+  asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+  return r;
 }
 
 // One tier of a row: update its N carried coordinates (biased code bytes in
@@ -284,9 +323,17 @@ __device__ __forceinline__ void token_build(TokenShared<N8, N4, NZ, MODE, WPB * 
 // scale, writing the new codes back into c.  Returns the new stored scale.
 // INT8: byte = q + 128, lim 127; INT4: byte = q + 8, lim 7.  Legacy mode
 // quantizes with the binary32 denominator.
+//
+// Clamping the rounded quotient to +-lim only matters when the divisor is
+// below den (a binary16-subnormal stored scale) or when an update is not
+// finite.  `finite_in` (per lane) says the update cannot overflow or be NaN
+// (finite scale, x, decay and B*dt of bounded size); when it holds on every
+// lane and every stored scale is zero, infinite or a normal binary16 value,
+// |RN(u / s)| <= lim (1 + 2^-11) / (1 - 2^-24) < lim + 1/2 and the wave takes
+// the quantizer without the clamp.
 template <int N, bool INT8, int MODE>
 __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, float x, const f32x4* bdt4,
-                                           const f32x4* cw4, float& acc) {
+                                           const f32x4* cw4, float& acc, bool finite_in) {
   constexpr float BIAS = INT8 ? 128.0f : 8.0f;
   constexpr float LIM = INT8 ? 127.0f : 7.0f;
   constexpr float TOP = INT8 ? QTOP127 : QTOP7;
@@ -302,7 +349,6 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
       cb_next = bdt4[i0 / 4 + 1];
       cw_next = cw4[i0 / 4 + 1];
     }
-    float au[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       // prior = q * s exactly: (q + bias) * s - bias * s, all exact
@@ -312,9 +358,9 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
       // ordered pin: chunk by chunk, each prior dies as soon as it is used
       asm volatile("" : "+v"(u));
       v[i0 + j] = u;
-      au[j] = __builtin_fabsf(u);
     }
-    amax = __builtin_fmaxf(amax, __builtin_fmaxf(__builtin_fmaxf(au[0], au[1]), __builtin_fmaxf(au[2], au[3])));
+    amax = max3_abs(amax, v[i0], v[i0 + 1]);
+    amax = max3_abs(amax, v[i0 + 2], v[i0 + 3]);
     __builtin_amdgcn_sched_barrier(0);
   }
   // Materialize the accumulator and the maximum here: otherwise the compiler
@@ -324,22 +370,37 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
   const float den = __builtin_fmaxf(div_by_recip(amax, LIM, 1.0f / LIM), 1e-8f);
   const float stored = round_to_half(den);
   float d, r;
+  bool unclamped;
   if constexpr (MODE == MODE_LEGACY) {
     d = den;
     r = 1.0f / den;
+    unclamped = finite_in;
   } else {
     // zero (underflowed) or infinite stored scale: the reference's quotient
     // is 0 and so is the code
     const bool zero = !(stored > 0.f) || stored == __builtin_inff();
     d = zero ? 1.f : stored;
-    r = zero ? 0.f : 1.0f / stored;
+    r = zero ? 0.f : recip_half(stored);
+    unclamped = finite_in && (zero || stored >= 0x1p-14f);
   }
+  // wave-uniform choice, re-tested per chunk (a branch around the whole loop
+  // makes the register allocator keep both versions' values apart)
+  const bool fast = __builtin_amdgcn_ballot_w64(!unclamped) == 0;
 #pragma unroll
   for (int i = 0; i < N / 4; ++i) {
-    const int q0 = quantize_code(v[4 * i], d, r, TOP);
-    const int q1 = quantize_code(v[4 * i + 1], d, r, TOP);
-    const int q2 = quantize_code(v[4 * i + 2], d, r, TOP);
-    const int q3 = quantize_code(v[4 * i + 3], d, r, TOP);
+    int q0, q1, q2, q3;
+    if (fast) {
+      q0 = quantize_code_unclamped(v[4 * i], d, r);
+      q1 = quantize_code_unclamped(v[4 * i + 1], d, r);
+      q2 = quantize_code_unclamped(v[4 * i + 2], d, r);
+      q3 = quantize_code_unclamped(v[4 * i + 3], d, r);
+    } else {
+      asm volatile("");   // keeps this a branch: the fast side must not pay for the clamp
+      q0 = quantize_code(v[4 * i], d, r, TOP);
+      q1 = quantize_code(v[4 * i + 1], d, r, TOP);
+      q2 = quantize_code(v[4 * i + 2], d, r, TOP);
+      q3 = quantize_code(v[4 * i + 3], d, r, TOP);
+    }
     uint32_t packed = pack4(q0, q1, q2, q3);
     packed = INT8 ? (packed ^ 0x80808080u) : ((packed & 0x0F0F0F0Fu) ^ 0x08080808u);
     asm volatile("" : "+v"(packed));
@@ -349,30 +410,23 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
   return stored;
 }
 
-// Orders a wave's LDS accesses across its lanes (the wave's own staging
-// tiles need no workgroup barrier).
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-}
-
 // One workgroup = WPB waves, each owning HPW head slots of 64 rows (the same
 // P block of NH = WPB * HPW consecutive heads of one B/C group and batch
 // row).  The packed rows of every slot stay in LDS, in the reference's SoA
 // field layout, for all L tokens; a slot is unpacked into VGPRs, stepped and
 // repacked in one pass per token.  The first token streams the slots in:
-// the next slot's rows are loaded into VGPRs while the current one computes.
-// Per-token shared values are built once per workgroup for all NH heads.
+// slot k+1 is fetched while slot k computes.  Every wave builds the token
+// values it reads itself, so the only workgroup barrier is the one that
+// publishes the ridge predictor (staged once, shared by all waves).
 template <int N8, int N4, int NZ, int MODE, int WPB, int HPW>
-__global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(WPB == 8 ? 4 : 1, 8)))
+__global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(WPB == 8 ? 4 : 2, 8)))
 void k_state_step(StepArgs a) {
   constexpr int W8 = N8 / 2;          // bytes per row of lo and of hi
   constexpr int W4 = N4 / 2;          // bytes per row of q4
   constexpr int NL = N8 + N4;         // carried coordinates
   constexpr int F = NL + 2;           // ridge predictor features
-  constexpr int NT = 64 * WPB;
   constexpr int NH = WPB * HPW;
+  constexpr int RZ = next_pow2(NZ);
   constexpr bool RIDGE = MODE == MODE_RIDGE;
   constexpr int O_LO = 0, O_HI = 64 * W8, O_Q4 = 128 * W8, O_S8 = O_Q4 + 64 * W4, O_S4 = O_S8 + 128;
   constexpr int O_LAT = O_S4 + 128;
@@ -380,17 +434,12 @@ void k_state_step(StepArgs a) {
   constexpr int C8 = N8 / 4, C4 = N4 / 4;   // carried code words (4 biased bytes each)
   constexpr int PRED_DW = RIDGE ? F * NZ / 2 : 1;   // F*NZ is even for every layout
   constexpr int PRED_OPS = (PRED_DW + 63) / 64;     // 64-dword transfers of the predictor
-  constexpr int PERM_PT = (128 + NT - 1) / NT;      // permutation bytes per thread
-  constexpr int BASIS_PT = (NZ + NT - 1) / NT;      // basis pairs per thread
   static_assert(N8 % 4 == 0 && N4 % 4 == 0 && N8 > 0 && N4 > 0, "tier widths must be positive multiples of 4");
+  static_assert(NZ % 4 == 0 && NL + NZ == 128, "dead tier read as 4-wide vectors");
   static_assert(!RIDGE || (F * NZ) % 2 == 0, "predictor staged as dwords");
   static_assert(TILE % 16 == 0, "tiles stay 16-byte aligned");
 
-  // small, often-read arrays first: their LDS offsets fit instruction immediates
-  __shared__ __align__(16) TokenShared<N8, N4, NZ, MODE, NH> sh;
-  __shared__ float s_D[NH];
-  __shared__ uint8_t s_perm[128];
-  __shared__ float s_basis[RIDGE ? 2 * NZ : 1];
+  __shared__ __align__(16) WaveToken<N8, N4, HPW> s_wt[WPB];
   __shared__ __align__(16) uint32_t s_pred32[PRED_OPS * 64];
   __shared__ __align__(16) uint8_t s_tile[NH][TILE];
 
@@ -404,36 +453,46 @@ void k_state_step(StepArgs a) {
   const int pbase = blockIdx.x * 64;
   const int nvalid = min(64, P - pbase);
   const bool valid = lane < nvalid;
-  const bool dword_tiles = (P & 1) == 0;   // every slot's row0 * W and nvalid * W are dword multiples
+  const bool dma_tiles = a.dma_tiles != 0;   // else the slots are staged through VGPRs
   const uint16_t* s_pred = (const uint16_t*)s_pred32;
+  WaveToken<N8, N4, HPW>& wt = s_wt[wave];
 
-  // vector memory operations per slot transfer (field_dma counts)
-  constexpr int SLOT_DMA = 2 * dma_ops(W8) + dma_ops(W4) + dma_ops(2) * (RIDGE ? 3 : 2);
+  // vector memory operations per slot transfer (and per state copy-out)
+  constexpr int SLOT_DMA = 2 * chunk_ops(W8) + chunk_ops(W4) + chunk_ops(2) * (RIDGE ? 3 : 2);
   static_assert(SLOT_DMA <= 63, "a slot's transfers must fit the vmcnt range");
   auto slot_row0 = [&](int hh) { return (b * H + h0 + hh) * P + pbase; };
-  auto slot_dma = [&](int hh) {   // even P: direct global -> LDS transfers
+  auto slot_dma = [&](int hh) {   // direct global -> LDS transfers
     const int row0 = slot_row0(hh);
     uint8_t* t = s_tile[hh];
-    field_dma<W8>(t + O_LO, a.lo, row0, nvalid, lane);
-    field_dma<W8>(t + O_HI, a.hi, row0, nvalid, lane);
-    field_dma<W4>(t + O_Q4, a.q4, row0, nvalid, lane);
-    field_dma<2>(t + O_S8, (const uint8_t*)a.s8, row0, nvalid, lane);
-    field_dma<2>(t + O_S4, (const uint8_t*)a.s4, row0, nvalid, lane);
-    if constexpr (RIDGE) field_dma<2>(t + O_LAT, a.latent, row0, nvalid, lane);
+    field_dma16<W8>(t + O_LO, a.lo, row0, nvalid, lane);
+    field_dma16<W8>(t + O_HI, a.hi, row0, nvalid, lane);
+    field_dma16<W4>(t + O_Q4, a.q4, row0, nvalid, lane);
+    field_dma16<2>(t + O_S8, (const uint8_t*)a.s8, row0, nvalid, lane);
+    field_dma16<2>(t + O_S4, (const uint8_t*)a.s4, row0, nvalid, lane);
+    if constexpr (RIDGE) field_dma16<2>(t + O_LAT, a.latent, row0, nvalid, lane);
   };
-  // at the first token, before slot k is read: issue slot k+1's transfers,
-  // then wait until only those are outstanding (vector memory operations
-  // complete in program order, so slot k's transfers and everything issued
-  // before them have landed)
+  constexpr int COPY_OPS = SLOT_DMA;   // one store instruction per transfer chunk
+  static_assert(SLOT_DMA + COPY_OPS + 1 <= 63, "vmcnt range");
+  // At the first token, before slot k is read: issue slot k+1's transfers,
+  // then wait until only the operations issued after slot k's transfers are
+  // outstanding (vector memory operations complete in program order), so no
+  // wait covers a store's write acknowledgement.  Those operations are slot
+  // k-1's y store (one store instruction), slot k-2's state copy-out when
+  // the first token is also the last (copy-outs trail by one slot), and slot
+  // k+1's transfers.
   auto slot_fetch_next_and_wait = [&](int k) {
-    if (dword_tiles && k + 1 < HPW) {
-      slot_dma((k + 1) * WPB + wave);
-      wait_vmcnt<SLOT_DMA>();
+    const bool more = dma_tiles && k + 1 < HPW;
+    if (more) slot_dma((k + 1) * WPB + wave);
+    const bool copy = L == 1 && k >= 2;
+    if (k == 0) {
+      if (more) wait_vmcnt<SLOT_DMA>(); else wait_vmcnt<0>();
+    } else if (more) {
+      if (copy) wait_vmcnt<SLOT_DMA + COPY_OPS + 1>(); else wait_vmcnt<SLOT_DMA + 1>();
     } else {
-      wait_vmcnt<0>();
+      if (copy) wait_vmcnt<COPY_OPS + 1>(); else wait_vmcnt<1>();
     }
   };
-  auto slot_copy_in = [&](int hh) {   // odd P: 16-bit transfers
+  auto slot_copy_in = [&](int hh) {   // other geometries: 16-bit transfers through VGPRs
     const int row0 = slot_row0(hh);
     uint8_t* t = s_tile[hh];
     wave_copy_in<W8>(t + O_LO, a.lo, row0, nvalid, lane);
@@ -446,13 +505,13 @@ void k_state_step(StepArgs a) {
   auto slot_copy_out = [&](int hh) {
     const int row0 = slot_row0(hh);
     const uint8_t* t = s_tile[hh];
-    if (dword_tiles) {
-      field_store<W8>(a.lo, t + O_LO, row0, nvalid, lane);
-      field_store<W8>(a.hi, t + O_HI, row0, nvalid, lane);
-      field_store<W4>(a.q4, t + O_Q4, row0, nvalid, lane);
-      field_store<2>((uint8_t*)a.s8, t + O_S8, row0, nvalid, lane);
-      field_store<2>((uint8_t*)a.s4, t + O_S4, row0, nvalid, lane);
-      if constexpr (RIDGE) field_store<2>(a.latent, t + O_LAT, row0, nvalid, lane);
+    if (dma_tiles) {
+      field_store16<W8>(a.lo, t + O_LO, row0, nvalid, lane);
+      field_store16<W8>(a.hi, t + O_HI, row0, nvalid, lane);
+      field_store16<W4>(a.q4, t + O_Q4, row0, nvalid, lane);
+      field_store16<2>((uint8_t*)a.s8, t + O_S8, row0, nvalid, lane);
+      field_store16<2>((uint8_t*)a.s4, t + O_S4, row0, nvalid, lane);
+      if constexpr (RIDGE) field_store16<2>(a.latent, t + O_LAT, row0, nvalid, lane);
       return;
     }
     wave_copy_out<W8>(a.lo, t + O_LO, row0, nvalid, lane);
@@ -463,78 +522,80 @@ void k_state_step(StepArgs a) {
     if constexpr (RIDGE) wave_copy_out<2>(a.latent, t + O_LAT, row0, nvalid, lane);
   };
 
-  // ---- prologue: the predictor's LDS transfer, then the register loads of the
-  // first token and the statics (one wait covers both), then the LDS transfer
-  // of the wave's first slot, which lands during the token build; each later
-  // slot is fetched while the previous one computes -----------------------------
-  if constexpr (RIDGE) {   // predictor rows of the group, spread over the waves
+  // ---- prologue: the wave's share of the predictor's LDS transfer, then the
+  // register loads of the first token and the statics (one wait covers both),
+  // then the LDS transfer of the wave's first slot, which lands while the
+  // token is built; each later slot is fetched while the previous computes --
+  // (order: the dt inputs, the predictor transfer, then the rest; the dt
+  // activation's wait for its inputs thus covers only the first two)
+  WaveRaw<HPW> raw;
+  wave_load_dt<WPB, HPW>(a, raw, b * L, h0, lane, wave);
+  const int hl = h0 + min(lane, HPW - 1) * WPB + wave;   // head of slot `lane` (lanes < HPW)
+  const float Ah = a.A[hl];
+  if constexpr (RIDGE) {
     const uint8_t* pg = (const uint8_t*)(a.pred + (size_t)g * F * NZ);
     for (int j = wave; j < PRED_OPS; j += WPB) lds_dma_b32(pg + 4 * min(j * 64 + lane, PRED_DW - 1),
                                                            lds_address(s_pred32 + 64 * j));
   }
-  TokenRaw<WPB, HPW> raw;
-  token_load<WPB, HPW>(a, raw, b * L, g, h0, pbase, tid, lane, wave);
-  const float Ah = (tid < NH) ? a.A[h0 + tid] : 0.f;
-  const float Dv = (tid < NH) ? load_param(a.D, a.d_f32, h0 + tid) : 0.f;
-  uint8_t permv[PERM_PT];
+  wave_load_rest<WPB, HPW>(a, raw, b * L, g, h0, pbase, lane, wave);
+  // statics, kept as loaded bits until the first token's full wait (a
+  // conversion here would make the compiler wait for them before the dt
+  // activation)
+  const uint32_t d_bits = a.d_f32 ? ((const uint32_t*)a.D)[hl] : (uint32_t)((const uint16_t*)a.D)[hl];
+  const uint32_t perm0 = a.perm[g * 128 + packed_lane<N8, N4>(lane)];
+  const uint32_t perm1 = a.perm[g * 128 + packed_lane<N8, N4>(64 + lane)];
+  uint32_t basis_w[2] = {0u, 0u};
+  uint32_t ls_w = 0u;
+  if constexpr (RIDGE) {
 #pragma unroll
-  for (int k = 0; k < PERM_PT; ++k) {
-    const int n = k * NT + tid;
-    permv[k] = (n < 128) ? a.perm[g * 128 + n] : (uint8_t)0;
+    for (int j = 0; j < 2; ++j) {
+      const int d0 = (RZ == 128) ? 2 * lane + j : lane;
+      basis_w[j] = ((const uint32_t*)a.basis)[g * NZ + min(d0, NZ - 1)];   // unused past NZ
+    }
+    ls_w = (uint32_t)a.lscale[g * 2] | ((uint32_t)a.lscale[g * 2 + 1] << 16);
   }
-  uint32_t basisv[BASIS_PT];
+  // dt activation of the first token while the other loads are in flight
+  float2 act = wave_dt_activation<HPW>(raw, Ah, a.db_f32);
+  // the predictor transfer and the register loads complete before any slot
+  // transfer is issued (the compiler's own waits for the register loads then
+  // never cover a slot transfer; no load may be scheduled past this wait)
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+  __builtin_amdgcn_sched_barrier(0);
+  if (dma_tiles) slot_dma(wave);
+  else {
+    for (int k = 0; k < HPW; ++k) slot_copy_in(k * WPB + wave);
+  }
+  if (lane < HPW) wt.D[lane] = a.d_f32 ? __builtin_bit_cast(float, d_bits) : h2f((uint16_t)d_bits);
+  const int pv0 = perm0 & 127, pv1 = perm1 & 127;   // raw B/C index of internal positions lane, lane + 64
+  float e0v[2] = {0.f, 0.f}, e1v[2] = {0.f, 0.f};   // dead-tier basis at the pair-tree positions
   float ls0 = 0.f, ls1 = 0.f, rls0 = 0.f, rls1 = 0.f;
   if constexpr (RIDGE) {
 #pragma unroll
-    for (int k = 0; k < BASIS_PT; ++k) {
-      const int i = k * NT + tid;
-      basisv[k] = (i < NZ) ? ((const uint32_t*)a.basis)[g * NZ + i] : 0u;
+    for (int j = 0; j < 2; ++j) {
+      e0v[j] = h2f((uint16_t)(basis_w[j] & 0xFFFFu));
+      e1v[j] = h2f((uint16_t)(basis_w[j] >> 16));
     }
-    ls0 = h2f(a.lscale[g * 2]);
-    ls1 = h2f(a.lscale[g * 2 + 1]);
+    ls0 = h2f((uint16_t)(ls_w & 0xFFFFu));
+    ls1 = h2f((uint16_t)(ls_w >> 16));
     rls0 = 1.0f / ls0;   // correctly rounded reciprocals
     rls1 = 1.0f / ls1;
   }
-  // the predictor transfer and the register loads complete before any slot
-  // transfer is issued (the compiler's own waits for the register loads then
-  // never cover a slot transfer)
-  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-  if (dword_tiles) slot_dma(wave);
-  if (tid < NH) s_D[tid] = Dv;
-#pragma unroll
-  for (int k = 0; k < PERM_PT; ++k) {
-    const int n = k * NT + tid;
-    if (n < 128) s_perm[n] = permv[k];
-  }
-  if constexpr (RIDGE) {
-#pragma unroll
-    for (int k = 0; k < BASIS_PT; ++k) {
-      const int i = k * NT + tid;
-      if (i < NZ) {
-        s_basis[i] = h2f((uint16_t)(basisv[k] & 0xFFFFu));
-        s_basis[NZ + i] = h2f((uint16_t)(basisv[k] >> 16));
-      }
-    }
-  }
-  if (!dword_tiles) {
-    for (int k = 0; k < HPW; ++k) slot_copy_in(k * WPB + wave);
-  }
-  token_store<N8, N4, NZ, MODE, WPB, HPW>(sh, raw, Ah, a.db_f32, tid, lane, wave);
-  __syncthreads();
 
   for (int t = 0; t < L; ++t) {
     const int bt = b * L + t;
-    if (t > 0) {
-      token_store<N8, N4, NZ, MODE, WPB, HPW>(sh, raw, Ah, a.db_f32, tid, lane, wave);
-      __syncthreads();
+    const WaveRaw<HPW> cur = raw;
+    if (t + 1 < L) {   // prefetch
+      wave_load_dt<WPB, HPW>(a, raw, bt + 1, h0, lane, wave);
+      wave_load_rest<WPB, HPW>(a, raw, bt + 1, g, h0, pbase, lane, wave);
     }
-    if (t + 1 < L) token_load<WPB, HPW>(a, raw, bt + 1, g, h0, pbase, tid, lane, wave);   // prefetch
-    token_build<N8, N4, NZ, MODE, WPB, HPW>(sh, s_perm, s_basis, s_pred, tid, lane, wave);
+    wave_token_build<N8, N4, NZ, MODE, HPW>(wt, cur, act, pv0, pv1, e0v, e1v, s_pred, t == 0, lane);
 
     for (int k = 0; k < HPW; ++k) {
       const int hh = k * WPB + wave;
       const int h = h0 + hh;
       if (t == 0) slot_fetch_next_and_wait(k);
+      if (t == L - 1 && k > 0) slot_copy_out(hh - WPB);   // the previous slot's state
       uint8_t* tile = s_tile[hh];
       uint16_t* t16 = (uint16_t*)tile;
 
@@ -564,39 +625,43 @@ void k_state_step(StepArgs a) {
         for (int i = 0; i < C4; ++i) c4[i] = 0x08080808u;
         sc8 = sc4 = z0 = z1 = 0.f;
       }
-      const float x = h2f(sh.xr[hh * 64 + lane]);
-      const float decay = sh.decay[hh];
-      const float dtv = sh.dtv[hh];
+      const float x = h2f(wt.x[k][lane]);
+      const float decay = wt.decay[k];
+      const float dtv = wt.dtv[k];
+      const bool base_ok = wt.bounded[k] != 0 && __builtin_fabsf(x) <= 65504.f;
 
       // ---- per tier: update, readout accumulation, requantization ---------------
       // (each tier is requantized before the next is updated, so only one
       // tier's updated values are live at a time)
-      const f32x4* bdt4 = (const f32x4*)sh.bdt[hh];
-      const f32x4* cw4;
-      if constexpr (RIDGE) cw4 = (const f32x4*)sh.cp; else cw4 = (const f32x4*)sh.c;
+      const f32x4* bdt4 = (const f32x4*)wt.bdt[k];
+      const f32x4* cw4 = (const f32x4*)wt.cw;
       float acc = 0.f;
-      sc8 = tier_step<N8, true, MODE>(c8, sc8, decay, x, bdt4, cw4, acc);
+      const bool ok8 = base_ok && __builtin_fabsf(sc8) <= 65504.f;
+      const bool ok4 = base_ok && __builtin_fabsf(sc4) <= 65504.f;
+      sc8 = tier_step<N8, true, MODE>(c8, sc8, decay, x, bdt4, cw4, acc, ok8);
       __builtin_amdgcn_sched_barrier(0);
-      sc4 = tier_step<N4, false, MODE>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc);
+      sc4 = tier_step<N4, false, MODE>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc, ok4);
       __builtin_amdgcn_sched_barrier(0);
       // readout: sum_i u_i c_i + corrections = decay * (sum_i prior_i (c_i +
       // corr_i) + latent terms) + x * (dt * sum_all b c + D)
       float out;
       uint32_t qz = 0;
       if constexpr (RIDGE) {
-        const float kz0 = sh.dots[1] + sh.dots[5], kz1 = sh.dots[2] + sh.dots[6];
-        out = decay * (acc + z0 * kz0 + z1 * kz1) + x * (dtv * sh.dots[0] + s_D[hh]);
+        out = decay * (acc + z0 * wt.dots[1] + z1 * wt.dots[2]) + x * (dtv * wt.dots[0] + wt.D[k]);
         // latent step (bit-exact): z <- z * decay + (x * dt) * (e . b_dead), requantized
         const float xdt = x * dtv;
-        const float zn0 = z0 * decay + xdt * sh.dots[3];
-        const float zn1 = z1 * decay + xdt * sh.dots[4];
+        const float zn0 = z0 * decay + xdt * wt.dots[3];
+        const float zn1 = z1 * decay + xdt * wt.dots[4];
         const float q0 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn0, ls0, rls0), -448.f), 448.f);
         const float q1 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn1, ls1, rls1), -448.f), 448.f);
         qz = f32_to_e4m3(q0) | (f32_to_e4m3(q1) << 8);
       } else {
-        out = decay * acc + x * (dtv * sh.dots[0] + s_D[hh]);
+        out = decay * acc + x * (dtv * wt.dots[0] + wt.D[k]);
       }
-      if (valid) a.y[((size_t)bt * H + h) * P + pbase + lane] = f2h(out);
+      {   // one unguarded store instruction: the range check drops rows past P
+        const __amdgpu_buffer_rsrc_t ry = raw_buffer(a.y + ((size_t)bt * H + h) * P + pbase, 2 * nvalid);
+        __builtin_amdgcn_raw_buffer_store_b16(f2h(out), ry, 2 * lane, 0, STORE_THROUGH);
+      }
 
       // ---- repack the slot row into the tile ---------------------------------------
       if (valid) {
@@ -611,9 +676,9 @@ void k_state_step(StepArgs a) {
         if constexpr (RIDGE) t16[O_LAT / 2 + lane] = (uint16_t)qz;
       }
       wave_sync();
-      if (t == L - 1) slot_copy_out(hh);
     }
-    if (t + 1 < L) __syncthreads();   // shared token values are rebuilt next iteration
+    if (t == L - 1) slot_copy_out((HPW - 1) * WPB + wave);
+    if (t + 1 < L) act = wave_dt_activation<HPW>(raw, Ah, a.db_f32);
   }
 }
 
@@ -692,6 +757,16 @@ static hipError_t dispatch_tier(const Dispatch& a, hipStream_t stream) {
 
 using namespace m2r;
 
+// 16-byte LDS transfers need every slot's field start and valid length to be
+// multiples of 16 bytes: P % 8 == 0 (fields are 2 to 38 bytes wide, all even)
+// and 16-byte aligned field arrays.
+static int dma_tiles_ok(int64_t P, std::initializer_list<const void*> fields) {
+  if (P % 8) return 0;
+  for (const void* f : fields)
+    if (f && ((uintptr_t)f & 15)) return 0;
+  return 1;
+}
+
 static int check_geometry(int64_t batch, int64_t L, int64_t H, int64_t P, int64_t G) {
   if (batch <= 0 || L <= 0 || H <= 0 || P <= 0 || G <= 0) return m2r_fail("state step: non-positive geometry");
   if (H % G) return m2r_fail("state step: heads must be divisible by groups");
@@ -711,7 +786,7 @@ extern "C" int m2r_state_step_ridge(const void* x, const void* dt, const float* 
   d.args = StepArgs{(const uint16_t*)x, (const uint16_t*)dt, A, (const uint16_t*)B, (const uint16_t*)C, D, dt_bias,
                     perm, (const uint16_t*)basis, (const uint16_t*)lscale, (const uint16_t*)pred, lo, hi, q4, latent,
                     (uint16_t*)s8, (uint16_t*)s4, (uint16_t*)y, (int)batch, (int)L, (int)H, (int)P, (int)G,
-                    d_is_f32, db_is_f32};
+                    d_is_f32, db_is_f32, dma_tiles_ok(P, {lo, hi, q4, latent, s8, s4})};
   d.n8_ = n8; d.n4_ = n4; d.nz_ = nz;
   hipError_t e = dispatch_ridge(d, stream);
   if (e == hipErrorInvalidValue) return m2r_fail("ridge step: unsupported tier layout");
@@ -727,7 +802,8 @@ extern "C" int m2r_state_step_tier(const void* x, const void* dt, const float* A
   Dispatch d{};
   d.args = StepArgs{(const uint16_t*)x, (const uint16_t*)dt, A, (const uint16_t*)B, (const uint16_t*)C, D, dt_bias,
                     perm, nullptr, nullptr, nullptr, lo, hi, q4, nullptr, (uint16_t*)s8, (uint16_t*)s4,
-                    (uint16_t*)y, (int)batch, (int)L, (int)H, (int)P, (int)G, d_is_f32, db_is_f32};
+                    (uint16_t*)y, (int)batch, (int)L, (int)H, (int)P, (int)G, d_is_f32, db_is_f32,
+                    dma_tiles_ok(P, {lo, hi, q4, s8, s4})};
   d.n8_ = n8; d.n4_ = n4; d.nz_ = nz;
   hipError_t e = dispatch_tier(d, stream);
   if (e == hipErrorInvalidValue) return m2r_fail("tier step: unsupported tier layout");
@@ -752,6 +828,7 @@ extern "C" int m2r_state_step_legacy(const void* x, const void* dt, const float*
   if (int e = check_geometry(batch, L, H, P, G)) return e;
   StepArgs args{(const uint16_t*)x, (const uint16_t*)dt, A, (const uint16_t*)B, (const uint16_t*)C, D, dt_bias,
                 perm, nullptr, nullptr, nullptr, lo, hi, q4, nullptr, (uint16_t*)s8, (uint16_t*)s4,
-                (uint16_t*)y, (int)batch, (int)L, (int)H, (int)P, (int)G, d_is_f32, db_is_f32};
+                (uint16_t*)y, (int)batch, (int)L, (int)H, (int)P, (int)G, d_is_f32, db_is_f32,
+                dma_tiles_ok(P, {lo, hi, q4, s8, s4})};
   return m2r_check(launch_layout<16, 64, 48, MODE_LEGACY>(args, stream), "legacy step launch");
 }

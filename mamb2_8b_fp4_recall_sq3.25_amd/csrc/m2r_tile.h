@@ -100,6 +100,64 @@ __device__ __forceinline__ void lds_dma_b32(const void* g, uint32_t lds) {
                : "=&s"(saved) : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
 }
 
+// Raw buffer resource over `bytes` bytes at `base` (gfx9-family dword 3:
+// 32-bit raw data, no swizzle): accesses at offsets >= bytes are dropped
+// (stores) or read 0 (loads) by the hardware range check.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_buffer(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+// The 16-byte form: lane l's 16 bytes at g land at M0 + 16 l.  Marked
+// non-temporal: every state byte is read once per launch.
+__device__ __forceinline__ void lds_dma_b128(const void* g, uint32_t lds) {
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off nt\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved) : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+
+// 16-byte transfers of one SoA field of a 64-row slot (64 * W bytes at
+// g + row0 * W) to or from the slot's LDS tile: one vector memory operation
+// per started 1 KiB chunk.
+constexpr int chunk_ops(int W) { return (64 * W + 1023) / 1024; }
+
+// Global -> LDS.  Lanes past the field stay idle; lanes past the nvalid valid
+// rows re-read the last valid chunk, whose copy lands in rows nobody reads.
+// Requires g + row0 * W to be 16-byte aligned and nvalid * W a multiple of
+// 16.  Issues exactly chunk_ops(W) operations.
+template <int W>
+__device__ __forceinline__ void field_dma16(uint8_t* lds, const uint8_t* g, int row0, int nvalid, int lane) {
+  constexpr int FB = 64 * W;
+  const uint8_t* base = g + (size_t)row0 * W;
+  const uint32_t l0 = lds_address(lds);
+  const int last = nvalid * W - 16;
+#pragma unroll
+  for (int k = 0; k < chunk_ops(W); ++k) {
+    const int o = k * 1024 + 16 * lane;
+    if (k * 1024 + 1024 <= FB || o < FB) lds_dma_b128(base + min(o, last), l0 + 1024 * k);
+  }
+}
+
+// Cache policy of the state and output stores: device scope (sc1) and
+// non-temporal, so they are written through during the launch instead of
+// staying dirty in the issuing XCD's L2 until the end-of-kernel writeback.
+constexpr int STORE_THROUGH = 16 | 2;
+
+// LDS -> global: all LDS reads first, then unguarded 16-byte buffer stores
+// whose range check drops everything past nvalid * W bytes (whole chunks,
+// under the same alignment requirements).  Issues exactly chunk_ops(W)
+// store instructions.
+template <int W>
+__device__ __forceinline__ void field_store16(uint8_t* g, const uint8_t* lds, int row0, int nvalid, int lane) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  constexpr int FB = 64 * W, NC = chunk_ops(W);
+  const __amdgpu_buffer_rsrc_t rsrc = raw_buffer(g + (size_t)row0 * W, nvalid * W);
+  u32x4 v[NC];
+#pragma unroll
+  for (int k = 0; k < NC; ++k) v[k] = *(const u32x4*)(lds + min(k * 1024 + 16 * lane, FB - 16));
+#pragma unroll
+  for (int k = 0; k < NC; ++k) __builtin_amdgcn_raw_buffer_store_b128(v[k], rsrc, k * 1024 + 16 * lane, 0, STORE_THROUGH);
+}
+
 // LDS DMA of one SoA field of a 64-row slot: 64 * W bytes at g + row0 * W
 // land at lds[0 .. 64 * W).  W / 4 dword transfers (64 lanes x 4 bytes)
 // plus, for W % 4 == 2, one transfer by lanes 0..31 cover the field exactly
@@ -163,12 +221,6 @@ __device__ __forceinline__ void field_dma(uint8_t* lds, const uint8_t* g, int ro
   }
 }
 
-// Raw buffer resource over `bytes` bytes at `base` (gfx9-family dword 3:
-// 32-bit raw data, no swizzle): accesses at offsets >= bytes are dropped
-// (stores) or read 0 (loads) by the hardware range check.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_buffer(const void* base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
-}
 
 // Stores one SoA field of a 64-row slot staged in LDS (64 * W bytes) to
 // g + row0 * W, nvalid rows: all LDS reads first, then unguarded dword

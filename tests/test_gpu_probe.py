@@ -41,6 +41,18 @@ def test_f16_conversions(oracle, device):
     assert (dev_unary(vals, 0, device) == oracle.unary(vals, 0)).all()
 
 
+def test_binary16_reciprocal_is_correctly_rounded(device):
+    """The kernels' reciprocal of a stored (binary16) scale: estimate plus one
+    Newton step.  Exhaustive over every positive finite binary16 value; the
+    reference is IEEE binary32 division."""
+    bits = np.arange(1, 0x7C00, dtype=np.uint32)
+    s = bits.astype(np.uint16).view(np.float16).astype(np.float32)
+    want = (np.float32(1.0) / s).astype(np.float32).view(np.uint32)
+    got = dev_unary(bits, 8, device)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"{bad.size} mismatches, first at f16 0x{int(bits[bad[0]]):04x}"
+
+
 def test_e4m3_conversions(oracle, device):
     every8 = np.arange(256, dtype=np.uint32)
     assert same_float_bits(dev_unary(every8, 3, device), oracle.unary(every8, 3)).all()

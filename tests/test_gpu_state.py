@@ -60,13 +60,14 @@ def assert_y_close(y_dev, y_ref, what):
 
 
 def run_ridge(oracle, device, layout, batch, L, H, P, G, seed, *, random_state=True, d_f32=False, db_f32=False,
-              dt_bias_zero=True):
+              dt_bias_zero=True, x_scale=1.0, scale_mu=-4.0):
     from mamba2_recall import ridge_codec
     n8, n4, nz = ridge_counts(layout)
     rng = np.random.default_rng(seed)
-    inp = cases.step_inputs(rng, batch, L, H, P, G, d_f32=d_f32, db_f32=db_f32, dt_bias_zero=dt_bias_zero)
+    inp = cases.step_inputs(rng, batch, L, H, P, G, d_f32=d_f32, db_f32=db_f32, dt_bias_zero=dt_bias_zero,
+                            x_scale=x_scale)
     sta = cases.ridge_statics(rng, G, n8, n4, nz)
-    st0 = (cases.random_packed_state(rng, batch, H, P, n8, n4, latent=True) if random_state
+    st0 = (cases.random_packed_state(rng, batch, H, P, n8, n4, latent=True, scale_mu=scale_mu) if random_state
            else cases.zero_packed_state(batch, H, P, n8, n4, latent=True))
     print(f"[ridge] layout={layout} B={batch} L={L} H={H} P={P} G={G} seed={seed}", flush=True)
     ref_state = cases.copy_state(st0)
@@ -86,12 +87,13 @@ def run_ridge(oracle, device, layout, batch, L, H, P, G, seed, *, random_state=T
 
 
 def run_tier(oracle, device, kind, layout, batch, L, H, P, G, seed, *, random_state=True, d_f32=False,
-             db_f32=False, dt_bias_zero=True):
+             db_f32=False, dt_bias_zero=True, x_scale=1.0, scale_mu=-4.0):
     from mamba2_recall import state_codec, tier_codec
     n8, n4, nz = tier_counts(layout)
     rng = np.random.default_rng(seed)
-    inp = cases.step_inputs(rng, batch, L, H, P, G, d_f32=d_f32, db_f32=db_f32, dt_bias_zero=dt_bias_zero)
-    st0 = (cases.random_packed_state(rng, batch, H, P, n8, n4) if random_state
+    inp = cases.step_inputs(rng, batch, L, H, P, G, d_f32=d_f32, db_f32=db_f32, dt_bias_zero=dt_bias_zero,
+                            x_scale=x_scale)
+    st0 = (cases.random_packed_state(rng, batch, H, P, n8, n4, scale_mu=scale_mu) if random_state
            else cases.zero_packed_state(batch, H, P, n8, n4))
     print(f"[{kind}] layout={layout} B={batch} L={L} H={H} P={P} G={G} seed={seed}", flush=True)
     ref_state = cases.copy_state(st0)
@@ -129,6 +131,16 @@ def test_ridge_reference_fixture_geometry(oracle, device, L):
     # scripts/check_state_ridge_training_v3.py:28 uses b,h,p,g = 1,8,16,2
     for layout in RIDGE_LAYOUTS:
         run_ridge(oracle, device, layout, batch=1, L=L, H=8, P=16, G=2, seed=13 + L, random_state=False)
+
+
+@pytest.mark.parametrize("x_scale,scale_mu", [(1e-5, -14.0), (3e-7, -17.0), (1e-9, -24.0)])
+def test_tiny_states_subnormal_stored_scales(oracle, device, x_scale, scale_mu):
+    """Updates small enough that the new stored scales are binary16
+    subnormals or underflow to zero: the rounded quotient can exceed the
+    limit there, so these rows take the clamping quantizer."""
+    run_ridge(oracle, device, "32_32_64", 2, 3, 32, 64, 2, 71, x_scale=x_scale, scale_mu=scale_mu)
+    run_tier(oracle, device, "tier", "16_64_48", 2, 3, 32, 64, 2, 72, x_scale=x_scale, scale_mu=scale_mu)
+    run_tier(oracle, device, "legacy", "16_64_48", 2, 3, 32, 64, 2, 73, x_scale=x_scale, scale_mu=scale_mu)
 
 
 def test_ridge_zero_state_and_f32_params(oracle, device):
