@@ -132,7 +132,7 @@ __global__ __launch_bounds__(64 * WPB) void k_dense3_step(Dense3Args a) {
         const int i = i0 + j;
         float prior = (i < 64) ? __builtin_fmaf(ubyte_f(c[i / 4], j), sc0, nb0)
                                : __builtin_fmaf(ubyte_f(c[i / 4], j), sc1, nb1);
-        float u = prior * decay + cb[j] * x;
+        float u = state_update(prior, decay, cb[j] * x);
         v[i] = u;
         acc = __builtin_fmaf(u, cc[j], acc);
         if (i < 64) amax0 = __builtin_fmaxf(amax0, __builtin_fabsf(u));
@@ -177,7 +177,7 @@ __global__ __launch_bounds__(64 * WPB) void k_dense3_step(Dense3Args a) {
 }
 
 // ---------------------------------------------------------------------------
-// FP16-carry control: state = half(state * decay + (B*dt) * x) after the
+// FP16-carry control: state = half(fma(state, decay, (B*dt) * x)) after the
 // readout y = sum(state * C) + x * D.  Optional statistics: sum over tokens
 // and the rows of each 16-row P tile of |FP16 carry| per coordinate.
 struct S16Args {
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(64) void k_s16_step(S16Args a) {
 #pragma unroll
     for (int n = 0; n < 128; ++n) {
       float dB = s_b[n] * dtv;
-      st[n] = st[n] * decay + dB * x;
+      st[n] = state_update(st[n], decay, dB * x);
       acc = __builtin_fmaf(st[n], s_c[n], acc);
     }
     asm volatile("" : "+v"(acc));

@@ -126,6 +126,14 @@ constexpr float QTOP127 = 0x1.fffffep+6f;   // below 128
 constexpr float QTOP7 = 0x1.fffffep+2f;     // below 8
 constexpr float QTOP3 = 0x1.fffffep+1f;     // below 4
 
+// The recurrent update of every codec: fma(state, decay, input) with
+// input = RN(RN(b * dt) * x) rounded separately, i.e. the reference's
+// `state * decay + (b * dt) * x` as Triton's floating-point fusion contracts
+// it (one rounding of state * decay + input).
+__device__ __forceinline__ float state_update(float state, float decay, float input) {
+  return __builtin_fmaf(state, decay, input);
+}
+
 // ---------------------------------------------------------------------------
 // Transcendentals.  The codec defines exp/log of a binary32 argument as the
 // binary32 rounding of a fixed binary64 evaluation that uses only IEEE

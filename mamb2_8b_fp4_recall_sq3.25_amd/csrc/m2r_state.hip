@@ -354,7 +354,7 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
       // prior = q * s exactly: (q + bias) * s - bias * s, all exact
       const float prior = __builtin_fmaf(ubyte_f(c[i0 / 4], j), sc, nb);
       acc = __builtin_fmaf(prior, cw[j], acc);
-      float u = prior * decay + cb[j] * x;
+      float u = state_update(prior, decay, cb[j] * x);
       // ordered pin: chunk by chunk, each prior dies as soon as it is used
       asm volatile("" : "+v"(u));
       v[i0 + j] = u;
@@ -648,10 +648,10 @@ void k_state_step(StepArgs a) {
       uint32_t qz = 0;
       if constexpr (RIDGE) {
         out = decay * (acc + z0 * wt.dots[1] + z1 * wt.dots[2]) + x * (dtv * wt.dots[0] + wt.D[k]);
-        // latent step (bit-exact): z <- z * decay + (x * dt) * (e . b_dead), requantized
+        // latent step (bit-exact): z <- fma(z, decay, (x * dt) * (e . b_dead)), requantized
         const float xdt = x * dtv;
-        const float zn0 = z0 * decay + xdt * wt.dots[3];
-        const float zn1 = z1 * decay + xdt * wt.dots[4];
+        const float zn0 = state_update(z0, decay, xdt * wt.dots[3]);
+        const float zn1 = state_update(z1, decay, xdt * wt.dots[4]);
         const float q0 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn0, ls0, rls0), -448.f), 448.f);
         const float q1 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn1, ls1, rls1), -448.f), 448.f);
         qz = f32_to_e4m3(q0) | (f32_to_e4m3(q1) << 8);

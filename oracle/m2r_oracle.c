@@ -155,6 +155,16 @@ float orc_softplus_dt(float v) {
   return v;
 }
 
+/* The recurrent update of every codec, written in the reference kernels as
+ * `state * decay + (b * dt) * x` (fp4_zero_predictor_codec_v1.py:135-136,149-150;
+ * state_ppl_codec_v10.py:123-124; state_codec.py:91,149-150;
+ * state_codec_dense3.py:129).  Triton compiles with floating-point fusion
+ * enabled by default, which contracts this sum into one fused multiply-add
+ * on its first product: state = fma(state, decay, RN(RN(b * dt) * x)).  The
+ * build defines the update that way (one rounding of state * decay + the
+ * rounded input term). */
+float orc_update(float state, float decay, float input_term) { return fmaf(state, decay, input_term); }
+
 /* _stored_quantize (state_ppl_codec_v6.py:52-61) */
 int32_t orc_stored_quantize(float value, float scale, float limit) {
   float safe = scale > 0.0f ? scale : 1.0f;
@@ -179,7 +189,8 @@ static float load_param(const void* p, int f32, int64_t i) {
 
 /* ------------------------------------------------ FP16-carry control step
  * _s16_scan (mamba2_recall/state_codec.py:65-102): per row the FP32 carry is
- * state*decay + (b*dt)*x (three roundings), read out against C with D*x,
+ * fma(state, decay, RN(RN(b*dt)*x)) (the contracted update, see
+ * orc_update), read out against C with D*x,
  * then rounded to FP16.  Statistics (optional, may be NULL): for every
  * (b, h, 16-row tile of P, coordinate) the sum over tokens and tile rows of
  * |FP16 carry|, accumulated in double and rounded once.  state is
@@ -211,9 +222,7 @@ int orc_s16_step(const uint16_t* X, const uint16_t* DT, const float* A, const ui
           double out = 0.0;
           for (int n = 0; n < 128; ++n) {
             const float db = orc_f16_to_f32(bv[n]) * dtv;
-            const float pd = v[n] * decay;
-            const float bx = db * x;
-            v[n] = pd + bx;
+            v[n] = orc_update(v[n], decay, db * x);
             out += (double)v[n] * (double)orc_f16_to_f32(cv[n]);
           }
           Y[(bt * H + h) * P + p] = orc_f32_to_f16((float)out + x * dv);
@@ -331,8 +340,11 @@ int orc_state_step(int mode, int n8, int n4, int nz, const uint16_t* X, const ui
       float dtv = orc_f16_to_f32(DT[bt * H + h]) + bias;
       dtv = orc_softplus_dt(dtv);
       float decay = orc_expf(av * dtv);
-      for (int n = 0; n < n8; ++n) { prior8[n] = st8[n]; st8[n] = prior8[n] * decay + (bv[n] * dtv) * x; }
-      for (int n = 0; n < n4; ++n) { prior4[n] = st4[n]; st4[n] = prior4[n] * decay + (bv[n8 + n] * dtv) * x; }
+      for (int n = 0; n < n8; ++n) { prior8[n] = st8[n]; st8[n] = orc_update(prior8[n], decay, (bv[n] * dtv) * x); }
+      for (int n = 0; n < n4; ++n) {
+        prior4[n] = st4[n];
+        st4[n] = orc_update(prior4[n], decay, (bv[n8 + n] * dtv) * x);
+      }
       float out = 0.0f;
       for (int n = 0; n < n8; ++n) out += st8[n] * cv[n];
       for (int n = 0; n < n4; ++n) out += st4[n] * cv[n8 + n];
@@ -345,8 +357,8 @@ int orc_state_step(int mode, int n8, int n4, int nz, const uint16_t* X, const ui
         for (int n = 0; n < n4; ++n) ap += prior4[n] * pc[n8 + n];
         out += decay * (ap + z0 * pc[n8 + n4] + z1 * pc[n8 + n4 + 1]);
         Y[xoff] = orc_f32_to_f16(out);
-        z0 = z0 * decay + (x * dtv) * d5[3];
-        z1 = z1 * decay + (x * dtv) * d5[4];
+        z0 = orc_update(z0, decay, (x * dtv) * d5[3]);
+        z1 = orc_update(z1, decay, (x * dtv) * d5[4]);
         qz0 = orc_f32_to_e4m3(fminf(fmaxf(z0 / ls0, -448.0f), 448.0f));
         qz1 = orc_f32_to_e4m3(fminf(fmaxf(z1 / ls1, -448.0f), 448.0f));
         z0 = orc_e4m3_to_f32(qz0) * ls0;
@@ -445,7 +457,7 @@ int orc_dense3_step(int table_kind, const uint16_t* X, const uint16_t* DT, const
         float bv = orc_f16_to_f32(Bm[(bt * G + g) * 128 + pos[n]]);
         float cv = orc_f16_to_f32(Cm[(bt * G + g) * 128 + pos[n]]);
         if (table_kind == 1) { bv = bv * wf[n]; cv = cv * rf[n]; }
-        st[n] = st[n] * decay + (bv * dtv) * x;
+        st[n] = orc_update(st[n], decay, (bv * dtv) * x);
         out += st[n] * cv;
       }
       out += x * dv;

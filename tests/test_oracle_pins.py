@@ -397,3 +397,153 @@ def test_s16_statistics_sum_stored_carry_per_tile(oracle):
                                collect_stats=True)
     assert (st2 == cur).all()                                           # one call == sequential calls
     assert np.allclose(stats, want, rtol=1e-6)
+
+
+# ---------------------------------------------------------------- contracted update
+# The reference kernels write the update as state * decay + (b * dt) * x and
+# Triton fuses it into fma(state, decay, RN(RN(b * dt) * x)).  Each pin below
+# builds one row whose first coordinate fixes the scale (b = 0 there, so both
+# forms agree on it) and whose second coordinate is searched so that the
+# fused and the separately rounded update give different stored values; the
+# oracle must produce the fused one.  Expected values come from an exact
+# rational evaluation of the fma.
+
+from fractions import Fraction
+
+
+def _rn32(fr):
+    """Nearest binary32 to the rational `fr`, ties to even."""
+    a = np.float32(float(fr))
+    best = None
+    for c in (np.nextafter(a, np.float32(-np.inf)), a, np.nextafter(a, np.float32(np.inf))):
+        key = (abs(Fraction(float(c)) - fr), int(np.array(c, np.float32).view(np.uint32)) & 1)
+        if best is None or key < best[0]:
+            best = (key, np.float32(c))
+    return best[1]
+
+
+def _fma32(a, b, c):
+    return _rn32(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c)))
+
+
+def _round_half_away(q):
+    q = np.asarray(q, np.float64)
+    return np.sign(q) * np.floor(np.abs(q) + 0.5)
+
+
+_DT, _A = 0.3, -0.7
+
+
+def _dt_decay(oracle):
+    dt = np.float32(np.float16(_DT))
+    dtv = oracle.unary(np.array([dt], np.float32).view(np.uint32), 7).view(np.float32)[0]
+    decay = oracle.unary(np.array([np.float32(_A) * dtv], np.float32).view(np.uint32), 5).view(np.float32)[0]
+    return dtv, decay
+
+
+def _search(priors, dtv, decay, code_of, valid=lambda u: np.ones(u.shape, bool), xs=(1.0,)):
+    """(prior, b, x) whose fused and separately rounded updates give
+    different codes (both updates `valid`); the first one verified exactly."""
+    b = np.arange(0, 0x7C00, dtype=np.uint16)
+    b = np.concatenate([b, b | 0x8000]).view(np.float16).astype(np.float32)
+    bdt = (b * dtv).astype(np.float32)
+    for x in xs:
+        x = np.float32(np.float16(x))
+        bx = (bdt * x).astype(np.float32)                       # RN(RN(b * dt) * x)
+        for p in priors:
+            p = np.float32(p)
+            sep = (np.float32(p * decay) + bx).astype(np.float32)
+            fus = (np.longdouble(p) * np.longdouble(decay) + bx.astype(np.longdouble)).astype(np.float32)
+            cand = np.nonzero((code_of(fus) != code_of(sep)) & valid(fus) & valid(sep))[0]
+            for i in cand[:4]:
+                f = _fma32(p, decay, bx[i])
+                if code_of(np.array([f]))[0] != code_of(sep[i:i + 1])[0]:
+                    return p, np.float16(b[i]), x, f, sep[i]
+    raise AssertionError("no discriminating pair found")
+
+
+def _one_row_inputs(b_first, b_second, x=1.0, G=1):
+    inp = dict(x=cases.f16(np.full((1, 1, 1, 1), x)), dt=cases.f16(np.full((1, 1, 1), _DT)),
+               A=np.array([_A], np.float32), C=np.zeros((1, 1, G, 128), np.uint16),
+               D=cases.f16(np.zeros(1)), dt_bias=cases.f16(np.zeros(1)),
+               perm=np.arange(128, dtype=np.uint8)[None].repeat(G, 0))
+    Bv = np.zeros(128, np.float32)
+    Bv[0], Bv[1] = b_first, b_second
+    inp["B"] = cases.f16(Bv[None, None, None])
+    return inp
+
+
+@pytest.mark.parametrize("mode", ["stored", "legacy"])
+def test_tier_update_is_fused(oracle, mode):
+    dtv, decay = _dt_decay(oracle)
+    q0 = 113                                                  # coordinate 0 (b = 0) sets the maximum
+    for s8 in (0.25, 0.3125, 0.375, 0.4375, 0.5625, 0.625):
+        s8 = np.float32(s8)
+        u0 = np.float32(np.float32(q0 * s8) * decay)
+        den = max(np.float32(u0 / np.float32(127)), np.float32(1e-8))
+        div = np.float32(np.float16(den)) if mode == "stored" else den
+
+        def code_of(u):
+            return np.clip(_round_half_away((u.astype(np.float32) / div).astype(np.float32)), -127, 127)
+        try:   # coordinate 0 stays the maximum
+            p, b, x, f, s = _search([q * s8 for q in range(-q0 + 20, q0 - 20) if q], dtv, decay, code_of,
+                                    lambda u: np.abs(u) < u0)
+            break
+        except AssertionError:
+            continue
+    else:
+        raise AssertionError("no discriminating pair found")
+    q1 = int(round(float(p) / float(s8)))
+    lo = np.zeros((1, 1, 1, 8), np.uint8)
+    hi = np.zeros((1, 1, 1, 8), np.uint8)
+    for n, q in ((0, q0), (1, q1)):
+        byte = q & 0xFF
+        lo[..., n // 2] |= np.uint8((byte & 15) << (4 * (n % 2)))
+        hi[..., n // 2] |= np.uint8((byte >> 4) << (4 * (n % 2)))
+    st = dict(lo=lo, hi=hi, q4=np.zeros((1, 1, 1, 32), np.uint8), s8=cases.f16(np.full((1, 1, 1), s8)),
+              s4=cases.f16(np.zeros((1, 1, 1))))
+    inp = _one_row_inputs(0.0, b, x)
+    m = oracle.MODE_STORED if mode == "stored" else oracle.MODE_LEGACY
+    oracle.state_step(m, 16, 64, 48, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], inp["dt_bias"],
+                      inp["perm"], None, None, None, st)
+    byte = ((int(st["hi"][0, 0, 0, 0]) >> 4) << 4) | (int(st["lo"][0, 0, 0, 0]) >> 4)
+    got = byte - 256 * (byte > 127)
+    assert got == code_of(np.array([f]))[0] != code_of(np.array([s]))[0]
+
+
+def test_dense3_update_is_fused(oracle):
+    """Observed through the readout: with C = e_1 and D = 0, y = half(u_1)."""
+    dtv, decay = _dt_decay(oracle)
+    sc = np.float32(0.25)
+
+    def code_of(u):
+        return u.astype(np.float32).astype(np.float16).view(np.uint16).astype(np.int64)
+
+    p, b, x, f, s = _search([q * sc for q in (-4, -3, -2, -1, 1, 2, 3)], dtv, decay, code_of)
+    q = np.zeros(128, np.int64)
+    q[1] = int(round(float(p) / float(sc)))
+    codes = np.zeros((1, 1, 1, 3, 16), np.uint8)
+    for k in range(3):
+        for j in range(16):
+            codes[0, 0, 0, k, j] = sum((((q[8 * j + bit] & 7) >> k) & 1) << bit for bit in range(8))
+    st = dict(codes=codes, scales=cases.f16(np.full((1, 1, 1, 2), sc)))
+    inp = _one_row_inputs(0.0, b, x)
+    inp["C"][0, 0, 0, 1] = cases.f16(np.array([1.0]))[0]
+    y = oracle.dense3_step(0, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], inp["dt_bias"],
+                           inp["perm"], st)
+    assert int(y[0, 0, 0, 0]) == code_of(np.array([f]))[0] != code_of(np.array([s]))[0]
+
+
+def test_s16_update_is_fused(oracle):
+    dtv, decay = _dt_decay(oracle)
+
+    def code_of(u):
+        return u.astype(np.float32).astype(np.float16).view(np.uint16).astype(np.int64)
+
+    vals = np.arange(0x3800, 0x4000, 7, dtype=np.uint16).view(np.float16).astype(np.float32)
+    p, b, x, f, s = _search(vals, dtv, decay, code_of)
+    st = np.zeros((1, 1, 1, 128), np.uint16)
+    st[0, 0, 0, 1] = cases.f16(np.array([p]))[0]
+    inp = _one_row_inputs(0.0, b, x)
+    oracle.s16_step(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], inp["dt_bias"], st)
+    assert int(st[0, 0, 0, 1]) == code_of(np.array([f]))[0] != code_of(np.array([s]))[0]
