@@ -418,7 +418,7 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
 // slot k+1 is fetched while slot k computes.  Every wave builds the token
 // values it reads itself, so the only workgroup barrier is the one that
 // publishes the ridge predictor (staged once, shared by all waves).
-template <int N8, int N4, int NZ, int MODE, int WPB, int HPW>
+template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA>
 __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(WPB == 8 ? 4 : 2, 8)))
 void k_state_step(StepArgs a) {
   constexpr int W8 = N8 / 2;          // bytes per row of lo and of hi
@@ -453,7 +453,7 @@ void k_state_step(StepArgs a) {
   const int pbase = blockIdx.x * 64;
   const int nvalid = min(64, P - pbase);
   const bool valid = lane < nvalid;
-  const bool dma_tiles = a.dma_tiles != 0;   // else the slots are staged through VGPRs
+  constexpr bool dma_tiles = DMA;   // a.dma_tiles: 16-byte LDS transfers, else staging through VGPRs
   const uint16_t* s_pred = (const uint16_t*)s_pred32;
   WaveToken<N8, N4, HPW>& wt = s_wt[wave];
 
@@ -505,7 +505,7 @@ void k_state_step(StepArgs a) {
   auto slot_copy_out = [&](int hh) {
     const int row0 = slot_row0(hh);
     const uint8_t* t = s_tile[hh];
-    if (dma_tiles) {
+    if constexpr (dma_tiles) {
       field_store16<W8>(a.lo, t + O_LO, row0, nvalid, lane);
       field_store16<W8>(a.hi, t + O_HI, row0, nvalid, lane);
       field_store16<W4>(a.q4, t + O_Q4, row0, nvalid, lane);
@@ -562,7 +562,7 @@ void k_state_step(StepArgs a) {
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
   __builtin_amdgcn_sched_barrier(0);
-  if (dma_tiles) slot_dma(wave);
+  if constexpr (dma_tiles) slot_dma(wave);
   else {
     for (int k = 0; k < HPW; ++k) slot_copy_in(k * WPB + wave);
   }
@@ -691,6 +691,14 @@ void k_state_step(StepArgs a) {
 // as waves_per_block * 16 + heads_per_wave.
 static std::atomic<int> g_forced_shape{0};
 
+template <int N8, int N4, int NZ, int MODE, int WPB, int HPW>
+static void launch_shape(const StepArgs& a, dim3 grid, hipStream_t stream) {
+  if (a.dma_tiles)
+    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, WPB, HPW, true>), grid, dim3(64 * WPB), 0, stream, a);
+  else
+    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, WPB, HPW, false>), grid, dim3(64 * WPB), 0, stream, a);
+}
+
 template <int N8, int N4, int NZ, int MODE>
 static hipError_t launch_layout(const StepArgs& a, hipStream_t stream) {
   const int pblocks = (a.P + 63) / 64;
@@ -700,25 +708,21 @@ static hipError_t launch_layout(const StepArgs& a, hipStream_t stream) {
   if (forced && hpg % ((forced >> 4) * (forced & 15)) == 0) {
     const int wpb = forced >> 4, hpw = forced & 15;
     dim3 grid(pblocks, a.H / (wpb * hpw), a.B);
-    if (wpb == 1) hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 1, 1>), grid, dim3(64), 0, stream, a);
-    else if (hpw == 1) hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 4, 1>), grid, dim3(256), 0, stream, a);
-    else if (wpb == 8) hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 8, 2>), grid, dim3(512), 0, stream, a);
-    else if (hpw == 2) hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 4, 2>), grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 4, 4>), grid, dim3(256), 0, stream, a);
+    if (wpb == 1) launch_shape<N8, N4, NZ, MODE, 1, 1>(a, grid, stream);
+    else if (hpw == 1) launch_shape<N8, N4, NZ, MODE, 4, 1>(a, grid, stream);
+    else if (wpb == 8) launch_shape<N8, N4, NZ, MODE, 8, 2>(a, grid, stream);
+    else if (hpw == 2) launch_shape<N8, N4, NZ, MODE, 4, 2>(a, grid, stream);
+    else launch_shape<N8, N4, NZ, MODE, 4, 4>(a, grid, stream);
     return hipGetLastError();
   }
   if (hpg % 16 == 0 && slots >= 16LL * 512) {
-    dim3 grid(pblocks, a.H / 16, a.B);
-    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 4, 4>), grid, dim3(256), 0, stream, a);
+    launch_shape<N8, N4, NZ, MODE, 4, 4>(a, dim3(pblocks, a.H / 16, a.B), stream);
   } else if (hpg % 8 == 0 && slots >= 8LL * 512) {
-    dim3 grid(pblocks, a.H / 8, a.B);
-    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 4, 2>), grid, dim3(256), 0, stream, a);
+    launch_shape<N8, N4, NZ, MODE, 4, 2>(a, dim3(pblocks, a.H / 8, a.B), stream);
   } else if (hpg % 4 == 0) {
-    dim3 grid(pblocks, a.H / 4, a.B);
-    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 4, 1>), grid, dim3(256), 0, stream, a);
+    launch_shape<N8, N4, NZ, MODE, 4, 1>(a, dim3(pblocks, a.H / 4, a.B), stream);
   } else {
-    dim3 grid(pblocks, a.H, a.B);
-    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, 1, 1>), grid, dim3(64), 0, stream, a);
+    launch_shape<N8, N4, NZ, MODE, 1, 1>(a, dim3(pblocks, a.H, a.B), stream);
   }
   return hipGetLastError();
 }
