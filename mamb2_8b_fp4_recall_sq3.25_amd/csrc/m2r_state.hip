@@ -127,7 +127,6 @@ __device__ __forceinline__ void bytes_to_plane4(const uint32_t* c, uint32_t* wq)
 template <int N8, int N4, int HPW>
 struct WaveToken {
   static constexpr int NL = N8 + N4;
-  uint32_t raw[128];                 // B row (dwords 0..63) then C row (64..127): f16 pairs, original order
   alignas(16) float b[128];          // internal order
   alignas(16) float c[128];
   alignas(16) float cw[NL];          // readout weights of the carried coordinates: c (+ ridge correction)
@@ -213,15 +212,18 @@ __device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, con
                                                  const float (&e1v)[2], const uint16_t* s_pred, bool first,
                                                  int lane) {
   constexpr int NL = N8 + N4, F = NL + 2, RZ = next_pow2(NZ);
-  wt.raw[lane] = (uint32_t)r.bc[0] | ((uint32_t)r.bc[1] << 16);
-  wt.raw[64 + lane] = (uint32_t)r.bc[2] | ((uint32_t)r.bc[3] << 16);
 #pragma unroll
   for (int k = 0; k < HPW; ++k) wt.x[k][lane] = r.xv[k];
   const float dtv = act.x;
-  wave_sync();
-  const uint16_t* raw16 = (const uint16_t*)wt.raw;
-  const float b0 = h2f(raw16[pv0]), b1 = h2f(raw16[pv1]);
-  const float c0 = h2f(raw16[128 + pv0]), c1 = h2f(raw16[128 + pv1]);
+  // gather: raw element i of the B (C) row is half i & 1 of lane i >> 1's pair
+  const int braw = (int)((uint32_t)r.bc[0] | ((uint32_t)r.bc[1] << 16));
+  const int craw = (int)((uint32_t)r.bc[2] | ((uint32_t)r.bc[3] << 16));
+  const uint32_t bw0 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (pv0 >> 1), braw);
+  const uint32_t bw1 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (pv1 >> 1), braw);
+  const uint32_t cw0 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (pv0 >> 1), craw);
+  const uint32_t cw1 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (pv1 >> 1), craw);
+  const float b0 = h2f((uint16_t)(bw0 >> (16 * (pv0 & 1)))), b1 = h2f((uint16_t)(bw1 >> (16 * (pv1 & 1))));
+  const float c0 = h2f((uint16_t)(cw0 >> (16 * (pv0 & 1)))), c1 = h2f((uint16_t)(cw1 >> (16 * (pv1 & 1))));
   // the carried coordinates' b are finite binary16 values (|b| <= 65504)
   const bool b_lane_ok = (lane >= NL || __builtin_fabsf(b0) <= 65504.f) &&
                          (64 + lane >= NL || __builtin_fabsf(b1) <= 65504.f);
@@ -256,23 +258,39 @@ __device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, con
     const int f1 = packed_lane<N8, N4>(min(64 + lane, F - 1));
     const uint16_t* p0 = s_pred + f0 * NZ;
     const uint16_t* p1 = s_pred + f1 * NZ;
-    float acc0 = 0.f, acc1 = 0.f;
+    // every LDS read of a half is issued before its first use; four partial
+    // sums per output (readout-only value: summation order free)
+    constexpr int Q = NZ / 4, QH = (Q + 1) / 2;
+    float a0[4] = {0.f, 0.f, 0.f, 0.f}, a1[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int d = 0; d < NZ; d += 4) {
-      const f32x4 cv = *(const f32x4*)(wt.c + NL + d);
-      const uint2 w0 = *(const uint2*)(p0 + d);
-      acc0 = __builtin_fmaf(cv.x, h2f((uint16_t)w0.x), acc0);
-      acc0 = __builtin_fmaf(cv.y, h2f((uint16_t)(w0.x >> 16)), acc0);
-      acc0 = __builtin_fmaf(cv.z, h2f((uint16_t)w0.y), acc0);
-      acc0 = __builtin_fmaf(cv.w, h2f((uint16_t)(w0.y >> 16)), acc0);
-      if constexpr (F > 64) {
-        const uint2 w1 = *(const uint2*)(p1 + d);
-        acc1 = __builtin_fmaf(cv.x, h2f((uint16_t)w1.x), acc1);
-        acc1 = __builtin_fmaf(cv.y, h2f((uint16_t)(w1.x >> 16)), acc1);
-        acc1 = __builtin_fmaf(cv.z, h2f((uint16_t)w1.y), acc1);
-        acc1 = __builtin_fmaf(cv.w, h2f((uint16_t)(w1.y >> 16)), acc1);
+    for (int h = 0; h < 2; ++h) {
+      f32x4 cv[QH];
+      uint2 w0[QH], w1[QH];
+#pragma unroll
+      for (int i = 0; i < QH; ++i) {
+        const int d = 4 * min(h * QH + i, Q - 1);
+        cv[i] = *(const f32x4*)(wt.c + NL + d);
+        w0[i] = *(const uint2*)(p0 + d);
+        if constexpr (F > 64) w1[i] = *(const uint2*)(p1 + d);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < QH; ++i) {
+        if (h * QH + i >= Q) break;
+        a0[0] = __builtin_fmaf(cv[i].x, h2f((uint16_t)w0[i].x), a0[0]);
+        a0[1] = __builtin_fmaf(cv[i].y, h2f((uint16_t)(w0[i].x >> 16)), a0[1]);
+        a0[2] = __builtin_fmaf(cv[i].z, h2f((uint16_t)w0[i].y), a0[2]);
+        a0[3] = __builtin_fmaf(cv[i].w, h2f((uint16_t)(w0[i].y >> 16)), a0[3]);
+        if constexpr (F > 64) {
+          a1[0] = __builtin_fmaf(cv[i].x, h2f((uint16_t)w1[i].x), a1[0]);
+          a1[1] = __builtin_fmaf(cv[i].y, h2f((uint16_t)(w1[i].x >> 16)), a1[1]);
+          a1[2] = __builtin_fmaf(cv[i].z, h2f((uint16_t)w1[i].y), a1[2]);
+          a1[3] = __builtin_fmaf(cv[i].w, h2f((uint16_t)(w1[i].y >> 16)), a1[3]);
+        }
       }
     }
+    const float acc0 = (a0[0] + a0[1]) + (a0[2] + a0[3]);
+    const float acc1 = (a1[0] + a1[1]) + (a1[2] + a1[3]);
     if (lane < NL) wt.cw[lane] = c0 + acc0;
     if (64 + lane < NL) wt.cw[64 + lane] = c1 + acc1;
     // correction of the latent coefficients: outputs NL and NL + 1
