@@ -355,7 +355,10 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
   constexpr float BIAS = INT8 ? 128.0f : 8.0f;
   constexpr float LIM = INT8 ? 127.0f : 7.0f;
   constexpr float TOP = INT8 ? QTOP127 : QTOP7;
-  const float nb = -BIAS * sc;   // exact
+  // prior = q * s exactly, from f16(1024 + byte) (exact: 11-bit integers) as
+  // (1024 + q + bias) * s - (1024 + bias) * s: both products have at most 22
+  // significant bits, so the fused multiply-add is exact
+  const float nb = -(1024.0f + BIAS) * sc;
   float v[N];
   float amax = 0.f;
   // the shared operands of chunk i+1 are read while chunk i computes
@@ -367,10 +370,13 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
       cb_next = bdt4[i0 / 4 + 1];
       cw_next = cw4[i0 / 4 + 1];
     }
+    // the chunk's code bytes as binary16 values 1024 + byte (exponent byte 0x64)
+    const uint32_t h01 = __builtin_amdgcn_perm(0x64646464u, c[i0 / 4], 0x04010400u);
+    const uint32_t h23 = __builtin_amdgcn_perm(0x64646464u, c[i0 / 4], 0x04030402u);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      // prior = q * s exactly: (q + bias) * s - bias * s, all exact
-      const float prior = __builtin_fmaf(ubyte_f(c[i0 / 4], j), sc, nb);
+      const uint32_t hw = j < 2 ? h01 : h23;
+      const float prior = __builtin_fmaf(h2f((uint16_t)(hw >> (16 * (j & 1)))), sc, nb);
       acc = __builtin_fmaf(prior, cw[j], acc);
       float u = state_update(prior, decay, cb[j] * x);
       // ordered pin: chunk by chunk, each prior dies as soon as it is used
