@@ -144,7 +144,8 @@ int m2r_fp4_decode_g64(const uint8_t* packed, const void* f16_scales, void* out_
  * (quantize_stored_probe): q = s > 0 ? clamp(roundf(RN(v/s)), +-limit) : 0,
  * limit 7 or 127.  m2r_probe_unary applies primitive `op` (0 f32->f16 bits,
  * 1 f16->f32, 2 f32->e4m3, 3 e4m3->f32, 4 roundf, 5 exp, 6 log, 7 dt
- * softplus, 8 reciprocal of a binary16 value) to u32 words; m2r_probe_div computes RN(a/d) in the kernels'
+ * softplus, 8 reciprocal of a binary16 value, 9 e4m3->f32 and 10 f32->e4m3
+ * by the FP8 instructions) to u32 words; m2r_probe_div computes RN(a/d) in the kernels'
  * reciprocal form.  These three have no counterpart besides the first.
  */
 int m2r_probe_stored_quantize(const float* v, const void* s_f16, int32_t* q, int64_t n, int limit, hipStream_t stream);

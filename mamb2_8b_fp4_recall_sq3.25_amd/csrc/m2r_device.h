@@ -61,6 +61,25 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
   return sign | code;
 }
 
+// The same conversions by gfx950's FP8 instructions, which use the OCP
+// E4M3FN format and round to nearest even.  Decoding byte SEL of w: the
+// hardware returns a negative quiet NaN for both NaN codes, so the sign is
+// taken from the code's own bit 7 (0x7F then decodes to the positive NaN, as
+// e4m3_to_f32 gives); every other code decodes to the same bits.  Encoding a
+// pair: defined for non-NaN |x| <= 448 (callers clamp first), where it equals
+// f32_to_e4m3 bit for bit; byte 0 of the result holds a, byte 1 b.  Both
+// identities are checked on the GPU (every code; encode over a dense sweep of
+// [-448, 448]).
+template <int SEL>
+__device__ __forceinline__ float e4m3_byte_to_f32(uint32_t w) {
+  const uint32_t f = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_f32_fp8((int)w, SEL));
+  const uint32_t sign = (w << (24 - 8 * SEL)) & 0x80000000u;
+  return __builtin_bit_cast(float, (f & 0x7FFFFFFFu) | sign);
+}
+__device__ __forceinline__ uint32_t f32x2_to_e4m3(float a, float b) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xFFFFu;
+}
+
 // z / ls for the latent byte, in reciprocal form (y = RN(1/ls)).  z is first
 // clamped to +-464*ls (exact: 464 has 5 significant bits, ls 11), beyond which
 // both this and IEEE division clamp to +-448 downstream; the sign of z is then

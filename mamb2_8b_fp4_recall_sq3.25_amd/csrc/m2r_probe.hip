@@ -45,6 +45,8 @@ __global__ void k_probe_stored_quantize(const float* v, const uint16_t* s, int32
 //  6: log recipe                       out f32 bits
 //  7: softplus_dt                      out f32 bits
 //  8: reciprocal of a binary16 value   out f32 bits (input: f16 bits)
+//  9: e4m3 byte -> f32, FP8 instruction out f32 bits
+// 10: f32 -> e4m3 byte, FP8 instruction out u32 (non-NaN |x| <= 448 only)
 __global__ void k_probe_unary(const uint32_t* in, uint32_t* out, int64_t n, int op) {
   int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
@@ -61,6 +63,8 @@ __global__ void k_probe_unary(const uint32_t* in, uint32_t* out, int64_t n, int 
     case 6: r = __builtin_bit_cast(uint32_t, xlogf(f)); break;
     case 7: r = __builtin_bit_cast(uint32_t, softplus_dt(f)); break;
     case 8: r = __builtin_bit_cast(uint32_t, recip_half(h2f((uint16_t)u))); break;
+    case 9: r = __builtin_bit_cast(uint32_t, e4m3_byte_to_f32<0>(u)); break;
+    case 10: r = f32x2_to_e4m3(f, 0.0f) & 0xFFu; break;
     default: r = 0; break;
   }
   out[i] = r;
@@ -110,7 +114,7 @@ extern "C" int m2r_probe_stored_quantize(const float* v, const void* s_f16, int3
 }
 
 extern "C" int m2r_probe_unary(const uint32_t* in, uint32_t* out, int64_t n, int op, hipStream_t stream) {
-  if (n < 0 || op < 0 || op > 8) return m2r_fail("probe: bad op");
+  if (n < 0 || op < 0 || op > 10) return m2r_fail("probe: bad op");
   if (n == 0) return 0;
   hipLaunchKernelGGL(k_probe_unary, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, in, out, n, op);
   return m2r_check(hipGetLastError(), "probe unary");

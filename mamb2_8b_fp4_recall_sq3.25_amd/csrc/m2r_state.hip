@@ -639,8 +639,8 @@ void k_state_step(StepArgs a) {
       float z0 = 0.f, z1 = 0.f;
       if constexpr (RIDGE) {
         const uint32_t lat = t16[O_LAT / 2 + lane];
-        z0 = e4m3_to_f32(lat & 0xFFu) * ls0;
-        z1 = e4m3_to_f32(lat >> 8) * ls1;
+        z0 = e4m3_byte_to_f32<0>(lat) * ls0;
+        z1 = e4m3_byte_to_f32<1>(lat) * ls1;
       }
       if (!valid) {   // rows past P: finite placeholders, never stored
 #pragma unroll
@@ -678,7 +678,7 @@ void k_state_step(StepArgs a) {
         const float zn1 = state_update(z1, decay, xdt * wt.dots[4]);
         const float q0 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn0, ls0, rls0), -448.f), 448.f);
         const float q1 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn1, ls1, rls1), -448.f), 448.f);
-        qz = f32_to_e4m3(q0) | (f32_to_e4m3(q1) << 8);
+        qz = f32x2_to_e4m3(q0, q1);   // q0, q1 are clamped, never NaN (maxNum drops a NaN)
       } else {
         out = decay * acc + x * (dtv * wt.dots[0] + wt.D[k]);
       }

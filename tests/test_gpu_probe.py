@@ -67,6 +67,34 @@ def test_e4m3_conversions(oracle, device):
     assert (dev_unary(vals, 2, device) == oracle.unary(vals, 2)).all()
 
 
+def test_e4m3_fp8_instructions(oracle, device):
+    """The FP8 instructions the state step uses for the latent bytes: decode
+    of every code bit for bit (NaN codes included: 0x7F is the positive
+    NaN), encode of non-NaN |x| <= 448 against the software conversion at
+    every code, every rounding midpoint and their binary32 neighbours, every
+    61st binary32 pattern of the range, binary32 subnormals and signed
+    zeros."""
+    every8 = np.arange(256, dtype=np.uint32)
+    got = dev_unary(every8, 9, device)
+    want = oracle.unary(every8, 3)
+    assert (got == want).all(), [hex(int(c)) for c in every8[got != want]]
+    fin = every8[(every8 & 0x7F) != 0x7F]
+    f = oracle.unary(fin, 3).view(np.float32)
+    f = np.sort(np.unique(f))
+    mids = ((f[:-1].astype(np.float64) + f[1:]) / 2).astype(np.float32)
+    near = np.concatenate([f, mids]).view(np.uint32).astype(np.int64)
+    near = np.concatenate([near + d for d in range(-4, 5)])
+    near = near[(near >= 0) & (near < 2 ** 32)].astype(np.uint32)
+    sweep = np.arange(0, 0x43E00001, 61, dtype=np.uint32)
+    vals = np.concatenate([near, sweep, sweep | 0x80000000, np.arange(1, 4096, dtype=np.uint32),
+                           np.array([0, 0x80000000, 0x43E00000, 0xC3E00000], np.uint32)])
+    vals = vals[np.abs(vals.view(np.float32)) <= 448.0]
+    got = dev_unary(vals, 10, device)
+    want = oracle.unary(vals, 2)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"{bad.size} mismatches, first at 0x{int(vals[bad[0]]):08x}"
+
+
 def test_round_and_transcendentals(oracle, device):
     rng = np.random.default_rng(4)
     vals = np.concatenate([floats_sample(rng, 1 << 20),
