@@ -529,13 +529,21 @@ void k_state_step(StepArgs a) {
   auto slot_copy_out = [&](int hh) {
     const int row0 = slot_row0(hh);
     const uint8_t* t = s_tile[hh];
-    if constexpr (dma_tiles) {
-      field_store16<W8>(a.lo, t + O_LO, row0, nvalid, lane);
-      field_store16<W8>(a.hi, t + O_HI, row0, nvalid, lane);
-      field_store16<W4>(a.q4, t + O_Q4, row0, nvalid, lane);
-      field_store16<2>((uint8_t*)a.s8, t + O_S8, row0, nvalid, lane);
-      field_store16<2>((uint8_t*)a.s4, t + O_S4, row0, nvalid, lane);
-      if constexpr (RIDGE) field_store16<2>(a.latent, t + O_LAT, row0, nvalid, lane);
+    if constexpr (dma_tiles) {   // every LDS read of the slot, then its stores
+      constexpr int C8W = chunk_ops(W8), C4W = chunk_ops(W4), C2 = chunk_ops(2);
+      u32x4 v[SLOT_DMA];
+      field_read16<W8>(t + O_LO, lane, v);
+      field_read16<W8>(t + O_HI, lane, v + C8W);
+      field_read16<W4>(t + O_Q4, lane, v + 2 * C8W);
+      field_read16<2>(t + O_S8, lane, v + 2 * C8W + C4W);
+      field_read16<2>(t + O_S4, lane, v + 2 * C8W + C4W + C2);
+      if constexpr (RIDGE) field_read16<2>(t + O_LAT, lane, v + 2 * C8W + C4W + 2 * C2);
+      field_write16<W8>(a.lo, v, row0, nvalid, lane);
+      field_write16<W8>(a.hi, v + C8W, row0, nvalid, lane);
+      field_write16<W4>(a.q4, v + 2 * C8W, row0, nvalid, lane);
+      field_write16<2>((uint8_t*)a.s8, v + 2 * C8W + C4W, row0, nvalid, lane);
+      field_write16<2>((uint8_t*)a.s4, v + 2 * C8W + C4W + C2, row0, nvalid, lane);
+      if constexpr (RIDGE) field_write16<2>(a.latent, v + 2 * C8W + C4W + 2 * C2, row0, nvalid, lane);
       return;
     }
     wave_copy_out<W8>(a.lo, t + O_LO, row0, nvalid, lane);
@@ -602,8 +610,10 @@ void k_state_step(StepArgs a) {
     }
     ls0 = h2f((uint16_t)(ls_w & 0xFFFFu));
     ls1 = h2f((uint16_t)(ls_w >> 16));
-    rls0 = 1.0f / ls0;   // correctly rounded reciprocals
-    rls1 = 1.0f / ls1;
+    // correctly rounded reciprocals: the latent scales are positive finite
+    // binary16 values (the statics contract every caller validates)
+    rls0 = recip_half(ls0);
+    rls1 = recip_half(ls1);
   }
 
   for (int t = 0; t < L; ++t) {

@@ -18,7 +18,7 @@ __device__ __forceinline__ float load_param(const void* p, int f32, int i) {
 // levels 0..5 of a 64-lane wave.  Levels 0-1 use quad_perm DPP; levels 2-3
 // use half-row / row mirrors, which pair each lane with a lane of the other
 // aligned half-block (equal to the xor partner's value once every lane of a
-// block holds the block sum); levels 4-5 use ds_bpermute lane exchanges.
+// block holds the block sum); levels 4-5 use the row-swap permutes.
 // IEEE addition is commutative, so all lanes of a pair obtain identical bits.
 template <int LEVEL>
 __device__ __forceinline__ float butterfly_add(float v) {
@@ -27,8 +27,17 @@ __device__ __forceinline__ float butterfly_add(float v) {
   if constexpr (LEVEL == 1) return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, false));
   if constexpr (LEVEL == 2) return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x141, 0xF, 0xF, false));
   if constexpr (LEVEL == 3) return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x140, 0xF, 0xF, false));
-  if constexpr (LEVEL == 4) return v + __shfl_xor(v, 16, 64);
-  if constexpr (LEVEL == 5) return v + __shfl_xor(v, 32, 64);
+  // levels 4-5: v_permlane16_swap / v_permlane32_swap of two copies of v
+  // leave, in every lane, the values of the lower and the upper half-block
+  // of its aligned 32- / 64-lane block; their sum is v + v[lane ^ 16 (32)]
+  if constexpr (LEVEL == 4) {
+    const auto r = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
+    return __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+  }
+  if constexpr (LEVEL == 5) {
+    const auto r = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
+    return __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+  }
   return v;
 }
 
@@ -142,20 +151,27 @@ __device__ __forceinline__ void field_dma16(uint8_t* lds, const uint8_t* g, int 
 // staying dirty in the issuing XCD's L2 until the end-of-kernel writeback.
 constexpr int STORE_THROUGH = 16 | 2;
 
-// LDS -> global: all LDS reads first, then unguarded 16-byte buffer stores
-// whose range check drops everything past nvalid * W bytes (whole chunks,
-// under the same alignment requirements).  Issues exactly chunk_ops(W)
-// store instructions.
+// LDS -> global in two halves, so that a caller reads every field of a slot
+// before its first store (the compiler does not move LDS reads above a
+// buffer store, and each read-wait-store round trip is an LDS latency):
+// field_read16 reads the chunk_ops(W) 16-byte chunks of lane `lane`;
+// field_write16 stores them with unguarded buffer stores whose range check
+// drops everything past nvalid * W bytes (whole chunks, under the same
+// alignment requirements) and issues exactly chunk_ops(W) store
+// instructions.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 template <int W>
-__device__ __forceinline__ void field_store16(uint8_t* g, const uint8_t* lds, int row0, int nvalid, int lane) {
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  constexpr int FB = 64 * W, NC = chunk_ops(W);
+__device__ __forceinline__ void field_read16(const uint8_t* lds, int lane, u32x4* v) {
+  constexpr int FB = 64 * W;
+#pragma unroll
+  for (int k = 0; k < chunk_ops(W); ++k) v[k] = *(const u32x4*)(lds + min(k * 1024 + 16 * lane, FB - 16));
+}
+template <int W>
+__device__ __forceinline__ void field_write16(uint8_t* g, const u32x4* v, int row0, int nvalid, int lane) {
   const __amdgpu_buffer_rsrc_t rsrc = raw_buffer(g + (size_t)row0 * W, nvalid * W);
-  u32x4 v[NC];
 #pragma unroll
-  for (int k = 0; k < NC; ++k) v[k] = *(const u32x4*)(lds + min(k * 1024 + 16 * lane, FB - 16));
-#pragma unroll
-  for (int k = 0; k < NC; ++k) __builtin_amdgcn_raw_buffer_store_b128(v[k], rsrc, k * 1024 + 16 * lane, 0, STORE_THROUGH);
+  for (int k = 0; k < chunk_ops(W); ++k)
+    __builtin_amdgcn_raw_buffer_store_b128(v[k], rsrc, k * 1024 + 16 * lane, 0, STORE_THROUGH);
 }
 
 // LDS DMA of one SoA field of a 64-row slot: 64 * W bytes at g + row0 * W
