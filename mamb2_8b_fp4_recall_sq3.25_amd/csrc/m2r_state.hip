@@ -190,6 +190,19 @@ __device__ __forceinline__ float2 wave_dt_activation(const WaveRaw<HPW>& r, floa
   return dt_activation(h2f(r.dt) + db, Ah);
 }
 
+// Wave priority from the number of head slots the wave still has to step
+// in this token (4 or more: highest).  Two workgroups share each CU, so each
+// SIMD runs two waves; its issue arbitration otherwise favours the older
+// wave, which runs ahead while the younger one finishes alone, a slot or more
+// later, with no second wave to hide its latencies.  With the priority the
+// wave that is behind wins the arbitration until it has caught up.
+__device__ __forceinline__ void wave_priority_by_slots_left(int left) {
+  if (left >= 4) __builtin_amdgcn_s_setprio(3);
+  else if (left == 3) __builtin_amdgcn_s_setprio(2);
+  else if (left == 2) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+}
+
 // Orders a wave's LDS accesses across its lanes (the wave's own regions
 // need no workgroup barrier).
 __device__ __forceinline__ void wave_sync() {
@@ -442,7 +455,7 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
 // slot k+1 is fetched while slot k computes.  Every wave builds the token
 // values it reads itself, so the only workgroup barrier is the one that
 // publishes the ridge predictor (staged once, shared by all waves).
-template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA>
+template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE>
 __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(WPB == 8 ? 4 : 2, 8)))
 void k_state_step(StepArgs a) {
   constexpr int W8 = N8 / 2;          // bytes per row of lo and of hi
@@ -472,7 +485,10 @@ void k_state_step(StepArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: per-wave values in SGPRs
   const int b = blockIdx.z;
   const int h0 = blockIdx.y * NH;
-  const int H = a.H, P = a.P, L = a.L;
+  const int H = a.H, P = a.P;
+  // ONE: the one-token (decode) instance, with a compile-time token count:
+  // no token loop, prefetch or loop-carried state
+  const int L = ONE ? 1 : a.L;
   const int g = h0 / (H / a.G);
   const int pbase = blockIdx.x * 64;
   const int nvalid = min(64, P - pbase);
@@ -504,9 +520,9 @@ void k_state_step(StepArgs a) {
   // k-1's y store (one store instruction), slot k-2's state copy-out when
   // the first token is also the last (copy-outs trail by one slot), and slot
   // k+1's transfers.
-  auto slot_fetch_next_and_wait = [&](int k) {
+  auto slot_fetch_next_and_wait = [&](int k, int hh) {
     const bool more = dma_tiles && k + 1 < HPW;
-    if (more) slot_dma((k + 1) * WPB + wave);
+    if (more) slot_dma(hh + WPB);
     const bool copy = L == 1 && k >= 2;
     if (k == 0) {
       if (more) wait_vmcnt<SLOT_DMA>(); else wait_vmcnt<0>();
@@ -626,9 +642,16 @@ void k_state_step(StepArgs a) {
     wave_token_build<N8, N4, NZ, MODE, HPW>(wt, cur, act, pv0, pv1, e0v, e1v, s_pred, t == 0, lane);
 
     for (int k = 0; k < HPW; ++k) {
-      const int hh = k * WPB + wave;
+      // The slot's head index, opaque to the optimizer: every address and
+      // buffer descriptor derived from it is then built here, where scalar
+      // work overlaps the other waves' vector work, instead of being hoisted
+      // out of the token loop for all slots at once (more scalar registers
+      // than exist: spills, and a long serial setup before the first token).
+      int hh = k * WPB + wave;
+      asm volatile("" : "+s"(hh));
       const int h = h0 + hh;
-      if (t == 0) slot_fetch_next_and_wait(k);
+      wave_priority_by_slots_left(HPW - k);
+      if (t == 0) slot_fetch_next_and_wait(k, hh);
       if (t == L - 1 && k > 0) slot_copy_out(hh - WPB);   // the previous slot's state
       uint8_t* tile = s_tile[hh];
       uint16_t* t16 = (uint16_t*)tile;
@@ -727,10 +750,13 @@ static std::atomic<int> g_forced_shape{0};
 
 template <int N8, int N4, int NZ, int MODE, int WPB, int HPW>
 static void launch_shape(const StepArgs& a, dim3 grid, hipStream_t stream) {
-  if (a.dma_tiles)
-    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, WPB, HPW, true>), grid, dim3(64 * WPB), 0, stream, a);
-  else
-    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, WPB, HPW, false>), grid, dim3(64 * WPB), 0, stream, a);
+  if (a.dma_tiles && a.L == 1) {
+    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, WPB, HPW, true, true>), grid, dim3(64 * WPB), 0, stream, a);
+  } else if (a.dma_tiles) {
+    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, WPB, HPW, true, false>), grid, dim3(64 * WPB), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, WPB, HPW, false, false>), grid, dim3(64 * WPB), 0, stream, a);
+  }
 }
 
 template <int N8, int N4, int NZ, int MODE>
