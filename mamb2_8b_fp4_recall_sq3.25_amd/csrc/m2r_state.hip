@@ -142,6 +142,17 @@ struct WaveToken {
   float dots[5];
 };
 
+// Per-token values of the ridge codec that the waves of a workgroup share
+// when they split the predictor correction (four or more waves): the readout
+// weights of the carried coordinates (c + correction), the latent
+// coefficients' corrections and the dead-tier dot products e.c and e.b, each
+// written by the wave that computes it and read after a workgroup barrier.
+template <int NL>
+struct GroupToken {
+  alignas(16) float cw[NL];
+  float ec[2], lc[2], eb[2];
+};
+
 // Inputs of one token that a wave loads one token ahead: its lane's two f16
 // of the group's B and of its C row, x of its rows in every head slot, and
 // for lanes < HPW the dt and dt_bias bits of head slot `lane`.  Nothing is
@@ -219,11 +230,11 @@ __device__ __forceinline__ void wave_sync() {
 // the ridge codec, the correction of the readout weights by the static
 // predictor and the dead-tier dot products.  `first`: the first token, whose
 // ridge correction waits for the workgroup's predictor transfer.
-template <int N8, int N4, int NZ, int MODE, int HPW>
-__device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, const WaveRaw<HPW>& r, float2 act,
-                                                 int pv0, int pv1, const float (&e0v)[2],
-                                                 const float (&e1v)[2], const uint16_t* s_pred, bool first,
-                                                 int lane) {
+template <int N8, int N4, int NZ, int MODE, int WPB, int HPW>
+__device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, GroupToken<N8 + N4>& gt,
+                                                 const WaveRaw<HPW>& r, float2 act, int pv0, int pv1,
+                                                 const float (&e0v)[2], const float (&e1v)[2],
+                                                 const uint16_t* s_pred, bool first, int lane, int wave) {
   constexpr int NL = N8 + N4, F = NL + 2, RZ = next_pow2(NZ);
 #pragma unroll
   for (int k = 0; k < HPW; ++k) wt.x[k][lane] = r.xv[k];
@@ -264,6 +275,62 @@ __device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, con
   } else {
     wave_sync();                 // the dead-tier c and b are read across lanes below
     if (first) __syncthreads();  // every wave's share of the predictor transfer has landed
+    if constexpr (WPB >= 4) {
+      // Split across the workgroup: wave w computes the corrections of
+      // internal outputs [w FW, (w + 1) FW), lanes l and l + 32 the two halves
+      // of the dead-tier sum of output w FW + (l & 31), and dead-tier tree w
+      // (w < 4); readout-only values, except the trees e.b (canonical, exact).
+      constexpr int FW = 8 * ((F + 8 * WPB - 1) / (8 * WPB));
+      static_assert(FW <= 32, "two lane halves per output");
+      const int jo = wave * FW + (lane & 31);
+      const uint16_t* pr = s_pred + packed_lane<N8, N4>(min(jo, F - 1)) * NZ;
+      constexpr int Q = NZ / 4, QH = (Q + 1) / 2;
+      const int qb = (lane >> 5) * QH;
+      f32x4 cv[QH];
+      uint2 w[QH];
+#pragma unroll
+      for (int i = 0; i < QH; ++i) {
+        const int q = min(qb + i, Q - 1);
+        cv[i] = *(const f32x4*)(wt.c + NL + 4 * q);
+        w[i] = *(const uint2*)(pr + 4 * q);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      float a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < QH; ++i) {
+        f32x4 c4 = cv[i];
+        if (Q % 2 && i == QH - 1 && qb + i >= Q) c4 = f32x4{0.f, 0.f, 0.f, 0.f};   // the upper half's extra quad
+        a[0] = __builtin_fmaf(c4.x, h2f((uint16_t)w[i].x), a[0]);
+        a[1] = __builtin_fmaf(c4.y, h2f((uint16_t)(w[i].x >> 16)), a[1]);
+        a[2] = __builtin_fmaf(c4.z, h2f((uint16_t)w[i].y), a[2]);
+        a[3] = __builtin_fmaf(c4.w, h2f((uint16_t)(w[i].y >> 16)), a[3]);
+      }
+      const int part = __builtin_bit_cast(int, (a[0] + a[1]) + (a[2] + a[3]));
+      const auto sw = __builtin_amdgcn_permlane32_swap(part, part, false, false);
+      const float corr = __builtin_bit_cast(float, (int)sw[0]) + __builtin_bit_cast(float, (int)sw[1]);
+      if (lane < FW && jo < F) {
+        if (jo < NL) gt.cw[jo] = wt.c[jo] + corr;
+        else gt.lc[jo - NL] = corr;
+      }
+      if (wave < 4) {   // tree `wave`: e0.c, e1.c, e0.b, e1.b
+        const float* src = wave < 2 ? wt.c : wt.b;
+        const float (&e)[2] = (wave & 1) ? e1v : e0v;
+        float v[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int d0 = (RZ == 128) ? 2 * lane + j : lane;
+          const bool in = (RZ == 128 || j == 0) && d0 < NZ;
+          v[j] = in ? e[j] * src[NL + (in ? d0 : 0)] : 0.f;
+        }
+        const float tsum = wave_pair_tree<RZ>(v[0], v[1]);
+        if (lane == 0) {
+          if (wave < 2) gt.ec[wave] = tsum;
+          else gt.eb[wave - 2] = tsum;
+        }
+      }
+      __syncthreads();   // the workgroup's shared token values are complete
+      return;
+    }
     // corr[j] = sum_d C[dead d] * pred[g, row(j), d] for output j = lane and
     // lane + 64 (rows past F recompute row F-1, unused); the dead-tier C is a
     // wave-uniform operand, the predictor row a per-lane one
@@ -477,6 +544,10 @@ void k_state_step(StepArgs a) {
   static_assert(TILE % 16 == 0, "tiles stay 16-byte aligned");
 
   __shared__ __align__(16) WaveToken<N8, N4, HPW> s_wt[WPB];
+  // split ridge correction: one record per token parity (a wave may build
+  // token t + 1 while another still reads token t)
+  constexpr bool SPLIT = RIDGE && WPB >= 4;
+  __shared__ __align__(16) GroupToken<NL> s_gt[SPLIT && !ONE ? 2 : 1];
   __shared__ __align__(16) uint32_t s_pred32[PRED_OPS * 64];
   __shared__ __align__(16) uint8_t s_tile[NH][TILE];
 
@@ -639,7 +710,14 @@ void k_state_step(StepArgs a) {
       wave_load_dt<WPB, HPW>(a, raw, bt + 1, h0, lane, wave);
       wave_load_rest<WPB, HPW>(a, raw, bt + 1, g, h0, pbase, lane, wave);
     }
-    wave_token_build<N8, N4, NZ, MODE, HPW>(wt, cur, act, pv0, pv1, e0v, e1v, s_pred, t == 0, lane);
+    GroupToken<NL>& gt = s_gt[SPLIT && !ONE ? (t & 1) : 0];
+    wave_token_build<N8, N4, NZ, MODE, WPB, HPW>(wt, gt, cur, act, pv0, pv1, e0v, e1v, s_pred, t == 0, lane, wave);
+    // readout weights and dead-tier dot products of this token
+    const float* cwt = SPLIT ? gt.cw : wt.cw;
+    const float dot1 = SPLIT ? gt.ec[0] + gt.lc[0] : wt.dots[1];
+    const float dot2 = SPLIT ? gt.ec[1] + gt.lc[1] : wt.dots[2];
+    const float dot3 = SPLIT ? gt.eb[0] : wt.dots[3];
+    const float dot4 = SPLIT ? gt.eb[1] : wt.dots[4];
 
     for (int k = 0; k < HPW; ++k) {
       // The slot's head index, opaque to the optimizer: every address and
@@ -691,7 +769,7 @@ void k_state_step(StepArgs a) {
       // (each tier is requantized before the next is updated, so only one
       // tier's updated values are live at a time)
       const f32x4* bdt4 = (const f32x4*)wt.bdt[k];
-      const f32x4* cw4 = (const f32x4*)wt.cw;
+      const f32x4* cw4 = (const f32x4*)cwt;
       float acc = 0.f;
       const bool ok8 = base_ok && __builtin_fabsf(sc8) <= 65504.f;
       const bool ok4 = base_ok && __builtin_fabsf(sc4) <= 65504.f;
@@ -704,11 +782,11 @@ void k_state_step(StepArgs a) {
       float out;
       uint32_t qz = 0;
       if constexpr (RIDGE) {
-        out = decay * (acc + z0 * wt.dots[1] + z1 * wt.dots[2]) + x * (dtv * wt.dots[0] + wt.D[k]);
+        out = decay * (acc + z0 * dot1 + z1 * dot2) + x * (dtv * wt.dots[0] + wt.D[k]);
         // latent step (bit-exact): z <- fma(z, decay, (x * dt) * (e . b_dead)), requantized
         const float xdt = x * dtv;
-        const float zn0 = state_update(z0, decay, xdt * wt.dots[3]);
-        const float zn1 = state_update(z1, decay, xdt * wt.dots[4]);
+        const float zn0 = state_update(z0, decay, xdt * dot3);
+        const float zn1 = state_update(z1, decay, xdt * dot4);
         const float q0 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn0, ls0, rls0), -448.f), 448.f);
         const float q1 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn1, ls1, rls1), -448.f), 448.f);
         qz = f32x2_to_e4m3(q0, q1);   // q0, q1 are clamped, never NaN (maxNum drops a NaN)
