@@ -53,7 +53,8 @@ struct StepArgs {
   uint16_t* y;             // f16 [B, L, H, P]
   int B, L, H, P, G;
   int d_f32, db_f32;
-  int dma_tiles;           // P % 8 == 0 and 16-byte aligned state fields: 16-byte LDS transfers
+  int dma_tiles;           // P % 8 == 0, 16-byte aligned state fields and predictor, 4-byte aligned
+                           // B and C: 16-byte LDS transfers and paired B/C loads
 };
 
 // Carried coordinates are held in an internal lane order that makes the
@@ -177,14 +178,23 @@ __device__ __forceinline__ void wave_load_dt(const StepArgs& a, WaveRaw<HPW>& r,
   r.db_lo = db[a.db_f32 ? 2 * h : h];
   r.db_hi = db[a.db_f32 ? 2 * h + 1 : h];
 }
-template <int WPB, int HPW>
+// ALIGNED: B and C are 4-byte aligned, so a lane's pair is one load each.
+template <int WPB, int HPW, bool ALIGNED>
 __device__ __forceinline__ void wave_load_rest(const StepArgs& a, WaveRaw<HPW>& r, int bt, int g, int h0,
                                                int pbase, int lane, int wave) {
   const size_t row = ((size_t)bt * a.G + g) * 128 + 2 * lane;
-  r.bc[0] = a.Bm[row];
-  r.bc[1] = a.Bm[row + 1];
-  r.bc[2] = a.Cm[row];
-  r.bc[3] = a.Cm[row + 1];
+  if constexpr (ALIGNED) {
+    const uint32_t bp = *(const uint32_t*)(a.Bm + row), cp = *(const uint32_t*)(a.Cm + row);
+    r.bc[0] = (uint16_t)bp;
+    r.bc[1] = (uint16_t)(bp >> 16);
+    r.bc[2] = (uint16_t)cp;
+    r.bc[3] = (uint16_t)(cp >> 16);
+  } else {
+    r.bc[0] = a.Bm[row];
+    r.bc[1] = a.Bm[row + 1];
+    r.bc[2] = a.Cm[row];
+    r.bc[3] = a.Cm[row + 1];
+  }
   const int p = min(pbase + lane, a.P - 1);   // rows past P read row P-1 (never stored)
 #pragma unroll
   for (int k = 0; k < HPW; ++k) {
@@ -538,6 +548,8 @@ void k_state_step(StepArgs a) {
   constexpr int C8 = N8 / 4, C4 = N4 / 4;   // carried code words (4 biased bytes each)
   constexpr int PRED_DW = RIDGE ? F * NZ / 2 : 1;   // F*NZ is even for every layout
   constexpr int PRED_OPS = (PRED_DW + 63) / 64;     // 64-dword transfers of the predictor
+  constexpr int PRED_OPS16 = (PRED_DW + 255) / 256; // 1 KiB transfers (aligned predictor)
+  static_assert(!RIDGE || (F * NZ * 2) % 16 == 0, "a group's predictor is a whole number of 16-byte chunks");
   static_assert(N8 % 4 == 0 && N4 % 4 == 0 && N8 > 0 && N4 > 0, "tier widths must be positive multiples of 4");
   static_assert(NZ % 4 == 0 && NL + NZ == 128, "dead tier read as 4-wide vectors");
   static_assert(!RIDGE || (F * NZ) % 2 == 0, "predictor staged as dwords");
@@ -548,7 +560,7 @@ void k_state_step(StepArgs a) {
   // token t + 1 while another still reads token t)
   constexpr bool SPLIT = RIDGE && WPB >= 4;
   __shared__ __align__(16) GroupToken<NL> s_gt[SPLIT && !ONE ? 2 : 1];
-  __shared__ __align__(16) uint32_t s_pred32[PRED_OPS * 64];
+  __shared__ __align__(16) uint32_t s_pred32[DMA ? PRED_OPS16 * 256 : PRED_OPS * 64];
   __shared__ __align__(16) uint8_t s_tile[NH][TILE];
 
   const int tid = threadIdx.x;
@@ -653,10 +665,15 @@ void k_state_step(StepArgs a) {
   const float Ah = a.A[hl];
   if constexpr (RIDGE) {
     const uint8_t* pg = (const uint8_t*)(a.pred + (size_t)g * F * NZ);
-    for (int j = wave; j < PRED_OPS; j += WPB) lds_dma_b32(pg + 4 * min(j * 64 + lane, PRED_DW - 1),
-                                                           lds_address(s_pred32 + 64 * j));
+    if constexpr (DMA) {   // 16-byte chunks; lanes past the end re-read the last one
+      for (int j = wave; j < PRED_OPS16; j += WPB)
+        lds_dma_b128(pg + 16 * min(j * 64 + lane, PRED_DW / 4 - 1), lds_address(s_pred32 + 256 * j));
+    } else {
+      for (int j = wave; j < PRED_OPS; j += WPB)
+        lds_dma_b32(pg + 4 * min(j * 64 + lane, PRED_DW - 1), lds_address(s_pred32 + 64 * j));
+    }
   }
-  wave_load_rest<WPB, HPW>(a, raw, b * L, g, h0, pbase, lane, wave);
+  wave_load_rest<WPB, HPW, DMA>(a, raw, b * L, g, h0, pbase, lane, wave);
   // statics, kept as loaded bits until the first token's full wait (a
   // conversion here would make the compiler wait for them before the dt
   // activation)
@@ -671,7 +688,8 @@ void k_state_step(StepArgs a) {
       const int d0 = (RZ == 128) ? 2 * lane + j : lane;
       basis_w[j] = ((const uint32_t*)a.basis)[g * NZ + min(d0, NZ - 1)];   // unused past NZ
     }
-    ls_w = (uint32_t)a.lscale[g * 2] | ((uint32_t)a.lscale[g * 2 + 1] << 16);
+    ls_w = DMA ? *(const uint32_t*)(a.lscale + g * 2)
+               : (uint32_t)a.lscale[g * 2] | ((uint32_t)a.lscale[g * 2 + 1] << 16);
   }
   // dt activation of the first token while the other loads are in flight
   float2 act = wave_dt_activation<HPW>(raw, Ah, a.db_f32);
@@ -708,7 +726,7 @@ void k_state_step(StepArgs a) {
     const WaveRaw<HPW> cur = raw;
     if (t + 1 < L) {   // prefetch
       wave_load_dt<WPB, HPW>(a, raw, bt + 1, h0, lane, wave);
-      wave_load_rest<WPB, HPW>(a, raw, bt + 1, g, h0, pbase, lane, wave);
+      wave_load_rest<WPB, HPW, DMA>(a, raw, bt + 1, g, h0, pbase, lane, wave);
     }
     GroupToken<NL>& gt = s_gt[SPLIT && !ONE ? (t & 1) : 0];
     wave_token_build<N8, N4, NZ, MODE, WPB, HPW>(wt, gt, cur, act, pv0, pv1, e0v, e1v, s_pred, t == 0, lane, wave);
@@ -902,10 +920,15 @@ using namespace m2r;
 // 16-byte LDS transfers need every slot's field start and valid length to be
 // multiples of 16 bytes: P % 8 == 0 (fields are 2 to 38 bytes wide, all even)
 // and 16-byte aligned field arrays.
-static int dma_tiles_ok(int64_t P, std::initializer_list<const void*> fields) {
+// The transfer-friendly instances need P % 8 == 0, 16-byte aligned state
+// fields (and ridge predictor), and 4-byte aligned B, C (and latent scales).
+static int dma_tiles_ok(int64_t P, std::initializer_list<const void*> align16,
+                        std::initializer_list<const void*> align4) {
   if (P % 8) return 0;
-  for (const void* f : fields)
+  for (const void* f : align16)
     if (f && ((uintptr_t)f & 15)) return 0;
+  for (const void* f : align4)
+    if (f && ((uintptr_t)f & 3)) return 0;
   return 1;
 }
 
@@ -928,7 +951,7 @@ extern "C" int m2r_state_step_ridge(const void* x, const void* dt, const float* 
   d.args = StepArgs{(const uint16_t*)x, (const uint16_t*)dt, A, (const uint16_t*)B, (const uint16_t*)C, D, dt_bias,
                     perm, (const uint16_t*)basis, (const uint16_t*)lscale, (const uint16_t*)pred, lo, hi, q4, latent,
                     (uint16_t*)s8, (uint16_t*)s4, (uint16_t*)y, (int)batch, (int)L, (int)H, (int)P, (int)G,
-                    d_is_f32, db_is_f32, dma_tiles_ok(P, {lo, hi, q4, latent, s8, s4})};
+                    d_is_f32, db_is_f32, dma_tiles_ok(P, {lo, hi, q4, latent, s8, s4, pred}, {B, C, lscale})};
   d.n8_ = n8; d.n4_ = n4; d.nz_ = nz;
   hipError_t e = dispatch_ridge(d, stream);
   if (e == hipErrorInvalidValue) return m2r_fail("ridge step: unsupported tier layout");
@@ -945,7 +968,7 @@ extern "C" int m2r_state_step_tier(const void* x, const void* dt, const float* A
   d.args = StepArgs{(const uint16_t*)x, (const uint16_t*)dt, A, (const uint16_t*)B, (const uint16_t*)C, D, dt_bias,
                     perm, nullptr, nullptr, nullptr, lo, hi, q4, nullptr, (uint16_t*)s8, (uint16_t*)s4,
                     (uint16_t*)y, (int)batch, (int)L, (int)H, (int)P, (int)G, d_is_f32, db_is_f32,
-                    dma_tiles_ok(P, {lo, hi, q4, s8, s4})};
+                    dma_tiles_ok(P, {lo, hi, q4, s8, s4}, {B, C})};
   d.n8_ = n8; d.n4_ = n4; d.nz_ = nz;
   hipError_t e = dispatch_tier(d, stream);
   if (e == hipErrorInvalidValue) return m2r_fail("tier step: unsupported tier layout");
@@ -971,6 +994,6 @@ extern "C" int m2r_state_step_legacy(const void* x, const void* dt, const float*
   StepArgs args{(const uint16_t*)x, (const uint16_t*)dt, A, (const uint16_t*)B, (const uint16_t*)C, D, dt_bias,
                 perm, nullptr, nullptr, nullptr, lo, hi, q4, nullptr, (uint16_t*)s8, (uint16_t*)s4,
                 (uint16_t*)y, (int)batch, (int)L, (int)H, (int)P, (int)G, d_is_f32, db_is_f32,
-                dma_tiles_ok(P, {lo, hi, q4, s8, s4})};
+                dma_tiles_ok(P, {lo, hi, q4, s8, s4}, {B, C})};
   return m2r_check(launch_layout<16, 64, 48, MODE_LEGACY>(args, stream), "legacy step launch");
 }
