@@ -596,24 +596,20 @@ void k_state_step(StepArgs a) {
   };
   constexpr int COPY_OPS = SLOT_DMA;   // one store instruction per transfer chunk
   static_assert(SLOT_DMA + COPY_OPS + 1 <= 63, "vmcnt range");
-  // At the first token, before slot k is read: issue slot k+1's transfers,
-  // then wait until only the operations issued after slot k's transfers are
-  // outstanding (vector memory operations complete in program order), so no
-  // wait covers a store's write acknowledgement.  Those operations are slot
-  // k-1's y store (one store instruction), slot k-2's state copy-out when
-  // the first token is also the last (copy-outs trail by one slot), and slot
-  // k+1's transfers.
-  auto slot_fetch_next_and_wait = [&](int k, int hh) {
-    const bool more = dma_tiles && k + 1 < HPW;
-    if (more) slot_dma(hh + WPB);
+  // At the first token, before slot k is read: wait until only the
+  // operations issued after slot k's transfers are outstanding (vector memory
+  // operations complete in program order), so no wait covers a store's write
+  // acknowledgement.  Slot k's transfers are issued in the middle of slot
+  // k-1 (slot 0's by the prologue); after them come slot k-2's state
+  // copy-out when the first token is also the last (copy-outs trail by one
+  // slot, also issued mid-slot) and slot k-1's y store (one store
+  // instruction).  (Loads the compiler issues in between, the next token's
+  // prefetch, only make a wait longer.)
+  auto slot_wait = [&](int k) {
     const bool copy = L == 1 && k >= 2;
-    if (k == 0) {
-      if (more) wait_vmcnt<SLOT_DMA>(); else wait_vmcnt<0>();
-    } else if (more) {
-      if (copy) wait_vmcnt<SLOT_DMA + COPY_OPS + 1>(); else wait_vmcnt<SLOT_DMA + 1>();
-    } else {
-      if (copy) wait_vmcnt<COPY_OPS + 1>(); else wait_vmcnt<1>();
-    }
+    if (k == 0) wait_vmcnt<0>();
+    else if (copy) wait_vmcnt<COPY_OPS + 1>();
+    else wait_vmcnt<1>();
   };
   auto slot_copy_in = [&](int hh) {   // other geometries: 16-bit transfers through VGPRs
     const int row0 = slot_row0(hh);
@@ -747,8 +743,7 @@ void k_state_step(StepArgs a) {
       asm volatile("" : "+s"(hh));
       const int h = h0 + hh;
       wave_priority_by_slots_left(HPW - k);
-      if (t == 0) slot_fetch_next_and_wait(k, hh);
-      if (t == L - 1 && k > 0) slot_copy_out(hh - WPB);   // the previous slot's state
+      if (t == 0) slot_wait(k);
       uint8_t* tile = s_tile[hh];
       uint16_t* t16 = (uint16_t*)tile;
 
@@ -793,7 +788,13 @@ void k_state_step(StepArgs a) {
       const bool ok4 = base_ok && __builtin_fabsf(sc4) <= 65504.f;
       sc8 = tier_step<N8, true, MODE>(c8, sc8, decay, x, bdt4, cw4, acc, ok8);
       __builtin_amdgcn_sched_barrier(0);
+      // the next slot's transfers and the previous slot's copy-out are
+      // issued between the tiers, where the other waves' arithmetic covers
+      // their issue time
+      if (dma_tiles && t == 0 && k + 1 < HPW) slot_dma(hh + WPB);
       sc4 = tier_step<N4, false, MODE>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc, ok4);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t == L - 1 && k > 0) slot_copy_out(hh - WPB);   // the previous slot's state
       __builtin_amdgcn_sched_barrier(0);
       // readout: sum_i u_i c_i + corrections = decay * (sum_i prior_i (c_i +
       // corr_i) + latent terms) + x * (dt * sum_all b c + D)
