@@ -256,6 +256,7 @@ __device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, Gro
   const uint32_t bw1 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (pv1 >> 1), braw);
   const uint32_t cw0 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (pv0 >> 1), craw);
   const uint32_t cw1 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (pv1 >> 1), craw);
+  __builtin_amdgcn_sched_barrier(0);   // all four exchanges in flight before the first use
   const float b0 = h2f((uint16_t)(bw0 >> (16 * (pv0 & 1)))), b1 = h2f((uint16_t)(bw1 >> (16 * (pv1 & 1))));
   const float c0 = h2f((uint16_t)(cw0 >> (16 * (pv0 & 1)))), c1 = h2f((uint16_t)(cw1 >> (16 * (pv1 & 1))));
   // the carried coordinates' b are finite binary16 values (|b| <= 65504)
@@ -304,6 +305,16 @@ __device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, Gro
         cv[i] = *(const f32x4*)(wt.c + NL + 4 * q);
         w[i] = *(const uint2*)(pr + 4 * q);
       }
+      const float cjo = wt.c[min(jo, NL - 1)];   // readout weight base of output jo (< NL)
+      // tree `wave` operands (waves 0..3: e0.c, e1.c, e0.b, e1.b), read
+      // unconditionally at clamped positions
+      const float* src = wave < 2 ? wt.c : wt.b;
+      float tv[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int d0 = (RZ == 128) ? 2 * lane + j : lane;
+        tv[j] = src[NL + min(d0, NZ - 1)];
+      }
       __builtin_amdgcn_sched_barrier(0);
       float a[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -319,18 +330,17 @@ __device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, Gro
       const auto sw = __builtin_amdgcn_permlane32_swap(part, part, false, false);
       const float corr = __builtin_bit_cast(float, (int)sw[0]) + __builtin_bit_cast(float, (int)sw[1]);
       if (lane < FW && jo < F) {
-        if (jo < NL) gt.cw[jo] = wt.c[jo] + corr;
+        if (jo < NL) gt.cw[jo] = cjo + corr;
         else gt.lc[jo - NL] = corr;
       }
-      if (wave < 4) {   // tree `wave`: e0.c, e1.c, e0.b, e1.b
-        const float* src = wave < 2 ? wt.c : wt.b;
+      if (wave < 4) {   // tree `wave`
         const float (&e)[2] = (wave & 1) ? e1v : e0v;
         float v[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const int d0 = (RZ == 128) ? 2 * lane + j : lane;
           const bool in = (RZ == 128 || j == 0) && d0 < NZ;
-          v[j] = in ? e[j] * src[NL + (in ? d0 : 0)] : 0.f;
+          v[j] = in ? e[j] * tv[j] : 0.f;
         }
         const float tsum = wave_pair_tree<RZ>(v[0], v[1]);
         if (lane == 0) {
