@@ -150,8 +150,8 @@ struct WaveToken {
 // written by the wave that computes it and read after a workgroup barrier.
 template <int NL>
 struct GroupToken {
-  alignas(16) float cw[NL];
-  float ec[2], lc[2], eb[2];
+  alignas(16) float cw[NL + 2];   // readout weights, then the latent coefficients' corrections
+  float tree[4];                  // e0.c, e1.c, e0.b, e1.b
 };
 
 // Inputs of one token that a wave loads one token ahead: its lane's two f16
@@ -316,6 +316,17 @@ __device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, Gro
         tv[j] = src[NL + min(d0, NZ - 1)];
       }
       __builtin_amdgcn_sched_barrier(0);
+      // tree `wave` (waves past 3 of an eight-wave group compute an unused
+      // copy), interleaved by the scheduler with the correction below
+      const float (&e)[2] = (wave & 1) ? e1v : e0v;
+      float v[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int d0 = (RZ == 128) ? 2 * lane + j : lane;
+        const bool in = (RZ == 128 || j == 0) && d0 < NZ;
+        v[j] = in ? e[j] * tv[j] : 0.f;
+      }
+      const float tsum = wave_pair_tree<RZ>(v[0], v[1]);
       float a[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int i = 0; i < QH; ++i) {
@@ -329,25 +340,8 @@ __device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, Gro
       const int part = __builtin_bit_cast(int, (a[0] + a[1]) + (a[2] + a[3]));
       const auto sw = __builtin_amdgcn_permlane32_swap(part, part, false, false);
       const float corr = __builtin_bit_cast(float, (int)sw[0]) + __builtin_bit_cast(float, (int)sw[1]);
-      if (lane < FW && jo < F) {
-        if (jo < NL) gt.cw[jo] = cjo + corr;
-        else gt.lc[jo - NL] = corr;
-      }
-      if (wave < 4) {   // tree `wave`
-        const float (&e)[2] = (wave & 1) ? e1v : e0v;
-        float v[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int d0 = (RZ == 128) ? 2 * lane + j : lane;
-          const bool in = (RZ == 128 || j == 0) && d0 < NZ;
-          v[j] = in ? e[j] * tv[j] : 0.f;
-        }
-        const float tsum = wave_pair_tree<RZ>(v[0], v[1]);
-        if (lane == 0) {
-          if (wave < 2) gt.ec[wave] = tsum;
-          else gt.eb[wave - 2] = tsum;
-        }
-      }
+      if (lane < FW && jo < F) gt.cw[jo] = (jo < NL ? cjo : 0.f) + corr;
+      if (lane == 0 && wave < 4) gt.tree[wave] = tsum;
       __syncthreads();   // the workgroup's shared token values are complete
       return;
     }
@@ -738,10 +732,10 @@ void k_state_step(StepArgs a) {
     wave_token_build<N8, N4, NZ, MODE, WPB, HPW>(wt, gt, cur, act, pv0, pv1, e0v, e1v, s_pred, t == 0, lane, wave);
     // readout weights and dead-tier dot products of this token
     const float* cwt = SPLIT ? gt.cw : wt.cw;
-    const float dot1 = SPLIT ? gt.ec[0] + gt.lc[0] : wt.dots[1];
-    const float dot2 = SPLIT ? gt.ec[1] + gt.lc[1] : wt.dots[2];
-    const float dot3 = SPLIT ? gt.eb[0] : wt.dots[3];
-    const float dot4 = SPLIT ? gt.eb[1] : wt.dots[4];
+    const float dot1 = SPLIT ? gt.tree[0] + gt.cw[NL] : wt.dots[1];
+    const float dot2 = SPLIT ? gt.tree[1] + gt.cw[NL + 1] : wt.dots[2];
+    const float dot3 = SPLIT ? gt.tree[2] : wt.dots[3];
+    const float dot4 = SPLIT ? gt.tree[3] : wt.dots[4];
 
     for (int k = 0; k < HPW; ++k) {
       // The slot's head index, opaque to the optimizer: every address and
