@@ -42,6 +42,8 @@ const char* m2r_last_error(void);
  *   basis f16[G,nz,2]; lscale f16[G,2] (> 0); pred f16[G,n8+n4+2,nz];
  *   lo,hi u8[rows,n8/2]; q4 u8[rows,n4/2]; latent e4m3[rows,2];
  *   s8,s4 f16[rows]; (n8,n4,nz) one of the seven published layouts.
+ * Fastest with P % 8 == 0, 16-byte aligned state arrays and pred, 4-byte
+ * aligned B, C and lscale; other alignments give the same results, slower.
  */
 int m2r_state_step_ridge(const void* x, const void* dt, const float* A, const void* B, const void* C,
                          const void* D, int d_is_f32, const void* dt_bias, int db_is_f32, const uint8_t* perm,
