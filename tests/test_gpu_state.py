@@ -311,3 +311,60 @@ def run_s16(oracle, device, batch, L, H, P, G, seed, collect):
 def test_s16_control_step(oracle, device):
     run_s16(oracle, device, 2, 3, 128, 64, 8, 81, collect=False)
     run_s16(oracle, device, 1, 5, 16, 40, 2, 82, collect=True)      # ragged statistics tile
+
+
+def test_ridge_2048_token_drift_batch64(oracle, device):
+    """The batch-64 drift check of the 56-layer benchmark configuration, on one
+    layer: independent seeded inputs per sequence, 2048 consecutive tokens in
+    blocks of 128 that alternate between 128 one-token calls (the per-token
+    requantize hook's pattern) and one 128-token call.  After every block the
+    packed state of sequences 0, 13, 37 and 63 equals the CPU oracle's bit for
+    bit, and their readout is within the tolerance."""
+    from mamba2_recall import ridge_codec
+    layout = "8_80_40"
+    n8, n4, nz = ridge_counts(layout)
+    batch, H, P, G, blocks, blk = 64, 128, 64, 8, 16, 128
+    sub = [0, 13, 37, 63]
+    rng = np.random.default_rng(2048)
+    par = cases.step_inputs(rng, 1, 1, H, P, G)          # A, D, dt_bias, perm
+    sta = cases.ridge_statics(rng, G, n8, n4, nz)
+    st0 = cases.random_packed_state(rng, batch, H, P, n8, n4, latent=True)
+
+    def rows_of(a):   # packed arrays are [batch, heads, dim, ...]
+        return np.ascontiguousarray(a[sub])
+
+    ref_state = {k: rows_of(v) for k, v in st0.items()}
+    state = ridge_codec.allocate_state(batch, H, P, 128, device, layout=layout)
+    to_state(st0, state, device)
+    A = torch.from_numpy(par["A"]).to(device)
+    D, db = dev16(par["D"], device), dev16(par["dt_bias"], device)
+    perm = torch.from_numpy(par["perm"]).to(device)
+    basis, ls, pred = (dev16(sta[k], device) for k in ("basis", "lscale", "pred"))
+    for k in range(blocks):
+        gen = torch.Generator(device=device).manual_seed(4096 + k)
+        x = torch.randn(batch, blk, H, P, generator=gen, device=device).half()
+        dt = torch.randn(batch, blk, H, generator=gen, device=device).half()
+        Bm = torch.randn(batch, blk, G, 128, generator=gen, device=device).half()
+        Cm = torch.randn(batch, blk, G, 128, generator=gen, device=device).half()
+        one_token = k % 2 == 0
+        print(f"[ridge drift] layout={layout} B={batch} block={k} tokens={k * blk}..{(k + 1) * blk - 1} "
+              f"one_token_calls={one_token}", flush=True)
+        if one_token:
+            ys = []
+            for t in range(blk):
+                yt, _ = ridge_codec.scan(x[:, t:t + 1].contiguous(), dt[:, t:t + 1].contiguous(), A,
+                                         Bm[:, t:t + 1].contiguous(), Cm[:, t:t + 1].contiguous(), D, db, state,
+                                         perm, basis, ls, pred, layout=layout, validate=(k == 0 and t == 0))
+                ys.append(yt)
+            y = torch.cat(ys, dim=1)
+        else:
+            y, _ = ridge_codec.scan(x, dt, A, Bm, Cm, D, db, state, perm, basis, ls, pred, layout=layout,
+                                    validate=False)
+        torch.cuda.synchronize()
+        host = lambda v: np.ascontiguousarray(v[sub].cpu().numpy().view(np.uint16))
+        y_ref = oracle.state_step(oracle.MODE_RIDGE, n8, n4, nz, host(x), host(dt), par["A"], host(Bm), host(Cm),
+                                  par["D"], par["dt_bias"], par["perm"], sta["basis"], sta["lscale"], sta["pred"],
+                                  ref_state)
+        got = {kk: rows_of(v) for kk, v in from_state(state).items()}
+        assert_state_equal(got, ref_state, f"ridge drift block {k}")
+        assert_y_close(y[sub], y_ref, f"ridge drift block {k}")
