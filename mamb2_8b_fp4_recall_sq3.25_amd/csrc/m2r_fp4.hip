@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) void k_fp4_g16(const uint32_t* __restrict__ co
       err |= ((s & 0x80u) && mag != 0u) ? FP4_ERR_SCALE_NEGATIVE : 0u;
       // a zero block may only hold codes 0 and 8 (both magnitudes zero)
       err |= (mag == 0u && (cw[k] & 0x77777777u) != 0u) ? FP4_ERR_ZERO_SCALE_CODE : 0u;
-      float hb = e4m3_to_f32(mag) * 0.5f;
+      float hb = e4m3_byte_to_f32<0>(mag) * 0.5f;   // FP8 instruction (0x7F: NaN, flagged above)
       u32x4 v = decode8<true>(cw[k], hb, gl, s >> 7, err);
       __builtin_nontemporal_store(v, out + u);
     }
