@@ -210,6 +210,69 @@ def fp4_full_decode(device, steps=3):
     return ms, nbytes / (ms * 1e-3) / 1e9
 
 
+def other_codecs(device, batch=64, launches=56, steps=10):
+    """Per-launch time of the other state codecs at the benchmark geometry
+    (one token, H=128, P=64, G=8), each a graph of `launches` launches of one
+    layer with resident inputs: the stored-scale tier codec (layout
+    32_32_64), the legacy sq3p25 codec, the dense 3-bit codec (permutation
+    table) and the FP16-carry control.  Bytes per launch are algorithmic: the
+    packed 52-byte rows in and out (256-byte FP16 rows for the control) plus
+    x, y, B, C and dt."""
+    import ctypes
+    from mamba2_recall import _native
+    p = _native.ptr
+    gen = torch.Generator(device=device).manual_seed(99)
+    f16 = torch.float16
+    x = torch.randn(batch, 1, H, P, generator=gen, device=device).to(f16)
+    dt = torch.randn(batch, 1, H, generator=gen, device=device).to(f16)
+    Bm = torch.randn(batch, 1, G, NSTATE, generator=gen, device=device).to(f16)
+    Cm = torch.randn(batch, 1, G, NSTATE, generator=gen, device=device).to(f16)
+    A = -torch.exp(torch.rand(H, generator=gen, device=device) * np.log(16.0))
+    D = torch.randn(H, generator=gen, device=device).to(f16)
+    db = torch.zeros(H, device=device, dtype=f16)
+    perm = torch.stack([torch.randperm(NSTATE, generator=gen, device=device) for _ in range(G)]).to(torch.uint8)
+    y = torch.empty_like(x)
+    rows = batch * H * P
+    u8 = lambda n: torch.randint(0, 256, (rows, n), generator=gen, device=device, dtype=torch.uint8)
+    sc = lambda n: (torch.rand(rows, n, generator=gen, device=device) * 0.01 + 1e-3).to(f16)
+    io = batch * (2 * 16384 + 4096 + 256)
+    lo, hi, q4, s8, s4 = u8(16), u8(16), u8(16), sc(1), sc(1)
+    codes, scales = u8(48), sc(2)
+    state16 = (torch.randn(rows, NSTATE, generator=gen, device=device) * 0.1).to(f16)
+    cases = {
+        "tier_32_32_64": (lambda h: _native.call(
+            "m2r_state_step_tier", p(x), p(dt), p(A), p(Bm), p(Cm), p(D), 0, p(db), 0, p(perm), p(lo), p(hi),
+            p(q4), p(s8), p(s4), p(y), batch, 1, H, P, G, 32, 32, 64, h), 2 * 52 * rows + io),
+        "legacy_sq3p25": (lambda h: _native.call(
+            "m2r_state_step_legacy", p(x), p(dt), p(A), p(Bm), p(Cm), p(D), 0, p(db), 0, p(perm), p(lo), p(hi),
+            p(q4), p(s8), p(s4), p(y), batch, 1, H, P, G, h), 2 * 52 * rows + io),
+        "dense3": (lambda h: _native.call(
+            "m2r_state_step_dense3", p(x), p(dt), p(A), p(Bm), p(Cm), p(D), 0, p(db), 0, p(perm), 0, p(codes),
+            p(scales), p(y), batch, 1, H, P, G, h), 2 * 52 * rows + io),
+        "s16_control": (lambda h: _native.call(
+            "m2r_state_step_s16", p(x), p(dt), p(A), p(Bm), p(Cm), p(D), 0, p(db), 0, p(state16), p(y), None,
+            batch, 1, H, P, G, h), 2 * 256 * rows + io),
+    }
+    out = {}
+    for name, (fn, nbytes) in cases.items():
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn(ctypes.c_void_p(s.cuda_stream))
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            h = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for _ in range(launches):
+                fn(h)
+        ms, _ = time_graph(g, steps, 2)
+        us = ms * 1e3 / launches
+        out[name] = dict(us_per_launch=round(us, 2), gbs=round(nbytes / (us * 1e-6) / 1e9, 1))
+        del g
+    return out
+
+
 def cpu_baseline(budget_s=12.0):
     """The C oracle (OpenMP over rows) on a bounded sample of the batch-64
     workload: the published layers in order at batch 8, repeated until the
@@ -297,6 +360,7 @@ def main():
         fp4_ms, fp4_gbs = fp4_full_decode(device)
         extra.update(fp4_g16_full_decode_ms=round(fp4_ms, 3), fp4_g16_full_decode_gbs=round(fp4_gbs, 1),
                      fp4_g16_full_decode_frac=round(fp4_gbs / HBM_PEAK_GBS, 4))
+    extra["other_codecs_b64"] = other_codecs(device)
     line = dict(
         metric=METRIC, value=round(gbs, 2), unit="GB/s", n_gpus=1, steps=args.steps, warmup=args.warmup,
         ms_per_step=round(ms, 5), higher_is_better=True, scaling="weak", vs_baseline=None, dtype="f32",

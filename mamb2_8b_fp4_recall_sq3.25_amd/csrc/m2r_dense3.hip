@@ -188,10 +188,20 @@ struct S16Args {
   int d_f32, db_f32;
 };
 
+// STAGED (state 16-byte aligned): the slot's 64 rows of 256 B move between
+// HBM and registers through LDS, as 1 KiB wave-wide transfers (16 per slot);
+// rows sit in LDS at a 272-byte pitch, so each group of 16 lanes reading
+// 16 bytes of its own row covers the 64 banks once.  Otherwise every lane
+// reads its row directly.
+constexpr int S16_PITCH = 68;   // dwords per staged row (64 + 4 padding)
+typedef uint32_t s16x4 __attribute__((ext_vector_type(4)));
+
+template <bool STAGED>
 __global__ __launch_bounds__(64) void k_s16_step(S16Args a) {
   __shared__ __align__(16) float s_b[128];
   __shared__ __align__(16) float s_c[128];
   __shared__ float s_acc[4][128];
+  __shared__ __align__(16) uint32_t s_rows[STAGED ? 64 * S16_PITCH : 4];
   const int lane = threadIdx.x;
   const int b = blockIdx.z, h = blockIdx.y;
   const int H = a.H, P = a.P, G = a.G, L = a.L;
@@ -199,10 +209,28 @@ __global__ __launch_bounds__(64) void k_s16_step(S16Args a) {
   const int pbase = blockIdx.x * 64;
   const int nvalid = min(64, P - pbase);
   const bool valid = lane < nvalid;
-  const size_t row = (size_t)(b * H + h) * P + pbase + lane;
+  const size_t row0 = (size_t)(b * H + h) * P + pbase;
+  const size_t row = row0 + lane;
   float st[128];
+  if constexpr (STAGED) {
+    const s16x4* src = (const s16x4*)(a.state + row0 * 128);
 #pragma unroll
-  for (int n = 0; n < 128; ++n) st[n] = valid ? h2f(a.state[row * 128 + n]) : 0.f;
+    for (int k = 0; k < 16; ++k) {   // chunk q = 64k + lane: row q / 16, 16-byte part q % 16
+      const int r = 4 * k + (lane >> 4), part = lane & 15;
+      const s16x4 v = r < nvalid ? src[64 * k + lane] : s16x4{0u, 0u, 0u, 0u};
+      *(s16x4*)(s_rows + r * S16_PITCH + 4 * part) = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int part = 0; part < 16; ++part) {
+      const s16x4 v = *(const s16x4*)(s_rows + lane * S16_PITCH + 4 * part);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) st[8 * part + e] = h2f((uint16_t)(v[e >> 1] >> (16 * (e & 1))));
+    }
+  } else {
+#pragma unroll
+    for (int n = 0; n < 128; ++n) st[n] = valid ? h2f(a.state[row * 128 + n]) : 0.f;
+  }
   for (int n = lane; n < 512; n += 64) (&s_acc[0][0])[n] = 0.f;
   const float av = a.A[h], Dh = load_param(a.D, a.d_f32, h), bias = load_param(a.dt_bias, a.db_f32, h);
   for (int t = 0; t < L; ++t) {
@@ -233,7 +261,24 @@ __global__ __launch_bounds__(64) void k_s16_step(S16Args a) {
     }
     __syncthreads();
   }
-  if (valid) {
+  if constexpr (STAGED) {
+    __syncthreads();   // every lane has read its row before the buffer is reused
+#pragma unroll
+    for (int part = 0; part < 16; ++part) {
+      s16x4 v;
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        v[w] = (uint32_t)f2h(st[8 * part + 2 * w]) | ((uint32_t)f2h(st[8 * part + 2 * w + 1]) << 16);
+      *(s16x4*)(s_rows + lane * S16_PITCH + 4 * part) = v;
+    }
+    __syncthreads();
+    s16x4* dst = (s16x4*)(a.state + row0 * 128);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int r = 4 * k + (lane >> 4), part = lane & 15;
+      if (r < nvalid) dst[64 * k + lane] = *(const s16x4*)(s_rows + r * S16_PITCH + 4 * part);
+    }
+  } else if (valid) {
 #pragma unroll
     for (int n = 0; n < 128; ++n) a.state[row * 128 + n] = f2h(st[n]);
   }
@@ -343,8 +388,11 @@ extern "C" int m2r_state_step_s16(const void* x, const void* dt, const float* A,
   S16Args args{(const uint16_t*)x, (const uint16_t*)dt, A, (const uint16_t*)B, (const uint16_t*)C, D, dt_bias,
                (uint16_t*)state, (uint16_t*)y, stats, (int)batch, (int)L, (int)H, (int)P, (int)G, d_is_f32,
                db_is_f32};
-  hipLaunchKernelGGL(k_s16_step, dim3((unsigned)((P + 63) / 64), (unsigned)H, (unsigned)batch), dim3(64), 0, stream,
-                     args);
+  const dim3 grid((unsigned)((P + 63) / 64), (unsigned)H, (unsigned)batch);
+  if (((uintptr_t)state & 15) == 0)
+    hipLaunchKernelGGL(k_s16_step<true>, grid, dim3(64), 0, stream, args);
+  else
+    hipLaunchKernelGGL(k_s16_step<false>, grid, dim3(64), 0, stream, args);
   return m2r_check(hipGetLastError(), "s16 step launch");
 }
 
