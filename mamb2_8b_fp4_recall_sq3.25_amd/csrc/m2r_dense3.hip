@@ -71,24 +71,24 @@ __global__ __launch_bounds__(64 * WPB) void k_dense3_step(Dense3Args a) {
   }
   __syncthreads();
 
-  // carry: byte k of c[i] = q[4i+k] + 4 (== 3-bit code ^ 4)
+  // carry: byte k of c[i] = q[4i+k] + 4 (== 3-bit code ^ 4).  Coordinate n
+  // is bit n % 32 of word 4j + n / 32 of plane j.  Four bits of a plane
+  // spread to bit 0 of four bytes as (nibble * 0x204081) & 0x01010101 (the
+  // partial products land on distinct bits, so nothing carries); the bias
+  // flips bit 2, i.e. plane 2 is read inverted.
   uint32_t c[32];
   {
     uint32_t w[12];
     lds_read_row<W>(tile, lane * W, w);
 #pragma unroll
+    for (int j = 8; j < 12; ++j) w[j] = ~w[j];
+#pragma unroll
     for (int i = 0; i < 32; ++i) {
-      uint32_t bytes = 0;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int n = 4 * i + k;
-        // plane j, byte n/8, bit n%8; plane j starts at byte 16j = word 4j
-        uint32_t u = 0;
-#pragma unroll
-        for (int j = 0; j < 3; ++j) u |= ((w[4 * j + (n >> 5)] >> (n & 31)) & 1u) << j;
-        bytes |= (u ^ 4u) << (8 * k);
-      }
-      c[i] = valid ? bytes : 0x04040404u;
+      const int wi = i >> 3, sh = 4 * (i & 7);
+      const uint32_t s0 = __umul24(__builtin_amdgcn_ubfe(w[wi], sh, 4), 0x204081u) & 0x01010101u;
+      const uint32_t s1 = __umul24(__builtin_amdgcn_ubfe(w[4 + wi], sh, 4), 0x204081u) & 0x01010101u;
+      const uint32_t s2 = __umul24(__builtin_amdgcn_ubfe(w[8 + wi], sh, 4), 0x204081u) & 0x01010101u;
+      c[i] = valid ? (s0 | (s1 << 1) | (s2 << 2)) : 0x04040404u;
     }
   }
   const float y3 = 1.0f / 3.0f;
@@ -160,14 +160,28 @@ __global__ __launch_bounds__(64 * WPB) void k_dense3_step(Dense3Args a) {
     __syncthreads();
   }
 
-  // planes: byte j of plane k holds bit k of (q & 7) for lanes 8j..8j+7
+  // planes: byte j of plane k holds bit k of (q & 7) for lanes 8j..8j+7.
+  // For 8 coordinates (two code words a, b), plane k's bits sit at bit k of
+  // each byte; (a & m) | (b & m) << 4 with m = 0x01010101 << k, times
+  // 0x01020408 >> k, leaves the 8 bits in the top byte (distinct partial
+  // products, no carries).  Bit 2 is read inverted (the bias).
   if (valid) {
-    uint32_t w[12] = {};
+    uint32_t w[12];
 #pragma unroll
-    for (int n = 0; n < 128; ++n) {
-      uint32_t u = ((c[n >> 2] >> (8 * (n & 3))) & 7u) ^ 4u;   // q & 7
+    for (int k = 0; k < 3; ++k) {
+      const uint32_t m = 0x01010101u << k, mul = 0x01020408u >> k;
+      uint32_t top[16];
 #pragma unroll
-      for (int j = 0; j < 3; ++j) w[4 * j + (n >> 5)] |= ((u >> j) & 1u) << (n & 31);
+      for (int t = 0; t < 16; ++t) {
+        const uint32_t ca = k == 2 ? ~c[2 * t] : c[2 * t], cb = k == 2 ? ~c[2 * t + 1] : c[2 * t + 1];
+        top[t] = ((ca & m) | ((cb & m) << 4)) * mul;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {   // top bytes of products 4q .. 4q+3 -> plane word q
+        const uint32_t lo = __builtin_amdgcn_perm(top[4 * q + 1], top[4 * q], 0x0c0c0703u);
+        const uint32_t hi = __builtin_amdgcn_perm(top[4 * q + 3], top[4 * q + 2], 0x07030c0cu);
+        w[4 * k + q] = lo | hi;
+      }
     }
     lds_write_row<W>(tile, lane * W, w);
   }
