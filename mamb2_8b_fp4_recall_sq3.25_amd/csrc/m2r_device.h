@@ -125,6 +125,16 @@ __device__ __forceinline__ float div_by_recip(float a, float d, float y) {
   return __builtin_fmaf(r, y, q0);
 }
 
+// The requantization denominator max(amax / lim, 1e-8) for amax >= 0 (a
+// maximum of absolute values, never NaN), with y = RN(1 / lim): the
+// reciprocal form is RN(amax / lim) for finite amax; an infinite amax gives
+// an infinite den, as IEEE division does (the reciprocal form's residual
+// would be NaN there).
+__device__ __forceinline__ float requant_den(float amax, float lim, float y) {
+  const float den = __builtin_fmaxf(div_by_recip(amax, lim, y), 1e-8f);
+  return amax == __builtin_inff() ? amax : den;
+}
+
 // roundf(RN(v/d)) as an integer, with y = RN(1/d), for quotients that need
 // no clamping (|RN(v/d)| < lim + 1/2).
 __device__ __forceinline__ int quantize_code_unclamped(float v, float d, float y) {
@@ -136,6 +146,9 @@ __device__ __forceinline__ int quantize_code_unclamped(float v, float d, float y
 // top = the largest binary32 below lim + 1.  roundf(q) is trunc(q + copysign(
 // pred(0.5), q)); clamping that sum to +-top before the truncating integer
 // conversion equals clamping the rounded value to +-lim.
+// (An infinite v with a finite divisor gives NaN here, where IEEE division
+// gives an infinity: the state kernels never divide an infinite update by a
+// finite scale, since that update's maximum makes the scale infinite.)
 __device__ __forceinline__ int quantize_code(float v, float d, float y, float top) {
   const float q = div_by_recip(v, d, y);
   const float t = q + __builtin_copysignf(0x1.fffffep-2f, q);
@@ -144,6 +157,30 @@ __device__ __forceinline__ int quantize_code(float v, float d, float y, float to
 constexpr float QTOP127 = 0x1.fffffep+6f;   // below 128
 constexpr float QTOP7 = 0x1.fffffep+2f;     // below 8
 constexpr float QTOP3 = 0x1.fffffep+1f;     // below 4
+
+// q * s exactly, for a code q held as binary16 (an integer of at most 11
+// bits) and any binary32 s: one mixed-precision fma with a -0 addend (x + -0
+// is x, also for signed zeros), so infinite and NaN scales give the IEEE
+// product as well.  `mz` is -0.0 passed through an empty asm by the caller
+// (a known -0 addend is folded into a plain product, which has no
+// mixed-precision form).
+__device__ __forceinline__ float dequant_h(_Float16 q, float s, float mz) {
+  return __builtin_fmaf((float)q, s, mz);
+}
+__device__ __forceinline__ float opaque_neg_zero() {
+  float mz = -0.0f;
+  asm volatile("" : "+s"(mz));
+  return mz;
+}
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Packed binary16 a + b kept as one packed add (the empty asm stops the
+// compiler from splitting it into two half-word adds).
+__device__ __forceinline__ f16x2 pk_add_h(f16x2 a, f16x2 b) {
+  uint32_t r = __builtin_bit_cast(uint32_t, a + b);
+  asm volatile("" : "+v"(r));
+  return __builtin_bit_cast(f16x2, r);
+}
 
 // The recurrent update of every codec: fma(state, decay, input) with
 // input = RN(RN(b * dt) * x) rounded separately, i.e. the reference's

@@ -32,7 +32,10 @@ __global__ void k_probe_stored_quantize(const float* v, const uint16_t* s, int32
   float sc = h2f(s[i]);
   bool z = !(sc > 0.f) || sc == __builtin_inff();
   float d = z ? 1.f : sc, r = z ? 0.f : 1.0f / sc;
-  q[i] = quantize_code(v[i], d, r, lim == 7.0f ? QTOP7 : QTOP127);
+  // an infinite value over a finite positive scale: IEEE gives the infinity
+  // (the kernels never form this quotient; see quantize_code)
+  const float vv = (!z && __builtin_isinf(v[i])) ? __builtin_copysignf(3e38f, v[i]) : v[i];
+  q[i] = sc > 0.f ? quantize_code(vv, d, r, lim == 7.0f ? QTOP7 : QTOP127) : 0;
 }
 
 // Elementwise primitives, selected by `op`:

@@ -26,6 +26,7 @@
 #include "m2r_tile.h"
 
 #include <atomic>
+#include <type_traits>
 #include <initializer_list>
 
 namespace m2r {
@@ -209,27 +210,6 @@ template <int HPW>
 __device__ __forceinline__ float2 wave_dt_activation(const WaveRaw<HPW>& r, float Ah, int db_f32) {
   const float db = db_f32 ? __builtin_bit_cast(float, (uint32_t)r.db_lo | ((uint32_t)r.db_hi << 16)) : h2f(r.db_lo);
   return dt_activation(h2f(r.dt) + db, Ah);
-}
-
-// Wave priority from the number of head slots the wave still has to step
-// in this token (4 or more: highest).  Two workgroups share each CU, so each
-// SIMD runs two waves; its issue arbitration otherwise favours the older
-// wave, which runs ahead while the younger one finishes alone, a slot or more
-// later, with no second wave to hide its latencies.  With the priority the
-// wave that is behind wins the arbitration until it has caught up.
-__device__ __forceinline__ void wave_priority_by_slots_left(int left) {
-  if (left >= 4) __builtin_amdgcn_s_setprio(3);
-  else if (left == 3) __builtin_amdgcn_s_setprio(2);
-  else if (left == 2) __builtin_amdgcn_s_setprio(1);
-  else __builtin_amdgcn_s_setprio(0);
-}
-
-// Orders a wave's LDS accesses across its lanes (the wave's own regions
-// need no workgroup barrier).
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
 // Builds the wave's token values from its landed raw inputs and the dt
@@ -420,15 +400,6 @@ __device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, Gro
   wave_sync();
 }
 
-// max(m, |a|, |b|) as one v_max3_f32 (IEEE maxNum: a quiet NaN operand is
-// ignored, as fmaxf does).  Written out because the compiler otherwise
-// canonicalizes each pinned operand first.
-__device__ __forceinline__ float max3_abs(float m, float a, float b) {
-  float r;
-  asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(m), "v"(a), "v"(b));
-  return r;
-}
-
 // One tier of a row: update its N carried coordinates (biased code bytes in
 // c[0 .. N/4)), accumulate the readout (prior * readout weight), then
 // requantize with den = max(RN(amax / lim), 1e-8) and the stored (binary16)
@@ -443,16 +414,22 @@ __device__ __forceinline__ float max3_abs(float m, float a, float b) {
 // lane and every stored scale is zero, infinite or a normal binary16 value,
 // |RN(u / s)| <= lim (1 + 2^-11) / (1 - 2^-24) < lim + 1/2 and the wave takes
 // the quantizer without the clamp.
-template <int N, bool INT8, int MODE>
+//
+// EXACT selects the dequantization form: false (every scale of the wave
+// finite) the fused (1024 + q + bias) * s - (1024 + bias) * s, one fma per
+// coordinate (exact: both products have at most 22 significant bits); true
+// q * s as a packed binary16 subtraction and a product, which is also the
+// IEEE product for infinite and NaN scales (where the fused form gives
+// inf - inf).
+template <int N, bool INT8, int MODE, bool EXACT>
 __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, float x, const f32x4* bdt4,
                                            const f32x4* cw4, float& acc, bool finite_in) {
   constexpr float BIAS = INT8 ? 128.0f : 8.0f;
   constexpr float LIM = INT8 ? 127.0f : 7.0f;
   constexpr float TOP = INT8 ? QTOP127 : QTOP7;
-  // prior = q * s exactly, from f16(1024 + byte) (exact: 11-bit integers) as
-  // (1024 + q + bias) * s - (1024 + bias) * s: both products have at most 22
-  // significant bits, so the fused multiply-add is exact
   const float nb = -(1024.0f + BIAS) * sc;
+  const f16x2 nbias = {(_Float16)(-(1024.0f + BIAS)), (_Float16)(-(1024.0f + BIAS))};
+  const float mz = EXACT ? opaque_neg_zero() : 0.f;
   float v[N];
   float amax = 0.f;
   // the shared operands of chunk i+1 are read while chunk i computes
@@ -467,10 +444,19 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
     // the chunk's code bytes as binary16 values 1024 + byte (exponent byte 0x64)
     const uint32_t h01 = __builtin_amdgcn_perm(0x64646464u, c[i0 / 4], 0x04010400u);
     const uint32_t h23 = __builtin_amdgcn_perm(0x64646464u, c[i0 / 4], 0x04030402u);
+    float pr[4];
+    if constexpr (EXACT) {
+      const f16x2 q01 = pk_add_h(__builtin_bit_cast(f16x2, h01), nbias);
+      const f16x2 q23 = pk_add_h(__builtin_bit_cast(f16x2, h23), nbias);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pr[j] = dequant_h((j < 2 ? q01 : q23)[j & 1], sc, mz);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pr[j] = __builtin_fmaf(h2f((uint16_t)((j < 2 ? h01 : h23) >> (16 * (j & 1)))), sc, nb);
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint32_t hw = j < 2 ? h01 : h23;
-      const float prior = __builtin_fmaf(h2f((uint16_t)(hw >> (16 * (j & 1)))), sc, nb);
+      const float prior = pr[j];
       acc = __builtin_fmaf(prior, cw[j], acc);
       float u = state_update(prior, decay, cb[j] * x);
       // ordered pin: chunk by chunk, each prior dies as soon as it is used
@@ -485,13 +471,19 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
   // sinks their chains (and every update behind the maximum) into the
   // requantization, which keeps every prior and LDS operand live at once.
   asm volatile("" : "+v"(acc), "+v"(amax));
-  const float den = __builtin_fmaxf(div_by_recip(amax, LIM, 1.0f / LIM), 1e-8f);
+  const float den = requant_den(amax, LIM, 1.0f / LIM);
   const float stored = round_to_half(den);
   float d, r;
   bool unclamped;
+  // stored scale not > 0: the reference's code is 0 whatever the update
+  // (also NaN): the clamp bound is then 0 (clamp(NaN, -0, 0) is -0 or 0)
+  float top = TOP;
   if constexpr (MODE == MODE_LEGACY) {
-    d = den;
-    r = 1.0f / den;
+    // an infinite den divides through d = 1, y = 0: RN(v / inf) is 0 for
+    // finite v (NaN, clamped to -lim, for infinite v, as IEEE gives)
+    const bool inf = den == __builtin_inff();
+    d = inf ? 1.0f : den;
+    r = inf ? 0.0f : 1.0f / den;
     unclamped = finite_in;
   } else {
     // zero (underflowed) or infinite stored scale: the reference's quotient
@@ -500,6 +492,7 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
     d = zero ? 1.f : stored;
     r = zero ? 0.f : recip_half(stored);
     unclamped = finite_in && (zero || stored >= 0x1p-14f);
+    top = stored > 0.f ? TOP : 0.0f;
   }
   // wave-uniform choice, re-tested per chunk (a branch around the whole loop
   // makes the register allocator keep both versions' values apart)
@@ -514,10 +507,10 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
       q3 = quantize_code_unclamped(v[4 * i + 3], d, r);
     } else {
       asm volatile("");   // keeps this a branch: the fast side must not pay for the clamp
-      q0 = quantize_code(v[4 * i], d, r, TOP);
-      q1 = quantize_code(v[4 * i + 1], d, r, TOP);
-      q2 = quantize_code(v[4 * i + 2], d, r, TOP);
-      q3 = quantize_code(v[4 * i + 3], d, r, TOP);
+      q0 = quantize_code(v[4 * i], d, r, top);
+      q1 = quantize_code(v[4 * i + 1], d, r, top);
+      q2 = quantize_code(v[4 * i + 2], d, r, top);
+      q3 = quantize_code(v[4 * i + 3], d, r, top);
     }
     uint32_t packed = pack4(q0, q1, q2, q3);
     packed = INT8 ? (packed ^ 0x80808080u) : ((packed & 0x0F0F0F0Fu) ^ 0x08080808u);
@@ -788,18 +781,28 @@ void k_state_step(StepArgs a) {
       const f32x4* bdt4 = (const f32x4*)wt.bdt[k];
       const f32x4* cw4 = (const f32x4*)cwt;
       float acc = 0.f;
-      const bool ok8 = base_ok && __builtin_fabsf(sc8) <= 65504.f;
-      const bool ok4 = base_ok && __builtin_fabsf(sc4) <= 65504.f;
-      sc8 = tier_step<N8, true, MODE>(c8, sc8, decay, x, bdt4, cw4, acc, ok8);
-      __builtin_amdgcn_sched_barrier(0);
-      // the next slot's transfers and the previous slot's copy-out are
-      // issued between the tiers, where the other waves' arithmetic covers
-      // their issue time
-      if (dma_tiles && t == 0 && k + 1 < HPW) slot_dma(hh + WPB);
-      sc4 = tier_step<N4, false, MODE>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc, ok4);
-      __builtin_amdgcn_sched_barrier(0);
-      if (t == L - 1 && k > 0) slot_copy_out(hh - WPB);   // the previous slot's state
-      __builtin_amdgcn_sched_barrier(0);
+      const bool fin8 = __builtin_fabsf(sc8) <= 65504.f, fin4 = __builtin_fabsf(sc4) <= 65504.f;
+      const bool ok8 = base_ok && fin8;
+      const bool ok4 = base_ok && fin4;
+      // one wave-uniform choice per slot between two copies of the tier code:
+      // the fused dequantization when every scale of the wave is finite, the
+      // exact products otherwise (non-finite scales are rare: the reference's
+      // controllers reject such states)
+      auto tiers = [&](auto exact) {
+        constexpr bool EX = decltype(exact)::value;
+        sc8 = tier_step<N8, true, MODE, EX>(c8, sc8, decay, x, bdt4, cw4, acc, ok8);
+        __builtin_amdgcn_sched_barrier(0);
+        // the next slot's transfers and the previous slot's copy-out are
+        // issued between the tiers, where the other waves' arithmetic covers
+        // their issue time
+        if (dma_tiles && t == 0 && k + 1 < HPW) slot_dma(hh + WPB);
+        sc4 = tier_step<N4, false, MODE, EX>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc, ok4);
+        __builtin_amdgcn_sched_barrier(0);
+        if (t == L - 1 && k > 0) slot_copy_out(hh - WPB);   // the previous slot's state
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      if (__builtin_amdgcn_ballot_w64(!(fin8 && fin4)) == 0) tiers(std::false_type{});
+      else tiers(std::true_type{});
       // readout: sum_i u_i c_i + corrections = decay * (sum_i prior_i (c_i +
       // corr_i) + latent terms) + x * (dt * sum_all b c + D)
       float out;
@@ -979,6 +982,8 @@ extern "C" int m2r_state_step_tier(const void* x, const void* dt, const float* A
   if (e == hipErrorInvalidValue) return m2r_fail("tier step: unsupported tier layout");
   return m2r_check(e, "tier step launch");
 }
+
+int m2r_forced_step_shape() { return g_forced_shape.load(std::memory_order_relaxed); }
 
 extern "C" int m2r_set_step_shape(int waves_per_block, int heads_per_wave) {
   const int w = waves_per_block, k = heads_per_wave;

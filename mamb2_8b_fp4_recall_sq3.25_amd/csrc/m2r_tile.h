@@ -133,6 +133,18 @@ constexpr int chunk_ops(int W) { return (64 * W + 1023) / 1024; }
 // rows re-read the last valid chunk, whose copy lands in rows nobody reads.
 // Requires g + row0 * W to be 16-byte aligned and nvalid * W a multiple of
 // 16.  Issues exactly chunk_ops(W) operations.
+// field_dma16_at takes the LDS byte address itself.
+template <int W>
+__device__ __forceinline__ void field_dma16_at(uint32_t l0, const uint8_t* g, int row0, int nvalid, int lane) {
+  constexpr int FB = 64 * W;
+  const uint8_t* base = g + (size_t)row0 * W;
+  const int last = nvalid * W - 16;
+#pragma unroll
+  for (int k = 0; k < chunk_ops(W); ++k) {
+    const int o = k * 1024 + 16 * lane;
+    if (k * 1024 + 1024 <= FB || o < FB) lds_dma_b128(base + min(o, last), l0 + 1024 * k);
+  }
+}
 template <int W>
 __device__ __forceinline__ void field_dma16(uint8_t* lds, const uint8_t* g, int row0, int nvalid, int lane) {
   constexpr int FB = 64 * W;
@@ -349,6 +361,36 @@ __device__ __forceinline__ uint32_t pack4(int q0, int q1, int q2, int q3) {
   uint32_t lo = __builtin_amdgcn_perm((uint32_t)q1, (uint32_t)q0, 0x0c0c0400u);  // q0.b0, q1.b0
   uint32_t hi = __builtin_amdgcn_perm((uint32_t)q3, (uint32_t)q2, 0x04000c0cu);  // q2.b0, q3.b0 in bytes 2,3
   return lo | hi;
+}
+
+// Wave priority from the number of head slots the wave still has to step
+// in this token (4 or more: highest).  Two workgroups share each CU, so each
+// SIMD runs two waves; its issue arbitration otherwise favours the older
+// wave, which runs ahead while the younger one finishes alone, a slot or more
+// later, with no second wave to hide its latencies.  With the priority the
+// wave that is behind wins the arbitration until it has caught up.
+__device__ __forceinline__ void wave_priority_by_slots_left(int left) {
+  if (left >= 4) __builtin_amdgcn_s_setprio(3);
+  else if (left == 3) __builtin_amdgcn_s_setprio(2);
+  else if (left == 2) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+}
+
+// Orders a wave's LDS accesses across its lanes (the wave's own regions
+// need no workgroup barrier).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// max(m, |a|, |b|) as one v_max3_f32 (IEEE maxNum: a quiet NaN operand is
+// ignored, as fmaxf does).  Written out because the compiler otherwise
+// canonicalizes each pinned operand first.
+__device__ __forceinline__ float max3_abs(float m, float a, float b) {
+  float r;
+  asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+  return r;
 }
 
 }  // namespace m2r

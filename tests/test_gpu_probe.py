@@ -120,6 +120,12 @@ def test_stored_quantize_every_scale_boundary(oracle, device, limit):
     scales = np.tile(np.repeat(s_bits, ks.size), 3)
     vals = np.concatenate([vals, -vals])
     scales = np.concatenate([scales, scales])
+    # non-finite values and scales: zero, negative, infinite and NaN scales
+    # against finite, infinite and NaN values
+    sp_s = np.array([0x0000, 0x8000, 0x3C00, 0xBC00, 0x7C00, 0xFC00, 0x7E00], np.uint16)
+    sp_v = np.array([0.0, 1.0, -3.5, np.inf, -np.inf, np.nan], np.float32)
+    vals = np.concatenate([vals, np.tile(sp_v, sp_s.size)])
+    scales = np.concatenate([scales, np.repeat(sp_s, sp_v.size)])
     want = oracle.stored_quantize(vals, scales, limit)
     vd = torch.from_numpy(vals).to(device)
     sd = torch.from_numpy(scales.view(np.int16)).to(device)

@@ -59,8 +59,32 @@ def assert_y_close(y_dev, y_ref, what):
     return err
 
 
+def plant_scales(rng, st0, fields, specials):
+    """Writes the binary16 bit patterns `specials` into randomly chosen
+    entries of the given scale fields (one field per entry, chosen at random)."""
+    for bits in specials:
+        f = fields[int(rng.integers(0, len(fields)))]
+        flat = st0[f].reshape(-1)
+        flat[int(rng.integers(0, flat.size))] = bits
+
+
+def assert_y_pattern_close(y_dev, y_ref, what):
+    """Readouts some of whose rows are not finite on both sides: the NaN and
+    infinite positions agree, the finite rows are within the tolerance."""
+    got = cases.f16_to_f32(y_dev.cpu().numpy().view(np.uint16))
+    want = cases.f16_to_f32(y_ref)
+    assert (np.isnan(got) == np.isnan(want)).all(), f"{what}: NaN readout rows differ"
+    assert (np.isinf(got) == np.isinf(want)).all(), f"{what}: infinite readout rows differ"
+    fin = np.isfinite(want)
+    err = cases.rel_l2(got[fin], want[fin])
+    assert err <= Y_TOL, f"{what}: y rel L2 {err:.3e} > {Y_TOL}"
+
+
+NONFINITE_SCALES = [0x7C00, 0xFC00, 0x7E00, 0x7C00, 0xFE00, 0x7C00]
+
+
 def run_ridge(oracle, device, layout, batch, L, H, P, G, seed, *, random_state=True, d_f32=False, db_f32=False,
-              dt_bias_zero=True, x_scale=1.0, scale_mu=-4.0):
+              dt_bias_zero=True, x_scale=1.0, scale_mu=-4.0, special_scales=None):
     from mamba2_recall import ridge_codec
     n8, n4, nz = ridge_counts(layout)
     rng = np.random.default_rng(seed)
@@ -69,6 +93,8 @@ def run_ridge(oracle, device, layout, batch, L, H, P, G, seed, *, random_state=T
     sta = cases.ridge_statics(rng, G, n8, n4, nz)
     st0 = (cases.random_packed_state(rng, batch, H, P, n8, n4, latent=True, scale_mu=scale_mu) if random_state
            else cases.zero_packed_state(batch, H, P, n8, n4, latent=True))
+    if special_scales is not None:
+        plant_scales(rng, st0, ("s8", "s4"), special_scales)
     print(f"[ridge] layout={layout} B={batch} L={L} H={H} P={P} G={G} seed={seed}", flush=True)
     ref_state = cases.copy_state(st0)
     y_ref = oracle.state_step(oracle.MODE_RIDGE, n8, n4, nz, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"],
@@ -83,11 +109,13 @@ def run_ridge(oracle, device, layout, batch, L, H, P, G, seed, *, random_state=T
                             pred, layout=layout)
     torch.cuda.synchronize()
     assert_state_equal(from_state(state), ref_state, f"ridge {layout}")
+    if special_scales is not None:
+        return assert_y_pattern_close(y, y_ref, f"ridge {layout}")
     return assert_y_close(y, y_ref, f"ridge {layout}")
 
 
 def run_tier(oracle, device, kind, layout, batch, L, H, P, G, seed, *, random_state=True, d_f32=False,
-             db_f32=False, dt_bias_zero=True, x_scale=1.0, scale_mu=-4.0):
+             db_f32=False, dt_bias_zero=True, x_scale=1.0, scale_mu=-4.0, special_scales=None):
     from mamba2_recall import state_codec, tier_codec
     n8, n4, nz = tier_counts(layout)
     rng = np.random.default_rng(seed)
@@ -95,6 +123,8 @@ def run_tier(oracle, device, kind, layout, batch, L, H, P, G, seed, *, random_st
                             x_scale=x_scale)
     st0 = (cases.random_packed_state(rng, batch, H, P, n8, n4, scale_mu=scale_mu) if random_state
            else cases.zero_packed_state(batch, H, P, n8, n4))
+    if special_scales is not None:
+        plant_scales(rng, st0, ("s8", "s4"), special_scales)
     print(f"[{kind}] layout={layout} B={batch} L={L} H={H} P={P} G={G} seed={seed}", flush=True)
     ref_state = cases.copy_state(st0)
     mode = oracle.MODE_LEGACY if kind == "legacy" else oracle.MODE_STORED
@@ -113,6 +143,8 @@ def run_tier(oracle, device, kind, layout, batch, L, H, P, G, seed, *, random_st
                                layout=layout)
     torch.cuda.synchronize()
     assert_state_equal(from_state(state), ref_state, f"{kind} {layout}")
+    if special_scales is not None:
+        return assert_y_pattern_close(y, y_ref, f"{kind} {layout}")
     return assert_y_close(y, y_ref, f"{kind} {layout}")
 
 
@@ -240,10 +272,16 @@ def test_sequential_tokens_equal_one_call(oracle, device):
     assert torch.equal(torch.cat(ys, 1), y_all)
 
 
-def run_dense3(oracle, device, kind, batch, L, H, P, G, seed, *, random_state=True):
+def run_dense3(oracle, device, kind, batch, L, H, P, G, seed, *, random_state=True, x_scale=1.0, scale_mu=-2.0,
+               special_scales=None, nonfinite_y=False):
+    """`special_scales`: binary16 bit patterns written into the scales of a
+    few rows (infinite or NaN stored scales).  Such rows' readout, and that of
+    rows whose readout overflows binary16 (`nonfinite_y`), is not finite on
+    both sides: y is then compared on the finite rows, plus the pattern of
+    NaN and infinite values."""
     from mamba2_recall import state_codec_dense3 as d3
     rng = np.random.default_rng(seed)
-    inp = cases.step_inputs(rng, batch, L, H, P, G)
+    inp = cases.step_inputs(rng, batch, L, H, P, G, x_scale=x_scale)
     if kind == "equalizer":
         table = rng.integers(-8, 9, size=(G, 128)).astype(np.int8)
     else:
@@ -251,9 +289,11 @@ def run_dense3(oracle, device, kind, batch, L, H, P, G, seed, *, random_state=Tr
     rows = (batch, H, P)
     if random_state:
         st0 = dict(codes=rng.integers(0, 256, size=rows + (3, 16), dtype=np.uint16).astype(np.uint8),
-                   scales=cases.f16(np.exp(rng.normal(-2.0, 0.5, size=rows + (2,)))))
+                   scales=cases.f16(np.exp(rng.normal(scale_mu, 0.5, size=rows + (2,)))))
     else:
         st0 = dict(codes=np.zeros(rows + (3, 16), np.uint8), scales=np.zeros(rows + (2,), np.uint16))
+    if special_scales is not None:
+        plant_scales(rng, st0, ("scales",), special_scales)
     print(f"[dense3 {kind}] B={batch} L={L} H={H} P={P} G={G} seed={seed}", flush=True)
     ref = cases.copy_state(st0)
     y_ref = oracle.dense3_step(1 if kind == "equalizer" else 0, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"],
@@ -265,6 +305,8 @@ def run_dense3(oracle, device, kind, batch, L, H, P, G, seed, *, random_state=Tr
                 torch.from_numpy(np.ascontiguousarray(table)).to(device), kind)
     torch.cuda.synchronize()
     assert_state_equal(from_state(state), ref, f"dense3 {kind}")
+    if special_scales is not None or nonfinite_y:
+        return assert_y_pattern_close(y, y_ref, f"dense3 {kind}")
     return assert_y_close(y, y_ref, f"dense3 {kind}")
 
 
@@ -280,6 +322,68 @@ def test_dense3_multi_token_small(oracle, device, kind):
 
 def test_dense3_wide_batch(oracle, device):
     run_dense3(oracle, device, "permutation", batch=32, L=1, H=128, P=64, G=8, seed=53)
+
+
+def test_dense3_benchmark_geometry(oracle, device):
+    # batch 64, one token: 16 heads per workgroup (four waves of four slots)
+    run_dense3(oracle, device, "permutation", batch=64, L=1, H=128, P=64, G=8, seed=54)
+    run_dense3(oracle, device, "equalizer", batch=64, L=1, H=128, P=64, G=8, seed=55)
+
+
+D3_SHAPES = [(1, 1), (4, 1), (4, 2), (4, 4)]
+
+
+@pytest.mark.parametrize("forced_shape", D3_SHAPES, indirect=True, ids=lambda s: f"w{s[0]}h{s[1]}")
+def test_dense3_every_workgroup_shape(oracle, device, forced_shape):
+    """Each (waves, head slots per wave) variant of the streaming kernel:
+    multi-token with ragged P (a 16-row second slot), one group and several,
+    one token from a zero state, both table kinds."""
+    run_dense3(oracle, device, "permutation", batch=2, L=3, H=32, P=80, G=2, seed=56)
+    run_dense3(oracle, device, "equalizer", batch=1, L=2, H=16, P=48, G=1, seed=57)
+    run_dense3(oracle, device, "permutation", batch=3, L=1, H=16, P=68, G=1, seed=58, random_state=False)
+
+
+def test_dense3_unaligned_geometry_staged_kernel(oracle, device):
+    # P % 4 != 0: slots cannot move as 16-byte transfers; the staged kernel runs
+    run_dense3(oracle, device, "permutation", batch=2, L=3, H=16, P=18, G=2, seed=59)
+    run_dense3(oracle, device, "equalizer", batch=1, L=1, H=8, P=33, G=1, seed=60)
+
+
+@pytest.mark.parametrize("x_scale,scale_mu", [(1e-5, -14.0), (1e-9, -24.0)])
+def test_dense3_tiny_states(oracle, device, x_scale, scale_mu):
+    """Half-row maxima small enough that den is the 1e-8 floor."""
+    run_dense3(oracle, device, "permutation", batch=2, L=3, H=32, P=64, G=2, seed=66, x_scale=x_scale,
+               scale_mu=scale_mu)
+
+
+def test_dense3_large_states(oracle, device):
+    """Updates large enough that some new stored scales overflow binary16 (and
+    some readouts with them)."""
+    run_dense3(oracle, device, "permutation", batch=2, L=1, H=32, P=64, G=2, seed=69, x_scale=1e4, scale_mu=6.0,
+               nonfinite_y=True)
+
+
+def test_dense3_non_finite_scales(oracle, device):
+    """Rows whose stored scale is +inf, -inf or NaN: their updates are not
+    finite, their maxima infinite, and the clamping quantizer with the
+    infinite-den division runs (NaN quotients clamp to -3)."""
+    run_dense3(oracle, device, "permutation", batch=2, L=1, H=32, P=64, G=2, seed=67,
+               special_scales=NONFINITE_SCALES)
+    run_dense3(oracle, device, "equalizer", batch=1, L=2, H=16, P=64, G=1, seed=68,
+               special_scales=NONFINITE_SCALES)
+    run_dense3(oracle, device, "permutation", batch=1, L=2, H=16, P=18, G=1, seed=70,
+               special_scales=NONFINITE_SCALES)   # the staged kernel
+
+
+def test_packed_rows_non_finite_scales(oracle, device):
+    """Packed rows whose INT8 or INT4 stored scale is +inf, -inf or NaN: the
+    tier maximum is infinite (den = inf) or the updates NaN, for the ridge,
+    stored-scale tier and legacy formats."""
+    run_ridge(oracle, device, "32_32_64", batch=2, L=2, H=32, P=64, G=2, seed=74, special_scales=NONFINITE_SCALES)
+    run_tier(oracle, device, "tier", "24_48_56", batch=2, L=2, H=32, P=64, G=2, seed=75,
+             special_scales=NONFINITE_SCALES)
+    run_tier(oracle, device, "legacy", "16_64_48", batch=2, L=2, H=32, P=64, G=2, seed=76,
+             special_scales=NONFINITE_SCALES)
 
 
 def run_s16(oracle, device, batch, L, H, P, G, seed, collect):
