@@ -11,8 +11,9 @@ bandwidth, a live roofline for the dominant kernel, and the CPU oracle
 timed on a bounded sample as a baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-fp4] [--skip-cpu]
-       python bench.py --only step|copy   (profiling runs: only the batch-64
-       step graph, or only a 256 MiB device copy used to calibrate counters)
+       python bench.py --only step|copy|codecs   (profiling runs: only the
+       batch-64 step graph, only a 256 MiB device copy used to calibrate
+       counters, or only the other codecs' batch-64 graphs)
 """
 from __future__ import annotations
 
@@ -158,20 +159,28 @@ def measured_traffic():
 
 
 def copy_bandwidth(device):
+    """Device-to-device copy (reads and writes interleaved, 1 GiB each way)
+    and a write-only stream (fill of 1 GiB): the two reference rates for the
+    HBM-bound kernels.  Returns (copy GB/s counting both directions, fill GB/s)."""
     a = torch.empty(1 << 30, dtype=torch.uint8, device=device)
     b = torch.empty_like(a)
-    b.copy_(a)
-    torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    for _ in range(10):
-        b.copy_(a)
-    ev1.record()
-    torch.cuda.synchronize()
-    gbs = 2 * a.numel() * 10 / (ev0.elapsed_time(ev1) * 1e-3) / 1e9
+
+    def rate(fn, nbytes):
+        fn()
+        torch.cuda.synchronize()
+        ev0.record()
+        for _ in range(10):
+            fn()
+        ev1.record()
+        torch.cuda.synchronize()
+        return nbytes * 10 / (ev0.elapsed_time(ev1) * 1e-3) / 1e9
+
+    copy_gbs = rate(lambda: b.copy_(a), 2 * a.numel())
+    fill_gbs = rate(lambda: b.fill_(7), b.numel())
     del a, b
     torch.cuda.empty_cache()
-    return gbs
+    return copy_gbs, fill_gbs
 
 
 def fp4_full_decode(device, steps=3):
@@ -311,7 +320,7 @@ def main():
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--skip-fp4", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=("step", "copy"), default=None)
+    ap.add_argument("--only", choices=("step", "copy", "codecs"), default=None)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the state codec and FP4 decode shard with no communication "
@@ -328,6 +337,10 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         print(json.dumps(dict(only="copy", bytes_read=a.numel(), bytes_written=a.numel(), launches=args.steps)))
+        return
+
+    if args.only == "codecs":
+        print(json.dumps(dict(only="codecs", other_codecs_b64=other_codecs(device, steps=args.steps))))
         return
 
     stack = RidgeStack(args.batch, device)
@@ -352,14 +365,16 @@ def main():
     del g1, stack1
     torch.cuda.empty_cache()
 
-    copy_gbs = copy_bandwidth(device)
+    copy_gbs, fill_gbs = copy_bandwidth(device)
     extra = dict(batch1_us_per_token=round(ms1 * 1e3, 2), batch1_gbs=round(step_bytes(1, PUBLISHED_LAYOUTS) / (ms1 * 1e-3) / 1e9, 1),
                  batch64_us_per_token=round(ms * 1e3, 2), wall_ms_per_step=round(wall_ms, 4),
-                 d2d_copy_gbs=round(copy_gbs, 1), hbm_frac_of_copy=round(gbs / copy_gbs, 4))
+                 d2d_copy_gbs=round(copy_gbs, 1), write_only_fill_gbs=round(fill_gbs, 1),
+                 hbm_frac_of_copy=round(gbs / copy_gbs, 4))
     if not args.skip_fp4:
         fp4_ms, fp4_gbs = fp4_full_decode(device)
         extra.update(fp4_g16_full_decode_ms=round(fp4_ms, 3), fp4_g16_full_decode_gbs=round(fp4_gbs, 1),
-                     fp4_g16_full_decode_frac=round(fp4_gbs / HBM_PEAK_GBS, 4))
+                     fp4_g16_full_decode_frac=round(fp4_gbs / HBM_PEAK_GBS, 4),
+                     fp4_g16_frac_of_copy=round(fp4_gbs / copy_gbs, 4))
     extra["other_codecs_b64"] = other_codecs(device)
     line = dict(
         metric=METRIC, value=round(gbs, 2), unit="GB/s", n_gpus=1, steps=args.steps, warmup=args.warmup,
