@@ -282,6 +282,126 @@ def other_codecs(device, batch=64, launches=56, steps=10):
     return out
 
 
+def e2e_decode(device, batches=(1, 16), prefill=8, tokens=32):
+    """BASELINE config 5, with a shortened continuation: a random-init Mamba-2
+    8B model (56 layers, d_model 4096, d_inner 8192, vocab 256000) whose
+    in_proj, out_proj, embedding and lm_head weights are decoded on the device
+    from seeded FP4 G16 packets (uniform nibbles; lognormal block scales sized
+    for unit-variance activations, global = max/448, E4M3 block bytes), with
+    the ridge-latent per-token requantize hook installed on every layer
+    (published layouts, seeded statics).  Greedy decode: a prefill of
+    `prefill` tokens, two untimed steps, then `tokens` timed steps of
+    backbone + lm_head + argmax, eager and replayed as one captured HIP graph
+    per step; the hook's per-call host validation is off (statics are
+    validated once).  Returns ms per generated token per batch size."""
+    import math
+    sys.path.insert(0, str(ROOT / "tests"))
+    import cases
+    from mamba2_model import random_model
+    from mamba2_recall import fp4, ridge_codec
+    model = random_model(device, seed=11)
+    gen = torch.Generator(device=device).manual_seed(12)
+    mats = [model.backbone.embedding.weight, model.lm_head.weight]
+    for layer in model.backbone.layers:
+        mats += [layer.mixer.in_proj.weight, layer.mixer.out_proj.weight]
+    for w in mats:
+        rows, cols = w.shape
+        packed = torch.randint(0, 256, (rows, cols // 2), generator=gen, device=device, dtype=torch.uint8)
+        # E|level|^2 of a uniform nibble is 68.5/8: scales for weight variance 1/cols
+        s = torch.exp(torch.randn((rows, cols // 16), generator=gen, device=device) * 0.5) / math.sqrt(8.5625 * cols)
+        g = (s.max() / 448.0).float().reshape(1)
+        sb = (s / g).clamp(0, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+        fp4.decode_into(packed, sb, g, w.data, rows=rows, columns=cols, group=16)
+        del packed, s, sb
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(13)
+    perms = torch.stack([torch.from_numpy(rng.permutation(128).astype(np.uint8)) for _ in range(56 * 8)])
+    perms = perms.reshape(56, 8, 128)
+    bases, scales, preds = [], [], []
+    for layout in PUBLISHED_LAYOUTS:
+        n8, n4, nz = ridge_counts(layout)
+        st = cases.ridge_statics(rng, G, n8, n4, nz)
+        bases.append(torch.from_numpy(st["basis"].view(np.float16)))
+        scales.append(torch.from_numpy(st["lscale"].view(np.float16)))
+        preds.append(torch.from_numpy(st["pred"].view(np.float16)))
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def snapshot(pq):
+        return [(e.conv.clone(), {k: v.clone() for k, v in e.state.tensors.items()}) for e in pq._cache]
+
+    def restore(pq, snap):
+        for e, (conv, tensors) in zip(pq._cache, snap):
+            e.conv.copy_(conv)
+            for k, v in tensors.items():
+                e.state.tensors[k].copy_(v)
+
+    out = {}
+    with torch.no_grad():
+        for batch in batches:
+            with ridge_codec.PredictorState(model, perms, PUBLISHED_LAYOUTS, bases, scales, preds) as pq:
+                pq.validate_each_step = False
+                ids = torch.randint(0, 256000, (batch, prefill), generator=gen, device=device)
+                h = pq.backbone(ids, reset=True)
+                nxt = model.lm_head(h[:, -1:]).float().argmax(-1)
+                for _ in range(2):
+                    nxt = model.lm_head(pq.backbone(nxt)).float().argmax(-1)
+                torch.cuda.synchronize()
+                snap, start = snapshot(pq), nxt.clone()
+                eager_ids = []
+                ev0.record()
+                for _ in range(tokens):
+                    nxt = model.lm_head(pq.backbone(nxt)).float().argmax(-1)
+                    eager_ids.append(nxt)
+                ev1.record()
+                torch.cuda.synchronize()
+                eager_ms = ev0.elapsed_time(ev1) / tokens
+                eager_state = {k: v.clone() for k, v in pq._cache[0].state.tensors.items()}
+                finite = bool(pq.assert_finite_cache())
+                # the same decode step captured once as a HIP graph: backbone
+                # (56 mixers around the codec kernel), lm_head, argmax, and the
+                # copy of the new token into the graph's input buffer
+                restore(pq, snap)
+                static_ids = start.clone()
+                side = torch.cuda.Stream()
+                side.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(side):   # capture warm-up on snapshots, then restored
+                    static_ids.copy_(model.lm_head(pq.backbone(static_ids)).float().argmax(-1))
+                torch.cuda.current_stream().wait_stream(side)
+                torch.cuda.synchronize()
+                restore(pq, snap)
+                static_ids.copy_(start)
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    static_ids.copy_(model.lm_head(pq.backbone(static_ids)).float().argmax(-1))
+                graph_ids = []
+                for _ in range(tokens):   # replay check: every step against the eager run
+                    graph.replay()
+                    graph_ids.append(static_ids.clone())
+                torch.cuda.synchronize()
+                same = all(torch.equal(a, b) for a, b in zip(eager_ids, graph_ids)) and all(
+                    torch.equal(pq._cache[0].state.tensors[k], v) for k, v in eager_state.items())
+                restore(pq, snap)
+                static_ids.copy_(start)
+                torch.cuda.synchronize()
+                ev0.record()
+                for _ in range(tokens):
+                    graph.replay()
+                ev1.record()
+                torch.cuda.synchronize()
+                graph_ms = ev0.elapsed_time(ev1) / tokens
+                del graph
+            out[f"batch{batch}"] = dict(eager_ms_per_token=round(eager_ms, 3), graph_ms_per_token=round(graph_ms, 3),
+                                        graph_tokens_per_s=round(batch * 1e3 / graph_ms, 1),
+                                        graph_matches_eager=same, finite_cache=finite)
+    del model
+    torch.cuda.empty_cache()
+    out["note"] = (f"random-init 8B, FP16 weights decoded from seeded FP4 G16; ridge hook on 56 layers; prefill "
+                   f"{prefill}, {tokens} timed greedy tokens; PyTorch mixer (GEMMs, conv, gated norm) around the "
+                   f"HIP codec kernel, eager and as one captured HIP graph per decode step (replays checked "
+                   f"token by token and on layer 0's packed state against the eager run)")
+    return out
+
+
 def cpu_baseline(budget_s=12.0):
     """The C oracle (OpenMP over rows) on a bounded sample of the batch-64
     workload: the published layers in order at batch 8, repeated until the
@@ -320,7 +440,8 @@ def main():
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--skip-fp4", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=("step", "copy", "codecs"), default=None)
+    ap.add_argument("--only", choices=("step", "copy", "codecs", "e2e"), default=None)
+    ap.add_argument("--e2e", action="store_true", help="also time the end-to-end 8B decode (BASELINE config 5)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the state codec and FP4 decode shard with no communication "
@@ -339,6 +460,9 @@ def main():
         print(json.dumps(dict(only="copy", bytes_read=a.numel(), bytes_written=a.numel(), launches=args.steps)))
         return
 
+    if args.only == "e2e":
+        print(json.dumps(dict(only="e2e", e2e_decode=e2e_decode(device))))
+        return
     if args.only == "codecs":
         print(json.dumps(dict(only="codecs", other_codecs_b64=other_codecs(device, steps=args.steps))))
         return
@@ -376,6 +500,8 @@ def main():
                      fp4_g16_full_decode_frac=round(fp4_gbs / HBM_PEAK_GBS, 4),
                      fp4_g16_frac_of_copy=round(fp4_gbs / copy_gbs, 4))
     extra["other_codecs_b64"] = other_codecs(device)
+    if args.e2e:
+        extra["e2e_decode"] = e2e_decode(device)
     line = dict(
         metric=METRIC, value=round(gbs, 2), unit="GB/s", n_gpus=1, steps=args.steps, warmup=args.warmup,
         ms_per_step=round(ms, 5), higher_is_better=True, scaling="weak", vs_baseline=None, dtype="f32",

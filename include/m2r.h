@@ -158,6 +158,21 @@ int m2r_probe_div(const float* a, const float* d, float* q, int64_t n, hipStream
  * the canonical adjacent-pair tree sums of in[64..191] / in[0..63]. */
 int m2r_probe_butterfly(const float* in, float* out, hipStream_t stream);
 
+/*
+ * One-token causal depthwise convolution update of the Mamba-2 mixer: roll
+ * the cached window one step, store the new projection column, and write
+ * out = silu(sum_t half(window_t * weight[c,t]) + bias[c]) in binary16.
+ * Replaces the PyTorch fallback of mamba2_recall/state_quant.py:289-297
+ * (the update branch of _convolution), with the same rounding sequence.
+ *   window f16 [B, C, width] addressed through element strides (ws_b, ws_c,
+ *   ws_t), updated in place; value f16 [B, C] with batch stride vs_b (channel
+ *   stride 1); weight f16 [C, width] contiguous; bias f16 [C] or NULL;
+ *   out f16 [B, C] contiguous; width must be 4; silu 1 applies the SiLU.
+ */
+int m2r_causal_conv_update(void* window, int64_t ws_b, int64_t ws_c, int64_t ws_t, const void* value, int64_t vs_b,
+                           const void* weight, const void* bias, void* out, int64_t batch, int64_t channels,
+                           int width, int silu, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,6 +35,7 @@ _SIGNATURES = {
     "m2r_probe_div": ([P, P, P, I64, P], I),
     "m2r_probe_butterfly": ([P, P, P], I),
     "m2r_set_step_shape": ([I, I], I),
+    "m2r_causal_conv_update": ([P, I64, I64, I64, P, I64, P, P, P, I64, I64, I, I, P], I),
 }
 
 

@@ -25,7 +25,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
-from . import state_codec
+from . import _native, state_codec
 
 _OWNERS = weakref.WeakKeyDictionary()
 
@@ -35,6 +35,28 @@ class _LayerCache:
     conv: torch.Tensor
     state: object
     tokens: int = 0
+
+
+def conv_update(window, value, weight, bias, *, silu=True):
+    """One-token causal convolution update on the device (the arithmetic of
+    the reference's PyTorch fallback, state_quant.py:289-297, in one HIP
+    kernel): rolls `window` [B,C,4] in place, appends `value` [B,C] and
+    returns silu(sum(window * weight) + bias) as a new FP16 [B,C] tensor."""
+    if (window.dtype != torch.float16 or value.dtype != torch.float16 or weight.dtype != torch.float16
+            or window.ndim != 3 or value.ndim != 2 or weight.ndim != 2 or window.shape[-1] != 4
+            or tuple(value.shape) != tuple(window.shape[:2]) or tuple(weight.shape) != tuple(window.shape[1:])
+            or value.stride(-1) != 1 or not weight.is_contiguous()
+            or (bias is not None and (bias.dtype != torch.float16 or tuple(bias.shape) != (window.shape[1],)
+                                      or not bias.is_contiguous()))):
+        raise ValueError("Convolution update expects FP16 window [B,C,4], value [B,C], weight [C,4], bias [C]")
+    for t in (window, value, weight) + (() if bias is None else (bias,)):
+        _native.require_device(t, "convolution operand")
+    batch, channels = value.shape
+    out = torch.empty((batch, channels), dtype=torch.float16, device=value.device)
+    _native.call("m2r_causal_conv_update", _native.ptr(window), window.stride(0), window.stride(1), window.stride(2),
+                 _native.ptr(value), value.stride(0), _native.ptr(weight), _native.ptr(bias), _native.ptr(out),
+                 batch, channels, 4, 1 if silu else 0, _native.stream_of(value))
+    return out
 
 
 def _native_conv_ops():
@@ -67,6 +89,7 @@ class _MixerController:
             raise ValueError("The packed state codec requires a CUDA model")
         self.permutations = self._validate_permutations(permutations)
         self._cache = []
+        self._rates = {}
         self._sums = [None] * len(self._mixers)
         self._counts = [0] * len(self._mixers)
         self._originals = []
@@ -262,7 +285,7 @@ class _MixerController:
             x = x.reshape(batch, length, self.HEADS, self.HEADDIM)
             bm = bm.reshape(batch, length, self.GROUPS, self.D_STATE)
             cm = cm.reshape(batch, length, self.GROUPS, self.D_STATE)
-            aa = -torch.exp(mx.A_log.float())
+            aa = self._decay_rates(index, mx)
             y, stats = self._scan_layer(index, mx, x, dt, aa, bm, cm, entry)
             if y.dtype != torch.float16 or tuple(y.shape) != (batch, length, self.HEADS, self.HEADDIM):
                 raise RuntimeError("State codec returned unexpected readout dtype/shape")
@@ -283,6 +306,17 @@ class _MixerController:
             self._failed = True
             raise
 
+    def _decay_rates(self, index, mx):
+        """A = -exp(float(A_log)) of one layer (state_quant.py:256), kept
+        between calls while the parameter is unchanged (same storage and
+        in-place version counter)."""
+        key = (mx.A_log.data_ptr(), mx.A_log._version)
+        cached = self._rates.get(index)
+        if cached is None or cached[0] != key:
+            cached = (key, -torch.exp(mx.A_log.float()))
+            self._rates[index] = cached
+        return cached[1]
+
     def _convolution(self, mx, xbc, entry):
         """Causal depthwise convolution with the cached window
         (state_quant.py:283-317): the one-token update rolls the window; a
@@ -293,12 +327,8 @@ class _MixerController:
         if entry.tokens > 0 and length == 1:
             value = xbc[:, 0, :]
             if update_op is None:
-                entry.conv.copy_(torch.roll(entry.conv, shifts=-1, dims=-1))
-                entry.conv[:, :, -1] = value
-                value = torch.sum(entry.conv * weight, dim=-1)
-                if mx.conv1d.bias is not None:
-                    value = value + mx.conv1d.bias
-                value = mx.act(value).to(dtype=xbc.dtype)
+                value = conv_update(entry.conv, value, weight, mx.conv1d.bias,
+                                    silu=mx.activation in ("silu", "swish"))
             else:
                 value = update_op(value, entry.conv, weight, mx.conv1d.bias, mx.activation)
             return value[:, None, :]
