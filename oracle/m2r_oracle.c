@@ -13,6 +13,7 @@
  *     mamba2_recall/state_codec.py:105-176 (_sq_scan)
  *   - dense 3-bit rows: mamba2_recall/state_codec_dense3.py:82-148 (_scan)
  *   - FP4 decode: mamba2_recall/fp4.py:100-103,151-154,225-250
+ *   - legacy diagnostic encode: mamba2_recall/state_codec.py:299-331
  * Division is C's correctly rounded `/` (the reference's div_rn; its `/`
  * sites are defined the same way), rounding is C roundf (half away from
  * zero), binary16/E4M3FN conversions round to nearest even.  The dead-tier
@@ -482,6 +483,42 @@ int orc_dense3_step(int table_kind, const uint16_t* X, const uint16_t* DT, const
     scales[r * 2 + 1] = orc_f32_to_f16(sc[1]);
   }
   return 0;
+}
+
+/* ------------------------------------------------- legacy diagnostic encode
+ * mamba2_recall/state_codec.py:299-331 (encode_state_, mode sq3p25): for each
+ * row of 128 FP32 coordinates in packed order, s8 = max(amax(|v[0:16]|) /
+ * 127, 1e-8), s4 = max(amax(|v[16:80]|) / 7, 1e-8) in binary32; codes
+ * sign(z) * floor(|z| + 0.5) of z = v / s, clamped to +-127 / +-7; nibble
+ * planes lo/hi (INT8 low and high nibbles, two coordinates per byte) and q4;
+ * stored scales half(s).  Coordinates 80..127 are not stored.
+ */
+static int32_t legacy_code(float v, float s, float limit) {
+  float z = v / s;
+  float sgn = z > 0.0f ? 1.0f : (z < 0.0f ? -1.0f : 0.0f);
+  float m = sgn * floorf(fabsf(z) + 0.5f);
+  return (int32_t)fminf(fmaxf(m, -limit), limit);
+}
+
+void orc_encode_legacy(const float* v, uint8_t* lo, uint8_t* hi, uint8_t* q4, uint16_t* s8, uint16_t* s4,
+                       int64_t rows) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* x = v + r * 128;
+    float m8 = 0.0f, m4 = 0.0f;
+    for (int n = 0; n < 16; ++n) m8 = fmaxf(m8, fabsf(x[n]));
+    for (int n = 16; n < 80; ++n) m4 = fmaxf(m4, fabsf(x[n]));
+    const float d8 = fmaxf(m8 / 127.0f, 1e-8f), d4 = fmaxf(m4 / 7.0f, 1e-8f);
+    int32_t q[80];
+    for (int n = 0; n < 16; ++n) q[n] = legacy_code(x[n], d8, 127.0f);
+    for (int n = 16; n < 80; ++n) q[n] = legacy_code(x[n], d4, 7.0f);
+    for (int j = 0; j < 8; ++j) {
+      lo[r * 8 + j] = (uint8_t)((q[2 * j] & 15) | ((q[2 * j + 1] & 15) << 4));
+      hi[r * 8 + j] = (uint8_t)(((q[2 * j] >> 4) & 15) | (((q[2 * j + 1] >> 4) & 15) << 4));
+    }
+    for (int j = 0; j < 32; ++j) q4[r * 32 + j] = (uint8_t)((q[16 + 2 * j] & 15) | ((q[17 + 2 * j] & 15) << 4));
+    s8[r] = orc_f32_to_f16(d8);
+    s4[r] = orc_f32_to_f16(d4);
+  }
 }
 
 /* ---------------------------------------------------------------- FP4 decode

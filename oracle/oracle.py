@@ -50,6 +50,7 @@ def lib():
         _lib.orc_check_round_identity.restype = I64
         _lib.orc_check_markstein.argtypes = [ctypes.c_uint64, I64, I, P]
         _lib.orc_check_markstein.restype = I64
+        _lib.orc_encode_legacy.argtypes = [P] * 6 + [I64]
         _lib.orc_check_latent_division.argtypes = [ctypes.c_uint64, I]
         _lib.orc_check_latent_division.restype = I64
     return _lib
@@ -155,3 +156,16 @@ def threads():
 
 def check_latent_division(seed: int, n_random_per_scale: int) -> int:
     return int(lib().orc_check_latent_division(seed, n_random_per_scale))
+
+
+def encode_legacy(v):
+    """state_codec.py:299-331 (encode_state_, sq3p25) on FP32 rows [..., 128]
+    in packed order; returns dict lo, hi [..., 8], q4 [..., 32] (uint8) and
+    s8, s4 [...] (binary16 bits)."""
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    lead = v.shape[:-1]
+    rows = int(np.prod(lead))
+    out = dict(lo=np.zeros(lead + (8,), np.uint8), hi=np.zeros(lead + (8,), np.uint8),
+               q4=np.zeros(lead + (32,), np.uint8), s8=np.zeros(lead, np.uint16), s4=np.zeros(lead, np.uint16))
+    lib().orc_encode_legacy(_p(v), _p(out["lo"]), _p(out["hi"]), _p(out["q4"]), _p(out["s8"]), _p(out["s4"]), rows)
+    return out

@@ -472,3 +472,25 @@ def test_ridge_2048_token_drift_batch64(oracle, device):
         got = {kk: rows_of(v) for kk, v in from_state(state).items()}
         assert_state_equal(got, ref_state, f"ridge drift block {k}")
         assert_y_close(y[sub], y_ref, f"ridge drift block {k}")
+
+
+def test_legacy_diagnostic_encode_matches_reference_vectors(device):
+    """m2r_state_encode_legacy through state_codec.encode_state_ against the
+    reference's own encode_state_ outputs (tests/golden/encode_legacy_vectors.npz),
+    bit-exact; and an FP16-overflowing row is rejected before the state is written."""
+    from pathlib import Path
+    from mamba2_recall import state_codec
+    g = np.load(Path(__file__).resolve().parent / "golden" / "encode_legacy_vectors.npz")
+    print("[legacy encode] golden vectors", g["dense"].shape, flush=True)
+    state = state_codec.allocate_state(2, 2, 64, 128, "sq3p25", device)
+    state_codec.encode_state_(state, torch.from_numpy(g["dense"]).to(device))
+    torch.cuda.synchronize()
+    got = from_state(state)
+    for k in ("lo", "hi", "q4", "s8", "s4"):
+        assert np.array_equal(got[k], g[k]), k
+    before = {k: v.clone() for k, v in state.tensors.items()}
+    big = torch.from_numpy(g["dense"]).to(device).clone()
+    big[0, 0, 0, 0] = 1e8
+    with pytest.raises(ValueError, match="Scale exceeds FP16 range"):
+        state_codec.encode_state_(state, big)
+    assert all(torch.equal(before[k], state.tensors[k]) for k in before)

@@ -547,3 +547,23 @@ def test_s16_update_is_fused(oracle):
     inp = _one_row_inputs(0.0, b, x)
     oracle.s16_step(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], inp["dt_bias"], st)
     assert int(st[0, 0, 0, 1]) == code_of(np.array([f]))[0] != code_of(np.array([s]))[0]
+
+
+def test_encode_legacy_matches_reference_vectors(oracle):
+    """The oracle's legacy diagnostic encoder (state_codec.py:299-331) against
+    the reference's own encode_state_ outputs (tests/golden/encode_legacy_vectors.npz,
+    written by tests/golden/make_encode_legacy_vectors.py): every nibble
+    plane byte and stored scale bit-exact, over Gaussian rows, exact
+    half-integer codes and one ulp either side (sign(z)*floor(|z|+0.5) rounds
+    ties away from zero, so a round-half-even encoder fails here), the 1e-8
+    scale floor, zero and signed-zero rows."""
+    g = np.load(Path(__file__).resolve().parent / "golden" / "encode_legacy_vectors.npz")
+    got = oracle.encode_legacy(g["dense"])
+    for k in ("lo", "hi", "q4", "s8", "s4"):
+        assert np.array_equal(got[k], g[k]), k
+    # the tie rows do exercise half-away rounding: an encoder rounding ties to
+    # even gives different codes on them
+    dense = g["dense"].reshape(-1, 128)
+    ties = dense[96:160:3, 1:16]
+    assert np.any(np.abs(ties - np.trunc(ties)) == 0.5)
+    assert not np.array_equal(np.rint(ties), np.sign(ties) * np.floor(np.abs(ties) + 0.5))
