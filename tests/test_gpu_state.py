@@ -494,3 +494,35 @@ def test_legacy_diagnostic_encode_matches_reference_vectors(device):
     with pytest.raises(ValueError, match="Scale exceeds FP16 range"):
         state_codec.encode_state_(state, big)
     assert all(torch.equal(before[k], state.tensors[k]) for k in before)
+
+
+def test_decode_state_matches_reference_vectors(device):
+    """The diagnostic decoders against the reference's own decode_state
+    outputs (tests/golden/decode_state_vectors.npz, written by
+    tests/golden/make_decode_state_vectors.py), bit for bit as FP32 patterns:
+    sq3p25 in packed order and scattered through a permutation; dense 3-bit
+    with no table, a permutation table and an equalizer table.  The packed
+    bytes are arbitrary and the scales include zero, negative zero, a binary16
+    subnormal and a negative value."""
+    from pathlib import Path
+    from mamba2_recall import state_codec, state_codec_dense3
+    g = np.load(Path(__file__).resolve().parent / "golden" / "decode_state_vectors.npz")
+    bits = lambda t: t.cpu().numpy().view(np.uint32)
+    print("[decode_state] sq3p25 and dense3 golden vectors", flush=True)
+    st = state_codec.allocate_state(1, 4, 16, 128, "sq3p25", device)
+    for k in ("lo", "hi", "q4"):
+        st.tensors[k].copy_(torch.from_numpy(g[f"sq_{k}"]).to(device))
+    for k in ("s8", "s4"):
+        st.tensors[k].copy_(torch.from_numpy(g[f"sq_{k}"].view(np.float16)).to(device))
+    perm = torch.from_numpy(g["perm"]).to(device)
+    assert np.array_equal(bits(state_codec.decode_state(st)), g["sq_decode"].view(np.uint32))
+    assert np.array_equal(bits(state_codec.decode_state(st, perm)), g["sq_decode_perm"].view(np.uint32))
+    ds = state_codec_dense3.allocate_state(1, 4, 16, 128, device)
+    ds.tensors["codes"].copy_(torch.from_numpy(g["d3_codes"]).to(device))
+    ds.tensors["scales"].copy_(torch.from_numpy(g["d3_scales"].view(np.float16)).to(device))
+    eq = torch.from_numpy(g["d3_equalizer"]).to(device)
+    assert np.array_equal(bits(state_codec_dense3.decode_state(ds)), g["d3_decode"].view(np.uint32))
+    assert np.array_equal(bits(state_codec_dense3.decode_state(ds, perm, "permutation")),
+                          g["d3_decode_perm"].view(np.uint32))
+    assert np.array_equal(bits(state_codec_dense3.decode_state(ds, eq, "equalizer")),
+                          g["d3_decode_eq"].view(np.uint32))
