@@ -526,3 +526,51 @@ def test_decode_state_matches_reference_vectors(device):
                           g["d3_decode_perm"].view(np.uint32))
     assert np.array_equal(bits(state_codec_dense3.decode_state(ds, eq, "equalizer")),
                           g["d3_decode_eq"].view(np.uint32))
+
+
+@pytest.mark.parametrize("length", [1, 17, 65])
+def test_ridge_reference_fixture_recipe_strided_and_compact(oracle, device, length):
+    """The forward half of the reference's own codec fixture
+    (scripts/check_state_ridge_training_v3.py:19-49): its seed and input
+    recipe (b,h,p,g = 1,8,16,2; one projection split into x*.05, B*.1, C*.1,
+    dt*.03; A = -1, D = 1, dt_bias = -3; basis N*.03, latent scale .001,
+    predictor N*.01; zero state), for the seven layouts, with projection-strided
+    views and compact copies.  The strided and compact scans agree exactly
+    (torch.equal, as the fixture requires of its two paths), and both equal
+    the oracle: packed state bit-exact, y within the tolerance."""
+    from mamba2_recall import ridge_codec
+    torch.manual_seed(2026093007)
+    b, h, p, g = 1, 8, 16, 2
+    for layout in RIDGE_LAYOUTS:
+        n8, n4, nz = ridge_counts(layout)
+        features = n8 + n4 + 2
+        projected = torch.randn(b, length, h * p + 2 * g * 128 + h, device=device).half()
+        xv, bv, cv, dv = torch.split(projected, (h * p, g * 128, g * 128, h), dim=-1)
+        xv.mul_(.05); bv.mul_(.1); cv.mul_(.1); dv.mul_(.03)
+        x, B, C, dt = xv.reshape(b, length, h, p), bv.reshape(b, length, g, 128), cv.reshape(b, length, g, 128), dv
+        if length > 1:
+            assert not all(t.is_contiguous() for t in (x, dt, B, C))
+        A = -torch.ones(h, device=device)
+        D = torch.ones(h, device=device).half()
+        bias = torch.full((h,), -3., device=device).half()
+        table = torch.stack([torch.randperm(128, device=device) for _ in range(g)]).to(torch.uint8)
+        basis = (torch.randn(g, nz, 2, device=device) * .03).half()
+        scale = torch.full((g, 2), .001, device=device).half()
+        predictor = (torch.randn(g, features, nz, device=device) * .01).half()
+        print(f"[ridge fixture recipe] layout={layout} L={length}", flush=True)
+        s_strided = ridge_codec.allocate_state(b, h, p, 128, device, layout=layout)
+        s_compact = ridge_codec.allocate_state(b, h, p, 128, device, layout=layout)
+        y_s, _ = ridge_codec.scan(x, dt, A, B, C, D, bias, s_strided, table, basis, scale, predictor, layout=layout)
+        xc, dtc, Bc, Cc = (t.contiguous() for t in (x, dt, B, C))
+        y_c, _ = ridge_codec.scan(xc, dtc, A, Bc, Cc, D, bias, s_compact, table, basis, scale, predictor,
+                                  layout=layout)
+        torch.cuda.synchronize()
+        assert torch.equal(y_s, y_c)
+        assert all(torch.equal(s_strided.tensors[k], s_compact.tensors[k]) for k in s_compact.tensors)
+        host = lambda t: np.ascontiguousarray(t.cpu().numpy().view(np.uint16))
+        ref_state = cases.zero_packed_state(b, h, p, n8, n4, latent=True)
+        y_ref = oracle.state_step(oracle.MODE_RIDGE, n8, n4, nz, host(xc), host(dtc), A.cpu().numpy(), host(Bc),
+                                  host(Cc), host(D), host(bias), table.cpu().numpy(), host(basis), host(scale),
+                                  host(predictor), ref_state)
+        assert_state_equal(from_state(s_compact), ref_state, f"ridge fixture recipe {layout}")
+        assert_y_close(y_c, y_ref, f"ridge fixture recipe {layout}")
