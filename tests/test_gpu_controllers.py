@@ -145,3 +145,35 @@ def test_tier_and_predictor_controllers(model, device):
     bad[3] = torch.zeros_like(bad[3])
     with pytest.raises(ValueError, match="Static predictor/basis/scale allocation differs"):
         ridge_codec.PredictorState(model, perms, LAYOUTS, bases, bad, preds)
+
+
+def test_repeated_reset_determinism(model, device):
+    """The reference's runtime invariant (run_fp4_ridge_resurface_v3.py:90-99,
+    cache_identity run_fp4_latent_state_quality_v1.py:49-61): two identical
+    requests after a reset give identical hidden states and identical bytes in
+    every cache tensor (convolution windows and packed rows), here for the
+    ridge hook with a prefill and two one-token steps."""
+    from mamba2_recall import ridge_codec
+    perms = tables(device)
+    rng = np.random.default_rng(12)
+    bases, scales, preds = [], [], []
+    for layout in LAYOUTS:
+        n8, n4, nz = cases.ridge_counts(layout)
+        s = cases.ridge_statics(rng, 8, n8, n4, nz)
+        bases.append(torch.from_numpy(s["basis"].view(np.float16)))
+        scales.append(torch.from_numpy(s["lscale"].view(np.float16)))
+        preds.append(torch.from_numpy(s["pred"].view(np.float16)))
+    tok = ids(device, 2, 6, seed=21)
+    runs = []
+    with ridge_codec.PredictorState(model, perms, LAYOUTS, bases, scales, preds) as pq:
+        for attempt in range(2):
+            print(f"[controllers] determinism run {attempt}", flush=True)
+            hs = [pq.backbone(tok[:, :4], reset=True)]
+            hs += [pq.backbone(tok[:, t:t + 1]) for t in (4, 5)]
+            cache = [(e.conv.clone(), {k: v.clone() for k, v in e.state.tensors.items()}) for e in pq._cache]
+            runs.append((hs, cache))
+    (h0, c0), (h1, c1) = runs
+    assert all(torch.equal(a, b) for a, b in zip(h0, h1))
+    for (conv0, st0), (conv1, st1) in zip(c0, c1):
+        assert torch.equal(conv0, conv1)
+        assert all(torch.equal(st0[k], st1[k]) for k in st0)
