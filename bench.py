@@ -282,7 +282,7 @@ def other_codecs(device, batch=64, launches=56, steps=10):
     return out
 
 
-def e2e_decode(device, batches=(1, 16), prefill=8, tokens=32):
+def e2e_decode(device, batches=(1, 4, 16), prefill=8, tokens=32):
     """BASELINE config 5, with a shortened continuation: a random-init Mamba-2
     8B model (56 layers, d_model 4096, d_inner 8192, vocab 256000) whose
     in_proj, out_proj, embedding and lm_head weights are decoded on the device
@@ -292,27 +292,32 @@ def e2e_decode(device, batches=(1, 16), prefill=8, tokens=32):
     (published layouts, seeded statics).  Greedy decode: a prefill of
     `prefill` tokens, two untimed steps, then `tokens` timed steps of
     backbone + lm_head + argmax, eager and replayed as one captured HIP graph
-    per step; the hook's per-call host validation is off (statics are
-    validated once).  Returns ms per generated token per batch size."""
+    per step, with the projections as FP16 GEMMs and (batch sizes the kernel
+    takes) as packed-resident FP4 GEMVs; the hook's per-call host validation
+    is off (statics are validated once).  Returns ms per generated token."""
     import math
+    import torch.nn.functional as F
     sys.path.insert(0, str(ROOT / "tests"))
     import cases
     from mamba2_model import random_model
     from mamba2_recall import fp4, ridge_codec
     model = random_model(device, seed=11)
     gen = torch.Generator(device=device).manual_seed(12)
-    mats = [model.backbone.embedding.weight, model.lm_head.weight]
-    for layer in model.backbone.layers:
-        mats += [layer.mixer.in_proj.weight, layer.mixer.out_proj.weight]
-    for w in mats:
+
+    def packet(w):
         rows, cols = w.shape
         packed = torch.randint(0, 256, (rows, cols // 2), generator=gen, device=device, dtype=torch.uint8)
         # E|level|^2 of a uniform nibble is 68.5/8: scales for weight variance 1/cols
-        s = torch.exp(torch.randn((rows, cols // 16), generator=gen, device=device) * 0.5) / math.sqrt(8.5625 * cols)
-        g = (s.max() / 448.0).float().reshape(1)
-        sb = (s / g).clamp(0, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+        sc = torch.exp(torch.randn((rows, cols // 16), generator=gen, device=device) * 0.5) / math.sqrt(8.5625 * cols)
+        g = (sc.max() / 448.0).float().reshape(1)
+        sb = (sc / g).clamp(0, 448).to(torch.float8_e4m3fn).view(torch.uint8)
         fp4.decode_into(packed, sb, g, w.data, rows=rows, columns=cols, group=16)
-        del packed, s, sb
+        return packed, sb, g
+
+    packet(model.backbone.embedding.weight)
+    packet(model.lm_head.weight)
+    packets = [dict(in_proj=packet(layer.mixer.in_proj.weight), out_proj=packet(layer.mixer.out_proj.weight))
+               for layer in model.backbone.layers]
     torch.cuda.synchronize()
     rng = np.random.default_rng(13)
     perms = torch.stack([torch.from_numpy(rng.permutation(128).astype(np.uint8)) for _ in range(56 * 8)])
@@ -326,6 +331,16 @@ def e2e_decode(device, batches=(1, 16), prefill=8, tokens=32):
         preds.append(torch.from_numpy(st["pred"].view(np.float16)))
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        ev0.record()
+        for _ in range(reps):
+            fn()
+        ev1.record()
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) / reps
+
     def snapshot(pq):
         return [(e.conv.clone(), {k: v.clone() for k, v in e.state.tensors.items()}) for e in pq._cache]
 
@@ -335,8 +350,73 @@ def e2e_decode(device, batches=(1, 16), prefill=8, tokens=32):
             for k, v in tensors.items():
                 e.state.tensors[k].copy_(v)
 
+    def decode_modes(pq, snap, start):
+        """Eager run from the snapshot, the same step captured as a HIP graph,
+        replays checked token by token and on layer 0's packed state."""
+        restore(pq, snap)
+        nxt, eager_ids, first_logits = start.clone(), [], None
+        torch.cuda.synchronize()
+        ev0.record()
+        for i in range(tokens):
+            logits = model.lm_head(pq.backbone(nxt)).float()
+            first_logits = logits.clone() if i == 0 else first_logits
+            nxt = logits.argmax(-1)
+            eager_ids.append(nxt)
+        ev1.record()
+        torch.cuda.synchronize()
+        eager_ms = ev0.elapsed_time(ev1) / tokens
+        eager_state = {k: v.clone() for k, v in pq._cache[0].state.tensors.items()}
+        finite = bool(pq.assert_finite_cache())
+        restore(pq, snap)
+        static_ids = start.clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):   # capture warm-up, then the snapshot is restored
+            static_ids.copy_(model.lm_head(pq.backbone(static_ids)).float().argmax(-1))
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        restore(pq, snap)
+        static_ids.copy_(start)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            static_ids.copy_(model.lm_head(pq.backbone(static_ids)).float().argmax(-1))
+        graph_ids = []
+        for _ in range(tokens):
+            graph.replay()
+            graph_ids.append(static_ids.clone())
+        torch.cuda.synchronize()
+        same = all(torch.equal(a, b) for a, b in zip(eager_ids, graph_ids)) and all(
+            torch.equal(pq._cache[0].state.tensors[k], v) for k, v in eager_state.items())
+        restore(pq, snap)
+        static_ids.copy_(start)
+        graph_ms = timed(graph.replay, tokens)
+        del graph
+        return dict(eager_ms=eager_ms, graph_ms=graph_ms, same=same, finite=finite, logits=first_logits)
+
     out = {}
     with torch.no_grad():
+        # the projections alone, batch 1: FP16 GEMM (hipBLASLt) vs the packed FP4
+        # GEMV, each as a graph of one launch per layer (device time per launch)
+        u1 = torch.randn(1, 4096, generator=gen, device=device).half()
+        u2 = torch.randn(1, 8192, generator=gen, device=device).half()
+        mods = [layer.mixer for layer in model.backbone.layers]
+
+        def graph_us(step):
+            step()
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                step()
+            us = timed(gr.replay, 20) * 1e3 / len(mods)
+            del gr
+            return round(us, 2)
+
+        out["projection_us_batch1"] = dict(
+            in_proj_fp16=graph_us(lambda: [F.linear(u1, m.in_proj.weight) for m in mods]),
+            in_proj_fp4_gemv=graph_us(lambda: [fp4.gemv_g16(*pk["in_proj"], u1) for pk in packets]),
+            out_proj_fp16=graph_us(lambda: [F.linear(u2, m.out_proj.weight) for m in mods]),
+            out_proj_fp4_gemv=graph_us(lambda: [fp4.gemv_g16(*pk["out_proj"], u2) for pk in packets]),
+            note="graph of 56 launches (one per layer's matrix), device time per launch")
         for batch in batches:
             with ridge_codec.PredictorState(model, perms, PUBLISHED_LAYOUTS, bases, scales, preds) as pq:
                 pq.validate_each_step = False
@@ -347,58 +427,28 @@ def e2e_decode(device, batches=(1, 16), prefill=8, tokens=32):
                     nxt = model.lm_head(pq.backbone(nxt)).float().argmax(-1)
                 torch.cuda.synchronize()
                 snap, start = snapshot(pq), nxt.clone()
-                eager_ids = []
-                ev0.record()
-                for _ in range(tokens):
-                    nxt = model.lm_head(pq.backbone(nxt)).float().argmax(-1)
-                    eager_ids.append(nxt)
-                ev1.record()
-                torch.cuda.synchronize()
-                eager_ms = ev0.elapsed_time(ev1) / tokens
-                eager_state = {k: v.clone() for k, v in pq._cache[0].state.tensors.items()}
-                finite = bool(pq.assert_finite_cache())
-                # the same decode step captured once as a HIP graph: backbone
-                # (56 mixers around the codec kernel), lm_head, argmax, and the
-                # copy of the new token into the graph's input buffer
-                restore(pq, snap)
-                static_ids = start.clone()
-                side = torch.cuda.Stream()
-                side.wait_stream(torch.cuda.current_stream())
-                with torch.cuda.stream(side):   # capture warm-up on snapshots, then restored
-                    static_ids.copy_(model.lm_head(pq.backbone(static_ids)).float().argmax(-1))
-                torch.cuda.current_stream().wait_stream(side)
-                torch.cuda.synchronize()
-                restore(pq, snap)
-                static_ids.copy_(start)
-                graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(graph):
-                    static_ids.copy_(model.lm_head(pq.backbone(static_ids)).float().argmax(-1))
-                graph_ids = []
-                for _ in range(tokens):   # replay check: every step against the eager run
-                    graph.replay()
-                    graph_ids.append(static_ids.clone())
-                torch.cuda.synchronize()
-                same = all(torch.equal(a, b) for a, b in zip(eager_ids, graph_ids)) and all(
-                    torch.equal(pq._cache[0].state.tensors[k], v) for k, v in eager_state.items())
-                restore(pq, snap)
-                static_ids.copy_(start)
-                torch.cuda.synchronize()
-                ev0.record()
-                for _ in range(tokens):
-                    graph.replay()
-                ev1.record()
-                torch.cuda.synchronize()
-                graph_ms = ev0.elapsed_time(ev1) / tokens
-                del graph
-            out[f"batch{batch}"] = dict(eager_ms_per_token=round(eager_ms, 3), graph_ms_per_token=round(graph_ms, 3),
-                                        graph_tokens_per_s=round(batch * 1e3 / graph_ms, 1),
-                                        graph_matches_eager=same, finite_cache=finite)
-    del model
+                r16 = decode_modes(pq, snap, start)
+                row = dict(eager_ms_per_token=round(r16["eager_ms"], 3), graph_ms_per_token=round(r16["graph_ms"], 3),
+                           graph_tokens_per_s=round(batch * 1e3 / r16["graph_ms"], 1),
+                           graph_matches_eager=r16["same"], finite_cache=r16["finite"])
+                if fp4.gemv_supported(batch, 4096):
+                    pq.use_packed_projections(packets, verify=(batch == batches[0]))
+                    rp = decode_modes(pq, snap, start)
+                    pq.use_packed_projections(None)
+                    rel = float((rp["logits"] - r16["logits"]).norm() / r16["logits"].norm())
+                    row.update(packed_fp4_graph_ms_per_token=round(rp["graph_ms"], 3),
+                               packed_fp4_graph_tokens_per_s=round(batch * 1e3 / rp["graph_ms"], 1),
+                               packed_fp4_eager_ms_per_token=round(rp["eager_ms"], 3),
+                               packed_fp4_graph_matches_eager=rp["same"], packed_fp4_finite_cache=rp["finite"],
+                               packed_fp4_first_logits_rel_l2_vs_fp16=round(rel, 6))
+            out[f"batch{batch}"] = row
+    del model, packets
     torch.cuda.empty_cache()
     out["note"] = (f"random-init 8B, FP16 weights decoded from seeded FP4 G16; ridge hook on 56 layers; prefill "
                    f"{prefill}, {tokens} timed greedy tokens; PyTorch mixer (GEMMs, conv, gated norm) around the "
                    f"HIP codec kernel, eager and as one captured HIP graph per decode step (replays checked "
-                   f"token by token and on layer 0's packed state against the eager run)")
+                   f"token by token and on layer 0's packed state against the eager run); packed_fp4: the "
+                   f"one-token in_proj/out_proj as packed-resident FP4 G16 GEMVs")
     return out
 
 

@@ -173,6 +173,24 @@ int m2r_causal_conv_update(void* window, int64_t ws_b, int64_t ws_c, int64_t ws_
                            const void* weight, const void* bias, void* out, int64_t batch, int64_t channels,
                            int width, int silu, hipStream_t stream);
 
+/*
+ * Packed-resident FP4 G16 matrix-vector product: y[m, n] = sum_k u[m, k] *
+ * w[n, k] with W read directly in the checkpoint's packed format.  Every
+ * weight is the binary16 value m2r_fp4_decode_g16 produces; products
+ * accumulate in binary32; y is FP16.  No counterpart in the reference, which
+ * decodes the whole model to resident FP16 before its GEMMs
+ * (mamba2_recall/fp4_checkpoint.py:345-405); this is the packed-resident
+ * GEMV that the reference lacks (README.md:40-41), for small-batch decode.
+ *   packed u8[N, K/2] (16-byte aligned), e4m3_scales u8[N, K/16] (2-byte
+ *   aligned), global_scale device f32; u f16 rows of K with row stride
+ *   u_stride (16-byte aligned, u_stride % 8 == 0); y f16 rows of N with row
+ *   stride y_stride.  M in {1, 2, 4}; K in {2048, 4096, 8192}.  The packet
+ *   must satisfy the decode checks (no error word here).
+ */
+int m2r_fp4_gemv_g16(const uint8_t* packed, const uint8_t* e4m3_scales, const float* global_scale, const void* u,
+                     int64_t u_stride, void* y, int64_t y_stride, int64_t M, int64_t N, int64_t K,
+                     hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -36,6 +36,7 @@ _SIGNATURES = {
     "m2r_probe_butterfly": ([P, P, P], I),
     "m2r_set_step_shape": ([I, I], I),
     "m2r_causal_conv_update": ([P, I64, I64, I64, P, I64, P, P, P, I64, I64, I, I, P], I),
+    "m2r_fp4_gemv_g16": ([P, P, P, P, I64, P, I64, I64, I64, I64, P], I),
 }
 
 

@@ -102,6 +102,49 @@ def decode_into(packed, scales, global_scale, out, *, rows, columns, group, err_
     return out
 
 
+GEMV_ROWS = (1, 2, 4)
+
+
+GEMV_COLUMNS = (2048, 4096, 8192)
+
+
+def gemv_supported(rows, columns):
+    """Whether gemv_g16 takes `rows` activation rows against a matrix of
+    `columns` inputs (1, 2 or 4 rows; 2048, 4096 or 8192 columns)."""
+    return rows in GEMV_ROWS and columns in GEMV_COLUMNS
+
+
+def gemv_g16(packed, scales, global_scale, u, *, out=None):
+    """y = u @ W.T for the FP4 G16 matrix W [N, K] kept packed (codes u8
+    [N, K/2], E4M3 block bytes u8 [N, K/16], device FP32 global scalar) and
+    FP16 activations u [M, K] (M in 1, 2, 4): the HIP kernel reads the packed
+    format directly and uses, for every weight, the binary16 value
+    decode_packet gives; products accumulate in binary32 and y is FP16
+    [M, N].  The packet must satisfy decode_packet's checks.  No host
+    synchronization."""
+    _need(isinstance(u, torch.Tensor) and u.dtype == torch.float16 and u.ndim == 2, "u must be FP16 [rows, K]")
+    rows, columns = u.shape
+    _need(packed.dtype == torch.uint8 and packed.ndim == 2 and packed.shape[1] * 2 == columns,
+          "packed codes must be uint8 [N, K/2]")
+    n = packed.shape[0]
+    sb = scales.view(torch.uint8) if scales.dtype == torch.float8_e4m3fn else scales
+    _need(sb.dtype == torch.uint8 and tuple(sb.shape) == (n, columns // 16), "block scales must be [N, K/16]")
+    _need(gemv_supported(rows, columns), "gemv_g16 supports 1, 2 or 4 rows and K of 2048, 4096 or 8192")
+    for t in (packed, sb, u, global_scale):
+        _native.require_device(t, "gemv operand")
+    packed, sb = packed.contiguous(), sb.contiguous()
+    if u.stride(1) != 1 or u.stride(0) % 8 or u.data_ptr() % 16:
+        u = u.contiguous()
+    if out is None:
+        out = torch.empty((rows, n), dtype=torch.float16, device=u.device)
+    _need(out.dtype == torch.float16 and tuple(out.shape) == (rows, n) and out.stride(1) == 1, "out must be FP16 [M, N]")
+    with torch.cuda.device(u.device):
+        _native.call("m2r_fp4_gemv_g16", _native.ptr(packed), _native.ptr(sb), _native.ptr(global_scale),
+                     _native.ptr(u), u.stride(0), _native.ptr(out), out.stride(0), rows, n, columns,
+                     _native.stream_of(u))
+    return out
+
+
 @torch.no_grad()
 def decode_packet(packet):
     """fp4.py:225-250: validate a packet and return its FP16 [rows, columns]

@@ -25,7 +25,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
-from . import _native, state_codec
+from . import _native, fp4, state_codec
 
 _OWNERS = weakref.WeakKeyDictionary()
 
@@ -90,6 +90,7 @@ class _MixerController:
         self.permutations = self._validate_permutations(permutations)
         self._cache = []
         self._rates = {}
+        self._packed = None
         self._sums = [None] * len(self._mixers)
         self._counts = [0] * len(self._mixers)
         self._originals = []
@@ -275,7 +276,7 @@ class _MixerController:
         try:
             # a one-token continuation keeps the native rank-two GEMM / norm shapes
             is_step = entry.tokens > 0 and length == 1
-            projected = mx.in_proj(u.squeeze(1) if is_step else u)
+            projected = self._project(index, "in_proj", mx, u.squeeze(1)) if is_step else mx.in_proj(u)
             zxbcdt = projected.unsqueeze(1) if is_step else projected
             bc = self.GROUPS * self.D_STATE
             z, xbc, dt = torch.split(zxbcdt, (self.D_INNER, self.D_INNER + 2 * bc, self.HEADS), dim=-1)
@@ -294,7 +295,7 @@ class _MixerController:
             # the gated norm stays a module call: external norm hooks see (y, z)
             y = y.reshape(batch, length, self.D_INNER)
             if is_step:
-                out = mx.out_proj(mx.norm(y[:, 0], z[:, 0])).unsqueeze(1)
+                out = self._project(index, "out_proj", mx, mx.norm(y[:, 0], z[:, 0])).unsqueeze(1)
             else:
                 out = mx.out_proj(mx.norm(y, z))
             entry.tokens += length
@@ -305,6 +306,57 @@ class _MixerController:
         except Exception:
             self._failed = True
             raise
+
+    def use_packed_projections(self, packets, verify=False):
+        """Run the one-token in_proj and out_proj of every layer as
+        packed-resident FP4 G16 GEMVs (fp4.gemv_g16) instead of FP16 GEMMs.
+        `packets[i]` is dict(in_proj=(codes, scales, global), out_proj=(...))
+        in the checkpoint's G16 format for layer i, or None to keep that
+        layer on its modules; `packets=None` turns the mode off.  The weights
+        the GEMV uses are the binary16 values of decode_packet, so only the
+        summation order of the projections changes; prefill steps and batch
+        sizes the GEMV does not take keep the modules.  `verify=True` decodes
+        every packet once and requires it to equal the module's weight bit
+        for bit."""
+        if packets is None:
+            self._packed = None
+            return self
+        if len(packets) != len(self._mixers):
+            raise ValueError("One packed-projection entry per layer required")
+        checked = []
+        for mx, entry in zip(self._mixers, packets):
+            if entry is None:
+                checked.append(None)
+                continue
+            pair = {}
+            for name in ("in_proj", "out_proj"):
+                module = getattr(mx, name)
+                codes, scales, global_scale = entry[name]
+                rows, cols = module.weight.shape
+                if (module.bias is not None or codes.dtype != torch.uint8 or tuple(codes.shape) != (rows, cols // 2)
+                        or tuple(scales.shape) != (rows, cols // 16) or codes.device != self.device
+                        or scales.device != self.device or global_scale.device != self.device
+                        or global_scale.numel() != 1 or global_scale.dtype != torch.float32):
+                    raise ValueError(f"Packed {name} does not match the layer's projection")
+                sb = scales.view(torch.uint8) if scales.dtype == torch.float8_e4m3fn else scales
+                if verify:
+                    decoded = fp4.decode_packet(dict(format="fp4_g16_e4m3", shape=[rows, cols], group_size=16,
+                                                     packed=codes, scales=sb.view(torch.float8_e4m3fn),
+                                                     global_scale=global_scale.reshape(())))
+                    if not torch.equal(decoded.view(torch.int16), module.weight.view(torch.int16)):
+                        raise ValueError(f"Packed {name} does not decode to the module's weight")
+                pair[name] = (codes.contiguous(), sb.contiguous(), global_scale.reshape(1))
+            checked.append(pair)
+        self._packed = checked
+        return self
+
+    def _project(self, index, name, mx, value):
+        """One-token projection: the packed GEMV when registered and the batch
+        size is supported, else the module."""
+        entry = self._packed[index] if self._packed is not None else None
+        if entry is not None and fp4.gemv_supported(value.shape[0], value.shape[1]):
+            return fp4.gemv_g16(*entry[name], value)
+        return getattr(mx, name)(value)
 
     def _decay_rates(self, index, mx):
         """A = -exp(float(A_log)) of one layer (state_quant.py:256), kept

@@ -121,3 +121,36 @@ def test_decode_errors_follow_reference_order(device):
     p2[:, -1] |= 0x30                                         # padding nibble (column 41) nonzero
     with pytest.raises(ValueError, match="Nonzero final-group padding"):
         decode_dev(p2, s2, g2, 2, 40, device)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 18560, 4096), (2, 1000, 4096), (4, 333, 4096), (1, 4096, 8192),
+                                   (2, 257, 8192), (4, 101, 8192), (1, 100, 2048), (4, 63, 2048), (1, 1, 4096)])
+def test_fp4_gemv_matches_decoded_weights(device, M, N, K):
+    """fp4.gemv_g16 (packed-resident FP4 G16 GEMV) against the product with
+    the decoded FP16 weights (decode_packet, bit-exact to the oracle) in
+    float64: relative L2 <= 1e-3 (north_star tolerance), and every output
+    within one binary16 ulp plus the binary32 accumulation bound K * 2^-22 *
+    sum|u w|.  Packets in the reference G16 format, with some zero-scale
+    groups holding codes 0 and 8."""
+    import torch
+    from mamba2_recall import fp4
+    gen = torch.Generator(device=device).manual_seed(M * 7919 + N)
+    print(f"[fp4 gemv] M={M} N={N} K={K}", flush=True)
+    packed = torch.randint(0, 256, (N, K // 2), generator=gen, device=device, dtype=torch.uint8)
+    s = torch.exp(torch.randn((N, K // 16), generator=gen, device=device) * 0.5 - 3.0)
+    g = (s.max() / 448.0).float().reshape(1)
+    sb = (s / g).clamp(0, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+    zero = torch.rand((N, K // 16), generator=gen, device=device) < 0.02
+    sb = torch.where(zero, torch.zeros_like(sb), sb)
+    codes = packed.view(N, K // 16, 8)
+    codes = torch.where(zero[..., None], codes & 0x88, codes).view(N, K // 2)
+    w = fp4.decode_packet(dict(format="fp4_g16_e4m3", shape=[N, K], group_size=16, packed=codes,
+                               scales=sb.view(torch.float8_e4m3fn), global_scale=g.reshape(())))
+    u = torch.randn((M, K), generator=gen, device=device).half()
+    y = fp4.gemv_g16(codes, sb, g, u)
+    ref = u.double() @ w.double().T
+    torch.cuda.synchronize()
+    err = (y.double() - ref).norm() / ref.norm()
+    assert float(err) <= 1e-3, float(err)
+    bound = (ref.abs() * 2.0 ** -11 + (u.double().abs() @ w.double().abs().T) * K * 2.0 ** -22 + 2.0 ** -24)
+    assert bool(((y.double() - ref).abs() <= bound).all())
