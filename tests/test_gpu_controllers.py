@@ -177,3 +177,58 @@ def test_repeated_reset_determinism(model, device):
     for (conv0, st0), (conv1, st1) in zip(c0, c1):
         assert torch.equal(conv0, conv1)
         assert all(torch.equal(st0[k], st1[k]) for k in st0)
+
+
+def test_packed_projections(model, device):
+    """use_packed_projections: the one-token in_proj/out_proj as packed FP4
+    GEMVs.  Packets whose decode equals the module weights pass verify=True
+    (the model's projections are first overwritten by the decode of seeded G16
+    packets); a packet that decodes differently is rejected; a one-token step
+    with the packed projections matches the FP16-module step within the
+    summation-order tolerance; prefill keeps the modules."""
+    import math
+    from mamba2_recall import fp4, ridge_codec
+    gen = torch.Generator(device=device).manual_seed(31)
+
+    def packet(w):
+        rows, cols = w.shape
+        packed = torch.randint(0, 256, (rows, cols // 2), generator=gen, device=device, dtype=torch.uint8)
+        s = torch.exp(torch.randn((rows, cols // 16), generator=gen, device=device) * 0.5) / math.sqrt(8.5625 * cols)
+        g = (s.max() / 448.0).float().reshape(1)
+        sb = (s / g).clamp(0, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+        fp4.decode_into(packed, sb, g, w.data, rows=rows, columns=cols, group=16)
+        return packed, sb, g
+
+    print("[controllers] packed projections: writing decoded packets into the projections", flush=True)
+    packets = [dict(in_proj=packet(layer.mixer.in_proj.weight), out_proj=packet(layer.mixer.out_proj.weight))
+               for layer in model.backbone.layers]
+    perms = tables(device)
+    rng = np.random.default_rng(14)
+    bases, scales, preds = [], [], []
+    for layout in LAYOUTS:
+        n8, n4, nz = cases.ridge_counts(layout)
+        s = cases.ridge_statics(rng, 8, n8, n4, nz)
+        bases.append(torch.from_numpy(s["basis"].view(np.float16)))
+        scales.append(torch.from_numpy(s["lscale"].view(np.float16)))
+        preds.append(torch.from_numpy(s["pred"].view(np.float16)))
+    tok = ids(device, 2, 5, seed=33)
+    with ridge_codec.PredictorState(model, perms, LAYOUTS, bases, scales, preds) as pq:
+        bad = list(packets)
+        bad[5] = dict(in_proj=packets[6]["in_proj"], out_proj=packets[5]["out_proj"])
+        with pytest.raises(ValueError, match="does not decode to the module's weight"):
+            pq.use_packed_projections(bad, verify=True)
+        pq.backbone(tok[:, :4], reset=True)
+        snap = [(e.conv.clone(), {k: v.clone() for k, v in e.state.tensors.items()}) for e in pq._cache]
+        h16 = pq.backbone(tok[:, 4:5])
+        for e, (conv, tensors) in zip(pq._cache, snap):
+            e.conv.copy_(conv)
+            for k, v in tensors.items():
+                e.state.tensors[k].copy_(v)
+            e.tokens -= 1
+        pq.use_packed_projections(packets, verify=True)
+        hp = pq.backbone(tok[:, 4:5])
+        pq.use_packed_projections(None)
+        torch.cuda.synchronize()
+        err = float((hp.float() - h16.float()).norm() / h16.float().norm())
+        print(f"[controllers] packed vs FP16 one-token hidden rel L2 {err:.2e}", flush=True)
+        assert bool(torch.isfinite(hp).all()) and err < 2e-2
