@@ -452,6 +452,57 @@ def e2e_decode(device, batches=(1, 4, 16), prefill=8, tokens=32):
     return out
 
 
+def loader_bench(device, layers=8, shard_limit=256 << 20):
+    """The packed-checkpoint loader (fp4_checkpoint.load_packed_tensors) on a
+    synthetic checkpoint in the reference's shard format: `layers` layers'
+    in_proj [18560, 4096] and out_proj [4096, 8192] as FP4 G16 parts of at
+    most `shard_limit` bytes, written to a temporary directory (so read from
+    the page cache), then loaded: pinned host buffers, host-to-device copies
+    and the device decode into resident FP16.  Returns the rates over packed
+    (file) bytes and decoded bytes."""
+    import tempfile
+    from mamba2_recall import fp4_checkpoint as ck
+    ledger = {"tensors": {}}
+    for i in range(layers):
+        ledger["tensors"][f"backbone.layers.{i}.mixer.in_proj.weight"] = {"kind": "fp4_g16_e4m3", "shape": [18560, 4096]}
+        ledger["tensors"][f"backbone.layers.{i}.mixer.out_proj.weight"] = {"kind": "fp4_g16_e4m3", "shape": [4096, 8192]}
+    plan = ck.make_plan(ledger, shard_limit)
+    rng = np.random.default_rng(21)
+    packed_bytes = decoded_bytes = 0
+    with tempfile.TemporaryDirectory() as tmp:
+        tmp = Path(tmp)
+        headers = {f: ck._create_shard(tmp / f, spec) for f, spec in ck._file_specs(plan).items()}
+
+        def write(path, key, data):
+            base, header = headers[path]
+            begin, end = header[key]["data_offsets"]
+            with open(tmp / path, "r+b") as f:
+                f.seek(base + begin)
+                f.write(data)
+
+        for name, item in sorted(plan.items()):
+            rows, cols = item["shape"]
+            write(item["global_scale_file"], "global_scale", np.float32(0.01).tobytes())
+            for part in item["parts"]:
+                n = part["row_stop"] - part["row_start"]
+                write(part["file"], "codes", rng.integers(0, 256, (n, cols // 2), dtype=np.uint8).tobytes())
+                write(part["file"], "block_scale_bytes", rng.integers(0x20, 0x60, (n, cols // 16), dtype=np.uint8).tobytes())
+            packed_bytes += rows * cols // 2 + rows * cols // 16 + 4
+            decoded_bytes += rows * cols * 2
+        ck.load_packed_tensors(tmp, plan, device=device)   # warm-up: page cache and pinned buffers
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        tensors = ck.load_packed_tensors(tmp, plan, device=device)
+        torch.cuda.synchronize()
+        secs = time.perf_counter() - t0
+        del tensors
+    torch.cuda.empty_cache()
+    return dict(matrices=len(plan), packed_bytes=packed_bytes, seconds=round(secs, 4),
+                packed_gbs=round(packed_bytes / secs / 1e9, 2), decoded_gbs=round(decoded_bytes / secs / 1e9, 2),
+                note="synthetic checkpoint in the reference shard format, files in the page cache; pinned host "
+                     "buffers, host-to-device copies and device decode; wall clock")
+
+
 def cpu_baseline(budget_s=12.0):
     """The C oracle (OpenMP over rows) on a bounded sample of the batch-64
     workload: the published layers in order at batch 8, repeated until the
@@ -490,7 +541,7 @@ def main():
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--skip-fp4", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=("step", "copy", "codecs", "e2e"), default=None)
+    ap.add_argument("--only", choices=("step", "copy", "codecs", "e2e", "loader"), default=None)
     ap.add_argument("--e2e", action="store_true", help="also time the end-to-end 8B decode (BASELINE config 5)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -510,6 +561,9 @@ def main():
         print(json.dumps(dict(only="copy", bytes_read=a.numel(), bytes_written=a.numel(), launches=args.steps)))
         return
 
+    if args.only == "loader":
+        print(json.dumps(dict(only="loader", loader=loader_bench(device))))
+        return
     if args.only == "e2e":
         print(json.dumps(dict(only="e2e", e2e_decode=e2e_decode(device))))
         return
