@@ -444,6 +444,23 @@ class _MixerController:
         raise NotImplementedError
 
 
+def permutations_from_statistics(statistics):
+    """run_statequant.py:81-83: the sq3p25 permutation table of a calibration.
+
+    ``statistics`` is the dict ``StateQuant.statistics()`` returns (or its
+    ``mean_abs`` tensor [layers, groups, 128]).  Each (layer, group) row lists
+    the coordinates by decreasing mean |FP16 carry|, equal means in coordinate
+    order (a stable sort), as uint8: the first 16 become the INT8 tier, the
+    next 64 the INT4 tier.  RuntimeError for non-finite statistics, as the
+    reference raises before sorting."""
+    mean_abs = statistics["mean_abs"] if isinstance(statistics, dict) else statistics
+    if not isinstance(mean_abs, torch.Tensor) or mean_abs.ndim != 3 or mean_abs.shape[-1] != state_codec.N:
+        raise ValueError("Expected calibration mean_abs [layers,groups,128]")
+    if not bool(torch.isfinite(mean_abs).all()):
+        raise RuntimeError("Nonfinite calibration statistics")
+    return torch.argsort(mean_abs, dim=-1, descending=True, stable=True).to(torch.uint8)
+
+
 class StateQuant(_MixerController):
     """Sequential s16 control or packed sq3p25 carry (state_quant.py:41-79).
 

@@ -95,6 +95,18 @@ def test_state_quant_s16_statistics(model, device):
         assert st["sum_abs"].shape == (56, 8, 128) and st["sum_abs"].dtype == torch.float64
         assert st["sample_count_per_group"].tolist() == [2 * 4 * 16 * 64] * 56
         assert bool(torch.isfinite(st["mean_abs"]).all())
+    # the reference's calibration flow (run_statequant.py:81-83): the table
+    # from these statistics drives a packed sq3p25 run
+    from mamba2_recall.state_quant import permutations_from_statistics
+    table = permutations_from_statistics(st)
+    assert table.dtype == torch.uint8 and tuple(table.shape) == (56, 8, 128)
+    ordered = torch.gather(st["mean_abs"], -1, table.long())
+    assert bool((ordered[..., :-1] >= ordered[..., 1:]).all())
+    with StateQuant(model, mode="sq3p25", permutations=table) as sq:
+        print("[controllers] sq3p25 with the calibrated table", flush=True)
+        h = sq.backbone(ids(device, 2, 3))
+        h = sq.backbone(ids(device, 2, 1, seed=6))
+        assert bool(torch.isfinite(h).all())
 
 
 @pytest.mark.parametrize("kind", ["permutation", "equalizer"])
