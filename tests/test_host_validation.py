@@ -1,0 +1,131 @@
+"""Host-side checks of the drop-in surface, on CPU tensors (no device work).
+
+The layout mapping is pinned by the layout triples of the reference's codec
+fixtures (`docs/evidence/fp_state_diagnostics/v12,v14/codec_fixture.json`:
+parent 'A_B_C' -> (A, B-4, C+4)); the allocation checks by the 52-byte row
+(`README.md:123`: 425,984 B per layer at batch 1).  Error classes and
+messages follow the reference's validators (cited per test).
+"""
+import pytest
+import torch
+
+from mamba2_recall import ridge_codec, state_codec, state_codec_dense3, tier_codec
+
+PUBLISHED = {  # layout: (n8, n4, nz, F)
+    "36_24_68": (36, 20, 72, 58), "16_64_48": (16, 60, 52, 78), "32_32_64": (32, 28, 68, 62),
+    "40_16_72": (40, 12, 76, 54), "24_48_56": (24, 44, 60, 70), "8_80_40": (8, 76, 44, 86),
+    "44_8_76": (44, 4, 80, 50),
+}
+
+
+@pytest.mark.parametrize("layout", sorted(PUBLISHED))
+def test_ridge_layout_mapping(layout):
+    d = ridge_codec.layout_descriptor(layout)
+    n8, n4, nz, features = PUBLISHED[layout]
+    assert (d["n8"], d["n4"], d["nzero"]) == (n8, n4, nz)
+    assert d["n8"] + d["n4"] + 2 == features
+    assert d["row_bytes"] == 52 and sum(d["tensor_widths"].values()) + 4 == 52
+
+
+def test_tier_layout_rejects_unknown():
+    # w4_state_repair_codec_v2.py:34-37
+    with pytest.raises(ValueError, match="Unknown fixed W4 state repair tier layout"):
+        tier_codec.layout_descriptor("36_24_69")
+    with pytest.raises(ValueError):
+        ridge_codec.layout_descriptor("not_a_layout")
+
+
+@pytest.mark.parametrize("layout", ["36_24_68", "8_80_40"])
+def test_ridge_state_allocation_and_validation(layout):
+    # fp4_zero_predictor_codec_v1.py:39-73
+    st = ridge_codec.allocate_state(1, 128, 64, 128, "cpu", layout=layout)
+    assert st.nbytes == 425_984
+    assert ridge_codec.validate_state(st, "cpu", layout)
+    with pytest.raises(ValueError, match="mode/inventory"):
+        ridge_codec.validate_state(st, "cpu", "44_8_76" if layout != "44_8_76" else "36_24_68")
+    lo = st.tensors["lo"]
+    st.tensors["lo"] = torch.zeros(lo.shape[:-1] + (lo.shape[-1] * 2,), dtype=torch.uint8)[..., ::2]
+    with pytest.raises(ValueError, match="backing allocation differs: lo"):
+        ridge_codec.validate_state(st, "cpu", layout)
+    st.tensors["lo"] = st.tensors["hi"]    # same shape and dtype, shared storage
+    with pytest.raises(ValueError, match="aliases"):
+        ridge_codec.validate_state(st, "cpu", layout)
+
+
+@pytest.mark.parametrize("args", [(1, 128, 64, 64), (0, 128, 64, 128), (1.0, 128, 64, 128)])
+def test_ridge_allocation_rejects_geometry(args):
+    with pytest.raises(ValueError, match="dstate=128"):
+        ridge_codec.allocate_state(*args, "cpu", layout="32_32_64")
+
+
+def test_legacy_state_is_52_bytes_per_row():
+    # state_codec.py:51-62
+    st = state_codec.allocate_state(2, 128, 64, 128, "sq3p25", "cpu")
+    assert sum(t.numel() * t.element_size() for t in st.tensors.values()) == 2 * 8192 * 52
+
+
+def test_permutation_validation():
+    # state_codec.py:179-184
+    perm = torch.stack([torch.randperm(128) for _ in range(8)]).to(torch.uint8)
+    state_codec.validate_permutation(perm, 8)
+    bad = perm.clone()
+    bad[5, 0] = bad[5, 1]
+    with pytest.raises(ValueError, match="exactly once"):
+        state_codec.validate_permutation(bad, 8)
+    with pytest.raises(ValueError, match="uint8"):
+        state_codec.validate_permutation(perm.long(), 8)
+    with pytest.raises(ValueError, match="uint8"):
+        state_codec.validate_permutation(perm[:7], 8)
+
+
+def test_dense3_table_validation():
+    # state_codec_dense3.py:53-64
+    perm = torch.stack([torch.randperm(128) for _ in range(8)]).to(torch.uint8)
+    state_codec_dense3.validate_table(perm, 8, "permutation")
+    eq = torch.randint(-8, 9, (8, 128), dtype=torch.int8)
+    state_codec_dense3.validate_table(eq, 8, "equalizer")
+    with pytest.raises(ValueError, match="kind"):
+        state_codec_dense3.validate_table(perm, 8, "both")
+    with pytest.raises(ValueError, match="dtype or shape"):
+        state_codec_dense3.validate_table(eq, 8, "permutation")
+    dup = perm.clone()
+    dup[2, 7] = dup[2, 9]
+    with pytest.raises(ValueError, match="exactly"):
+        state_codec_dense3.validate_table(dup, 8, "permutation")
+    for v in (-9, 9):
+        hot = eq.clone()
+        hot[4, 100] = v
+        with pytest.raises(ValueError, match=r"\[-8,8\]"):
+            state_codec_dense3.validate_table(hot, 8, "equalizer")
+
+
+def test_dense3_allocation():
+    # state_codec_dense3.py:43-50
+    st = state_codec_dense3.allocate_state(1, 128, 64, 128, "cpu")
+    assert sum(t.numel() * t.element_size() for t in st.tensors.values()) == 425_984
+    with pytest.raises(ValueError, match="dstate128"):
+        state_codec_dense3.allocate_state(1, 128, 64, 127, "cpu")
+
+
+def scan_inputs(batch=1, L=1):
+    x = torch.zeros(batch, L, 128, 64, dtype=torch.float16)
+    dt = torch.zeros(batch, L, 128, dtype=torch.float16)
+    A = -torch.ones(128)
+    B = torch.zeros(batch, L, 8, 128, dtype=torch.float16)
+    return x, dt, A, B, B.clone(), torch.zeros(128, dtype=torch.float16), torch.zeros(128, dtype=torch.float16)
+
+
+def test_scans_reject_host_tensors():
+    # state_codec.py:203-210, state_codec_dense3.py:151-160, fp4_zero_predictor_codec_v1.py:185-195:
+    # every scan requires device FP16 x before anything else
+    x, dt, A, B, C, D, db = scan_inputs()
+    st = state_codec.allocate_state(1, 128, 64, 128, "sq3p25", "cpu")
+    perm = torch.stack([torch.randperm(128) for _ in range(8)]).to(torch.uint8)
+    with pytest.raises(ValueError, match="x must be CUDA FP16"):
+        state_codec.scan(x, dt, A, B, C, D, db, st, permutation=perm)
+    d3 = state_codec_dense3.allocate_state(1, 128, 64, 128, "cpu")
+    with pytest.raises(ValueError, match="x must be CUDA FP16"):
+        state_codec_dense3.scan(x, dt, A, B, C, D, db, d3, perm)
+    rs = ridge_codec.allocate_state(1, 128, 64, 128, "cpu", layout="32_32_64")
+    with pytest.raises(ValueError, match="x must be CUDA FP16"):
+        ridge_codec.scan(x, dt, A, B, C, D, db, rs, perm, None, None, None, layout="32_32_64")
