@@ -8,7 +8,7 @@ HIP graph; inputs and packed states are resident in HBM.  Also reported:
 the same step at batch 1 (µs/token, graph of 56 launches), the full 8B FP4
 G16 decode, the measured device-to-device copy
 bandwidth, a live roofline for the dominant kernel, and the CPU oracle
-timed on a bounded sample as a baseline.
+timed on a bounded sample (state step and FP4 decode) as a baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-fp4] [--skip-cpu]
        python bench.py --only step|copy|codecs   (profiling runs: only the
@@ -503,10 +503,11 @@ def loader_bench(device, layers=8, shard_limit=256 << 20):
                      "buffers, host-to-device copies and device decode; wall clock")
 
 
-def cpu_baseline(budget_s=12.0):
+def cpu_baseline(budget_s=12.0, fp4_budget_s=3.0):
     """The C oracle (OpenMP over rows) on a bounded sample of the batch-64
     workload: the published layers in order at batch 8, repeated until the
-    budget is spent; throughput in algorithmic GB/s."""
+    budget is spent; throughput in algorithmic GB/s.  Beside it, the oracle's
+    FP4 G16 decode on a bounded sample of the full-set workload."""
     sys.path.insert(0, str(ROOT / "tests"))
     import cases
     from oracle import oracle
@@ -528,9 +529,27 @@ def cpu_baseline(budget_s=12.0):
         if elapsed >= budget_s:
             break
     cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    # FP4 G16 decode: one in_proj and one out_proj matrix per round (the
+    # reference's sample for the full-set rate), algorithmic bytes = codes +
+    # block scales + FP16 output
+    fp4_bytes, fp4_s, rounds = 0, 0.0, 0
+    while fp4_s < fp4_budget_s:
+        for rows, cols in ((18560, 4096), (4096, 8192)):
+            codes = rng.integers(0, 256, (rows, cols // 2), dtype=np.uint8)
+            blocks = rng.integers(0x30, 0x48, (rows, cols // 16), dtype=np.uint8)
+            t0 = time.perf_counter()
+            _, err = oracle.fp4_decode(16, codes, blocks, 1.0 / 448.0, rows, cols)
+            fp4_s += time.perf_counter() - t0
+            if err:
+                raise RuntimeError(f"CPU FP4 baseline: decode rejected a valid packet (bits {err})")
+            fp4_bytes += rows * cols // 2 + rows * cols // 16 + 2 * rows * cols
+        rounds += 1
     return dict(value=round(done_bytes / elapsed / 1e9, 4), unit="GB/s", cores=cores, kind="port",
                 sample=f"C oracle (OpenMP over rows), {layers} published ridge layer steps in order at batch "
-                       f"{batch}, 1 token each, {elapsed:.1f} s")
+                       f"{batch}, 1 token each, {elapsed:.1f} s",
+                fp4_g16_decode=dict(value=round(fp4_bytes / fp4_s / 1e9, 3), unit="GB/s", cores=cores, kind="port",
+                                    sample=f"C oracle, {rounds} x (in_proj [18560,4096] + out_proj [4096,8192]), "
+                                           f"{fp4_s:.1f} s"))
 
 
 def main():
