@@ -393,6 +393,7 @@ def load_packed_model(directory, *, device="cuda", chunk_rows=512, progress=None
         else:
             raise ValueError("Unknown native tensor: " + name)
     need(not any(t.is_meta for t in model.state_dict().values()), "Incomplete packed checkpoint reload")
+    need(model.backbone.embedding.weight.data_ptr() != model.lm_head.weight.data_ptr(), "Unexpected tied embeddings")
     model._fp4_receipt = dict(ledger, serialization="safetensors_packed_checkpoint",
                               source_checkpoint_required=False,
                               packed_checkpoint_manifest_sha256=sha_file(Path(directory) / "weight_manifest.json"))

@@ -66,23 +66,38 @@ def validate_state(state, device, layout):
     return True
 
 
-def validate_statics(permutation, basis, latent_scale, predictor, *, groups, layout, device):
-    """The static-table checks of scan() (fp4_zero_predictor_codec_v1.py:203-217);
-    these synchronize with the device, so controllers run them once."""
+def check_static_metadata(permutation, basis, latent_scale, predictor, *, groups, layout, device):
+    """Host-only part of scan()'s static-table checks
+    (fp4_zero_predictor_codec_v1.py:203-217): dtype, shape and device of the
+    permutation, bases, latent scales and predictor.  The kernel indexes these
+    tables by the shapes checked here, so every scan runs this, whatever its
+    `validate` flag; it reads tensor metadata only and never synchronizes."""
     spec = layout_descriptor(layout)
-    if (permutation.dtype != torch.uint8 or tuple(permutation.shape) != (groups, 128)
+    if (not all(isinstance(v, torch.Tensor) for v in (permutation, basis, latent_scale, predictor))
+            or permutation.dtype != torch.uint8 or tuple(permutation.shape) != (groups, 128)
             or permutation.device != device
             or basis.dtype != torch.float16 or tuple(basis.shape) != (groups, spec["nzero"], 2)
             or basis.device != device
             or latent_scale.dtype != torch.float16 or tuple(latent_scale.shape) != (groups, 2)
-            or latent_scale.device != device or not bool(torch.isfinite(basis).all())
-            or not bool(torch.isfinite(latent_scale).all())
-            or not bool((latent_scale > 0).all())):
+            or latent_scale.device != device):
         raise ValueError("Latent static basis/scales differ")
     features = spec["n8"] + spec["n4"] + 2
     if (predictor.dtype != torch.float16 or tuple(predictor.shape) != (groups, features, spec["nzero"])
-            or predictor.device != device or not predictor.is_contiguous()
-            or not bool(torch.isfinite(predictor).all())):
+            or predictor.device != device or not predictor.is_contiguous()):
+        raise ValueError("Static zero-tier predictor differs")
+
+
+def validate_statics(permutation, basis, latent_scale, predictor, *, groups, layout, device):
+    """The static-table checks of scan() (fp4_zero_predictor_codec_v1.py:203-217):
+    the metadata checks, then the value checks (finite bases, scales and
+    predictor, positive latent scales), which synchronize with the device, so
+    controllers run them once."""
+    check_static_metadata(permutation, basis, latent_scale, predictor, groups=groups, layout=layout,
+                          device=device)
+    if (not bool(torch.isfinite(basis).all()) or not bool(torch.isfinite(latent_scale).all())
+            or not bool((latent_scale > 0).all())):
+        raise ValueError("Latent static basis/scales differ")
+    if not bool(torch.isfinite(predictor).all()):
         raise ValueError("Static zero-tier predictor differs")
 
 
@@ -96,7 +111,8 @@ def scan(x, dt, A, B, C, D, dt_bias, state, permutation, basis, latent_scale, pr
     is computed inside the kernel.  With validate=True the static tables and
     the finiteness of the correction are checked here exactly as the
     reference does (five device synchronizations); validate=False skips
-    those checks, for callers that validated the statics once.
+    only those value checks, for callers that validated the statics once:
+    the tables' dtype, shape and device are checked on every call.
     """
     spec = layout_descriptor(layout)
     if not isinstance(x, torch.Tensor) or x.ndim != 4 or x.dtype != torch.float16 or not x.is_cuda:
@@ -115,6 +131,8 @@ def scan(x, dt, A, B, C, D, dt_bias, state, permutation, basis, latent_scale, pr
             or any(v.dtype != torch.float16 for v in (dt, B, C))
             or any(v.dtype not in (torch.float16, torch.float32) for v in (D, dt_bias))):
         raise ValueError("Latent scan dtype/grouping differs")
+    check_static_metadata(permutation, basis, latent_scale, predictor, groups=groups, layout=layout,
+                          device=x.device)
     if validate:
         validate_statics(permutation, basis, latent_scale, predictor, groups=groups, layout=layout,
                          device=x.device)

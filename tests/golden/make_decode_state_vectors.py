@@ -9,6 +9,9 @@ The fixture is data only.  Usage: python make_decode_state_vectors.py
 [reference root]."""
 import importlib.util
 import sys
+
+# importing the reference by path must never write bytecode into its checkout
+sys.dont_write_bytecode = True
 from pathlib import Path
 
 import numpy as np

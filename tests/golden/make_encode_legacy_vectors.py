@@ -7,6 +7,9 @@ from the reference is copied.  Usage: python make_encode_legacy_vectors.py
 [reference root]."""
 import importlib.util
 import sys
+
+# importing the reference by path must never write bytecode into its checkout
+sys.dont_write_bytecode = True
 from pathlib import Path
 
 import numpy as np

@@ -83,6 +83,41 @@ def test_g16_every_code_every_scale_byte(oracle, device):
         assert int((closed != got).sum()) == 0
 
 
+def _assert_equal_in_chunks(got_dev, want, rows_per_chunk=16384):
+    for r0 in range(0, want.shape[0], rows_per_chunk):
+        got = got_dev[r0:r0 + rows_per_chunk].cpu().numpy().view(np.uint16)
+        bad = int((got != want[r0:r0 + rows_per_chunk]).sum())
+        assert bad == 0, f"rows {r0}..: {bad} mismatched FP16 weights"
+
+
+def test_g16_grid_stride_sweeps_embedding_matrix(oracle, device):
+    """The [256000, 4096] embedding / lm_head matrix of the full 8B set:
+    131,072,000 eight-weight units, more than the 16,777,216 units one grid of
+    the decode covers, so every workgroup runs several grid-stride sweeps."""
+    rows, cols = 256000, 4096
+    rng = np.random.default_rng(256000)
+    packed = rng.integers(0, 256, size=(rows, cols // 2), dtype=np.uint8)
+    s = np.exp(rng.normal(-3.0, 0.5, size=(rows, cols // 16))).astype(np.float32)
+    g = np.float32(s.max() / 448.0)
+    sb = torch.from_numpy(np.clip(s / g, 0, 448)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    del s
+    print(f"[fp4 g16 sweeps] rows={rows} cols={cols} units={rows * cols // 8}", flush=True)
+    want, err = oracle.fp4_decode(16, packed, sb, g, rows, cols)
+    assert err == 0
+    _assert_equal_in_chunks(decode_dev(packed, sb, g, rows, cols, device), want)
+
+
+def test_g64_grid_stride_sweeps(oracle, device):
+    rows, cols = 40000, 4096          # 20,480,000 units: a second, partial sweep
+    rng = np.random.default_rng(40000)
+    packed = rng.integers(0, 256, size=(rows, cols // 2), dtype=np.uint8)
+    sc = np.exp(rng.normal(-3.0, 0.5, size=(rows, cols // 64))).astype(np.float16).view(np.uint16)
+    print(f"[fp4 g64 sweeps] rows={rows} cols={cols} units={rows * cols // 8}", flush=True)
+    want, err = oracle.fp4_decode(64, packed, sc, 1.0, rows, cols)
+    assert err == 0
+    _assert_equal_in_chunks(decode_dev(packed, sc, None, rows, cols, device, group=64), want)
+
+
 @pytest.mark.parametrize("rows,cols", [(64, 4096), (7, 192), (3, 100)])
 def test_g64_random_bit_exact(oracle, device, rows, cols):
     rng = np.random.default_rng(rows + cols)

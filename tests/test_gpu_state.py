@@ -189,9 +189,47 @@ def test_ridge_ragged_p(oracle, device):
     run_ridge(oracle, device, "36_24_68", batch=2, L=2, H=16, P=80, G=2, seed=16)
 
 
-def test_ridge_model_batch_sixteen_head_blocks(oracle, device):
-    # the benchmark geometry (batch 64, one token) selects 16 heads per workgroup
-    run_ridge(oracle, device, "32_32_64", batch=64, L=1, H=128, P=64, G=8, seed=19)
+@pytest.mark.parametrize("layout", RIDGE_LAYOUTS)
+def test_ridge_model_batch_sixteen_head_blocks(oracle, device, layout):
+    # the benchmark geometry (batch 64, one token) selects 16 heads per
+    # workgroup: every one-token instance the headline benchmark times
+    run_ridge(oracle, device, layout, batch=64, L=1, H=128, P=64, G=8, seed=19)
+
+
+def test_tier_and_legacy_benchmark_geometry(oracle, device):
+    # the batch-64 one-token instances of the other packed formats that the
+    # benchmark times beside the ridge step
+    run_tier(oracle, device, "tier", "32_32_64", batch=64, L=1, H=128, P=64, G=8, seed=24)
+    run_tier(oracle, device, "legacy", "16_64_48", batch=64, L=1, H=128, P=64, G=8, seed=33)
+
+
+def test_ridge_unvalidated_scan_still_checks_table_shapes(device):
+    """validate=False skips only the synchronizing value checks: a predictor,
+    permutation or basis of the wrong shape or dtype is rejected before the
+    kernel would index past it."""
+    from mamba2_recall import ridge_codec
+    layout = "32_32_64"
+    n8, n4, nz = ridge_counts(layout)
+    rng = np.random.default_rng(90)
+    inp = cases.step_inputs(rng, 1, 1, 128, 64, 8)
+    sta = cases.ridge_statics(rng, 8, n8, n4, nz)
+    print("[ridge validate=False] mis-shaped statics", flush=True)
+    state = ridge_codec.allocate_state(1, 128, 64, 128, device, layout=layout)
+    t = {k: devp(v, device) for k, v in inp.items() if k != "perm"}
+    perm = torch.from_numpy(inp["perm"]).to(device)
+    basis, ls, pred = (dev16(sta[k], device) for k in ("basis", "lscale", "pred"))
+    args = (t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["dt_bias"], state)
+    with pytest.raises(ValueError, match="predictor differs"):
+        ridge_codec.scan(*args, perm, basis, ls, pred[:, :-4].contiguous(), layout=layout, validate=False)
+    with pytest.raises(ValueError, match="predictor differs"):
+        ridge_codec.scan(*args, perm, basis, ls, pred.float(), layout=layout, validate=False)
+    with pytest.raises(ValueError, match="basis/scales differ"):
+        ridge_codec.scan(*args, perm[:4], basis, ls, pred, layout=layout, validate=False)
+    with pytest.raises(ValueError, match="basis/scales differ"):
+        ridge_codec.scan(*args, perm, basis[:, :8], ls, pred, layout=layout, validate=False)
+    before = {k: v.clone() for k, v in state.tensors.items()}
+    torch.cuda.synchronize()
+    assert all(torch.equal(before[k], state.tensors[k]) for k in before)
 
 
 SHAPES = [(1, 1), (4, 1), (4, 2), (4, 4), (8, 2)]

@@ -129,3 +129,58 @@ def test_scans_reject_host_tensors():
     rs = ridge_codec.allocate_state(1, 128, 64, 128, "cpu", layout="32_32_64")
     with pytest.raises(ValueError, match="x must be CUDA FP16"):
         ridge_codec.scan(x, dt, A, B, C, D, db, rs, perm, None, None, None, layout="32_32_64")
+
+
+def _ridge_statics(layout, groups=8):
+    d = ridge_codec.layout_descriptor(layout)
+    features = d["n8"] + d["n4"] + 2
+    perm = torch.stack([torch.randperm(128) for _ in range(groups)]).to(torch.uint8)
+    basis = torch.zeros(groups, d["nzero"], 2, dtype=torch.float16)
+    ls = torch.full((groups, 2), 1e-3, dtype=torch.float16)
+    pred = torch.zeros(groups, features, d["nzero"], dtype=torch.float16)
+    return perm, basis, ls, pred
+
+
+@pytest.mark.parametrize("bad", ["pred_shape", "pred_dtype", "pred_strided", "perm_shape", "basis_shape",
+                                 "lscale_dtype"])
+def test_ridge_static_metadata_checks_never_skipped(bad):
+    # fp4_zero_predictor_codec_v1.py:203-217: the kernel indexes the tables by
+    # these shapes, so scan(validate=False) still runs this host-only part
+    layout = "32_32_64"
+    perm, basis, ls, pred = _ridge_statics(layout)
+    ridge_codec.check_static_metadata(perm, basis, ls, pred, groups=8, layout=layout, device=torch.device("cpu"))
+    if bad == "pred_shape":
+        pred = pred[:, :-1].contiguous()
+    elif bad == "pred_dtype":
+        pred = pred.float()
+    elif bad == "pred_strided":
+        pred = torch.zeros(pred.shape[:-1] + (2 * pred.shape[-1],), dtype=torch.float16)[..., ::2]
+    elif bad == "perm_shape":
+        perm = perm[:7]
+    elif bad == "basis_shape":
+        basis = basis[:, :-1]
+    else:
+        ls = ls.float()
+    msg = "predictor differs" if bad.startswith("pred") else "basis/scales differ"
+    with pytest.raises(ValueError, match=msg):
+        ridge_codec.check_static_metadata(perm, basis, ls, pred, groups=8, layout=layout,
+                                          device=torch.device("cpu"))
+
+
+def test_ridge_value_checks_reject_nonfinite_and_nonpositive():
+    layout = "44_8_76"
+    perm, basis, ls, pred = _ridge_statics(layout)
+    dev = torch.device("cpu")
+    ridge_codec.validate_statics(perm, basis, ls, pred, groups=8, layout=layout, device=dev)
+    for which in ("basis", "ls_zero", "ls_inf", "pred"):
+        b, l, p = basis.clone(), ls.clone(), pred.clone()
+        if which == "basis":
+            b[3, 5, 1] = float("nan")
+        elif which == "ls_zero":
+            l[2, 0] = 0
+        elif which == "ls_inf":
+            l[2, 1] = float("inf")
+        else:
+            p[1, 2, 3] = float("-inf")
+        with pytest.raises(ValueError):
+            ridge_codec.validate_statics(perm, b, l, p, groups=8, layout=layout, device=dev)

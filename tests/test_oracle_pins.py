@@ -567,3 +567,352 @@ def test_encode_legacy_matches_reference_vectors(oracle):
     ties = dense[96:160:3, 1:16]
     assert np.any(np.abs(ties - np.trunc(ties)) == 0.5)
     assert not np.array_equal(np.rint(ties), np.sign(ties) * np.floor(np.abs(ties) + 0.5))
+
+
+# --------------------------------------------- latent update and its E4M3 bytes
+
+def _e4m3_byte(q):
+    """float32 -> E4M3FN byte by torch's conversion (round to nearest even)."""
+    return int(torch.tensor([float(q)], dtype=torch.float32).to(torch.float8_e4m3fn).view(torch.uint8)[0])
+
+
+def _e4m3_value(byte):
+    return float(torch.tensor([byte], dtype=torch.uint8).view(torch.float8_e4m3fn).float()[0])
+
+
+def _latent_expect(z, decay, xdt, dot_b, ls):
+    """Exact rational restatement of one latent step
+    (scripts/fp4_zero_predictor_codec_v1.py:149-152): z' = RN(z*decay + RN(xdt*dot_b)),
+    byte = E4M3(clamp(RN(z'/ls), -448, 448)).  Returns (z', byte)."""
+    inp = _rn32(Fraction(float(xdt)) * Fraction(float(dot_b)))
+    zn = _rn32(Fraction(float(z)) * Fraction(float(decay)) + Fraction(float(inp)))
+    q = _rn32(Fraction(float(zn)) / Fraction(float(ls)))
+    return zn, _e4m3_byte(min(max(float(q), -448.0), 448.0))
+
+
+def _one_hot_latent_call(oracle, layout, x0, lat0, *, dt, A, b, c, ls, d0, d1, L2=True):
+    """One head of P rows through the ridge oracle with a one-hot dead-tier
+    basis (e0 = 0.5 at dead lane d0, e1 = 0.5 at d1), B and C nonzero only at
+    d0/d1 (token 0), zero predictor, zero carried tiers, D = 0.  With L2 a
+    second token follows with x = 0, B = 0 and C = 2 at d0: its readout is
+    exactly half(decay * z0) of the requantized latent coefficient."""
+    n8, n4, nz = cases.ridge_counts(layout)
+    rows = len(x0)
+    L = 2 if L2 else 1
+    live = n8 + n4
+    x = np.zeros((1, L, 1, rows), np.float32)
+    x[0, 0, 0] = x0
+    Bm = np.zeros((1, L, 1, 128), np.float32)
+    Cm = np.zeros((1, L, 1, 128), np.float32)
+    Bm[0, 0, 0, live + d0], Bm[0, 0, 0, live + d1] = b
+    Cm[0, 0, 0, live + d0], Cm[0, 0, 0, live + d1] = c
+    if L2:
+        Cm[0, 1, 0, live + d0] = 2.0
+    inp = dict(x=cases.f16(x), dt=cases.f16(np.full((1, L, 1), dt)), A=np.array([A], np.float32),
+               B=cases.f16(Bm), C=cases.f16(Cm), D=cases.f16(np.zeros(1)), dt_bias=cases.f16(np.zeros(1)),
+               perm=np.arange(128, dtype=np.uint8)[None])
+    basis = np.zeros((1, nz, 2), np.float32)
+    basis[0, d0, 0] = 0.5
+    basis[0, d1, 1] = 0.5
+    sta = dict(basis=cases.f16(basis), lscale=cases.f16(np.array([ls], np.float32)),
+               pred=np.zeros((1, n8 + n4 + 2, nz), np.uint16))
+    st = cases.zero_packed_state(1, 1, rows, n8, n4, latent=True)
+    st["latent"][0, 0] = np.asarray(lat0, np.uint8)
+    y = _ridge(oracle, layout, inp, sta, st)
+    return st["latent"][0, 0], y
+
+
+def _latent_case_table():
+    """(x, initial byte of coefficient 0) rows for ls0 = 1/16, dt = 32
+    (softplus identity branch), decay 1, b0 = 1/16: 16 z0' = v0 + 16 x exactly,
+    so these hit E4M3 ties (to even), the +-448 clamp, the subnormal range and
+    signed zero."""
+    one, v256, mv256 = 0x38, 0x78, 0xF8
+    return [
+        (2.0 ** -8, one),            # 1.0625: tie 1.0 | 1.125 -> 1.0 (even)
+        (3 * 2.0 ** -8, one),        # 1.1875: tie 1.125 | 1.25 -> 1.25
+        (5 * 2.0 ** -8, one),        # 1.3125: tie 1.25 | 1.375 -> 1.25
+        (2.0 ** -7, one),            # 1.125 exact
+        (1.0, v256),                 # 272: tie 256 | 288 -> 256
+        (3.0, v256),                 # 304: tie 288 | 320 -> 320
+        (12.0, v256),                # 448 exact
+        (13.0, v256),                # 464 -> clamp 448
+        (46.5, v256),                # 1000 -> clamp 448
+        (-20.0, mv256),              # -576 -> clamp -448
+        (-12.0, mv256),              # -448 exact
+        (3 * 2.0 ** -14, 0x00),      # 1.5 * 2^-9: tie 2^-9 | 2^-8 -> 2^-8 (even)
+        (2.0 ** -14, 0x00),          # 2^-10: tie 0 | 2^-9 -> 0 (even)
+        (2.0 ** -14 + 2.0 ** -24, 0x00),   # just above: 2^-9
+        (-(2.0 ** -14), 0x00),       # -2^-10: tie -> -0
+        (-0.0, 0x80),                # -0 stays -0
+        (0.0, 0x00),
+        (-2.0 ** -8, 0xB8),          # -1.0625: tie -> -1.0
+    ]
+
+
+def test_latent_update_known_answers(oracle):
+    """The ridge latent step and its E4M3 requantization
+    (scripts/fp4_zero_predictor_codec_v1.py:149-152, 176-179) on a one-hot basis,
+    against exact rational arithmetic and torch's E4M3FN conversion: E4M3
+    ties to even, the +-448 clamp, subnormals, signed zero; coefficient 1
+    through a non-power-of-two latent scale; and the second token's readout,
+    which must use the requantized coefficient."""
+    layout = "32_32_64"
+    d0, d1 = 3, 66
+    b = (2.0 ** -4, 2.0 ** -3)               # b0 != b1: a swapped e0/e1 changes every row
+    c = (0.75, -1.5)                          # C differs from B at both dead lanes
+    # coefficient 1's scale: binary16 0x1468, for which z1' = 1.9375 ls1 (an
+    # E4M3 tie, to even 2.0) is reached from 1.875 ls1 with x = ls1/32, while
+    # z1' * RN(1/ls1) rounds to 1.875: a quotient by the rounded reciprocal fails
+    ls1 = float(np.uint16(0x1468).view(np.float16))
+    ls = (2.0 ** -4, ls1)
+    table = _latent_case_table()
+    special1 = {len(table): 0x3F, len(table) + 1: 0xBF}
+    table += [(ls1 / 32, 0x38), (-ls1 / 32, 0x38)]
+    rng = np.random.default_rng(151)
+    while len(table) < 64:                    # plus random rows
+        table.append((float(np.float16(rng.normal(0, 4))), int(cases.random_e4m3_bytes(rng, (1,))[0])))
+    x0 = np.array([t[0] for t in table], np.float32)
+    lat0 = np.stack([np.array([t[1] for t in table], np.uint8),
+                     cases.random_e4m3_bytes(rng, (len(table),))], -1)
+    for r, byte in special1.items():
+        lat0[r, 1] = byte
+    got, y = _one_hot_latent_call(oracle, layout, x0, lat0, dt=32.0, A=0.0, b=b, c=c, ls=ls, d0=d0, d1=d1)
+    dtv, decay = np.float32(32.0), np.float32(1.0)
+    swapped_differs = False
+    for r, (xv, _) in enumerate(table):
+        xdt = np.float32(np.float32(np.float16(xv)) * dtv)
+        for k in range(2):
+            z = np.float32(_e4m3_value(int(lat0[r, k])) * np.float32(np.float16(ls[k])))
+            zn, byte = _latent_expect(z, decay, xdt, np.float32(0.5 * b[k]), np.float16(ls[k]))
+            # token 1 (x = 0, B = 0): z'' = RN(zq + 0), so -0 becomes +0
+            zq = np.float32(np.float32(_e4m3_value(byte)) * np.float32(np.float16(ls[k])))
+            _, byte = _latent_expect(zq, decay, np.float32(0.0), np.float32(0.0), np.float16(ls[k]))
+            assert int(got[r, k]) == byte, (r, k, xv, float(zn), hex(int(got[r, k])), hex(byte))
+            _, wrong = _latent_expect(z, decay, xdt, np.float32(0.5 * b[1 - k]), np.float16(ls[k]))
+            swapped_differs |= wrong != byte
+        # token 1: y = half(z0 requantized), not half(z0')
+        zq = np.float32(_e4m3_value(int(got[r, 0])) * np.float32(2.0 ** -4))
+        assert int(y[0, 1, 0, r]) == int(cases.f16(np.array([zq]))[0]), r
+    assert swapped_differs
+    assert [int(got[r, 1]) for r in special1] == [0x40, 0xC0]
+    # the table's first rows are ties whose requantized value differs from z'
+    z0n = (np.float32(1.0) + x0[:2]).astype(np.float32) / 16
+    assert not np.array_equal(cases.f16(z0n), y[0, 1, 0, :2])
+
+
+def test_latent_update_general_decay_matches_exact_arithmetic(oracle):
+    """Random x, dt (softplus branch), A (decay < 1), B at the dead lanes,
+    initial latent bytes and latent scales: every byte equals the exact
+    rational z' = RN(z*decay + RN(RN(x*dt)*dot_b)) requantized, with dt and
+    decay from the oracle's exp/log (pinned against libm above)."""
+    layout = "44_8_76"
+    d0, d1 = 0, 79
+    rng = np.random.default_rng(152)
+    for trial in range(6):
+        dt = float(np.float16(rng.normal(0, 1)))
+        A = float(-np.exp(rng.uniform(0, np.log(16))))
+        b = tuple(float(np.float16(v)) for v in rng.normal(0, 1, 2))
+        c = tuple(float(np.float16(v)) for v in rng.normal(0, 1, 2))
+        ls = tuple(float(np.float16(v)) for v in np.exp(rng.normal(-6, 1, 2)))
+        x0 = cases.f16_to_f32(cases.f16(rng.normal(0, 2, 64)))
+        lat0 = cases.random_e4m3_bytes(rng, (64, 2))
+        got, _ = _one_hot_latent_call(oracle, layout, x0, lat0, dt=dt, A=A, b=b, c=c, ls=ls, d0=d0, d1=d1,
+                                      L2=False)
+        dtv = oracle.unary(np.array([np.float32(np.float16(dt))]).view(np.uint32), 7).view(np.float32)[0]
+        decay = oracle.unary(np.array([np.float32(A) * dtv], np.float32).view(np.uint32), 5).view(np.float32)[0]
+        for r in range(64):
+            xdt = np.float32(x0[r] * dtv)
+            for k in range(2):
+                dot_b = np.float32(np.float32(0.5) * np.float32(np.float16(b[k])))
+                z = np.float32(np.float32(_e4m3_value(int(lat0[r, k]))) * np.float32(np.float16(ls[k])))
+                _, byte = _latent_expect(z, decay, xdt, dot_b, np.float16(ls[k]))
+                assert int(got[r, k]) == byte, (trial, r, k)
+
+
+# -------------------------------------- dense 3-bit requantization and bit planes
+
+def _d3_expect(u, half_scale_policy="den"):
+    """state_codec_dense3.py:133-145 for one row of 128 updated values u
+    (float32), by exact rationals: den = max(RN(amax/3), 1e-8) per half,
+    q = clamp(roundf(RN(u/den)), +-3) (ties away from zero), stored half(den).
+    half_scale_policy="stored" divides by the stored binary16 scale instead
+    (a plausible mistake the pin must reject)."""
+    q = np.zeros(128, np.int64)
+    scales = np.zeros(2, np.uint16)
+    for hh in range(2):
+        seg = u[64 * hh:64 * hh + 64]
+        amax = max(abs(Fraction(float(v))) for v in seg)
+        den = max(_rn32(amax / 3), np.float32(1e-8))
+        st = np.float16(den)
+        div = Fraction(float(den)) if half_scale_policy == "den" else Fraction(float(st))
+        for i, v in enumerate(seg):
+            if div == 0:
+                qq = 0
+            else:
+                t = Fraction(float(_rn32(Fraction(float(v)) / div)))
+                mag = math.floor(abs(t) + Fraction(1, 2))
+                qq = int(mag if t >= 0 else -mag)
+            q[64 * hh + i] = min(max(qq, -3), 3)
+        scales[hh] = st.view(np.uint16)
+    return q, scales
+
+
+def _d3_planes(q):
+    """Bit planes of 3-bit two's-complement codes, by numpy's little-endian
+    bit packing (coordinate 8j + b is bit b of byte j of each plane)."""
+    u = (np.asarray(q, np.int64) & 7).astype(np.uint8)
+    return np.stack([np.packbits(((u >> k) & 1).astype(np.uint8), bitorder="little") for k in range(3)])
+
+
+def _d3_call(oracle, prior_q, prior_s, x, bvec):
+    """One head of P rows through the dense 3-bit oracle with decay 1 (A = 0)
+    and dt = 32 (softplus's identity branch): u = RN(prior + RN(32 b x)) per
+    coordinate, exactly known.  Returns (state after, u per row)."""
+    P = len(x)
+    codes = np.stack([_d3_planes(q).reshape(48) for q in prior_q]).reshape(1, 1, P, 3, 16)
+    scales = cases.f16(prior_s).reshape(1, 1, P, 2)
+    B = np.zeros((1, 1, 1, 128), np.float32)
+    B[0, 0, 0] = bvec
+    inp = dict(x=cases.f16(np.asarray(x, np.float32).reshape(1, 1, 1, P)), dt=cases.f16(np.full((1, 1, 1), 32.0)),
+               A=np.zeros(1, np.float32), B=cases.f16(B), C=cases.f16(np.zeros((1, 1, 1, 128))),
+               D=cases.f16(np.zeros(1)), dt_bias=cases.f16(np.zeros(1)))
+    st = dict(codes=codes, scales=scales.copy())
+    oracle.dense3_step(0, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], inp["dt_bias"],
+                       np.arange(128, dtype=np.uint8)[None], st)
+    f = lambda a: Fraction(float(a))
+    bdt = (cases.f16_to_f32(inp["B"][0, 0, 0]) * np.float32(32.0)).astype(np.float32)
+    us = []
+    for r in range(P):
+        prior = (np.asarray(prior_q[r]) * np.repeat(cases.f16_to_f32(scales[0, 0, r]), 64)).astype(np.float32)
+        xv = cases.f16_to_f32(inp["x"][0, 0, 0, r])
+        us.append(np.array([_rn32(f(prior[n]) + f(np.float32(bdt[n] * xv))) for n in range(128)], np.float32))
+    return st, us
+
+
+def test_dense3_requantization_and_packing_known_answers(oracle):
+    """The dense 3-bit requantization and bit-plane packing
+    (mamba2_recall/state_codec_dense3.py:133-145) with decay 1 and a known
+    input term (u = RN(prior + RN(32 b x)) exactly): codes, planes and stored
+    scales against exact rationals, numpy's little-endian bit packing and
+    numpy's binary16 rounding.  Rows cover exact k + 1/2 quotients (ties away
+    from zero: a round-half-even quantizer fails), the 1e-8 denominator floor
+    (binary16 scale 0), and random rows on which dividing by the stored
+    binary16 scale instead of den gives other codes."""
+    rng = np.random.default_rng(133)
+    # call 1: exact ties.  Coordinates 0 and 64 carry 3 * 2^m (code 3, scale
+    # 2^m), so den = 2^m in both halves; every other coordinate gets only the
+    # input term (k + 1/2) 2^m: b_n = (k + 1/2) 2^m0 / 32, x_r = 2^(m_r - m0)
+    m0, P = -4, 8
+    halves = np.resize(np.array([0.5, -0.5, 1.5, -1.5, 2.5, -2.5]), 128)
+    halves[0] = halves[64] = 0.0
+    bvec = (halves * 2.0 ** m0 / 32).astype(np.float32)
+    prior_q = np.zeros((P, 128), np.int64)
+    prior_q[:, 0] = prior_q[:, 64] = 3
+    ms = np.arange(P) - 6
+    prior_s = np.repeat((2.0 ** ms)[:, None], 2, 1).astype(np.float32)
+    st, us = _d3_call(oracle, prior_q, prior_s, 2.0 ** (ms - m0), bvec)
+    for r in range(P):
+        q, sc = _d3_expect(us[r])
+        assert np.array_equal(us[r] / np.float32(2.0 ** ms[r]), halves + 3 * (np.arange(128) % 64 == 0))
+        assert np.array_equal(st["codes"][0, 0, r], _d3_planes(q)), r
+        assert np.array_equal(st["scales"][0, 0, r], sc), r
+        h = halves[1:64]                                                  # ties away from zero
+        assert (q[1:64] == np.sign(h) * np.floor(np.abs(h) + 0.5)).all()
+        assert (q[1:64] != np.rint(h)).any()
+    # call 2: zero priors and input terms below 3e-8 (rows 0-3, x = 2^-24: den
+    # is the 1e-8 floor, stored scale 0), then random priors and input terms
+    P = 40
+    prior_q = rng.integers(-4, 4, (P, 128))
+    prior_q[:4] = 0
+    prior_s = np.exp(rng.normal(-3, 0.5, (P, 2))).astype(np.float16).astype(np.float32)
+    x = cases.f16_to_f32(cases.f16(rng.normal(0, 1, P)))
+    x[:4] = 2.0 ** -24
+    bvec = cases.f16_to_f32(cases.f16(rng.normal(0, 0.004, 128)))
+    st, us = _d3_call(oracle, prior_q, prior_s, x, bvec)
+    stored_differs = 0
+    for r in range(P):
+        q, sc = _d3_expect(us[r])
+        assert np.array_equal(st["codes"][0, 0, r], _d3_planes(q)), r
+        assert np.array_equal(st["scales"][0, 0, r], sc), r
+        stored_differs += int(not np.array_equal(q, _d3_expect(us[r], "stored")[0]))
+    assert not st["scales"][0, 0, :4].any() and st["codes"][0, 0, :4].any()
+    assert stored_differs > 0           # dividing by half(den) would be caught
+
+
+# ------------------------------------------------------------- G64 closed form
+
+def test_fp4_g64_closed_form_all_codes_scale_sweep(oracle):
+    """G64 decode (mamba2_recall/fp4.py:151-154, G64 branch): w =
+    half(lev[c & 7] * sign(c) * float(f16 scale)) with one rounding and no
+    global scale, for all 16 codes x every non-negative finite binary16 scale
+    (subnormals, +-0, 65504), against numpy's IEEE float32 product and
+    binary16 rounding; products that overflow binary16 raise only the
+    nonfinite-weight bit.  A global scale passed with G64 is ignored."""
+    lev = np.float32([0, .5, 1, 1.5, 2, 3, 4, 6])
+    scale_bits = np.concatenate([np.arange(0, 0x7C00, dtype=np.uint16), np.uint16([0x8000])])
+    rows = scale_bits.size
+    codes = np.tile(np.repeat(np.arange(16, dtype=np.uint8), 4), (rows, 1))   # 64 columns
+    zero = (scale_bits & 0x7FFF) == 0
+    codes[zero] = np.where(np.isin(codes[zero], (0, 8)), codes[zero], 0)
+    packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
+    sc = scale_bits[:, None].copy()
+    val = lev[codes & 7] * np.where(codes & 8, np.float32(-1), np.float32(1))
+    with np.errstate(over="ignore"):
+        want = (val * sc.view(np.float16).astype(np.float32)).astype(np.float32).astype(np.float16).view(np.uint16)
+    overflow = ((want & 0x7FFF) >= 0x7C00).any()
+    assert overflow
+    for g in (1.0, 0.37):
+        out, err = oracle.fp4_decode(64, packed, sc, g, rows, 64)
+        assert err == 8, err
+        assert np.array_equal(out, want)
+    ok = (scale_bits & 0x7FFF) < 0x5400           # |6 * scale| < 65504: no overflow
+    out, err = oracle.fp4_decode(64, np.ascontiguousarray(packed[ok]), np.ascontiguousarray(sc[ok]), 3.0,
+                                 int(ok.sum()), 64)
+    assert err == 0 and np.array_equal(out, want[ok])
+    # the global scale must not apply, and the scale is binary16, not E4M3
+    with np.errstate(over="ignore"):
+        scaled = (val * sc.view(np.float16).astype(np.float32) * np.float32(0.37)).astype(np.float16).view(np.uint16)
+    assert not np.array_equal(scaled, want)
+    # signs of zero: code 8 under a +0 scale is -0, code 0 under -0 is -0
+    assert (out[0, 32:36] == 0x8000).all() and (out[0, :4] == 0).all()
+    neg0 = np.nonzero(scale_bits == 0x8000)[0][0]
+    full, _ = oracle.fp4_decode(64, packed, sc, 1.0, rows, 64)
+    assert (full[neg0, :4] == 0x8000).all() and (full[neg0, 32:36] == 0).all()
+
+
+def test_latent_update_is_fused(oracle):
+    """The latent step is one fused multiply-add, z' = fma(z, decay,
+    RN(RN(x*dt)*dot_b)), like the tier update: a row whose fused and
+    separately rounded z' give different E4M3 bytes (found by search, checked
+    with exact rationals) must store the fused one."""
+    dtv, decay = _dt_decay(oracle)
+    ls = np.float16(2.0 ** -6)
+    b = np.arange(0, 0x7C00, dtype=np.uint16)
+    b = np.concatenate([b, b | 0x8000]).view(np.float16).astype(np.float32)
+    dot_b = (np.float32(0.5) * b).astype(np.float32)
+    x = np.float32(1.0)
+    inp = (np.float32(x * dtv) * dot_b).astype(np.float32)             # RN(RN(x*dt)*dot_b)
+
+    def byte_of(u):
+        q = np.clip((u.astype(np.float32) / np.float32(ls)).astype(np.float32), -448, 448)
+        return torch.from_numpy(q.astype(np.float32)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+    found = None
+    for vb in range(0x08, 0x78):
+        z = np.float32(np.float32(_e4m3_value(vb)) * np.float32(ls))
+        sep = (np.float32(z * decay) + inp).astype(np.float32)
+        fus = (np.longdouble(z) * np.longdouble(decay) + inp.astype(np.longdouble)).astype(np.float32)
+        for i in np.nonzero(byte_of(fus) != byte_of(sep))[0][:4]:
+            f = _fma32(z, decay, inp[i])
+            if byte_of(np.array([f]))[0] != byte_of(sep[i:i + 1])[0]:
+                found = (vb, float(b[i]), f, sep[i])
+                break
+        if found:
+            break
+    assert found, "no discriminating row found"
+    vb, bv, f, s = found
+    # dead lane 0 carries e0 = 0.5 and B = bv; dt and A as in the search
+    got, _ = _one_hot_latent_call(oracle, "32_32_64", np.float32([x]), np.uint8([[vb, 0]]), dt=_DT, A=_A,
+                                  b=(bv, 0.0), c=(0.0, 0.0), ls=(float(ls), 1.0), d0=0, d1=1, L2=False)
+    assert int(got[0, 0]) == int(byte_of(np.array([f]))[0]) != int(byte_of(np.array([s]))[0])
