@@ -158,6 +158,28 @@ constexpr float QTOP127 = 0x1.fffffep+6f;   // below 128
 constexpr float QTOP7 = 0x1.fffffep+2f;     // below 8
 constexpr float QTOP3 = 0x1.fffffep+1f;     // below 4
 
+// Biased code by the magic-number rounding, for a quotient that needs no
+// clamping: t = RN(v y + 1.5 2^23 + bias) lies in [2^23, 2^24), where the
+// spacing is 1, so t = 1.5 2^23 + bias + rint(v y) (one rounding of the exact
+// product) and the low bits of t are the code plus its bias.  f = RN(v y -
+// rint(v y)) is the rounding residual.  rint(v y) is roundf(RN(v / d)) unless
+// v / d lies near a half-integer:
+//   |v y - v / d| <= |v / d| 2^-24 (y = RN(1 / d), a normal binary32 value),
+//   |RN(v / d) - v / d| <= ulp(v / d) / 2, and |f| is exact to 2^-25.
+// With |v / d| < lim + 1/2 (the unclamped case), |f| <= RESIDUAL_OK puts
+// RN(v / d) strictly within 1/2 of rint(v y), where roundf and rint agree:
+//   lim 127: 2^-17 + 2^-18 + 2^-25 < 2^-16, so RESIDUAL_OK8 = 1/2 - 2^-16;
+//   lim 7 (and 3): 2^-21 + 2^-22 + 2^-25 < 2^-20; RESIDUAL_OK4 = 1/2 - 2^-19.
+// Exact half-integer products give |f| = 1/2 and always take the exact path.
+constexpr float RESIDUAL_OK8 = 0.5f - 0x1p-16f;
+constexpr float RESIDUAL_OK4 = 0.5f - 0x1p-19f;
+__device__ __forceinline__ uint32_t round_residual_code(float v, float y, float bias, float& f) {
+  const float magic = 0x1.8p23f + bias;
+  const float t = __builtin_fmaf(v, y, magic);
+  f = __builtin_fmaf(v, y, -(t - magic));
+  return __builtin_bit_cast(uint32_t, t);
+}
+
 // q * s exactly, for a code q held as binary16 (an integer of at most 11
 // bits) and any binary32 s: one mixed-precision fma with a -0 addend (x + -0
 // is x, also for signed zeros), so infinite and NaN scales give the IEEE

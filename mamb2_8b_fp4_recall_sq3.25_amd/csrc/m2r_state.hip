@@ -497,26 +497,52 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
   // wave-uniform choice, re-tested per chunk (a branch around the whole loop
   // makes the register allocator keep both versions' values apart)
   const bool fast = __builtin_amdgcn_ballot_w64(!unclamped) == 0;
+  if (fast) {
+    // the biased code as the low byte of t = RN(u r + 1.5 2^23 + bias) =
+    // 1.5 2^23 + bias + rint(u r), with a running maximum of the rounding
+    // residuals |f| = |RN(u r - rint(u r))| (round_residual_code)
+    float fmax_res = 0.f;
 #pragma unroll
-  for (int i = 0; i < N / 4; ++i) {
-    int q0, q1, q2, q3;
-    if (fast) {
-      q0 = quantize_code_unclamped(v[4 * i], d, r);
-      q1 = quantize_code_unclamped(v[4 * i + 1], d, r);
-      q2 = quantize_code_unclamped(v[4 * i + 2], d, r);
-      q3 = quantize_code_unclamped(v[4 * i + 3], d, r);
-    } else {
-      asm volatile("");   // keeps this a branch: the fast side must not pay for the clamp
-      q0 = quantize_code(v[4 * i], d, r, top);
-      q1 = quantize_code(v[4 * i + 1], d, r, top);
-      q2 = quantize_code(v[4 * i + 2], d, r, top);
-      q3 = quantize_code(v[4 * i + 3], d, r, top);
+    for (int i = 0; i < N / 4; ++i) {
+      float f[4];
+      uint32_t tb[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tb[j] = round_residual_code(v[4 * i + j], r, BIAS, f[j]);
+      fmax_res = max3_abs(fmax_res, f[0], f[1]);
+      fmax_res = max3_abs(fmax_res, f[2], f[3]);
+      uint32_t packed = pack4((int)tb[0], (int)tb[1], (int)tb[2], (int)tb[3]);
+      asm volatile("" : "+v"(packed));
+      c[i] = packed;
+      __builtin_amdgcn_sched_barrier(0);
     }
-    uint32_t packed = pack4(q0, q1, q2, q3);
-    packed = INT8 ? (packed ^ 0x80808080u) : ((packed & 0x0F0F0F0Fu) ^ 0x08080808u);
-    asm volatile("" : "+v"(packed));
-    c[i] = packed;
-    __builtin_amdgcn_sched_barrier(0);
+    // A lane whose u r lies within the residual margin of a half-integer may
+    // round differently from roundf(RN(u / d)): the wave then requantizes the
+    // tier with the exact quotients (rare: about 2 N margin per lane).
+    if (__builtin_amdgcn_ballot_w64(fmax_res > (INT8 ? RESIDUAL_OK8 : RESIDUAL_OK4)) != 0) {
+#pragma unroll
+      for (int i = 0; i < N / 4; ++i) {
+        const int q0 = quantize_code_unclamped(v[4 * i], d, r);
+        const int q1 = quantize_code_unclamped(v[4 * i + 1], d, r);
+        const int q2 = quantize_code_unclamped(v[4 * i + 2], d, r);
+        const int q3 = quantize_code_unclamped(v[4 * i + 3], d, r);
+        uint32_t packed = pack4(q0, q1, q2, q3);
+        packed = INT8 ? (packed ^ 0x80808080u) : ((packed & 0x0F0F0F0Fu) ^ 0x08080808u);
+        c[i] = packed;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      const int q0 = quantize_code(v[4 * i], d, r, top);
+      const int q1 = quantize_code(v[4 * i + 1], d, r, top);
+      const int q2 = quantize_code(v[4 * i + 2], d, r, top);
+      const int q3 = quantize_code(v[4 * i + 3], d, r, top);
+      uint32_t packed = pack4(q0, q1, q2, q3);
+      packed = INT8 ? (packed ^ 0x80808080u) : ((packed & 0x0F0F0F0Fu) ^ 0x08080808u);
+      asm volatile("" : "+v"(packed));
+      c[i] = packed;
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   return stored;
 }

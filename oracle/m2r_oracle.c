@@ -719,3 +719,62 @@ int64_t orc_check_latent_division(uint64_t seed, int n_random_per_scale) {
   }
   return bad;
 }
+
+/* The device's fast quantizer for quotients that need no clamping: with
+ * y = RN(1/d) and magic = 1.5 * 2^23 + bias, t = fma(v, y, magic) holds
+ * bias + rint(v*y) in its low bits and f = fma(v, y, -(t - magic)) is the
+ * rounding residual.  The device keeps that code unless |f| exceeds the
+ * residual bound thr (thr8 for lim 127, thr4 for lim 7 and 3), in which case
+ * it requantizes with the exact quotient.  Counts the (v, d) pairs with
+ * |f| <= thr whose fast code differs from roundf(v / d) (IEEE division), or
+ * whose low byte is not (code + bias) mod 256.  Inputs: pseudo-random scales
+ * (normal binary16 values, and binary32 values >= 2^-26 for the binary32
+ * denominators of the legacy codec) with quotients uniform in
+ * |v / d| <= lim + 0.49, and every half-integer boundary (k + 1/2) * d moved
+ * by up to +-40 ulps, both signs.  `flagged` receives the number of pairs
+ * sent to the exact path. */
+int64_t orc_check_residual_round(uint64_t seed, int64_t n_random, int n_boundary_scales, float thr8, float thr4,
+                                 int64_t* flagged) {
+  int64_t bad = 0, flg = 0;
+#pragma omp parallel for reduction(+ : bad, flg) schedule(static)
+  for (int64_t i = 0; i < n_random + (int64_t)n_boundary_scales; ++i) {
+    uint64_t z = seed + (uint64_t)i * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    const int li = (int)((z >> 3) % 3);
+    const float lim = li == 0 ? 127.0f : (li == 1 ? 7.0f : 3.0f);
+    const float bias = li == 0 ? 128.0f : (li == 1 ? 8.0f : 4.0f);
+    const float thr = li == 0 ? thr8 : thr4;
+    float d;
+    if (z & 1) d = orc_f16_to_f32((uint16_t)(0x0400 + (uint16_t)((z >> 8) % (0x7BFF - 0x0400 + 1))));
+    else d = bits_f((uint32_t)(0x32800000u + ((z >> 8) % (0x7F000000u - 0x32800000u))));
+    const float y = 1.0f / d;
+    const float magic = 0x1.8p23f + bias;
+    float vs[2 * 81 * 2 + 1];
+    int nv = 0;
+    if (i < n_random) {
+      const float u = (bits_f((uint32_t)(0x3F800000u | ((z >> 20) & 0x7FFFFFu))) - 1.5f) * 2.0f * (lim + 0.49f);
+      vs[nv++] = u * d;
+    } else {
+      const int k = (int)((z >> 40) % (uint64_t)lim);     /* boundary k + 1/2 for k < lim */
+      const uint32_t mb = f_bits(((float)k + 0.5f) * d);  /* exact */
+      for (int du = -40; du <= 40; ++du) {
+        vs[nv++] = bits_f(mb + du);
+        vs[nv++] = -bits_f(mb + du);
+      }
+    }
+    for (int j = 0; j < nv; ++j) {
+      const float v = vs[j];
+      if (!isfinite(v) || fabsf(v / d) > lim + 0.49f) continue;
+      const float t = fmaf(v, y, magic);
+      const float f = fmaf(v, y, -(t - magic));
+      if (fabsf(f) > thr) { ++flg; continue; }
+      const int fast = (int)(t - magic);
+      const int exact = (int)roundf(v / d);
+      if (fast != exact || ((f_bits(t) - (uint32_t)(exact + (int)bias)) & 0xFFu) != 0u) ++bad;
+    }
+  }
+  if (flagged) *flagged = flg;
+  return bad;
+}

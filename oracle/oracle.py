@@ -51,6 +51,8 @@ def lib():
         _lib.orc_check_markstein.argtypes = [ctypes.c_uint64, I64, I, P]
         _lib.orc_check_markstein.restype = I64
         _lib.orc_encode_legacy.argtypes = [P] * 6 + [I64]
+        _lib.orc_check_residual_round.argtypes = [ctypes.c_uint64, I64, I, ctypes.c_float, ctypes.c_float, P]
+        _lib.orc_check_residual_round.restype = I64
         _lib.orc_check_latent_division.argtypes = [ctypes.c_uint64, I]
         _lib.orc_check_latent_division.restype = I64
     return _lib
@@ -148,6 +150,14 @@ def check_markstein(seed: int, n_random: int, n_boundary_scales: int):
     div_bad = ctypes.c_int64(0)
     bad = lib().orc_check_markstein(seed, n_random, n_boundary_scales, ctypes.byref(div_bad))
     return int(bad), int(div_bad.value)
+
+
+def check_residual_round(seed: int, n_random: int, n_boundary_scales: int, thr8: float, thr4: float):
+    """Returns (fast codes that differ from roundf(v / d), pairs sent to the
+    exact path)."""
+    flagged = ctypes.c_int64(0)
+    bad = lib().orc_check_residual_round(seed, n_random, n_boundary_scales, thr8, thr4, ctypes.byref(flagged))
+    return int(bad), int(flagged.value)
 
 
 def threads():
