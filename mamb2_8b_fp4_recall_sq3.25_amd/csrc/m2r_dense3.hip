@@ -396,39 +396,50 @@ __device__ __forceinline__ float d3_half(const uint32_t (&w)[12], uint32_t (&nw)
   const float d = inf ? 1.0f : den;
   const float r = inf ? 0.0f : 1.0f / den;
   const bool fast = __builtin_amdgcn_ballot_w64(!ok) == 0;
+  // codes (two's complement bytes: bits 0..2 are the 3-bit code) into the
+  // plane words; `codes4(i0)` packs the codes of internal positions i0..i0+3
+  auto to_planes = [&](auto codes4) {
 #pragma unroll
-  for (int wl = 0; wl < 2; ++wl) {
-    uint32_t z[3] = {0u, 0u, 0u};
+    for (int wl = 0; wl < 2; ++wl) {
+      uint32_t z[3] = {0u, 0u, 0u};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t pk[2];
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t pk0 = codes4(32 * wl + 8 * j), pk1 = codes4(32 * wl + 8 * j + 4);
+        // bits 0..2: codes of h = 0, bits 4..6: h = 1 (bits 3 and 7 are never selected)
+        const uint32_t xw = (pk0 & 0x07070707u) | ((pk1 << 4) & 0xF8F8F8F8u);
+        const uint32_t yw = rotl_dev(xw, j);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int i0 = 32 * wl + 8 * j + 4 * h;
-        int q0, q1, q2, q3;
-        if (fast) {
-          q0 = quantize_code_unclamped(v[i0], d, r);
-          q1 = quantize_code_unclamped(v[i0 + 1], d, r);
-          q2 = quantize_code_unclamped(v[i0 + 2], d, r);
-          q3 = quantize_code_unclamped(v[i0 + 3], d, r);
-        } else {
-          asm volatile("");   // keeps this a branch: the fast side must not pay for the clamp
-          q0 = quantize_code(v[i0], d, r, QTOP3);
-          q1 = quantize_code(v[i0 + 1], d, r, QTOP3);
-          q2 = quantize_code(v[i0 + 2], d, r, QTOP3);
-          q3 = quantize_code(v[i0 + 3], d, r, QTOP3);
-        }
-        pk[h] = pack4(q0, q1, q2, q3);   // two's complement bytes: bits 0..2 are the 3-bit code
+        for (int k = 0; k < 3; ++k) z[k] |= yw & d3_mask(k, j);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      // bits 0..2: codes of h = 0, bits 4..6: h = 1 (bits 3 and 7 are never selected)
-      const uint32_t xw = (pk[0] & 0x07070707u) | ((pk[1] << 4) & 0xF8F8F8F8u);
-      const uint32_t yw = rotl_dev(xw, j);
 #pragma unroll
-      for (int k = 0; k < 3; ++k) z[k] |= yw & d3_mask(k, j);
-      __builtin_amdgcn_sched_barrier(0);
+      for (int k = 0; k < 3; ++k) nw[4 * k + 2 * HF + wl] = rotr_dev(z[k], k);
     }
+  };
+  if (fast) {
+    // the code as the low bits of t = RN(v r + 1.5 2^23) = 1.5 2^23 + rint(v r),
+    // with a running maximum of the rounding residuals (round_residual_code)
+    float fmax_res = 0.f;
+    to_planes([&](int i0) {
+      float f[4];
+      uint32_t tb[4];
 #pragma unroll
-    for (int k = 0; k < 3; ++k) nw[4 * k + 2 * HF + wl] = rotr_dev(z[k], k);
+      for (int m = 0; m < 4; ++m) tb[m] = round_residual_code(v[i0 + m], r, 0.0f, f[m]);
+      fmax_res = max3_abs(fmax_res, f[0], f[1]);
+      fmax_res = max3_abs(fmax_res, f[2], f[3]);
+      return pack4((int)tb[0], (int)tb[1], (int)tb[2], (int)tb[3]);
+    });
+    // a lane near a rounding boundary: the half row again with exact quotients
+    if (__builtin_amdgcn_ballot_w64(fmax_res > RESIDUAL_OK4) != 0)
+      to_planes([&](int i0) {
+        return pack4(quantize_code_unclamped(v[i0], d, r), quantize_code_unclamped(v[i0 + 1], d, r),
+                     quantize_code_unclamped(v[i0 + 2], d, r), quantize_code_unclamped(v[i0 + 3], d, r));
+      });
+  } else {
+    to_planes([&](int i0) {
+      return pack4(quantize_code(v[i0], d, r, QTOP3), quantize_code(v[i0 + 1], d, r, QTOP3),
+                   quantize_code(v[i0 + 2], d, r, QTOP3), quantize_code(v[i0 + 3], d, r, QTOP3));
+    });
   }
   return stored;
 }
