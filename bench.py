@@ -146,16 +146,32 @@ def time_graph(g, steps, warmup):
 TRAFFIC_PROFILE = ROOT / "profiles" / "state_step_b64_pmc_traffic.txt"
 
 
+STEP_KERNEL_SOURCES = ("m2r_state.hip", "m2r_device.h", "m2r_tile.h")
+
+
+def step_kernel_digest():
+    """First 16 hex digits of the SHA-256 of the step kernel's sources (in
+    STEP_KERNEL_SOURCES order): the key under which a traffic profile of that
+    kernel is valid."""
+    import hashlib
+    h = hashlib.sha256()
+    for name in STEP_KERNEL_SOURCES:
+        h.update((ROOT / "mamb2_8b_fp4_recall_sq3.25_amd" / "csrc" / name).read_bytes())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic():
     """HBM bytes per launch of the step kernel at batch 64, from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (copy-calibrated), or None."""
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (copy-calibrated), or None when
+    the summary is missing or was measured on other kernel sources than the
+    ones in this tree (its kernel_source_sha16 line)."""
     try:
-        for line in TRAFFIC_PROFILE.read_text().splitlines():
-            if line.startswith("traffic_bytes_per_launch"):
-                return int(line.split("=")[1].strip())
-    except (OSError, ValueError, IndexError):
+        fields = dict(line.split("=", 1) for line in TRAFFIC_PROFILE.read_text().splitlines() if "=" in line)
+        if fields.get("kernel_source_sha16", "").strip() != step_kernel_digest():
+            return None
+        return int(fields["traffic_bytes_per_launch"].strip())
+    except (OSError, ValueError, KeyError):
         return None
-    return None
 
 
 def copy_bandwidth(device):
@@ -183,7 +199,60 @@ def copy_bandwidth(device):
     return copy_gbs, fill_gbs
 
 
-def fp4_full_decode(device, steps=3):
+# (bytes read, 16-byte vectors written) per unit
+MIXES = {"read_only": (16, 0), "write_only": (0, 1), "copy_1to1": (16, 1), "fp4_mix_22to78": (32, 7),
+         "fp4_shape_20to80": (4, 1)}
+
+
+def stream_ceiling(device, reps=10):
+    """HBM ceilings measured by the library's hand-written streaming kernel
+    (m2r_stream_probe): read-only, write-only, 1:1 (the state step's mix) and
+    22:78 read:write (the FP4 G16 decode's 4.5 bytes read per 16 written),
+    and a 4-byte read per 16-byte write (20:80: the decode's access shape,
+    256 B read and 1 KiB written per wave instruction).
+    Variants: 1 GiB or 4 GiB moved per launch; one unit per lane per step or
+    bursts of 8 units' loads before their stores; a grid of 2048 or 16384
+    workgroups striding over the buffer, or one step per wave; the default or
+    the non-temporal cache policy.  Returns GB/s of bytes moved per variant
+    and the best per mix."""
+    import ctypes
+    from mamba2_recall import _native
+    src = torch.empty(2 << 30, dtype=torch.uint8, device=device)
+    dst = torch.empty(4 << 30, dtype=torch.uint8, device=device)
+    src.fill_(3)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    h = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out, best = {}, {}
+    for name, (r, w) in MIXES.items():
+        per_unit = r + 16 * w
+        for size in (1 << 30, 4 << 30):
+            units = min((src.numel() // r) if r else 1 << 62, (dst.numel() // (16 * w)) if w else 1 << 62,
+                        size // per_unit)
+            for burst, blocks, nt in [(b, g, n) for b in ((1, 4) if r == 4 else (1, 8)) for g in (2048, 16384, 0)
+                                      for n in (0, 1)]:
+                u = units - units % (64 * burst)
+
+                def run():
+                    _native.call("m2r_stream_probe", _native.ptr(src), _native.ptr(dst), u, r, w, burst, blocks, nt, h)
+                run()
+                torch.cuda.synchronize()
+                ev0.record()
+                for _ in range(reps):
+                    run()
+                ev1.record()
+                torch.cuda.synchronize()
+                gbs = u * per_unit * reps / (ev0.elapsed_time(ev1) * 1e-3) / 1e9
+                key = f"{name}/{size >> 30}GiB/burst{burst}/{'blocks' + str(blocks) if blocks else 'onestep'}/{'nt' if nt else 'default'}"
+                out[key] = round(gbs, 1)
+                best[name] = max(best.get(name, 0.0), round(gbs, 1))
+    del src, dst
+    torch.cuda.empty_cache()
+    return dict(best_gbs=best, variants_gbs=out,
+                note="m2r_stream_probe: 16-byte loads/stores, contiguous 1 KiB per wave instruction, "
+                     "256-thread workgroups; GB/s of bytes read + written")
+
+
+def fp4_full_decode(device, steps=10):
     """56 x in_proj [18560,4096] + 56 x out_proj [4096,8192]
     + embedding and lm_head [256000,4096]; random nibbles, lognormal(-3,0.5)
     block scales in the reference G16 format (E4M3 of s/global, global =
@@ -560,7 +629,7 @@ def main():
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--skip-fp4", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=("step", "copy", "codecs", "e2e", "loader"), default=None)
+    ap.add_argument("--only", choices=("step", "copy", "codecs", "e2e", "loader", "ceiling"), default=None)
     ap.add_argument("--e2e", action="store_true", help="also time the end-to-end 8B decode (BASELINE config 5)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -571,15 +640,21 @@ def main():
     device = torch.device("cuda:0")
     from mamba2_recall import _native
     _native.lib()
-    if args.only == "copy":
-        a = torch.empty(256 << 20, dtype=torch.uint8, device=device)
+    if args.only == "copy":   # counter calibration: the probe's 1:1 copy of 256 MiB, known bytes each way
+        import ctypes
+        a = torch.full((256 << 20,), 3, dtype=torch.uint8, device=device)
         b = torch.empty_like(a)
+        h = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         for _ in range(args.steps):
-            b.copy_(a)
+            _native.call("m2r_stream_probe", _native.ptr(a), _native.ptr(b), a.numel() // 16, 16, 1, 1, 2048, 0, h)
         torch.cuda.synchronize()
-        print(json.dumps(dict(only="copy", bytes_read=a.numel(), bytes_written=a.numel(), launches=args.steps)))
+        print(json.dumps(dict(only="copy", kernel="k_stream_probe<16, 1, 1, false>", bytes_read=a.numel(),
+                              bytes_written=a.numel(), launches=args.steps)))
         return
 
+    if args.only == "ceiling":
+        print(json.dumps(dict(only="ceiling", ceiling=stream_ceiling(device))))
+        return
     if args.only == "loader":
         print(json.dumps(dict(only="loader", loader=loader_bench(device))))
         return
@@ -613,15 +688,21 @@ def main():
     torch.cuda.empty_cache()
 
     copy_gbs, fill_gbs = copy_bandwidth(device)
+    ceiling = stream_ceiling(device)
+    best = ceiling["best_gbs"]
     extra = dict(batch1_us_per_token=round(ms1 * 1e3, 2), batch1_gbs=round(step_bytes(1, PUBLISHED_LAYOUTS) / (ms1 * 1e-3) / 1e9, 1),
                  batch64_us_per_token=round(ms * 1e3, 2), wall_ms_per_step=round(wall_ms, 4),
                  d2d_copy_gbs=round(copy_gbs, 1), write_only_fill_gbs=round(fill_gbs, 1),
-                 hbm_frac_of_copy=round(gbs / copy_gbs, 4))
+                 hbm_frac_of_copy=round(gbs / copy_gbs, 4),
+                 hbm_ceiling_best_gbs=best,
+                 step_frac_of_1to1_ceiling=round(achieved / best["copy_1to1"], 4))
     if not args.skip_fp4:
         fp4_ms, fp4_gbs = fp4_full_decode(device)
+        fp4_ceiling = max(best["fp4_mix_22to78"], best["fp4_shape_20to80"])
         extra.update(fp4_g16_full_decode_ms=round(fp4_ms, 3), fp4_g16_full_decode_gbs=round(fp4_gbs, 1),
                      fp4_g16_full_decode_frac=round(fp4_gbs / HBM_PEAK_GBS, 4),
-                     fp4_g16_frac_of_copy=round(fp4_gbs / copy_gbs, 4))
+                     fp4_g16_frac_of_copy=round(fp4_gbs / copy_gbs, 4),
+                     fp4_g16_frac_of_mix_ceiling=round(fp4_gbs / fp4_ceiling, 4))
     extra["other_codecs_b64"] = other_codecs(device)
     if args.e2e:
         extra["e2e_decode"] = e2e_decode(device)

@@ -135,6 +135,17 @@ int m2r_state_encode_legacy(const float* v, uint8_t* lo, uint8_t* hi, uint8_t* q
 int m2r_fp4_decode_g16(const uint8_t* packed, const uint8_t* e4m3_scales, const float* global_scale, void* out_f16,
                        int64_t rows, int64_t cols, uint32_t* err_flag, hipStream_t stream);
 
+/*
+ * Tuning and test hook for m2r_fp4_decode_g16 (cols % 16 == 0): units of 8
+ * weights per thread (1, 2, 4 or 8; 0 restores the automatic choice), the
+ * grid cap in 256-thread workgroups (0: no cap, one pass; a cap makes the
+ * workgroups stride over the matrix) and non-temporal (1) or default (0)
+ * output stores.  While a shape is forced, m2r_fp4_decode_g64 takes the same
+ * grid cap.  Process-wide; results do not depend on the shape.  No
+ * counterpart in the reference.
+ */
+int m2r_set_fp4_decode_shape(int units_per_thread, int max_blocks, int nontemporal);
+
 /* FP4 E2M1 G64 decode with f16 scales u16[rows, ceil(cols/64)]; same error bits
  * (32 unused).  Replaces mamba2_recall/fp4.py:225-250, G64 branch. */
 int m2r_fp4_decode_g64(const uint8_t* packed, const void* f16_scales, void* out_f16, int64_t rows, int64_t cols,
@@ -157,6 +168,23 @@ int m2r_probe_div(const float* a, const float* d, float* q, int64_t n, hipStream
  * level-l butterfly pair sum of in[lane] (l = 0..5); out[384] / out[385] are
  * the canonical adjacent-pair tree sums of in[64..191] / in[0..63]. */
 int m2r_probe_butterfly(const float* in, float* out, hipStream_t stream);
+
+/*
+ * HBM streaming probe (measurement only; no counterpart in the reference):
+ * `units` units, each reading `read_bytes` bytes (0, 4, 16 or 32) and writing
+ * `writes` 16-byte vectors (src: units*read_bytes bytes, dst:
+ * units*writes*16 bytes, at least 16; both 16-byte aligned); every store
+ * instruction of a wave is a contiguous 1 KiB, every load a contiguous
+ * 64*min(read_bytes,16) bytes; each lane issues `burst` units' loads before
+ * their stores, over a grid-stride grid of `blocks` workgroups of 256 threads
+ * (0: one step per wave), with the default (nontemporal = 0) or the
+ * non-temporal cache policy.  (read_bytes, writes, burst) in {(16,0), (0,1),
+ * (16,1), (32,7)} x burst {1, 8}, or (4,1) with burst 1 or 4; units a
+ * multiple of 64*burst.  Gives the read-only, write-only, 1:1, 22:78 (the FP4
+ * G16 decode's byte mix) and dword-read 20:80 (its access shape) ceilings.
+ */
+int m2r_stream_probe(const void* src, void* dst, int64_t units, int read_bytes, int writes, int burst, int blocks,
+                     int nontemporal, hipStream_t stream);
 
 /*
  * One-token causal depthwise convolution update of the Mamba-2 mixer: roll

@@ -20,6 +20,8 @@
 #include "m2r_device.h"
 #include "m2r_abi_util.h"
 
+#include <atomic>
+
 namespace m2r {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -75,7 +77,7 @@ __device__ __forceinline__ void report(uint32_t err, uint32_t* flag) {
 
 // G16, cols % 16 == 0: unit u covers weights [8u, 8u+8) of the flattened
 // matrix; its block scale byte is u/2.
-template <int UPT>
+template <int UPT, bool NT>
 __global__ __launch_bounds__(256) void k_fp4_g16(const uint32_t* __restrict__ codes,
                                                  const uint8_t* __restrict__ scales,
                                                  const float* __restrict__ global_scale,
@@ -104,7 +106,8 @@ __global__ __launch_bounds__(256) void k_fp4_g16(const uint32_t* __restrict__ co
       err |= (mag == 0u && (cw[k] & 0x77777777u) != 0u) ? FP4_ERR_ZERO_SCALE_CODE : 0u;
       float hb = e4m3_byte_to_f32<0>(mag) * 0.5f;   // FP8 instruction (0x7F: NaN, flagged above)
       u32x4 v = decode8<true>(cw[k], hb, gl, s >> 7, err);
-      __builtin_nontemporal_store(v, out + u);
+      if constexpr (NT) __builtin_nontemporal_store(v, out + u);
+      else out[u] = v;
     }
   }
   report(err, flag);
@@ -194,13 +197,24 @@ __global__ __launch_bounds__(256) void k_fp4_padded(const uint8_t* __restrict__ 
   report(err, flag);
 }
 
-static int grid_for(int64_t n_units, int upt) {
+static int grid_for(int64_t n_units, int upt, int64_t cap) {
   int64_t per_block = 256LL * upt;
   int64_t blocks = (n_units + per_block - 1) / per_block;
-  const int64_t cap = 256LL * 64;   // 64 workgroups per CU at most; loop covers the rest
-  if (blocks > cap) blocks = cap;
+  if (cap > 0 && blocks > cap) blocks = cap;   // the grid-stride loop covers the rest
   if (blocks < 1) blocks = 1;
+  if (blocks > 0x7FFFFFFF) blocks = 0x7FFFFFFF;
   return (int)blocks;
+}
+
+// G16 decode shape forced through m2r_set_fp4_decode_shape (0 = automatic):
+// units per thread, grid cap in workgroups, non-temporal stores.
+static std::atomic<int> g_fp4_upt{0}, g_fp4_cap{0}, g_fp4_nt{1};
+
+template <int UPT>
+static void launch_g16(bool nt, dim3 grid, hipStream_t stream, const uint32_t* codes, const uint8_t* scales,
+                       const float* gl, u32x4* out, int64_t n_units, uint32_t* flag) {
+  if (nt) hipLaunchKernelGGL((k_fp4_g16<UPT, true>), grid, dim3(256), 0, stream, codes, scales, gl, out, n_units, flag);
+  else hipLaunchKernelGGL((k_fp4_g16<UPT, false>), grid, dim3(256), 0, stream, codes, scales, gl, out, n_units, flag);
 }
 
 }  // namespace m2r
@@ -211,10 +225,21 @@ extern "C" int m2r_fp4_decode_g16(const uint8_t* packed, const uint8_t* e4m3_sca
                                   void* out_f16, int64_t rows, int64_t cols, uint32_t* err_flag, hipStream_t stream) {
   if (rows <= 0 || cols <= 0) return m2r_fail("fp4 g16: non-positive shape");
   if (cols % 16 == 0) {
-    int64_t n_units = rows * cols / 8;
-    constexpr int UPT = 4;
-    hipLaunchKernelGGL((k_fp4_g16<UPT>), dim3(grid_for(n_units, UPT)), dim3(256), 0, stream,
-                       (const uint32_t*)packed, e4m3_scales, global_scale, (u32x4*)out_f16, n_units, err_flag);
+    const int64_t n_units = rows * cols / 8;
+    const int forced = g_fp4_upt.load(std::memory_order_relaxed);
+    const int upt = forced ? forced : 4;
+    // automatic: four units per thread, one pass (no grid cap), non-temporal
+    // stores: the fastest of 1/2/4/8 units x caps 2048/4096/16384/none x
+    // store policies on the full 8B weight set
+    const int64_t cap = forced ? g_fp4_cap.load(std::memory_order_relaxed) : 0;
+    const bool nt = forced ? g_fp4_nt.load(std::memory_order_relaxed) != 0 : true;
+    const dim3 grid(grid_for(n_units, upt, cap));
+    const uint32_t* codes = (const uint32_t*)packed;
+    u32x4* out = (u32x4*)out_f16;
+    if (upt == 1) launch_g16<1>(nt, grid, stream, codes, e4m3_scales, global_scale, out, n_units, err_flag);
+    else if (upt == 2) launch_g16<2>(nt, grid, stream, codes, e4m3_scales, global_scale, out, n_units, err_flag);
+    else if (upt == 8) launch_g16<8>(nt, grid, stream, codes, e4m3_scales, global_scale, out, n_units, err_flag);
+    else launch_g16<4>(nt, grid, stream, codes, e4m3_scales, global_scale, out, n_units, err_flag);
   } else {
     int64_t groups = (cols + 15) / 16;
     int64_t n = rows * groups;
@@ -230,7 +255,8 @@ extern "C" int m2r_fp4_decode_g64(const uint8_t* packed, const void* f16_scales,
   if (cols % 64 == 0) {
     int64_t n_units = rows * cols / 8;
     constexpr int UPT = 4;
-    hipLaunchKernelGGL((k_fp4_g64<UPT>), dim3(grid_for(n_units, UPT)), dim3(256), 0, stream,
+    const int64_t cap = g_fp4_upt.load(std::memory_order_relaxed) ? g_fp4_cap.load(std::memory_order_relaxed) : 0;
+    hipLaunchKernelGGL((k_fp4_g64<UPT>), dim3(grid_for(n_units, UPT, cap)), dim3(256), 0, stream,
                        (const uint32_t*)packed, (const uint16_t*)f16_scales, (u32x4*)out_f16, n_units, err_flag);
   } else {
     int64_t groups = (cols + 63) / 64;
@@ -239,4 +265,14 @@ extern "C" int m2r_fp4_decode_g64(const uint8_t* packed, const void* f16_scales,
                        f16_scales, (const float*)nullptr, (uint16_t*)out_f16, rows, cols, err_flag);
   }
   return m2r_check(hipGetLastError(), "fp4 g64 launch");
+}
+
+extern "C" int m2r_set_fp4_decode_shape(int units_per_thread, int max_blocks, int nontemporal) {
+  const int u = units_per_thread;
+  if (!(u == 0 || u == 1 || u == 2 || u == 4 || u == 8) || max_blocks < 0)
+    return m2r_fail("fp4 decode shape: units per thread 1, 2, 4 or 8 (0 = automatic), max_blocks >= 0");
+  g_fp4_cap.store(max_blocks, std::memory_order_relaxed);
+  g_fp4_nt.store(nontemporal ? 1 : 0, std::memory_order_relaxed);
+  g_fp4_upt.store(u, std::memory_order_relaxed);
+  return 0;
 }

@@ -2,6 +2,7 @@
 // arithmetic primitives of the codec for exhaustive known-answer testing.
 #include <stdio.h>
 #include <string.h>
+#include <type_traits>
 #include "m2r_device.h"
 #include "m2r_abi_util.h"
 #include "m2r_tile.h"
@@ -98,9 +99,101 @@ __global__ __launch_bounds__(64) void k_probe_butterfly(const float* in, float* 
   if (lane == 0) { out[384] = t128; out[385] = t64; }
 }
 
+// HBM streaming probe: the bandwidth ceiling of a read:write byte mix, with
+// nothing computed.  A unit reads RB bytes (0, 4, 16 or 32) and writes W
+// 16-byte vectors.  A wave owns 64 * BURST consecutive units per grid-stride
+// step; it first issues all of the step's loads, then all of its stores;
+// every store instruction is a contiguous 1 KiB, every load instruction a
+// contiguous 64 * min(RB, 16) bytes (load k of burst j covers the source
+// block's load-sized elements 64 (j RL + k) + lane, RL loads per unit).
+// Stores write the XOR of the unit's loads (or the unit index when RB = 0);
+// with W = 0 the loads fold into one word that is stored only if it equals a
+// value the test data never produces, so the loads stay live.  NT:
+// non-temporal loads and stores, else the default cache policy.
+template <int RB, int W, int BURST, bool NT>
+__global__ __launch_bounds__(256) void k_stream_probe(const void* src, u32x4* dst, int64_t units) {
+  constexpr int LB = RB >= 16 ? 16 : (RB > 0 ? 4 : 16);   // bytes per lane per load
+  constexpr int RL = RB / LB;                              // loads per unit
+  typedef typename std::conditional<LB == 16, u32x4, uint32_t>::type LT;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 6;
+  const int64_t nwaves = ((int64_t)gridDim.x * 256) >> 6;
+  constexpr int64_t STEP = 64 * BURST;
+  uint32_t fold = 0u;
+  for (int64_t base = wave * STEP; base < units; base += nwaves * STEP) {
+    LT v[BURST * (RL > 0 ? RL : 1)];
+    if constexpr (RL > 0) {
+      const LT* s = (const LT*)src + base * RL;
+#pragma unroll
+      for (int i = 0; i < BURST * RL; ++i) v[i] = NT ? __builtin_nontemporal_load(s + 64 * i + lane) : s[64 * i + lane];
+    }
+    if constexpr (W > 0) {
+      u32x4* d = dst + base * W;
+#pragma unroll
+      for (int j = 0; j < BURST; ++j) {
+        u32x4 val;
+        if constexpr (RL > 0) {
+          LT x = v[j * RL];
+#pragma unroll
+          for (int k = 1; k < RL; ++k) x ^= v[j * RL + k];
+          if constexpr (LB == 16) val = x;
+          else val = u32x4{x, x + 1u, x + 2u, x + 3u};
+        } else {
+          const uint32_t u = (uint32_t)(base + 64 * j + lane);
+          val = u32x4{u, u, u, u};
+        }
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+          if constexpr (NT) __builtin_nontemporal_store(val, d + 64 * (j * W + k) + lane);
+          else d[64 * (j * W + k) + lane] = val;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < BURST * RL; ++i) {
+        if constexpr (LB == 16) fold ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+        else fold ^= v[i];
+      }
+    }
+  }
+  if constexpr (W == 0) {
+    if (fold == 0x9E3779B9u) dst[0] = u32x4{fold, fold, fold, fold};
+  }
+}
+
 }  // namespace m2r
 
 using namespace m2r;
+
+// (RB, W, BURST, NT) instances: read-only, write-only, 1:1 copy, 2:7 vectors
+// (22:78, the FP4 G16 decode's byte mix), and a dword read per 16-byte write
+// (20:80, the FP4 decode's access shape: 256 B read and 1 KiB written per
+// wave instruction), each streamed unit by unit or in bursts of 8 units per
+// lane, with the default or the non-temporal cache policy.
+extern "C" int m2r_stream_probe(const void* src, void* dst, int64_t units, int read_bytes, int writes, int burst,
+                                int blocks, int nontemporal, hipStream_t stream) {
+  if (units <= 0 || blocks < 0 || burst <= 0 || units % (64 * (int64_t)burst))
+    return m2r_fail("stream probe: bad geometry");
+  if (blocks == 0) {   // one grid-stride step per wave
+    const int64_t b = (units / (64 * (int64_t)burst) + 3) / 4;
+    if (b > 0x7FFFFFFF) return m2r_fail("stream probe: grid too large");
+    blocks = (int)b;
+  }
+  if ((read_bytes > 0 && !src) || !dst || (((uintptr_t)src | (uintptr_t)dst) & 15)) return m2r_fail("stream probe: bad buffers");
+  const dim3 grid((unsigned)blocks), block(256);
+  u32x4* d = (u32x4*)dst;
+#define M2R_PROBE(r, w, b)                                                                          \
+  if (read_bytes == r && writes == w && burst == b) {                                               \
+    if (nontemporal) hipLaunchKernelGGL((k_stream_probe<r, w, b, true>), grid, block, 0, stream, src, d, units); \
+    else hipLaunchKernelGGL((k_stream_probe<r, w, b, false>), grid, block, 0, stream, src, d, units);  \
+    return m2r_check(hipGetLastError(), "stream probe");                                            \
+  }
+  M2R_PROBE(16, 0, 1) M2R_PROBE(16, 0, 8) M2R_PROBE(0, 1, 1) M2R_PROBE(0, 1, 8)
+  M2R_PROBE(16, 1, 1) M2R_PROBE(16, 1, 8) M2R_PROBE(32, 7, 1) M2R_PROBE(32, 7, 8)
+  M2R_PROBE(4, 1, 1) M2R_PROBE(4, 1, 4)
+#undef M2R_PROBE
+  return m2r_fail("stream probe: (read bytes, writes, burst) must be (16,0), (0,1), (16,1) or (32,7) with burst 1 or 8, or (4,1) with burst 1 or 4");
+}
 
 extern "C" int m2r_probe_butterfly(const float* in, float* out, hipStream_t stream) {
   hipLaunchKernelGGL(k_probe_butterfly, dim3(1), dim3(64), 0, stream, in, out);

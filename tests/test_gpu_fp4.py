@@ -90,10 +90,10 @@ def _assert_equal_in_chunks(got_dev, want, rows_per_chunk=16384):
         assert bad == 0, f"rows {r0}..: {bad} mismatched FP16 weights"
 
 
-def test_g16_grid_stride_sweeps_embedding_matrix(oracle, device):
-    """The [256000, 4096] embedding / lm_head matrix of the full 8B set:
-    131,072,000 eight-weight units, more than the 16,777,216 units one grid of
-    the decode covers, so every workgroup runs several grid-stride sweeps."""
+def test_g16_embedding_matrix_bit_exact(oracle, device):
+    """The [256000, 4096] embedding / lm_head matrix of the full 8B set
+    (131,072,000 eight-weight units) at the automatic decode shape: one pass
+    of 128,000 workgroups."""
     rows, cols = 256000, 4096
     rng = np.random.default_rng(256000)
     packed = rng.integers(0, 256, size=(rows, cols // 2), dtype=np.uint8)
@@ -101,20 +101,59 @@ def test_g16_grid_stride_sweeps_embedding_matrix(oracle, device):
     g = np.float32(s.max() / 448.0)
     sb = torch.from_numpy(np.clip(s / g, 0, 448)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
     del s
-    print(f"[fp4 g16 sweeps] rows={rows} cols={cols} units={rows * cols // 8}", flush=True)
+    print(f"[fp4 g16 embedding] rows={rows} cols={cols} units={rows * cols // 8}", flush=True)
     want, err = oracle.fp4_decode(16, packed, sb, g, rows, cols)
     assert err == 0
     _assert_equal_in_chunks(decode_dev(packed, sb, g, rows, cols, device), want)
 
 
+def _forced_fp4_shape(upt, cap, nt):
+    from mamba2_recall import _native
+    lib = _native.lib()
+    assert lib.m2r_set_fp4_decode_shape(upt, cap, nt) == 0
+    return lib
+
+
+@pytest.mark.parametrize("upt,cap,nt", [(1, 2048, 1), (2, 4096, 0), (4, 2048, 1), (4, 0, 0), (8, 1024, 0),
+                                        (8, 0, 1)])
+def test_g16_forced_shapes_and_grid_stride_sweeps(oracle, device, upt, cap, nt):
+    """Every decode shape the tuning hook offers gives the oracle's weights:
+    1-8 units per thread, default and non-temporal stores, and grid caps of
+    1024-4096 workgroups, which make each workgroup stride over the
+    [4096, 8192] out_proj matrix (4,194,304 units) in 2 to 16 sweeps."""
+    rows, cols = 4096, 8192
+    rng = np.random.default_rng(upt * 100 + cap + nt)
+    packed = rng.integers(0, 256, size=(rows, cols // 2), dtype=np.uint8)
+    s = np.exp(rng.normal(-3.0, 0.5, size=(rows, cols // 16))).astype(np.float32)
+    g = np.float32(s.max() / 448.0)
+    sb = torch.from_numpy(np.clip(s / g, 0, 448)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    print(f"[fp4 g16 shape] upt={upt} cap={cap} nt={nt}", flush=True)
+    want, err = oracle.fp4_decode(16, packed, sb, g, rows, cols)
+    assert err == 0
+    lib = _forced_fp4_shape(upt, cap, nt)
+    try:
+        got = decode_dev(packed, sb, g, rows, cols, device)
+    finally:
+        lib.m2r_set_fp4_decode_shape(0, 0, 1)
+    _assert_equal_in_chunks(got, want)
+
+
 def test_g64_grid_stride_sweeps(oracle, device):
-    rows, cols = 40000, 4096          # 20,480,000 units: a second, partial sweep
+    """G64 under a forced grid cap of 2048 workgroups: 20,480,000 units in
+    ten sweeps."""
+    rows, cols = 40000, 4096
     rng = np.random.default_rng(40000)
     packed = rng.integers(0, 256, size=(rows, cols // 2), dtype=np.uint8)
     sc = np.exp(rng.normal(-3.0, 0.5, size=(rows, cols // 64))).astype(np.float16).view(np.uint16)
     print(f"[fp4 g64 sweeps] rows={rows} cols={cols} units={rows * cols // 8}", flush=True)
     want, err = oracle.fp4_decode(64, packed, sc, 1.0, rows, cols)
     assert err == 0
+    lib = _forced_fp4_shape(4, 2048, 1)
+    try:
+        got = decode_dev(packed, sc, None, rows, cols, device, group=64)
+    finally:
+        lib.m2r_set_fp4_decode_shape(0, 0, 1)
+    _assert_equal_in_chunks(got, want)
     _assert_equal_in_chunks(decode_dev(packed, sc, None, rows, cols, device, group=64), want)
 
 
