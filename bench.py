@@ -11,9 +11,11 @@ bandwidth, a live roofline for the dominant kernel, and the CPU oracle
 timed on a bounded sample (state step and FP4 decode) as a baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-fp4] [--skip-cpu]
-       python bench.py --only step|copy|codecs   (profiling runs: only the
-       batch-64 step graph, only a 256 MiB device copy used to calibrate
-       counters, or only the other codecs' batch-64 graphs)
+       python bench.py --only step|copy|codecs|layers|ceiling|e2e|loader
+       (profiling runs: only the step graph at --batch, only a 256 MiB copy
+       used to calibrate counters, only the other codecs' batch-64 graphs,
+       only the one-launch multi-layer step at --batch, only the HBM
+       ceilings, only the end-to-end decode, only the checkpoint loader)
 """
 from __future__ import annotations
 
@@ -126,6 +128,38 @@ class RidgeStack:
             self.launch_all(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
         torch.cuda.synchronize()
         return g
+
+
+def layers_one_launch(stack, steps, warmup):
+    """The same 56-layer one-token step as one launch of the multi-layer
+    kernel (m2r_state_step_ridge_layers: every workgroup reads its layer's
+    arguments from a table in device memory), captured as a one-node graph
+    after the table's first copy (replays reuse the staged table).  Returns ms
+    per 56-layer step."""
+    import ctypes
+    from mamba2_recall import ridge_codec
+    steps_ = [dict(x=d["x"], dt=d["dt"], A=d["A"], B=d["B"], C=d["C"], D=d["D"], dt_bias=d["dt_bias"],
+                   state=d["state"], permutation=d["perm"], basis=d["basis"], latent_scale=d["lscale"],
+                   predictor=d["pred"], layout=d["layout"], y=d["y"]) for d in stack.layers]
+    table = ridge_codec.layer_table(steps_)
+    n = len(steps_)
+    ws = torch.empty(ridge_codec.layers_workspace_bytes(n), dtype=torch.uint8, device=stack.device)
+    x = steps_[0]["x"]
+    args = (ctypes.byref(table), n, x.shape[0], H, P, G, stack.native.ptr(ws), ws.numel())
+    stack.native.call("m2r_state_step_ridge_layers", *args, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    import time as _t
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(warmup):
+        stack.native.call("m2r_state_step_ridge_layers", *args, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    ev0.record()
+    for _ in range(steps):
+        stack.native.call("m2r_state_step_ridge_layers", *args, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    ev1.record()
+    torch.cuda.synchronize()
+    eager_ms = ev0.elapsed_time(ev1) / steps
+    return eager_ms
 
 
 def time_graph(g, steps, warmup):
@@ -629,7 +663,7 @@ def main():
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--skip-fp4", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=("step", "copy", "codecs", "e2e", "loader", "ceiling"), default=None)
+    ap.add_argument("--only", choices=("step", "copy", "codecs", "e2e", "loader", "ceiling", "layers"), default=None)
     ap.add_argument("--e2e", action="store_true", help="also time the end-to-end 8B decode (BASELINE config 5)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -665,6 +699,11 @@ def main():
         print(json.dumps(dict(only="codecs", other_codecs_b64=other_codecs(device, steps=args.steps))))
         return
 
+    if args.only == "layers":   # the one-launch multi-layer step alone (profiling runs)
+        stack = RidgeStack(args.batch, device)
+        ms = layers_one_launch(stack, args.steps, args.warmup)
+        print(json.dumps(dict(only="layers", batch=args.batch, ms_per_step=round(ms, 5))))
+        return
     stack = RidgeStack(args.batch, device)
     g = stack.graph()
     ms, wall_ms = time_graph(g, args.steps, args.warmup)
@@ -684,6 +723,7 @@ def main():
     stack1 = RidgeStack(1, device, seed=2027)
     g1 = stack1.graph()
     ms1, _ = time_graph(g1, max(args.steps, 50), args.warmup)
+    ms1_one = layers_one_launch(stack1, max(args.steps, 50), args.warmup)
     del g1, stack1
     torch.cuda.empty_cache()
 
@@ -691,6 +731,9 @@ def main():
     ceiling = stream_ceiling(device)
     best = ceiling["best_gbs"]
     extra = dict(batch1_us_per_token=round(ms1 * 1e3, 2), batch1_gbs=round(step_bytes(1, PUBLISHED_LAYOUTS) / (ms1 * 1e-3) / 1e9, 1),
+                 batch1_one_launch_us_per_token=round(ms1_one * 1e3, 2),
+                 batch1_one_launch_note="the 56 synthetic layers as one launch of the multi-layer kernel "
+                                        "(layer table copied from the host every call), not a graph of 56 launches",
                  batch64_us_per_token=round(ms * 1e3, 2), wall_ms_per_step=round(wall_ms, 4),
                  d2d_copy_gbs=round(copy_gbs, 1), write_only_fill_gbs=round(fill_gbs, 1),
                  hbm_frac_of_copy=round(gbs / copy_gbs, 4),

@@ -187,6 +187,47 @@ int m2r_stream_probe(const void* src, void* dst, int64_t units, int read_bytes, 
                      int nontemporal, hipStream_t stream);
 
 /*
+ * One launch of the one-token ridge-latent step over many layers whose inputs
+ * are all resident: every workgroup reads its layer's arguments from a table
+ * and runs the per-layer step on them (results identical to one
+ * m2r_state_step_ridge call per layer with L = 1).  No counterpart in the
+ * reference, which steps one layer per mixer call; it is the one-launch
+ * all-layers variant of the batch-1 step (a 56-layer token otherwise takes
+ * 56 launches).  Requirements on every layer: a published layout, P % 8 == 0,
+ * 16-byte aligned lo, hi, q4, latent, s8, s4 and pred, 4-byte aligned B, C
+ * and lscale; all layers share batch, H, P and G; batch * nlayers <= 65535.
+ * The entry point copies the table (host array `layers`, reusable when the
+ * call returns) into `workspace`, a 16-byte aligned device buffer of at
+ * least m2r_state_step_ridge_layers_workspace(nlayers) bytes, on `stream`.
+ */
+typedef struct m2r_ridge_layer {
+  const void* x;        /* f16 [B,1,H,P] */
+  const void* dt;       /* f16 [B,1,H] */
+  const float* A;       /* f32 [H] */
+  const void* B;        /* f16 [B,1,G,128] */
+  const void* C;        /* f16 [B,1,G,128] */
+  const void* D;        /* f16 or f32 [H] */
+  const void* dt_bias;  /* f16 or f32 [H] */
+  const uint8_t* perm;  /* u8 [G,128] */
+  const void* basis;    /* f16 [G,nz,2] */
+  const void* lscale;   /* f16 [G,2] */
+  const void* pred;     /* f16 [G,n8+n4+2,nz] */
+  uint8_t* lo;
+  uint8_t* hi;
+  uint8_t* q4;
+  uint8_t* latent;
+  void* s8;
+  void* s4;
+  void* y;              /* f16 [B,1,H,P] */
+  int32_t n8, n4, nz;
+  int32_t d_is_f32, db_is_f32;
+  int32_t reserved;
+} m2r_ridge_layer;
+int64_t m2r_state_step_ridge_layers_workspace(int nlayers);
+int m2r_state_step_ridge_layers(const m2r_ridge_layer* layers, int nlayers, int64_t batch, int64_t H, int64_t P,
+                                int64_t G, void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
  * One-token causal depthwise convolution update of the Mamba-2 mixer: roll
  * the cached window one step, store the new projection column, and write
  * out = silu(sum_t half(window_t * weight[c,t]) + bias[c]) in binary16.

@@ -1,873 +1,12 @@
-// Fused Mamba-2 selective-state step + per-token requantization of the packed
-// 52-byte recurrent-state rows, for gfx950.
-//
-// One kernel template covers the three same-byte row formats of the
-// reference:
-//   MODE_LEGACY  sq3p25 16/64/48, quantized with the binary32 denominator
-//                (mamba2_recall/state_codec.py:105-176, _sq_scan)
-//   MODE_STORED  stored-scale INT8/INT4/zero tiers
-//                (scripts/state_ppl_codec_v10.py:78-154, _tier_scan;
-//                 scripts/state_ppl_codec_v6.py:83-195 stored_scale path)
-//   MODE_RIDGE   INT8/INT4 tiers + two E4M3 latent coefficients + the static
-//                zero-tier ridge predictor
-//                (scripts/fp4_zero_predictor_codec_v1.py:76-236, _latent_scan
-//                 and the einsum correction of scan())
-//
-// Mapping: one lane owns one state row r = (b, h, p); a wave owns 64
-// consecutive p of one head; a workgroup owns WPB heads of the same B/C
-// group.  The row's live coordinates (N8 + N4, compile-time) stay in VGPRs
-// for all L tokens.  Packed SoA rows are staged through LDS so that every
-// global access is a contiguous wave-wide transfer.  Per-token values shared
-// by the group (permuted B/C, dt activation, B*dt, ridge correction, dead-tier
-// dot products) are computed once per workgroup into LDS and read back as
-// wave-uniform broadcasts.
-#include "m2r_device.h"
+// Host dispatch and C ABI of the fused state step (kernel in m2r_step.h).
+#include "m2r_step.h"
 #include "m2r_abi_util.h"
-#include "m2r_tile.h"
 
 #include <atomic>
 #include <type_traits>
 #include <initializer_list>
 
 namespace m2r {
-
-enum { MODE_LEGACY = 0, MODE_STORED = 1, MODE_RIDGE = 2 };
-
-struct StepArgs {
-  const uint16_t* x;       // f16 [B, L, H, P]
-  const uint16_t* dt;      // f16 [B, L, H]
-  const float* A;          // f32 [H]
-  const uint16_t* Bm;      // f16 [B, L, G, 128]
-  const uint16_t* Cm;      // f16 [B, L, G, 128]
-  const void* D;           // f16 or f32 [H]
-  const void* dt_bias;     // f16 or f32 [H]
-  const uint8_t* perm;     // u8 [G, 128]: packed lane n holds coordinate perm[g, n]
-  const uint16_t* basis;   // f16 [G, NZ, 2]   (ridge)
-  const uint16_t* lscale;  // f16 [G, 2]       (ridge)
-  const uint16_t* pred;    // f16 [G, F, NZ]   (ridge), F = N8 + N4 + 2
-  uint8_t* lo;             // u8 [rows, N8/2]  low nibbles of the INT8 tier
-  uint8_t* hi;             // u8 [rows, N8/2]  high nibbles of the INT8 tier
-  uint8_t* q4;             // u8 [rows, N4/2]  INT4 tier
-  uint8_t* latent;         // e4m3 [rows, 2]   (ridge)
-  uint16_t* s8;            // f16 [rows]
-  uint16_t* s4;            // f16 [rows]
-  uint16_t* y;             // f16 [B, L, H, P]
-  int B, L, H, P, G;
-  int d_f32, db_f32;
-  int dma_tiles;           // P % 8 == 0, 16-byte aligned state fields and predictor, 4-byte aligned
-                           // B and C: 16-byte LDS transfers and paired B/C loads
-};
-
-// Carried coordinates are held in an internal lane order that makes the
-// conversion between the nibble planes and code bytes two bitfield inserts
-// per four coordinates: within each tier, every full group of 8 packed lanes
-// is ordered (0,2,4,6,1,3,5,7) and a final group of 4 is ordered (0,2,1,3).
-// packed_lane<N8,N4>(j) is the packed lane of internal position j (< N8+N4);
-// the zero tier keeps its natural order.
-constexpr int tier_packed_of(int j, int T) {
-  const int g = j / 8, k = j % 8;
-  if (g * 8 + 8 <= T) return g * 8 + (k < 4 ? 2 * k : 2 * (k - 4) + 1);
-  return g * 8 + (k < 2 ? 2 * k : 2 * (k - 2) + 1);
-}
-template <int N8, int N4>
-__device__ __forceinline__ int packed_lane(int j) {
-  return j < N8 ? tier_packed_of(j, N8) : (j < N8 + N4 ? N8 + tier_packed_of(j - N8, N4) : j);
-}
-
-// nibble-plane words -> carried code-byte words for one tier.
-// INT8: lo/hi plane words (8 lanes per word); byte = (q + 128) = code ^ 0x80.
-template <int N>
-__device__ __forceinline__ void planes_to_bytes8(const uint32_t* wl, const uint32_t* wh, uint32_t* c) {
-#pragma unroll
-  for (int g = 0; g < (N + 7) / 8; ++g) {
-    const uint32_t hb = wh[g] ^ 0x88888888u;                                   // bias via the high nibble
-    const uint32_t e = (wl[g] & 0x0F0F0F0Fu) | ((hb << 4) & 0xF0F0F0F0u);
-    const uint32_t o = ((wl[g] >> 4) & 0x0F0F0F0Fu) | (hb & 0xF0F0F0F0u);
-    if (g * 8 + 8 <= N) { c[2 * g] = e; c[2 * g + 1] = o; }
-    else c[2 * g] = (e & 0xFFFFu) | (o << 16);
-  }
-}
-// INT4: q4 plane words; byte = (q + 8) = nibble ^ 8.
-template <int N>
-__device__ __forceinline__ void plane_to_bytes4(const uint32_t* wq, uint32_t* c) {
-#pragma unroll
-  for (int g = 0; g < (N + 7) / 8; ++g) {
-    const uint32_t q = wq[g] ^ 0x88888888u;
-    const uint32_t e = q & 0x0F0F0F0Fu, o = (q >> 4) & 0x0F0F0F0Fu;
-    if (g * 8 + 8 <= N) { c[2 * g] = e; c[2 * g + 1] = o; }
-    else c[2 * g] = (e & 0xFFFFu) | (o << 16);
-  }
-}
-// carried bytes -> nibble-plane words (inverse of the two above)
-template <int N>
-__device__ __forceinline__ void bytes_to_planes8(const uint32_t* c, uint32_t* wl, uint32_t* wh) {
-#pragma unroll
-  for (int g = 0; g < (N + 7) / 8; ++g) {
-    uint32_t e, o;
-    if (g * 8 + 8 <= N) { e = c[2 * g]; o = c[2 * g + 1]; }
-    else { e = c[2 * g] & 0xFFFFu; o = c[2 * g] >> 16; }
-    wl[g] = (e & 0x0F0F0F0Fu) | ((o << 4) & 0xF0F0F0F0u);
-    wh[g] = (((e >> 4) & 0x0F0F0F0Fu) | (o & 0xF0F0F0F0u)) ^ 0x88888888u;
-  }
-}
-template <int N>
-__device__ __forceinline__ void bytes_to_plane4(const uint32_t* c, uint32_t* wq) {
-#pragma unroll
-  for (int g = 0; g < (N + 7) / 8; ++g) {
-    uint32_t e, o;
-    if (g * 8 + 8 <= N) { e = c[2 * g]; o = c[2 * g + 1]; }
-    else { e = c[2 * g] & 0xFFFFu; o = c[2 * g] >> 16; }
-    wq[g] = ((e & 0x0F0F0F0Fu) | ((o << 4) & 0xF0F0F0F0u)) ^ 0x88888888u;
-  }
-}
-
-// Per-token values of one wave, in the wave's own LDS region.  Only the
-// wave's own lanes read them, so building them needs no workgroup barrier:
-// the raw B/C rows, the permuted b and c, B*dt per head slot, the readout
-// weights of the carried coordinates, x of the wave's rows and per-slot and
-// per-token scalars.
-template <int N8, int N4, int HPW>
-struct WaveToken {
-  static constexpr int NL = N8 + N4;
-  alignas(16) float b[128];          // internal order
-  alignas(16) float c[128];
-  alignas(16) float cw[NL];          // readout weights of the carried coordinates: c (+ ridge correction)
-  alignas(16) float bdt[HPW][NL];    // RN(b * dt) per head slot
-  uint16_t x[HPW][64];               // x of the wave's rows, per head slot
-  float dtv[HPW], decay[HPW], D[HPW];
-  // per head slot: 1 when B*dt and the decay are bounded (|.| < 2^100), so
-  // that the state update of finite operands is finite
-  uint32_t bounded[HPW];
-  // 0: sum of b*c over all 128 coordinates (readout); 1, 2: dead-tier e0.c,
-  // e1.c plus the ridge correction of the latent coefficients (readout);
-  // 3, 4: dead-tier e0.b, e1.b (canonical trees, exact)
-  float dots[5];
-};
-
-// Per-token values of the ridge codec that the waves of a workgroup share
-// when they split the predictor correction (four or more waves): the readout
-// weights of the carried coordinates (c + correction), the latent
-// coefficients' corrections and the dead-tier dot products e.c and e.b, each
-// written by the wave that computes it and read after a workgroup barrier.
-template <int NL>
-struct GroupToken {
-  alignas(16) float cw[NL + 2];   // readout weights, then the latent coefficients' corrections
-  float tree[4];                  // e0.c, e1.c, e0.b, e1.b
-};
-
-// Inputs of one token that a wave loads one token ahead: its lane's two f16
-// of the group's B and of its C row, x of its rows in every head slot, and
-// for lanes < HPW the dt and dt_bias bits of head slot `lane`.  Nothing is
-// converted at load time, so no wait is needed until the token is built.
-template <int HPW>
-struct WaveRaw {
-  uint16_t bc[4];              // B[2 lane], B[2 lane + 1], C[2 lane], C[2 lane + 1]
-  uint16_t xv[HPW];
-  uint16_t dt, db_lo, db_hi;   // dt_bias: f16 bits, or the halves of f32 bits
-};
-
-// The dt inputs are loaded first: the dt activation of the first token
-// starts as soon as they land, while the other loads are still in flight.
-// Every load here is unconditional, with clamped indices (a conditional load
-// makes the compiler wait for it at the end of its branch).
-template <int WPB, int HPW>
-__device__ __forceinline__ void wave_load_dt(const StepArgs& a, WaveRaw<HPW>& r, int bt, int h0, int lane,
-                                             int wave) {
-  const int h = h0 + min(lane, HPW - 1) * WPB + wave;   // lanes >= HPW repeat the last slot
-  const uint16_t* db = (const uint16_t*)a.dt_bias;
-  r.dt = a.dt[(size_t)bt * a.H + h];
-  r.db_lo = db[a.db_f32 ? 2 * h : h];
-  r.db_hi = db[a.db_f32 ? 2 * h + 1 : h];
-}
-// ALIGNED: B and C are 4-byte aligned, so a lane's pair is one load each.
-template <int WPB, int HPW, bool ALIGNED>
-__device__ __forceinline__ void wave_load_rest(const StepArgs& a, WaveRaw<HPW>& r, int bt, int g, int h0,
-                                               int pbase, int lane, int wave) {
-  const size_t row = ((size_t)bt * a.G + g) * 128 + 2 * lane;
-  if constexpr (ALIGNED) {
-    const uint32_t bp = *(const uint32_t*)(a.Bm + row), cp = *(const uint32_t*)(a.Cm + row);
-    r.bc[0] = (uint16_t)bp;
-    r.bc[1] = (uint16_t)(bp >> 16);
-    r.bc[2] = (uint16_t)cp;
-    r.bc[3] = (uint16_t)(cp >> 16);
-  } else {
-    r.bc[0] = a.Bm[row];
-    r.bc[1] = a.Bm[row + 1];
-    r.bc[2] = a.Cm[row];
-    r.bc[3] = a.Cm[row + 1];
-  }
-  const int p = min(pbase + lane, a.P - 1);   // rows past P read row P-1 (never stored)
-#pragma unroll
-  for (int k = 0; k < HPW; ++k) {
-    const int h = h0 + k * WPB + wave;
-    r.xv[k] = a.x[((size_t)bt * a.H + h) * a.P + p];
-  }
-}
-
-// dt activation of head slot `lane` (lanes < HPW; the others compute a copy
-// of the last slot's, unused).
-template <int HPW>
-__device__ __forceinline__ float2 wave_dt_activation(const WaveRaw<HPW>& r, float Ah, int db_f32) {
-  const float db = db_f32 ? __builtin_bit_cast(float, (uint32_t)r.db_lo | ((uint32_t)r.db_hi << 16)) : h2f(r.db_lo);
-  return dt_activation(h2f(r.dt) + db, Ah);
-}
-
-// Builds the wave's token values from its landed raw inputs and the dt
-// activation `act` of head slot `lane` (lanes < HPW): raw rows and x, dt and
-// decay per head slot, b and c gathered through
-// the permutation (lane holds internal positions lane and lane + 64, whose
-// raw indices are pv0 and pv1), B*dt, sum b.c, the readout weights and, for
-// the ridge codec, the correction of the readout weights by the static
-// predictor and the dead-tier dot products.  `first`: the first token, whose
-// ridge correction waits for the workgroup's predictor transfer.
-template <int N8, int N4, int NZ, int MODE, int WPB, int HPW>
-__device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, GroupToken<N8 + N4>& gt,
-                                                 const WaveRaw<HPW>& r, float2 act, int pv0, int pv1,
-                                                 const float (&e0v)[2], const float (&e1v)[2],
-                                                 const uint16_t* s_pred, bool first, int lane, int wave) {
-  constexpr int NL = N8 + N4, F = NL + 2, RZ = next_pow2(NZ);
-#pragma unroll
-  for (int k = 0; k < HPW; ++k) wt.x[k][lane] = r.xv[k];
-  const float dtv = act.x;
-  // gather: raw element i of the B (C) row is half i & 1 of lane i >> 1's pair
-  const int braw = (int)((uint32_t)r.bc[0] | ((uint32_t)r.bc[1] << 16));
-  const int craw = (int)((uint32_t)r.bc[2] | ((uint32_t)r.bc[3] << 16));
-  const uint32_t bw0 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (pv0 >> 1), braw);
-  const uint32_t bw1 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (pv1 >> 1), braw);
-  const uint32_t cw0 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (pv0 >> 1), craw);
-  const uint32_t cw1 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (pv1 >> 1), craw);
-  __builtin_amdgcn_sched_barrier(0);   // all four exchanges in flight before the first use
-  const float b0 = h2f((uint16_t)(bw0 >> (16 * (pv0 & 1)))), b1 = h2f((uint16_t)(bw1 >> (16 * (pv1 & 1))));
-  const float c0 = h2f((uint16_t)(cw0 >> (16 * (pv0 & 1)))), c1 = h2f((uint16_t)(cw1 >> (16 * (pv1 & 1))));
-  // the carried coordinates' b are finite binary16 values (|b| <= 65504)
-  const bool b_lane_ok = (lane >= NL || __builtin_fabsf(b0) <= 65504.f) &&
-                         (64 + lane >= NL || __builtin_fabsf(b1) <= 65504.f);
-  const bool b_ok = __builtin_amdgcn_ballot_w64(!b_lane_ok) == 0;
-  if (lane < HPW) {
-    wt.dtv[lane] = act.x;
-    wt.decay[lane] = act.y;
-    wt.bounded[lane] = (b_ok && 65504.f * __builtin_fabsf(act.x) < 0x1p100f && __builtin_fabsf(act.y) < 0x1p100f);
-  }
-  wt.b[lane] = b0;
-  wt.b[64 + lane] = b1;
-  wt.c[lane] = c0;
-  wt.c[64 + lane] = c1;
-#pragma unroll
-  for (int k = 0; k < HPW; ++k) {
-    const float dk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, dtv), k));
-    if (lane < NL) wt.bdt[k][lane] = b0 * dk;
-    if (64 + lane < NL) wt.bdt[k][64 + lane] = b1 * dk;
-  }
-  const float sbc = wave_sum(b0 * c0 + b1 * c1);
-  if (lane == 0) wt.dots[0] = sbc;
-  if constexpr (MODE != MODE_RIDGE) {
-    if (lane < NL) wt.cw[lane] = c0;
-    if (64 + lane < NL) wt.cw[64 + lane] = c1;
-  } else {
-    wave_sync();                 // the dead-tier c and b are read across lanes below
-    if (first) __syncthreads();  // every wave's share of the predictor transfer has landed
-    if constexpr (WPB >= 4) {
-      // Split across the workgroup: wave w computes the corrections of
-      // internal outputs [w FW, (w + 1) FW), lanes l and l + 32 the two halves
-      // of the dead-tier sum of output w FW + (l & 31), and dead-tier tree w
-      // (w < 4); readout-only values, except the trees e.b (canonical, exact).
-      constexpr int FW = 8 * ((F + 8 * WPB - 1) / (8 * WPB));
-      static_assert(FW <= 32, "two lane halves per output");
-      const int jo = wave * FW + (lane & 31);
-      const uint16_t* pr = s_pred + packed_lane<N8, N4>(min(jo, F - 1)) * NZ;
-      constexpr int Q = NZ / 4, QH = (Q + 1) / 2;
-      const int qb = (lane >> 5) * QH;
-      f32x4 cv[QH];
-      uint2 w[QH];
-#pragma unroll
-      for (int i = 0; i < QH; ++i) {
-        const int q = min(qb + i, Q - 1);
-        cv[i] = *(const f32x4*)(wt.c + NL + 4 * q);
-        w[i] = *(const uint2*)(pr + 4 * q);
-      }
-      const float cjo = wt.c[min(jo, NL - 1)];   // readout weight base of output jo (< NL)
-      // tree `wave` operands (waves 0..3: e0.c, e1.c, e0.b, e1.b), read
-      // unconditionally at clamped positions
-      const float* src = wave < 2 ? wt.c : wt.b;
-      float tv[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int d0 = (RZ == 128) ? 2 * lane + j : lane;
-        tv[j] = src[NL + min(d0, NZ - 1)];
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      // tree `wave` (waves past 3 of an eight-wave group compute an unused
-      // copy), interleaved by the scheduler with the correction below
-      const float (&e)[2] = (wave & 1) ? e1v : e0v;
-      float v[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int d0 = (RZ == 128) ? 2 * lane + j : lane;
-        const bool in = (RZ == 128 || j == 0) && d0 < NZ;
-        v[j] = in ? e[j] * tv[j] : 0.f;
-      }
-      const float tsum = wave_pair_tree<RZ>(v[0], v[1]);
-      float a[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int i = 0; i < QH; ++i) {
-        f32x4 c4 = cv[i];
-        if (Q % 2 && i == QH - 1 && qb + i >= Q) c4 = f32x4{0.f, 0.f, 0.f, 0.f};   // the upper half's extra quad
-        a[0] = __builtin_fmaf(c4.x, h2f((uint16_t)w[i].x), a[0]);
-        a[1] = __builtin_fmaf(c4.y, h2f((uint16_t)(w[i].x >> 16)), a[1]);
-        a[2] = __builtin_fmaf(c4.z, h2f((uint16_t)w[i].y), a[2]);
-        a[3] = __builtin_fmaf(c4.w, h2f((uint16_t)(w[i].y >> 16)), a[3]);
-      }
-      const int part = __builtin_bit_cast(int, (a[0] + a[1]) + (a[2] + a[3]));
-      const auto sw = __builtin_amdgcn_permlane32_swap(part, part, false, false);
-      const float corr = __builtin_bit_cast(float, (int)sw[0]) + __builtin_bit_cast(float, (int)sw[1]);
-      if (lane < FW && jo < F) gt.cw[jo] = (jo < NL ? cjo : 0.f) + corr;
-      if (lane == 0 && wave < 4) gt.tree[wave] = tsum;
-      __syncthreads();   // the workgroup's shared token values are complete
-      return;
-    }
-    // corr[j] = sum_d C[dead d] * pred[g, row(j), d] for output j = lane and
-    // lane + 64 (rows past F recompute row F-1, unused); the dead-tier C is a
-    // wave-uniform operand, the predictor row a per-lane one
-    const int f0 = packed_lane<N8, N4>(min(lane, F - 1));
-    const int f1 = packed_lane<N8, N4>(min(64 + lane, F - 1));
-    const uint16_t* p0 = s_pred + f0 * NZ;
-    const uint16_t* p1 = s_pred + f1 * NZ;
-    // every LDS read of a half is issued before its first use; four partial
-    // sums per output (readout-only value: summation order free)
-    constexpr int Q = NZ / 4, QH = (Q + 1) / 2;
-    float a0[4] = {0.f, 0.f, 0.f, 0.f}, a1[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      f32x4 cv[QH];
-      uint2 w0[QH], w1[QH];
-#pragma unroll
-      for (int i = 0; i < QH; ++i) {
-        const int d = 4 * min(h * QH + i, Q - 1);
-        cv[i] = *(const f32x4*)(wt.c + NL + d);
-        w0[i] = *(const uint2*)(p0 + d);
-        if constexpr (F > 64) w1[i] = *(const uint2*)(p1 + d);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < QH; ++i) {
-        if (h * QH + i >= Q) break;
-        a0[0] = __builtin_fmaf(cv[i].x, h2f((uint16_t)w0[i].x), a0[0]);
-        a0[1] = __builtin_fmaf(cv[i].y, h2f((uint16_t)(w0[i].x >> 16)), a0[1]);
-        a0[2] = __builtin_fmaf(cv[i].z, h2f((uint16_t)w0[i].y), a0[2]);
-        a0[3] = __builtin_fmaf(cv[i].w, h2f((uint16_t)(w0[i].y >> 16)), a0[3]);
-        if constexpr (F > 64) {
-          a1[0] = __builtin_fmaf(cv[i].x, h2f((uint16_t)w1[i].x), a1[0]);
-          a1[1] = __builtin_fmaf(cv[i].y, h2f((uint16_t)(w1[i].x >> 16)), a1[1]);
-          a1[2] = __builtin_fmaf(cv[i].z, h2f((uint16_t)w1[i].y), a1[2]);
-          a1[3] = __builtin_fmaf(cv[i].w, h2f((uint16_t)(w1[i].y >> 16)), a1[3]);
-        }
-      }
-    }
-    const float acc0 = (a0[0] + a0[1]) + (a0[2] + a0[3]);
-    const float acc1 = (a1[0] + a1[1]) + (a1[2] + a1[3]);
-    if (lane < NL) wt.cw[lane] = c0 + acc0;
-    if (64 + lane < NL) wt.cw[64 + lane] = c1 + acc1;
-    // correction of the latent coefficients: outputs NL and NL + 1
-    const float lc0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                    __builtin_bit_cast(int, NL < 64 ? acc0 : acc1), NL % 64));
-    const float lc1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                    __builtin_bit_cast(int, NL + 1 < 64 ? acc0 : acc1), (NL + 1) % 64));
-    // dead-tier dot products: canonical adjacent-pair trees (products at
-    // 2 lane + j when RZ == 128, else at lane)
-    float v[4][2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int d0 = (RZ == 128) ? 2 * lane + j : lane;
-      const bool in = (RZ == 128 || j == 0) && d0 < NZ;
-      const int d = in ? d0 : 0;
-      const float bb = wt.b[NL + d], cc = wt.c[NL + d];
-      v[0][j] = in ? e0v[j] * cc : 0.f;
-      v[1][j] = in ? e1v[j] * cc : 0.f;
-      v[2][j] = in ? e0v[j] * bb : 0.f;
-      v[3][j] = in ? e1v[j] * bb : 0.f;
-    }
-    const float ec0 = wave_pair_tree<RZ>(v[0][0], v[0][1]);
-    const float ec1 = wave_pair_tree<RZ>(v[1][0], v[1][1]);
-    const float eb0 = wave_pair_tree<RZ>(v[2][0], v[2][1]);
-    const float eb1 = wave_pair_tree<RZ>(v[3][0], v[3][1]);
-    if (lane == 0) {
-      wt.dots[1] = ec0 + lc0;
-      wt.dots[2] = ec1 + lc1;
-      wt.dots[3] = eb0;
-      wt.dots[4] = eb1;
-    }
-  }
-  wave_sync();
-}
-
-// One tier of a row: update its N carried coordinates (biased code bytes in
-// c[0 .. N/4)), accumulate the readout (prior * readout weight), then
-// requantize with den = max(RN(amax / lim), 1e-8) and the stored (binary16)
-// scale, writing the new codes back into c.  Returns the new stored scale.
-// INT8: byte = q + 128, lim 127; INT4: byte = q + 8, lim 7.  Legacy mode
-// quantizes with the binary32 denominator.
-//
-// Clamping the rounded quotient to +-lim only matters when the divisor is
-// below den (a binary16-subnormal stored scale) or when an update is not
-// finite.  `finite_in` (per lane) says the update cannot overflow or be NaN
-// (finite scale, x, decay and B*dt of bounded size); when it holds on every
-// lane and every stored scale is zero, infinite or a normal binary16 value,
-// |RN(u / s)| <= lim (1 + 2^-11) / (1 - 2^-24) < lim + 1/2 and the wave takes
-// the quantizer without the clamp.
-//
-// EXACT selects the dequantization form: false (every scale of the wave
-// finite) the fused (1024 + q + bias) * s - (1024 + bias) * s, one fma per
-// coordinate (exact: both products have at most 22 significant bits); true
-// q * s as a packed binary16 subtraction and a product, which is also the
-// IEEE product for infinite and NaN scales (where the fused form gives
-// inf - inf).
-template <int N, bool INT8, int MODE, bool EXACT>
-__device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, float x, const f32x4* bdt4,
-                                           const f32x4* cw4, float& acc, bool finite_in) {
-  constexpr float BIAS = INT8 ? 128.0f : 8.0f;
-  constexpr float LIM = INT8 ? 127.0f : 7.0f;
-  constexpr float TOP = INT8 ? QTOP127 : QTOP7;
-  const float nb = -(1024.0f + BIAS) * sc;
-  const f16x2 nbias = {(_Float16)(-(1024.0f + BIAS)), (_Float16)(-(1024.0f + BIAS))};
-  const float mz = EXACT ? opaque_neg_zero() : 0.f;
-  float v[N];
-  float amax = 0.f;
-  // the shared operands of chunk i+1 are read while chunk i computes
-  f32x4 cb_next = bdt4[0], cw_next = cw4[0];
-#pragma unroll
-  for (int i0 = 0; i0 < N; i0 += 4) {
-    const f32x4 cb = cb_next, cw = cw_next;
-    if (i0 + 4 < N) {
-      cb_next = bdt4[i0 / 4 + 1];
-      cw_next = cw4[i0 / 4 + 1];
-    }
-    // the chunk's code bytes as binary16 values 1024 + byte (exponent byte 0x64)
-    const uint32_t h01 = __builtin_amdgcn_perm(0x64646464u, c[i0 / 4], 0x04010400u);
-    const uint32_t h23 = __builtin_amdgcn_perm(0x64646464u, c[i0 / 4], 0x04030402u);
-    float pr[4];
-    if constexpr (EXACT) {
-      const f16x2 q01 = pk_add_h(__builtin_bit_cast(f16x2, h01), nbias);
-      const f16x2 q23 = pk_add_h(__builtin_bit_cast(f16x2, h23), nbias);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) pr[j] = dequant_h((j < 2 ? q01 : q23)[j & 1], sc, mz);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) pr[j] = __builtin_fmaf(h2f((uint16_t)((j < 2 ? h01 : h23) >> (16 * (j & 1)))), sc, nb);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float prior = pr[j];
-      acc = __builtin_fmaf(prior, cw[j], acc);
-      float u = state_update(prior, decay, cb[j] * x);
-      // ordered pin: chunk by chunk, each prior dies as soon as it is used
-      asm volatile("" : "+v"(u));
-      v[i0 + j] = u;
-    }
-    amax = max3_abs(amax, v[i0], v[i0 + 1]);
-    amax = max3_abs(amax, v[i0 + 2], v[i0 + 3]);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  // Materialize the accumulator and the maximum here: otherwise the compiler
-  // sinks their chains (and every update behind the maximum) into the
-  // requantization, which keeps every prior and LDS operand live at once.
-  asm volatile("" : "+v"(acc), "+v"(amax));
-  const float den = requant_den(amax, LIM, 1.0f / LIM);
-  const float stored = round_to_half(den);
-  float d, r;
-  bool unclamped;
-  // stored scale not > 0: the reference's code is 0 whatever the update
-  // (also NaN): the clamp bound is then 0 (clamp(NaN, -0, 0) is -0 or 0)
-  float top = TOP;
-  if constexpr (MODE == MODE_LEGACY) {
-    // an infinite den divides through d = 1, y = 0: RN(v / inf) is 0 for
-    // finite v (NaN, clamped to -lim, for infinite v, as IEEE gives)
-    const bool inf = den == __builtin_inff();
-    d = inf ? 1.0f : den;
-    r = inf ? 0.0f : 1.0f / den;
-    unclamped = finite_in;
-  } else {
-    // zero (underflowed) or infinite stored scale: the reference's quotient
-    // is 0 and so is the code
-    const bool zero = !(stored > 0.f) || stored == __builtin_inff();
-    d = zero ? 1.f : stored;
-    r = zero ? 0.f : recip_half(stored);
-    unclamped = finite_in && (zero || stored >= 0x1p-14f);
-    top = stored > 0.f ? TOP : 0.0f;
-  }
-  // wave-uniform choice, re-tested per chunk (a branch around the whole loop
-  // makes the register allocator keep both versions' values apart)
-  const bool fast = __builtin_amdgcn_ballot_w64(!unclamped) == 0;
-  if (fast) {
-    // the biased code as the low byte of t = RN(u r + 1.5 2^23 + bias) =
-    // 1.5 2^23 + bias + rint(u r), with a running maximum of the rounding
-    // residuals |f| = |RN(u r - rint(u r))| (round_residual_code)
-    float fmax_res = 0.f;
-#pragma unroll
-    for (int i = 0; i < N / 4; ++i) {
-      float f[4];
-      uint32_t tb[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) tb[j] = round_residual_code(v[4 * i + j], r, BIAS, f[j]);
-      fmax_res = max3_abs(fmax_res, f[0], f[1]);
-      fmax_res = max3_abs(fmax_res, f[2], f[3]);
-      uint32_t packed = pack4((int)tb[0], (int)tb[1], (int)tb[2], (int)tb[3]);
-      asm volatile("" : "+v"(packed));
-      c[i] = packed;
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // A lane whose u r lies within the residual margin of a half-integer may
-    // round differently from roundf(RN(u / d)): the wave then requantizes the
-    // tier with the exact quotients (rare: about 2 N margin per lane).
-    if (__builtin_amdgcn_ballot_w64(fmax_res > (INT8 ? RESIDUAL_OK8 : RESIDUAL_OK4)) != 0) {
-#pragma unroll
-      for (int i = 0; i < N / 4; ++i) {
-        const int q0 = quantize_code_unclamped(v[4 * i], d, r);
-        const int q1 = quantize_code_unclamped(v[4 * i + 1], d, r);
-        const int q2 = quantize_code_unclamped(v[4 * i + 2], d, r);
-        const int q3 = quantize_code_unclamped(v[4 * i + 3], d, r);
-        uint32_t packed = pack4(q0, q1, q2, q3);
-        packed = INT8 ? (packed ^ 0x80808080u) : ((packed & 0x0F0F0F0Fu) ^ 0x08080808u);
-        c[i] = packed;
-      }
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < N / 4; ++i) {
-      const int q0 = quantize_code(v[4 * i], d, r, top);
-      const int q1 = quantize_code(v[4 * i + 1], d, r, top);
-      const int q2 = quantize_code(v[4 * i + 2], d, r, top);
-      const int q3 = quantize_code(v[4 * i + 3], d, r, top);
-      uint32_t packed = pack4(q0, q1, q2, q3);
-      packed = INT8 ? (packed ^ 0x80808080u) : ((packed & 0x0F0F0F0Fu) ^ 0x08080808u);
-      asm volatile("" : "+v"(packed));
-      c[i] = packed;
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-  return stored;
-}
-
-// One workgroup = WPB waves, each owning HPW head slots of 64 rows (the same
-// P block of NH = WPB * HPW consecutive heads of one B/C group and batch
-// row).  The packed rows of every slot stay in LDS, in the reference's SoA
-// field layout, for all L tokens; a slot is unpacked into VGPRs, stepped and
-// repacked in one pass per token.  The first token streams the slots in:
-// slot k+1 is fetched while slot k computes.  Every wave builds the token
-// values it reads itself, so the only workgroup barrier is the one that
-// publishes the ridge predictor (staged once, shared by all waves).
-template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE>
-__global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(WPB == 8 ? 4 : 2, 8)))
-void k_state_step(StepArgs a) {
-  constexpr int W8 = N8 / 2;          // bytes per row of lo and of hi
-  constexpr int W4 = N4 / 2;          // bytes per row of q4
-  constexpr int NL = N8 + N4;         // carried coordinates
-  constexpr int F = NL + 2;           // ridge predictor features
-  constexpr int NH = WPB * HPW;
-  constexpr int RZ = next_pow2(NZ);
-  constexpr bool RIDGE = MODE == MODE_RIDGE;
-  constexpr int O_LO = 0, O_HI = 64 * W8, O_Q4 = 128 * W8, O_S8 = O_Q4 + 64 * W4, O_S4 = O_S8 + 128;
-  constexpr int O_LAT = O_S4 + 128;
-  constexpr int TILE = O_LAT + (RIDGE ? 128 : 0) + 16;   // 16 bytes of slack for row reads
-  constexpr int C8 = N8 / 4, C4 = N4 / 4;   // carried code words (4 biased bytes each)
-  constexpr int PRED_DW = RIDGE ? F * NZ / 2 : 1;   // F*NZ is even for every layout
-  constexpr int PRED_OPS = (PRED_DW + 63) / 64;     // 64-dword transfers of the predictor
-  constexpr int PRED_OPS16 = (PRED_DW + 255) / 256; // 1 KiB transfers (aligned predictor)
-  static_assert(!RIDGE || (F * NZ * 2) % 16 == 0, "a group's predictor is a whole number of 16-byte chunks");
-  static_assert(N8 % 4 == 0 && N4 % 4 == 0 && N8 > 0 && N4 > 0, "tier widths must be positive multiples of 4");
-  static_assert(NZ % 4 == 0 && NL + NZ == 128, "dead tier read as 4-wide vectors");
-  static_assert(!RIDGE || (F * NZ) % 2 == 0, "predictor staged as dwords");
-  static_assert(TILE % 16 == 0, "tiles stay 16-byte aligned");
-
-  __shared__ __align__(16) WaveToken<N8, N4, HPW> s_wt[WPB];
-  // split ridge correction: one record per token parity (a wave may build
-  // token t + 1 while another still reads token t)
-  constexpr bool SPLIT = RIDGE && WPB >= 4;
-  __shared__ __align__(16) GroupToken<NL> s_gt[SPLIT && !ONE ? 2 : 1];
-  __shared__ __align__(16) uint32_t s_pred32[DMA ? PRED_OPS16 * 256 : PRED_OPS * 64];
-  __shared__ __align__(16) uint8_t s_tile[NH][TILE];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: per-wave values in SGPRs
-  const int b = blockIdx.z;
-  const int h0 = blockIdx.y * NH;
-  const int H = a.H, P = a.P;
-  // ONE: the one-token (decode) instance, with a compile-time token count:
-  // no token loop, prefetch or loop-carried state
-  const int L = ONE ? 1 : a.L;
-  const int g = h0 / (H / a.G);
-  const int pbase = blockIdx.x * 64;
-  const int nvalid = min(64, P - pbase);
-  const bool valid = lane < nvalid;
-  constexpr bool dma_tiles = DMA;   // a.dma_tiles: 16-byte LDS transfers, else staging through VGPRs
-  const uint16_t* s_pred = (const uint16_t*)s_pred32;
-  WaveToken<N8, N4, HPW>& wt = s_wt[wave];
-
-  // vector memory operations per slot transfer (and per state copy-out)
-  constexpr int SLOT_DMA = 2 * chunk_ops(W8) + chunk_ops(W4) + chunk_ops(2) * (RIDGE ? 3 : 2);
-  static_assert(SLOT_DMA <= 63, "a slot's transfers must fit the vmcnt range");
-  auto slot_row0 = [&](int hh) { return (b * H + h0 + hh) * P + pbase; };
-  auto slot_dma = [&](int hh) {   // direct global -> LDS transfers
-    const int row0 = slot_row0(hh);
-    uint8_t* t = s_tile[hh];
-    field_dma16<W8>(t + O_LO, a.lo, row0, nvalid, lane);
-    field_dma16<W8>(t + O_HI, a.hi, row0, nvalid, lane);
-    field_dma16<W4>(t + O_Q4, a.q4, row0, nvalid, lane);
-    field_dma16<2>(t + O_S8, (const uint8_t*)a.s8, row0, nvalid, lane);
-    field_dma16<2>(t + O_S4, (const uint8_t*)a.s4, row0, nvalid, lane);
-    if constexpr (RIDGE) field_dma16<2>(t + O_LAT, a.latent, row0, nvalid, lane);
-  };
-  constexpr int COPY_OPS = SLOT_DMA;   // one store instruction per transfer chunk
-  static_assert(SLOT_DMA + COPY_OPS + 1 <= 63, "vmcnt range");
-  // At the first token, before slot k is read: wait until only the
-  // operations issued after slot k's transfers are outstanding (vector memory
-  // operations complete in program order), so no wait covers a store's write
-  // acknowledgement.  Slot k's transfers are issued in the middle of slot
-  // k-1 (slot 0's by the prologue); after them come slot k-2's state
-  // copy-out when the first token is also the last (copy-outs trail by one
-  // slot, also issued mid-slot) and slot k-1's y store (one store
-  // instruction).  (Loads the compiler issues in between, the next token's
-  // prefetch, only make a wait longer.)
-  auto slot_wait = [&](int k) {
-    const bool copy = L == 1 && k >= 2;
-    if (k == 0) wait_vmcnt<0>();
-    else if (copy) wait_vmcnt<COPY_OPS + 1>();
-    else wait_vmcnt<1>();
-  };
-  auto slot_copy_in = [&](int hh) {   // other geometries: 16-bit transfers through VGPRs
-    const int row0 = slot_row0(hh);
-    uint8_t* t = s_tile[hh];
-    wave_copy_in<W8>(t + O_LO, a.lo, row0, nvalid, lane);
-    wave_copy_in<W8>(t + O_HI, a.hi, row0, nvalid, lane);
-    wave_copy_in<W4>(t + O_Q4, a.q4, row0, nvalid, lane);
-    wave_copy_in<2>(t + O_S8, (const uint8_t*)a.s8, row0, nvalid, lane);
-    wave_copy_in<2>(t + O_S4, (const uint8_t*)a.s4, row0, nvalid, lane);
-    if constexpr (RIDGE) wave_copy_in<2>(t + O_LAT, a.latent, row0, nvalid, lane);
-  };
-  auto slot_copy_out = [&](int hh) {
-    const int row0 = slot_row0(hh);
-    const uint8_t* t = s_tile[hh];
-    if constexpr (dma_tiles) {   // every LDS read of the slot, then its stores
-      constexpr int C8W = chunk_ops(W8), C4W = chunk_ops(W4), C2 = chunk_ops(2);
-      u32x4 v[SLOT_DMA];
-      field_read16<W8>(t + O_LO, lane, v);
-      field_read16<W8>(t + O_HI, lane, v + C8W);
-      field_read16<W4>(t + O_Q4, lane, v + 2 * C8W);
-      field_read16<2>(t + O_S8, lane, v + 2 * C8W + C4W);
-      field_read16<2>(t + O_S4, lane, v + 2 * C8W + C4W + C2);
-      if constexpr (RIDGE) field_read16<2>(t + O_LAT, lane, v + 2 * C8W + C4W + 2 * C2);
-      field_write16<W8>(a.lo, v, row0, nvalid, lane);
-      field_write16<W8>(a.hi, v + C8W, row0, nvalid, lane);
-      field_write16<W4>(a.q4, v + 2 * C8W, row0, nvalid, lane);
-      field_write16<2>((uint8_t*)a.s8, v + 2 * C8W + C4W, row0, nvalid, lane);
-      field_write16<2>((uint8_t*)a.s4, v + 2 * C8W + C4W + C2, row0, nvalid, lane);
-      if constexpr (RIDGE) field_write16<2>(a.latent, v + 2 * C8W + C4W + 2 * C2, row0, nvalid, lane);
-      return;
-    }
-    wave_copy_out<W8>(a.lo, t + O_LO, row0, nvalid, lane);
-    wave_copy_out<W8>(a.hi, t + O_HI, row0, nvalid, lane);
-    wave_copy_out<W4>(a.q4, t + O_Q4, row0, nvalid, lane);
-    wave_copy_out<2>((uint8_t*)a.s8, t + O_S8, row0, nvalid, lane);
-    wave_copy_out<2>((uint8_t*)a.s4, t + O_S4, row0, nvalid, lane);
-    if constexpr (RIDGE) wave_copy_out<2>(a.latent, t + O_LAT, row0, nvalid, lane);
-  };
-
-  // ---- prologue: the wave's share of the predictor's LDS transfer, then the
-  // register loads of the first token and the statics (one wait covers both),
-  // then the LDS transfer of the wave's first slot, which lands while the
-  // token is built; each later slot is fetched while the previous computes --
-  // (order: the dt inputs, the predictor transfer, then the rest; the dt
-  // activation's wait for its inputs thus covers only the first two)
-  WaveRaw<HPW> raw;
-  wave_load_dt<WPB, HPW>(a, raw, b * L, h0, lane, wave);
-  const int hl = h0 + min(lane, HPW - 1) * WPB + wave;   // head of slot `lane` (lanes < HPW)
-  const float Ah = a.A[hl];
-  if constexpr (RIDGE) {
-    const uint8_t* pg = (const uint8_t*)(a.pred + (size_t)g * F * NZ);
-    if constexpr (DMA) {   // 16-byte chunks; lanes past the end re-read the last one
-      for (int j = wave; j < PRED_OPS16; j += WPB)
-        lds_dma_b128(pg + 16 * min(j * 64 + lane, PRED_DW / 4 - 1), lds_address(s_pred32 + 256 * j));
-    } else {
-      for (int j = wave; j < PRED_OPS; j += WPB)
-        lds_dma_b32(pg + 4 * min(j * 64 + lane, PRED_DW - 1), lds_address(s_pred32 + 64 * j));
-    }
-  }
-  wave_load_rest<WPB, HPW, DMA>(a, raw, b * L, g, h0, pbase, lane, wave);
-  // statics, kept as loaded bits until the first token's full wait (a
-  // conversion here would make the compiler wait for them before the dt
-  // activation)
-  const uint32_t d_bits = a.d_f32 ? ((const uint32_t*)a.D)[hl] : (uint32_t)((const uint16_t*)a.D)[hl];
-  const uint32_t perm0 = a.perm[g * 128 + packed_lane<N8, N4>(lane)];
-  const uint32_t perm1 = a.perm[g * 128 + packed_lane<N8, N4>(64 + lane)];
-  uint32_t basis_w[2] = {0u, 0u};
-  uint32_t ls_w = 0u;
-  if constexpr (RIDGE) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int d0 = (RZ == 128) ? 2 * lane + j : lane;
-      basis_w[j] = ((const uint32_t*)a.basis)[g * NZ + min(d0, NZ - 1)];   // unused past NZ
-    }
-    ls_w = DMA ? *(const uint32_t*)(a.lscale + g * 2)
-               : (uint32_t)a.lscale[g * 2] | ((uint32_t)a.lscale[g * 2 + 1] << 16);
-  }
-  // dt activation of the first token while the other loads are in flight
-  float2 act = wave_dt_activation<HPW>(raw, Ah, a.db_f32);
-  // the predictor transfer and the register loads complete before any slot
-  // transfer is issued (the compiler's own waits for the register loads then
-  // never cover a slot transfer; no load may be scheduled past this wait)
-  __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-  __builtin_amdgcn_sched_barrier(0);
-  if constexpr (dma_tiles) slot_dma(wave);
-  else {
-    for (int k = 0; k < HPW; ++k) slot_copy_in(k * WPB + wave);
-  }
-  if (lane < HPW) wt.D[lane] = a.d_f32 ? __builtin_bit_cast(float, d_bits) : h2f((uint16_t)d_bits);
-  const int pv0 = perm0 & 127, pv1 = perm1 & 127;   // raw B/C index of internal positions lane, lane + 64
-  float e0v[2] = {0.f, 0.f}, e1v[2] = {0.f, 0.f};   // dead-tier basis at the pair-tree positions
-  float ls0 = 0.f, ls1 = 0.f, rls0 = 0.f, rls1 = 0.f;
-  if constexpr (RIDGE) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      e0v[j] = h2f((uint16_t)(basis_w[j] & 0xFFFFu));
-      e1v[j] = h2f((uint16_t)(basis_w[j] >> 16));
-    }
-    ls0 = h2f((uint16_t)(ls_w & 0xFFFFu));
-    ls1 = h2f((uint16_t)(ls_w >> 16));
-    // correctly rounded reciprocals: the latent scales are positive finite
-    // binary16 values (the statics contract every caller validates)
-    rls0 = recip_half(ls0);
-    rls1 = recip_half(ls1);
-  }
-
-  for (int t = 0; t < L; ++t) {
-    const int bt = b * L + t;
-    const WaveRaw<HPW> cur = raw;
-    if (t + 1 < L) {   // prefetch
-      wave_load_dt<WPB, HPW>(a, raw, bt + 1, h0, lane, wave);
-      wave_load_rest<WPB, HPW, DMA>(a, raw, bt + 1, g, h0, pbase, lane, wave);
-    }
-    GroupToken<NL>& gt = s_gt[SPLIT && !ONE ? (t & 1) : 0];
-    wave_token_build<N8, N4, NZ, MODE, WPB, HPW>(wt, gt, cur, act, pv0, pv1, e0v, e1v, s_pred, t == 0, lane, wave);
-    // readout weights and dead-tier dot products of this token
-    const float* cwt = SPLIT ? gt.cw : wt.cw;
-    const float dot1 = SPLIT ? gt.tree[0] + gt.cw[NL] : wt.dots[1];
-    const float dot2 = SPLIT ? gt.tree[1] + gt.cw[NL + 1] : wt.dots[2];
-    const float dot3 = SPLIT ? gt.tree[2] : wt.dots[3];
-    const float dot4 = SPLIT ? gt.tree[3] : wt.dots[4];
-
-    for (int k = 0; k < HPW; ++k) {
-      // The slot's head index, opaque to the optimizer: every address and
-      // buffer descriptor derived from it is then built here, where scalar
-      // work overlaps the other waves' vector work, instead of being hoisted
-      // out of the token loop for all slots at once (more scalar registers
-      // than exist: spills, and a long serial setup before the first token).
-      int hh = k * WPB + wave;
-      asm volatile("" : "+s"(hh));
-      const int h = h0 + hh;
-      wave_priority_by_slots_left(HPW - k);
-      if (t == 0) slot_wait(k);
-      uint8_t* tile = s_tile[hh];
-      uint16_t* t16 = (uint16_t*)tile;
-
-      // ---- unpack the slot: carried codes, internal lane order ------------------
-      // byte k of c8[i] is q8 + 128 of internal coordinate 4i+k, of c4[i] q4 + 8
-      uint32_t c8[C8], c4[C4];
-      {
-        uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4], wq[(W4 + 3) / 4];
-        lds_read_row<W8>(tile + O_LO, lane * W8, wl);
-        lds_read_row<W8>(tile + O_HI, lane * W8, wh);
-        planes_to_bytes8<N8>(wl, wh, c8);
-        lds_read_row<W4>(tile + O_Q4, lane * W4, wq);
-        plane_to_bytes4<N4>(wq, c4);
-      }
-      float sc8 = h2f(t16[O_S8 / 2 + lane]);
-      float sc4 = h2f(t16[O_S4 / 2 + lane]);
-      float z0 = 0.f, z1 = 0.f;
-      if constexpr (RIDGE) {
-        const uint32_t lat = t16[O_LAT / 2 + lane];
-        z0 = e4m3_byte_to_f32<0>(lat) * ls0;
-        z1 = e4m3_byte_to_f32<1>(lat) * ls1;
-      }
-      if (!valid) {   // rows past P: finite placeholders, never stored
-#pragma unroll
-        for (int i = 0; i < C8; ++i) c8[i] = 0x80808080u;
-#pragma unroll
-        for (int i = 0; i < C4; ++i) c4[i] = 0x08080808u;
-        sc8 = sc4 = z0 = z1 = 0.f;
-      }
-      const float x = h2f(wt.x[k][lane]);
-      const float decay = wt.decay[k];
-      const float dtv = wt.dtv[k];
-      const bool base_ok = wt.bounded[k] != 0 && __builtin_fabsf(x) <= 65504.f;
-
-      // ---- per tier: update, readout accumulation, requantization ---------------
-      // (each tier is requantized before the next is updated, so only one
-      // tier's updated values are live at a time)
-      const f32x4* bdt4 = (const f32x4*)wt.bdt[k];
-      const f32x4* cw4 = (const f32x4*)cwt;
-      float acc = 0.f;
-      const bool fin8 = __builtin_fabsf(sc8) <= 65504.f, fin4 = __builtin_fabsf(sc4) <= 65504.f;
-      const bool ok8 = base_ok && fin8;
-      const bool ok4 = base_ok && fin4;
-      // one wave-uniform choice per slot between two copies of the tier code:
-      // the fused dequantization when every scale of the wave is finite, the
-      // exact products otherwise (non-finite scales are rare: the reference's
-      // controllers reject such states)
-      auto tiers = [&](auto exact) {
-        constexpr bool EX = decltype(exact)::value;
-        sc8 = tier_step<N8, true, MODE, EX>(c8, sc8, decay, x, bdt4, cw4, acc, ok8);
-        __builtin_amdgcn_sched_barrier(0);
-        // the next slot's transfers and the previous slot's copy-out are
-        // issued between the tiers, where the other waves' arithmetic covers
-        // their issue time
-        if (dma_tiles && t == 0 && k + 1 < HPW) slot_dma(hh + WPB);
-        sc4 = tier_step<N4, false, MODE, EX>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc, ok4);
-        __builtin_amdgcn_sched_barrier(0);
-        if (t == L - 1 && k > 0) slot_copy_out(hh - WPB);   // the previous slot's state
-        __builtin_amdgcn_sched_barrier(0);
-      };
-      if (__builtin_amdgcn_ballot_w64(!(fin8 && fin4)) == 0) tiers(std::false_type{});
-      else tiers(std::true_type{});
-      // readout: sum_i u_i c_i + corrections = decay * (sum_i prior_i (c_i +
-      // corr_i) + latent terms) + x * (dt * sum_all b c + D)
-      float out;
-      uint32_t qz = 0;
-      if constexpr (RIDGE) {
-        out = decay * (acc + z0 * dot1 + z1 * dot2) + x * (dtv * wt.dots[0] + wt.D[k]);
-        // latent step (bit-exact): z <- fma(z, decay, (x * dt) * (e . b_dead)), requantized
-        const float xdt = x * dtv;
-        const float zn0 = state_update(z0, decay, xdt * dot3);
-        const float zn1 = state_update(z1, decay, xdt * dot4);
-        const float q0 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn0, ls0, rls0), -448.f), 448.f);
-        const float q1 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn1, ls1, rls1), -448.f), 448.f);
-        qz = f32x2_to_e4m3(q0, q1);   // q0, q1 are clamped, never NaN (maxNum drops a NaN)
-      } else {
-        out = decay * acc + x * (dtv * wt.dots[0] + wt.D[k]);
-      }
-      {   // one unguarded store instruction: the range check drops rows past P
-        const __amdgpu_buffer_rsrc_t ry = raw_buffer(a.y + ((size_t)bt * H + h) * P + pbase, 2 * nvalid);
-        __builtin_amdgcn_raw_buffer_store_b16(f2h(out), ry, 2 * lane, 0, STORE_THROUGH);
-      }
-
-      // ---- repack the slot row into the tile ---------------------------------------
-      if (valid) {
-        uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4], wq[(W4 + 3) / 4];
-        bytes_to_planes8<N8>(c8, wl, wh);
-        lds_write_row<W8>(tile + O_LO, lane * W8, wl);
-        lds_write_row<W8>(tile + O_HI, lane * W8, wh);
-        bytes_to_plane4<N4>(c4, wq);
-        lds_write_row<W4>(tile + O_Q4, lane * W4, wq);
-        t16[O_S8 / 2 + lane] = f2h(sc8);
-        t16[O_S4 / 2 + lane] = f2h(sc4);
-        if constexpr (RIDGE) t16[O_LAT / 2 + lane] = (uint16_t)qz;
-      }
-      wave_sync();
-    }
-    if (t == L - 1) slot_copy_out((HPW - 1) * WPB + wave);
-    if (t + 1 < L) act = wave_dt_activation<HPW>(raw, Ah, a.db_f32);
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Host dispatch over the supported tier layouts.  Heads per workgroup grow

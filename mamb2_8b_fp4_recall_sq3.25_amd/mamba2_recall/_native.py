@@ -39,7 +39,16 @@ _SIGNATURES = {
     "m2r_set_step_shape": ([I, I], I),
     "m2r_causal_conv_update": ([P, I64, I64, I64, P, I64, P, P, P, I64, I64, I, I, P], I),
     "m2r_fp4_gemv_g16": ([P, P, P, P, I64, P, I64, I64, I64, I64, P], I),
+    "m2r_state_step_ridge_layers_workspace": ([I], I64),
+    "m2r_state_step_ridge_layers": ([P, I, I64, I64, I64, I64, P, I64, P], I),
 }
+
+
+class RidgeLayer(ctypes.Structure):
+    """m2r_ridge_layer of include/m2r.h: one layer of the multi-layer step."""
+    _fields_ = [(n, ctypes.c_void_p) for n in ("x", "dt", "A", "B", "C", "D", "dt_bias", "perm", "basis", "lscale",
+                                                "pred", "lo", "hi", "q4", "latent", "s8", "s4", "y")] + \
+               [(n, ctypes.c_int32) for n in ("n8", "n4", "nz", "d_is_f32", "db_is_f32", "reserved")]
 
 
 class NativeLibraryMissing(RuntimeError):

@@ -8,9 +8,11 @@ host synchronization).  The scan runs the HIP kernel m2r_state_step_ridge.
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
-from . import _packed, tier_codec
+from . import _native, _packed, tier_codec
 from .state_codec import PackedState
 
 RP = 16
@@ -146,6 +148,85 @@ def scan(x, dt, A, B, C, D, dt_bias, state, permutation, basis, latent_scale, pr
                               n8=spec["n8"], n4=spec["n4"], nz=spec["nzero"], basis=basis,
                               lscale=latent_scale, pred=predictor)
     return y, None
+
+
+def layer_table(steps):
+    """The C-ABI layer table (an array of m2r_ridge_layer) of `steps`, for
+    scan_layers and callers that launch the multi-layer step themselves.
+    Each step is a dict with scan()'s tensor arguments (x, dt, A, B, C, D,
+    dt_bias, state, permutation, basis, latent_scale, predictor), its
+    `layout` and `y`, an FP16 output of x's shape; every layer has one token
+    and the same batch, heads, dim and groups.  Shapes, dtypes, devices and
+    the statics' metadata are checked here; the statics' values are taken as
+    validated (scan's validate=False)."""
+    if not steps:
+        raise ValueError("At least one layer required")
+    x0 = steps[0]["x"]
+    table = (_native.RidgeLayer * len(steps))()
+    for i, st in enumerate(steps):
+        x, state, layout = st["x"], st["state"], st["layout"]
+        spec = layout_descriptor(layout)
+        if (not isinstance(x, torch.Tensor) or x.ndim != 4 or x.dtype != torch.float16 or not x.is_cuda
+                or x.shape != x0.shape or x.device != x0.device or x.shape[1] != 1):
+            raise ValueError("Every layer needs CUDA FP16 x of one shape [batch,1,heads,dim]")
+        batch, _, heads, dim = x.shape
+        if dim % RP or state.shape != (batch, heads, dim, 128):
+            raise ValueError("Positive sequence and matching latent state required")
+        validate_state(state, x.device, layout)
+        B, C = st["B"], st["C"]
+        groups = B.shape[2] if B.ndim == 4 else 0
+        expected = ((st["dt"], (batch, 1, heads)), (st["A"], (heads,)), (B, (batch, 1, groups, 128)),
+                    (C, (batch, 1, groups, 128)), (st["D"], (heads,)), (st["dt_bias"], (heads,)),
+                    (st["y"], tuple(x.shape)))
+        for value, shape in expected:
+            if tuple(value.shape) != shape or value.device != x.device or not value.is_contiguous():
+                raise ValueError("Latent scan input geometry/device differs")
+        if (groups < 1 or heads % groups or st["A"].dtype != torch.float32 or st["y"].dtype != torch.float16
+                or any(v.dtype != torch.float16 for v in (st["dt"], B, C))
+                or any(v.dtype not in (torch.float16, torch.float32) for v in (st["D"], st["dt_bias"]))):
+            raise ValueError("Latent scan dtype/grouping differs")
+        check_static_metadata(st["permutation"], st["basis"], st["latent_scale"], st["predictor"], groups=groups,
+                              layout=layout, device=x.device)
+        t = state.tensors
+        e = table[i]
+        for name, value in (("x", x), ("dt", st["dt"]), ("A", st["A"]), ("B", B), ("C", C), ("D", st["D"]),
+                            ("dt_bias", st["dt_bias"]), ("perm", st["permutation"]), ("basis", st["basis"]),
+                            ("lscale", st["latent_scale"]), ("pred", st["predictor"]), ("lo", t["lo"]),
+                            ("hi", t["hi"]), ("q4", t["q4"]), ("latent", t["latent"]), ("s8", t["s8"]),
+                            ("s4", t["s4"]), ("y", st["y"])):
+            setattr(e, name, value.data_ptr())
+        e.n8, e.n4, e.nz = spec["n8"], spec["n4"], spec["nzero"]
+        e.d_is_f32 = int(st["D"].dtype == torch.float32)
+        e.db_is_f32 = int(st["dt_bias"].dtype == torch.float32)
+    return table
+
+
+@torch.no_grad()
+def scan_layers(steps, *, workspace=None):
+    """One launch of the one-token ridge step over several resident layers,
+    each exactly as scan(..., validate=False) with one token would step it
+    (its packed carry mutated, its readout written to step["y"]).  No
+    counterpart in the reference, whose mixers step one layer per call: this
+    is the one-launch variant for independent layers (the synthetic 56-layer
+    benchmark, or separate states stepped together).  `workspace`: a uint8
+    CUDA tensor of at least layers_workspace_bytes(len(steps)) bytes for the
+    device copy of the layer table (allocated here when None)."""
+    table = layer_table(steps)
+    x = steps[0]["x"]
+    batch, _, heads, dim = x.shape
+    groups = steps[0]["B"].shape[2]
+    need = layers_workspace_bytes(len(steps))
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    if workspace.dtype != torch.uint8 or workspace.device != x.device or workspace.numel() < need:
+        raise ValueError("Layer-table workspace too small")
+    _native.call("m2r_state_step_ridge_layers", ctypes.byref(table), len(steps), batch, heads, dim, groups,
+                 _native.ptr(workspace), workspace.numel(), _native.stream_of(x))
+    return [st["y"] for st in steps]
+
+
+def layers_workspace_bytes(nlayers):
+    return int(_native.lib().m2r_state_step_ridge_layers_workspace(int(nlayers)))
 
 
 class PredictorState(tier_codec.StateRepairV2):

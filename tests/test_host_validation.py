@@ -184,3 +184,33 @@ def test_ridge_value_checks_reject_nonfinite_and_nonpositive():
             p[1, 2, 3] = float("-inf")
         with pytest.raises(ValueError):
             ridge_codec.validate_statics(perm, b, l, p, groups=8, layout=layout, device=dev)
+
+
+def test_layers_step_rejects_bad_calls_before_any_launch():
+    """The multi-layer step validates on the host: no layers, an unsupported
+    layout, misaligned state arrays and a short workspace are rejected with
+    a message, before anything is enqueued (fake, never dereferenced device
+    addresses)."""
+    import ctypes
+    from mamba2_recall import _native
+    lib = _native.lib()
+    layer = _native.RidgeLayer()
+    for i, (name, _) in enumerate(_native.RidgeLayer._fields_[:18]):
+        setattr(layer, name, 0x10000 * (i + 1))
+    layer.n8, layer.n4, layer.nz = 32, 28, 68
+    arr = (_native.RidgeLayer * 1)(layer)
+
+    def err(*args):
+        rc = lib.m2r_state_step_ridge_layers(*args)
+        assert rc != 0
+        return lib.m2r_last_error().decode()
+
+    assert "no layers" in err(ctypes.byref(arr), 0, 1, 128, 64, 8, 0x900000, 1 << 20, None)
+    assert "workspace" in err(ctypes.byref(arr), 1, 1, 128, 64, 8, 0x900000, 8, None)
+    arr[0].n8 = 30
+    assert "layout" in err(ctypes.byref(arr), 1, 1, 128, 64, 8, 0x900000, 1 << 20, None)
+    arr[0].n8, arr[0].lo = 32, 0x10008
+    assert "16-byte" in err(ctypes.byref(arr), 1, 1, 128, 64, 8, 0x900000, 1 << 20, None)
+    arr[0].lo = 0x10000
+    assert "multiple of 8" in err(ctypes.byref(arr), 1, 1, 128, 60, 8, 0x900000, 1 << 20, None)
+    assert lib.m2r_state_step_ridge_layers_workspace(56) == 56 * lib.m2r_state_step_ridge_layers_workspace(1)
