@@ -228,6 +228,22 @@ int m2r_state_step_ridge_layers(const m2r_ridge_layer* layers, int nlayers, int6
                                 int64_t G, void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
+ * The same one-launch multi-layer step with no workspace argument and no
+ * allocation of any kind (no hipMalloc/hipFree, no host heap): the device copy
+ * of the layer table goes to a static device array of the library, at most
+ * M2R_LAYERS_NOALLOC_MAX layers per call (larger calls are rejected).  No
+ * counterpart in the reference; it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation).  Every call on one GPU shares that GPU's array (and the
+ * library's host staging buffer, under a lock): calls that overlap on one
+ * GPU, from other streams or host threads, race; calls on one stream are
+ * ordered.  Results equal m2r_state_step_ridge_layers'.
+ */
+#define M2R_LAYERS_NOALLOC_MAX 256
+int m2r_state_step_ridge_layers_noalloc(const m2r_ridge_layer* layers, int nlayers, int64_t batch, int64_t H,
+                                        int64_t P, int64_t G, hipStream_t stream);
+
+/*
  * One-token causal depthwise convolution update of the Mamba-2 mixer: roll
  * the cached window one step, store the new projection column, and write
  * out = silu(sum_t half(window_t * weight[c,t]) + bias[c]) in binary16.

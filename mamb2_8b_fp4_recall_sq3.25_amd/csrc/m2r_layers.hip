@@ -10,12 +10,15 @@
 // 55 serial prologues per token; the results are those of the per-layer
 // launches, bit for bit.
 //
-// The table is staged by the entry point into a workspace in device memory
-// that the caller passes (m2r_state_step_ridge_layers_workspace(n) bytes).
+// The table is staged by the entry point into device memory: into a
+// workspace the caller passes (m2r_state_step_ridge_layers), or into a static
+// device array that the library owns (m2r_state_step_ridge_layers_noalloc,
+// for callers that cannot allocate).
 #include "m2r_step.h"
 #include "m2r_abi_util.h"
 #include "../../include/m2r.h"
 
+#include <mutex>
 #include <vector>
 
 namespace m2r {
@@ -75,6 +78,41 @@ void k_state_step_layers(const LayerEntry* __restrict__ table, int batch) {
 #undef M2R_LAYER_CASE
 }
 
+// Static staging area of the no-allocation entry point: the device copy of
+// one call's layer table, at most M2R_LAYERS_NOALLOC_MAX layers (48 KiB).
+// Each GPU the library runs on holds its own copy for the life of the
+// process; calls that overlap on one GPU (other streams, other host threads)
+// race on it.
+__device__ __align__(256) uint8_t scratch[M2R_LAYERS_NOALLOC_MAX * sizeof(LayerEntry)];
+
+// The device address of `scratch` on each device, resolved once per device
+// with that device current (the array's name is a host-side stand-in that
+// must never reach a kernel or a copy).
+static constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+static int scratch_address(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return m2r_fail("layers step (no-alloc): no current device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return m2r_check(e, "layers step (no-alloc): scratch address");
+    if (!p) return m2r_fail("layers step (no-alloc): scratch address is null");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+// Host staging of the no-allocation entry point's table: a fixed buffer
+// under a lock (no host allocation either).
+static LayerEntry g_noalloc_table[M2R_LAYERS_NOALLOC_MAX];
+static std::mutex g_noalloc_mu;
+
 static int layout_id(int n8, int n4, int nz) {
   for (int k = 0; k < 7; ++k)
     if (kLayouts[k][0] == n8 && kLayouts[k][1] == n4 && kLayouts[k][2] == nz) return k;
@@ -85,7 +123,7 @@ static bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)
 
 // Validates the call, fills `table` and picks the workgroup shape.
 static int build_table(const m2r_ridge_layer* layers, int nlayers, int64_t batch, int64_t H, int64_t P, int64_t G,
-                       std::vector<LayerEntry>& table, int& wpb, int& hpw) {
+                       LayerEntry* table, int& wpb, int& hpw) {
   if (!layers || nlayers <= 0) return m2r_fail("layers step: no layers");
   if (batch <= 0 || H <= 0 || P <= 0 || G <= 0) return m2r_fail("layers step: non-positive geometry");
   if (H % G) return m2r_fail("layers step: heads must be divisible by groups");
@@ -98,7 +136,6 @@ static int build_table(const m2r_ridge_layer* layers, int nlayers, int64_t batch
   else if (hpg % 8 == 0 && slots >= 8LL * 512) { wpb = 4; hpw = 2; }
   else if (hpg % 4 == 0) { wpb = 4; hpw = 1; }
   else return m2r_fail("layers step: heads per group must be a multiple of 4");
-  table.resize((size_t)nlayers);
   for (int i = 0; i < nlayers; ++i) {
     const m2r_ridge_layer& l = layers[i];
     const int id = layout_id(l.n8, l.n4, l.nz);
@@ -147,7 +184,9 @@ extern "C" int m2r_state_step_ridge_layers(const m2r_ridge_layer* layers, int nl
                                            int64_t P, int64_t G, void* workspace, int64_t workspace_bytes,
                                            hipStream_t stream) {
   int wpb = 0, hpw = 0;
-  if (int e = build_table(layers, nlayers, batch, H, P, G, t_table, wpb, hpw)) return e;
+  if (nlayers > 65535) return m2r_fail("layers step: batch x layers exceeds the grid limit 65535");
+  if (nlayers > 0) t_table.resize((size_t)nlayers);
+  if (int e = build_table(layers, nlayers, batch, H, P, G, t_table.data(), wpb, hpw)) return e;
   const int64_t need = m2r_state_step_ridge_layers_workspace(nlayers);
   if (!workspace || !aligned(workspace, 16) || workspace_bytes < need)
     return m2r_fail("layers step: workspace must be 16-byte aligned and hold m2r_state_step_ridge_layers_workspace(nlayers) bytes");
@@ -155,4 +194,20 @@ extern "C" int m2r_state_step_ridge_layers(const m2r_ridge_layer* layers, int nl
                         "layers step table copy"))
     return e;
   return launch_layers((const LayerEntry*)workspace, nlayers, batch, H, P, wpb, hpw, stream);
+}
+
+extern "C" int m2r_state_step_ridge_layers_noalloc(const m2r_ridge_layer* layers, int nlayers, int64_t batch,
+                                                   int64_t H, int64_t P, int64_t G, hipStream_t stream) {
+  if (nlayers > M2R_LAYERS_NOALLOC_MAX)
+    return m2r_fail("layers step (no-alloc): more than M2R_LAYERS_NOALLOC_MAX (256) layers in one call");
+  void* dev_table = nullptr;
+  if (int e = scratch_address(&dev_table)) return e;
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  int wpb = 0, hpw = 0;
+  if (int e = build_table(layers, nlayers, batch, H, P, G, g_noalloc_table, wpb, hpw)) return e;
+  const size_t bytes = (size_t)m2r_state_step_ridge_layers_workspace(nlayers);
+  if (int e = m2r_check(hipMemcpyAsync(dev_table, g_noalloc_table, bytes, hipMemcpyHostToDevice, stream),
+                        "layers step (no-alloc) table copy"))
+    return e;
+  return launch_layers((const LayerEntry*)dev_table, nlayers, batch, H, P, wpb, hpw, stream);
 }

@@ -41,6 +41,7 @@ _SIGNATURES = {
     "m2r_fp4_gemv_g16": ([P, P, P, P, I64, P, I64, I64, I64, I64, P], I),
     "m2r_state_step_ridge_layers_workspace": ([I], I64),
     "m2r_state_step_ridge_layers": ([P, I, I64, I64, I64, I64, P, I64, P], I),
+    "m2r_state_step_ridge_layers_noalloc": ([P, I, I64, I64, I64, I64, P], I),
 }
 
 
