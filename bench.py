@@ -10,7 +10,7 @@ G16 decode, the measured device-to-device copy
 bandwidth, a live roofline for the dominant kernel, and the CPU oracle
 timed on a bounded sample (state step and FP4 decode) as a baseline.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-fp4] [--skip-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-fp4] [--skip-cpu] [--skip-e2e]
        python bench.py --only step|copy|codecs|layers|ceiling|e2e|loader
        (profiling runs: only the step graph at --batch, only a 256 MiB copy
        used to calibrate counters, only the other codecs' batch-64 graphs,
@@ -385,7 +385,7 @@ def other_codecs(device, batch=64, launches=56, steps=10):
     return out
 
 
-def e2e_decode(device, batches=(1, 4, 16), prefill=8, tokens=32):
+def e2e_decode(device, batches=(1, 4, 16), prefill=8, tokens=256, eager_tokens=64):
     """BASELINE config 5, with a shortened continuation: a random-init Mamba-2
     8B model (56 layers, d_model 4096, d_inner 8192, vocab 256000) whose
     in_proj, out_proj, embedding and lm_head weights are decoded on the device
@@ -394,10 +394,14 @@ def e2e_decode(device, batches=(1, 4, 16), prefill=8, tokens=32):
     the ridge-latent per-token requantize hook installed on every layer
     (published layouts, seeded statics).  Greedy decode: a prefill of
     `prefill` tokens, two untimed steps, then `tokens` timed steps of
-    backbone + lm_head + argmax, eager and replayed as one captured HIP graph
-    per step, with the projections as FP16 GEMMs and (batch sizes the kernel
-    takes) as packed-resident FP4 GEMVs; the hook's per-call host validation
-    is off (statics are validated once).  Returns ms per generated token."""
+    backbone + lm_head + argmax, eager, and with the backbone replayed as one
+    captured HIP graph per step (lm_head and argmax stay eager), with the
+    projections as FP16 GEMMs and (batch sizes the kernel takes) as
+    packed-resident FP4 GEMVs; the hook's per-call host validation
+    is off (statics are validated once).  The eager run covers the first
+    `eager_tokens` steps (its ids and layer 0's packed state are the
+    reference the graph replays are checked against); the graph is timed over
+    `tokens` steps.  Returns ms per generated token."""
     import math
     import torch.nn.functional as F
     sys.path.insert(0, str(ROOT / "tests"))
@@ -444,6 +448,13 @@ def e2e_decode(device, batches=(1, 4, 16), prefill=8, tokens=32):
         torch.cuda.synchronize()
         return ev0.elapsed_time(ev1) / reps
 
+    def next_ids(hidden):
+        # lm_head and the argmax over 256000 logits run eagerly, outside the
+        # captured graphs: that argmax is a multi-workgroup torch reduction
+        # that clears its semaphores with hipMemsetAsync, and memset nodes in
+        # captured graphs are not reliable on replay
+        return model.lm_head(hidden[:, -1:]).float().argmax(-1)
+
     def snapshot(pq):
         return [(e.conv.clone(), {k: v.clone() for k, v in e.state.tensors.items()}) for e in pq._cache]
 
@@ -455,44 +466,50 @@ def e2e_decode(device, batches=(1, 4, 16), prefill=8, tokens=32):
 
     def decode_modes(pq, snap, start):
         """Eager run from the snapshot, the same step captured as a HIP graph,
-        replays checked token by token and on layer 0's packed state."""
+        replays checked token by token and on layer 0's packed state against
+        the eager run, then `tokens` replays timed from the snapshot."""
         restore(pq, snap)
         nxt, eager_ids, first_logits = start.clone(), [], None
         torch.cuda.synchronize()
         ev0.record()
-        for i in range(tokens):
-            logits = model.lm_head(pq.backbone(nxt)).float()
+        for i in range(eager_tokens):
+            logits = model.lm_head(pq.backbone(nxt)[:, -1:]).float()
             first_logits = logits.clone() if i == 0 else first_logits
             nxt = logits.argmax(-1)
             eager_ids.append(nxt)
         ev1.record()
         torch.cuda.synchronize()
-        eager_ms = ev0.elapsed_time(ev1) / tokens
+        eager_ms = ev0.elapsed_time(ev1) / eager_tokens
         eager_state = {k: v.clone() for k, v in pq._cache[0].state.tensors.items()}
-        finite = bool(pq.assert_finite_cache())
         restore(pq, snap)
         static_ids = start.clone()
+        static_hidden = torch.empty(start.shape[0], 1, 4096, dtype=torch.float16, device=device)
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):   # capture warm-up, then the snapshot is restored
-            static_ids.copy_(model.lm_head(pq.backbone(static_ids)).float().argmax(-1))
+            static_hidden.copy_(pq.backbone(static_ids))
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         restore(pq, snap)
-        static_ids.copy_(start)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            static_ids.copy_(model.lm_head(pq.backbone(static_ids)).float().argmax(-1))
-        graph_ids = []
-        for _ in range(tokens):
+            static_hidden.copy_(pq.backbone(static_ids))
+
+        def step():   # one decode step: the backbone graph, then the eager head and feedback
             graph.replay()
+            static_ids.copy_(next_ids(static_hidden))
+
+        graph_ids = []
+        for _ in range(eager_tokens):
+            step()
             graph_ids.append(static_ids.clone())
         torch.cuda.synchronize()
         same = all(torch.equal(a, b) for a, b in zip(eager_ids, graph_ids)) and all(
             torch.equal(pq._cache[0].state.tensors[k], v) for k, v in eager_state.items())
         restore(pq, snap)
         static_ids.copy_(start)
-        graph_ms = timed(graph.replay, tokens)
+        graph_ms = timed(step, tokens)
+        finite = bool(pq.assert_finite_cache())
         del graph
         return dict(eager_ms=eager_ms, graph_ms=graph_ms, same=same, finite=finite, logits=first_logits)
 
@@ -524,10 +541,9 @@ def e2e_decode(device, batches=(1, 4, 16), prefill=8, tokens=32):
             with ridge_codec.PredictorState(model, perms, PUBLISHED_LAYOUTS, bases, scales, preds) as pq:
                 pq.validate_each_step = False
                 ids = torch.randint(0, 256000, (batch, prefill), generator=gen, device=device)
-                h = pq.backbone(ids, reset=True)
-                nxt = model.lm_head(h[:, -1:]).float().argmax(-1)
+                nxt = next_ids(pq.backbone(ids, reset=True))
                 for _ in range(2):
-                    nxt = model.lm_head(pq.backbone(nxt)).float().argmax(-1)
+                    nxt = next_ids(pq.backbone(nxt))
                 torch.cuda.synchronize()
                 snap, start = snapshot(pq), nxt.clone()
                 r16 = decode_modes(pq, snap, start)
@@ -548,10 +564,12 @@ def e2e_decode(device, batches=(1, 4, 16), prefill=8, tokens=32):
     del model, packets
     torch.cuda.empty_cache()
     out["note"] = (f"random-init 8B, FP16 weights decoded from seeded FP4 G16; ridge hook on 56 layers; prefill "
-                   f"{prefill}, {tokens} timed greedy tokens; PyTorch mixer (GEMMs, conv, gated norm) around the "
-                   f"HIP codec kernel, eager and as one captured HIP graph per decode step (replays checked "
-                   f"token by token and on layer 0's packed state against the eager run); packed_fp4: the "
-                   f"one-token in_proj/out_proj as packed-resident FP4 G16 GEMVs")
+                   f"{prefill}; {eager_tokens} eager greedy tokens (the reference the graph replays are checked "
+                   f"against, token by token and on layer 0's packed state) and {tokens} timed greedy tokens, each "
+                   f"one replay of the captured backbone graph plus the eager lm_head, argmax and token "
+                   f"feedback; PyTorch mixer (GEMMs, gated norm) around the HIP "
+                   f"codec and convolution-update kernels; packed_fp4: the one-token in_proj/out_proj as "
+                   f"packed-resident FP4 G16 GEMVs")
     return out
 
 
@@ -664,7 +682,7 @@ def main():
     ap.add_argument("--skip-fp4", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", choices=("step", "copy", "codecs", "e2e", "loader", "ceiling", "layers"), default=None)
-    ap.add_argument("--e2e", action="store_true", help="also time the end-to-end 8B decode (BASELINE config 5)")
+    ap.add_argument("--skip-e2e", action="store_true", help="skip the end-to-end 8B decode (BASELINE config 5)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the state codec and FP4 decode shard with no communication "
@@ -747,8 +765,8 @@ def main():
                      fp4_g16_frac_of_copy=round(fp4_gbs / copy_gbs, 4),
                      fp4_g16_frac_of_mix_ceiling=round(fp4_gbs / fp4_ceiling, 4))
     extra["other_codecs_b64"] = other_codecs(device)
-    if args.e2e:
-        extra["e2e_decode"] = e2e_decode(device)
+    if not args.skip_e2e:
+        extra["e2e_decode"] = e2e_decode(device, batches=(1, 16))
     line = dict(
         metric=METRIC, value=round(gbs, 2), unit="GB/s", n_gpus=1, steps=args.steps, warmup=args.warmup,
         ms_per_step=round(ms, 5), higher_is_better=True, scaling="weak", vs_baseline=None, dtype="f32",

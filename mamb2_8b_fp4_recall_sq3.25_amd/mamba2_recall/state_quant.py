@@ -18,16 +18,19 @@ the dense 3-bit, stored-scale tier and ridge-latent controllers.
 """
 from __future__ import annotations
 
-import types
 import weakref
 from dataclasses import dataclass
+from typing import Optional
 
 import torch
 import torch.nn.functional as F
 
 from . import _native, fp4, state_codec
 
-_OWNERS = weakref.WeakKeyDictionary()
+# Installed controllers, keyed by the identity of the model each owns.  Values
+# are held weakly; the installed per-layer hooks keep a controller alive until
+# close() removes them and the entry.
+_CLAIMS: "weakref.WeakValueDictionary[int, _MixerController]" = weakref.WeakValueDictionary()
 
 
 @dataclass
@@ -35,6 +38,34 @@ class _LayerCache:
     conv: torch.Tensor
     state: object
     tokens: int = 0
+
+
+@dataclass
+class _Request:
+    """Caches and ordering state of the request in flight: the layer caches,
+    the layer the next mixer call must be for, the token count every layer of
+    the current backbone call must see, and whether a call failed."""
+    batch: int
+    layers: list
+    next_layer: int = 0
+    call_tokens: Optional[int] = None
+    failed: bool = False
+
+
+class _LayerHook:
+    """Installed as one mixer's `forward` (an instance attribute shadowing the
+    class method), so module hooks registered on the mixer still run around it."""
+
+    __slots__ = ("controller", "index", "module")
+
+    def __init__(self, controller, index, module):
+        self.controller, self.index, self.module = controller, index, module
+
+    def __call__(self, u, seqlen=None, seq_idx=None, cu_seqlens=None, inference_params=None):
+        return self.controller._forward(self.index, self.module, u, seqlen, seq_idx, cu_seqlens, inference_params)
+
+
+_MISSING = object()
 
 
 def conv_update(window, value, weight, bias, *, silu=True):
@@ -70,9 +101,11 @@ def _native_conv_ops():
 
 
 class _MixerController:
-    """Install / reset / request-ordering logic around one codec
-    (state_quant.py:59-281).  Geometry constants describe the Mamba-2 8B
-    mixer; the model is checked against them at construction."""
+    """Owns the per-token state of a frozen Mamba-2 8B model while installed:
+    every mixer call runs in_proj -> causal conv -> split -> one codec call ->
+    the mixer's gated norm as a module call -> out_proj, with the request
+    ordering the reference enforces (state_quant.py:59-281).  A codec
+    subclass supplies `_new_state`, `_scan_layer` and `cache_breakdown`."""
 
     LAYERS, D_MODEL, HEADS, HEADDIM, D_STATE, GROUPS, D_CONV, D_INNER = 56, 4096, 128, 64, 128, 8, 4, 8192
     PARAMETER_TENSORS, PARAMETER_COUNT = 507, 8_236_999_680
@@ -88,18 +121,32 @@ class _MixerController:
         if self.device.type != "cuda":
             raise ValueError("The packed state codec requires a CUDA model")
         self.permutations = self._validate_permutations(permutations)
-        self._cache = []
+        bc = self.GROUPS * self.D_STATE
+        # split sizes of the in_proj output (z, x|B|C, dt) and of the
+        # convolution output (x, B, C)
+        self._in_sizes = (self.D_INNER, self.D_INNER + 2 * bc, self.HEADS)
+        self._conv_sizes = (self.D_INNER, bc, bc)
+        self._request: Optional[_Request] = None
+        self._hooks = {}          # mixer index -> (module, forward it shadowed or _MISSING)
+        self._running = False     # inside backbone()
         self._rates = {}
         self._packed = None
-        self._sums = [None] * len(self._mixers)
-        self._counts = [0] * len(self._mixers)
-        self._originals = []
-        self._batch_size = None
-        self._expected_layer = 0
-        self._call_length = None
-        self._failed = False
-        self._installed = False
-        self._inside_backbone = False
+        self._stat_sums = {}      # layer index -> FP64 [groups, 128] totals
+        self._stat_counts = [0] * len(self._mixers)
+
+    # ------------------------------------------------------------- compatibility
+    @property
+    def _cache(self):
+        """The layer caches of the request in flight (empty when cleared)."""
+        return self._request.layers if self._request is not None else []
+
+    @property
+    def _batch_size(self):
+        return self._request.batch if self._request is not None else None
+
+    @property
+    def _installed(self):
+        return bool(self._hooks)
 
     # ---------------------------------------------------------------- geometry
     @property
@@ -155,23 +202,18 @@ class _MixerController:
 
     # ---------------------------------------------------------------- lifetime
     def install(self):
-        """Replace every mixer's forward; state_quant.py:135-151."""
+        """Put a hook in front of every mixer's forward (the reference's
+        install, state_quant.py:135-151: one owner per model)."""
         if self._installed:
             raise RuntimeError("StateQuant controller is already installed")
-        owner = _OWNERS.get(self.model)
-        if owner is not None and owner() is not None:
+        key = id(self.model)
+        if _CLAIMS.get(key) is not None:
             raise RuntimeError("Another StateQuant controller owns this model")
-        _OWNERS[self.model] = weakref.ref(self)
+        _CLAIMS[key] = self
         try:
             for index, mx in enumerate(self._mixers):
-                self._originals.append((mx, mx.forward))
-
-                def forward(module, u, seqlen=None, seq_idx=None, cu_seqlens=None, inference_params=None,
-                            _index=index):
-                    return self._forward(_index, module, u, seqlen, seq_idx, cu_seqlens, inference_params)
-
-                mx.forward = types.MethodType(forward, mx)
-            self._installed = True
+                self._hooks[index] = (mx, mx.__dict__.get("forward", _MISSING))
+                mx.forward = _LayerHook(self, index, mx)
         except Exception:
             self.close()
             raise
@@ -185,37 +227,38 @@ class _MixerController:
         return False
 
     def close(self):
-        for mx, original in reversed(self._originals):
-            mx.forward = original
-        self._originals.clear()
-        self._installed = False
-        owner = _OWNERS.get(self.model)
-        if owner is not None and owner() is self:
-            del _OWNERS[self.model]
+        """Remove the hooks (restoring whatever forward each mixer had),
+        release the model and drop the request caches."""
+        while self._hooks:
+            _, (mx, shadowed) = self._hooks.popitem()
+            if shadowed is _MISSING:
+                mx.__dict__.pop("forward", None)
+            else:
+                mx.forward = shadowed
+        if _CLAIMS.get(id(self.model)) is self:
+            del _CLAIMS[id(self.model)]
         self.clear()
 
     def clear(self):
         """Release all request caches, retaining calibration totals and tables."""
-        self._cache.clear()
-        self._batch_size = None
-        self._expected_layer = 0
-        self._call_length = None
-        self._failed = False
+        self._request = None
 
     @torch.no_grad()
     def reset(self, batch_size=1):
-        """Allocate fresh zero caches (state_quant.py:177-193)."""
+        """Start a request: zero caches for every layer (state_quant.py:177-193)."""
         if not self._installed:
             raise RuntimeError("Install the controller before resetting caches")
         if not isinstance(batch_size, int) or isinstance(batch_size, bool) or batch_size <= 0:
             raise ValueError("batch_size must be a positive integer")
         self.clear()
+        layers = []
         for index in range(len(self._mixers)):
-            # channels-last window, as the native convolution state is strided
-            conv = torch.zeros(batch_size, self.D_CONV, self._conv_channels, device=self.device,
-                               dtype=torch.float16).transpose(1, 2)
-            self._cache.append(_LayerCache(conv=conv, state=self._new_state(batch_size, index)))
-        self._batch_size = batch_size
+            # the window is channels-last in memory (the layout of the
+            # native convolution state), viewed as [batch, channels, 4]
+            window = torch.zeros(batch_size, self.D_CONV, self._conv_channels, device=self.device,
+                                 dtype=torch.float16).permute(0, 2, 1)
+            layers.append(_LayerCache(conv=window, state=self._new_state(batch_size, index)))
+        self._request = _Request(batch=batch_size, layers=layers)
         self._after_reset(batch_size)
         return self
 
@@ -224,88 +267,103 @@ class _MixerController:
 
     @torch.no_grad()
     def backbone(self, ids, reset=False):
-        """Hidden states of model.backbone(ids), advancing this controller's
-        cache (state_quant.py:195-217)."""
+        """model.backbone(ids) with every mixer going through this controller
+        (state_quant.py:195-217): the request's caches are used and advanced."""
         if not self._installed:
             raise RuntimeError("StateQuant controller is not installed")
         if not isinstance(ids, torch.Tensor) or ids.ndim != 2 or ids.shape[1] == 0:
             raise ValueError("Input IDs must be nonempty [batch,tokens]")
         if ids.device != self.device or ids.dtype != torch.long:
             raise ValueError("Input IDs must be CUDA int64 on the model device")
-        if self._inside_backbone:
+        if self._running:
             raise RuntimeError("Concurrent/reentrant backbone invocation is unsupported")
-        if reset or not self._cache:
+        if reset or self._request is None:
             self.reset(ids.shape[0])
-        self._inside_backbone = True
+        self._running = True
         try:
-            result = self.model.backbone(ids)
-            if self._expected_layer != 0:
+            hidden = self.model.backbone(ids)
+            if self._request.next_layer != 0:
                 raise RuntimeError("Backbone did not execute every state-quantized layer")
-            return result
         except Exception:
-            self._failed = True
+            if self._request is not None:
+                self._request.failed = True
             raise
         finally:
-            self._inside_backbone = False
+            self._running = False
+        return hidden
 
     # ---------------------------------------------------------------- one layer
-    @torch.no_grad()
-    def _forward(self, index, mx, u, seqlen, seq_idx, cu_seqlens, inference_params):
-        """state_quant.py:219-281: guards, then the mixer step around the codec."""
-        if not self._installed or self._failed:
+    def _admit(self, index, u, extras):
+        """The reference's checks before a mixer call (state_quant.py:219-247),
+        in its order; returns the layer's cache."""
+        if not self._installed or (self._request is not None and self._request.failed):
             raise RuntimeError("Controller is inactive or failed; reset before reusing it")
-        if any(value is not None for value in (seqlen, seq_idx, cu_seqlens, inference_params)):
+        if any(value is not None for value in extras):
             raise ValueError("Use controller-owned caches; native InferenceParams/varlen are unsupported")
-        if (not isinstance(u, torch.Tensor) or u.ndim != 3 or u.dtype != torch.float16
-                or u.device != self.device or u.shape[-1] != self.D_MODEL or u.shape[1] == 0):
+        well_formed = (isinstance(u, torch.Tensor) and u.ndim == 3 and u.dtype == torch.float16
+                       and u.device == self.device and u.shape[-1] == self.D_MODEL and u.shape[1] > 0)
+        if not well_formed:
             raise ValueError("Mixer input must be CUDA FP16 [batch,tokens,4096]")
-        if not self._cache:
+        if self._request is None:
             if index != 0:
                 raise RuntimeError("A new request must start with backbone layer zero")
             self.reset(u.shape[0])
-        if u.shape[0] != self._batch_size or index != self._expected_layer:
+        request = self._request
+        if u.shape[0] != request.batch or index != request.next_layer:
             raise RuntimeError("Batch shape or backbone layer order changed without a reset")
-        length = u.shape[1]
+        tokens = u.shape[1]
         if index == 0:
-            if len({entry.tokens for entry in self._cache}) != 1:
+            positions = {layer.tokens for layer in request.layers}
+            if len(positions) != 1:
                 raise RuntimeError("Per-layer cache positions disagree; reset the request")
-            self._call_length = length
-        elif length != self._call_length:
+            request.call_tokens = tokens
+        elif tokens != request.call_tokens:
             raise RuntimeError("Backbone layers received different token counts")
-        entry = self._cache[index]
+        return request.layers[index]
+
+    @torch.no_grad()
+    def _forward(self, index, mx, u, seqlen, seq_idx, cu_seqlens, inference_params):
+        """One mixer call: admission checks, then the mixer around the codec."""
+        layer = self._admit(index, u, (seqlen, seq_idx, cu_seqlens, inference_params))
         try:
-            # a one-token continuation keeps the native rank-two GEMM / norm shapes
-            is_step = entry.tokens > 0 and length == 1
-            projected = self._project(index, "in_proj", mx, u.squeeze(1)) if is_step else mx.in_proj(u)
-            zxbcdt = projected.unsqueeze(1) if is_step else projected
-            bc = self.GROUPS * self.D_STATE
-            z, xbc, dt = torch.split(zxbcdt, (self.D_INNER, self.D_INNER + 2 * bc, self.HEADS), dim=-1)
-            xbc = self._convolution(mx, xbc, entry)
-            x, bm, cm = torch.split(xbc, (self.D_INNER, bc, bc), dim=-1)
-            batch = u.shape[0]
-            x = x.reshape(batch, length, self.HEADS, self.HEADDIM)
-            bm = bm.reshape(batch, length, self.GROUPS, self.D_STATE)
-            cm = cm.reshape(batch, length, self.GROUPS, self.D_STATE)
-            aa = self._decay_rates(index, mx)
-            y, stats = self._scan_layer(index, mx, x, dt, aa, bm, cm, entry)
-            if y.dtype != torch.float16 or tuple(y.shape) != (batch, length, self.HEADS, self.HEADDIM):
-                raise RuntimeError("State codec returned unexpected readout dtype/shape")
-            if self.collect_stats:
-                self._accumulate_statistics(index, stats, batch, length)
-            # the gated norm stays a module call: external norm hooks see (y, z)
-            y = y.reshape(batch, length, self.D_INNER)
-            if is_step:
-                out = self._project(index, "out_proj", mx, mx.norm(y[:, 0], z[:, 0])).unsqueeze(1)
-            else:
-                out = mx.out_proj(mx.norm(y, z))
-            entry.tokens += length
-            self._expected_layer = (index + 1) % len(self._mixers)
-            if self._expected_layer == 0:
-                self._call_length = None
-            return out
+            out = self._mixer(index, mx, u, layer)
         except Exception:
-            self._failed = True
+            self._request.failed = True
             raise
+        request = self._request
+        request.next_layer = index + 1 if index + 1 < len(self._mixers) else 0
+        if request.next_layer == 0:
+            request.call_tokens = None
+        return out
+
+    def _mixer(self, index, mx, u, layer):
+        batch, tokens = u.shape[0], u.shape[1]
+        # a one-token continuation runs the projections and the norm on rank-2
+        # inputs (the shapes the native step uses, and the ones norm hooks see)
+        step = layer.tokens > 0 and tokens == 1
+        if step:
+            zxbcdt = self._project(index, "in_proj", mx, u[:, 0])[:, None]
+        else:
+            zxbcdt = mx.in_proj(u)
+        z, xbc, dt = torch.split(zxbcdt, self._in_sizes, dim=-1)
+        xbc = self._conv_step(mx, xbc[:, 0], layer)[:, None] if step else self._conv_prefill(mx, xbc, layer)
+        x, bm, cm = torch.split(xbc, self._conv_sizes, dim=-1)
+        y, stats = self._scan_layer(index, mx, x.reshape(batch, tokens, self.HEADS, self.HEADDIM), dt,
+                                    self._decay_rates(index, mx),
+                                    bm.reshape(batch, tokens, self.GROUPS, self.D_STATE),
+                                    cm.reshape(batch, tokens, self.GROUPS, self.D_STATE), layer)
+        if y.dtype != torch.float16 or tuple(y.shape) != (batch, tokens, self.HEADS, self.HEADDIM):
+            raise RuntimeError("State codec returned unexpected readout dtype/shape")
+        if self.collect_stats:
+            self._accumulate_statistics(index, stats, batch, tokens)
+        # the gated norm is called as a module, so its hooks see (y, z)
+        y = y.reshape(batch, tokens, self.D_INNER)
+        if step:
+            out = self._project(index, "out_proj", mx, mx.norm(y[:, 0], z[:, 0]))[:, None]
+        else:
+            out = mx.out_proj(mx.norm(y, z))
+        layer.tokens += tokens
+        return out
 
     def use_packed_projections(self, packets, verify=False):
         """Run the one-token in_proj and out_proj of every layer as
@@ -369,62 +427,68 @@ class _MixerController:
             self._rates[index] = cached
         return cached[1]
 
-    def _convolution(self, mx, xbc, entry):
-        """Causal depthwise convolution with the cached window
-        (state_quant.py:283-317): the one-token update rolls the window; a
-        prefill prepends the cached raw inputs and refreshes the window."""
-        update_op, conv_op = _native_conv_ops()
-        length = xbc.shape[1]
+    # ---------------------------------------------------------------- convolution
+    # Same arithmetic as the reference's _convolution (state_quant.py:283-317):
+    # mamba_ssm's fused kernels when present, otherwise its PyTorch fallback
+    # (the one-token update as the HIP kernel conv_update).
+    def _conv_step(self, mx, column, layer):
+        """One token: shift the cached window, append `column` [B, C], return
+        the activated convolution output [B, C]."""
+        update_op, _ = _native_conv_ops()
         weight = mx.conv1d.weight[:, 0, :]
-        if entry.tokens > 0 and length == 1:
-            value = xbc[:, 0, :]
-            if update_op is None:
-                value = conv_update(entry.conv, value, weight, mx.conv1d.bias,
-                                    silu=mx.activation in ("silu", "swish"))
-            else:
-                value = update_op(value, entry.conv, weight, mx.conv1d.bias, mx.activation)
-            return value[:, None, :]
-        raw = xbc.transpose(1, 2)
-        prefix = 0
-        if entry.tokens > 0:
-            # only past raw projections are prepended; the causal result then
-            # covers exactly the requested continuation positions
-            raw = torch.cat((entry.conv[:, :, 1:], raw), dim=-1)
-            prefix = self.D_CONV - 1
-        entry.conv.copy_(F.pad(raw, (self.D_CONV - raw.shape[-1], 0)))
-        if conv_op is None:
-            result = mx.act(mx.conv1d(raw).transpose(1, 2)[:, :-(self.D_CONV - 1)])
+        if update_op is not None:
+            return update_op(column, layer.conv, weight, mx.conv1d.bias, mx.activation)
+        return conv_update(layer.conv, column, weight, mx.conv1d.bias, silu=mx.activation in ("silu", "swish"))
+
+    def _conv_prefill(self, mx, xbc, layer):
+        """Several tokens (or the first): the causal convolution over the
+        cached history (the window's last D_CONV - 1 raw inputs, after the
+        first call) followed by the new inputs; the window then holds the last
+        D_CONV raw inputs, zero-padded on the left."""
+        _, fused_op = _native_conv_ops()
+        tokens = xbc.shape[1]
+        fresh = xbc.transpose(1, 2)                              # [B, C, tokens]
+        history = self.D_CONV - 1 if layer.tokens > 0 else 0
+        series = torch.cat((layer.conv[:, :, 1:], fresh), dim=-1) if history else fresh
+        kept = min(self.D_CONV, series.shape[-1])
+        if kept < self.D_CONV:
+            layer.conv.zero_()
+        layer.conv[:, :, self.D_CONV - kept:].copy_(series[:, :, series.shape[-1] - kept:])
+        if fused_op is not None:
+            out = fused_op(series, mx.conv1d.weight[:, 0, :], bias=mx.conv1d.bias, activation=mx.activation,
+                           seq_idx=None).transpose(1, 2)
         else:
-            result = conv_op(raw, weight, bias=mx.conv1d.bias, activation=mx.activation, seq_idx=None).transpose(1, 2)
-        return result[:, prefix:prefix + length]
+            out = mx.act(mx.conv1d(series).transpose(1, 2)[:, :series.shape[-1]])
+        return out[:, history:history + tokens]
 
     # ---------------------------------------------------------------- statistics
     def _accumulate_statistics(self, index, stats, batch, length):
-        """state_quant.py:319-330: FP64 group totals of |FP16 carry|."""
+        """Adds one codec call's |FP16 carry| sums to the layer's FP64 totals per
+        (group, coordinate) (state_quant.py:319-330)."""
         tiles = (self.HEADDIM + 15) // 16
+        expected = (batch, self.HEADS, tiles, self.D_STATE)
         if (not isinstance(stats, torch.Tensor) or stats.dtype != torch.float32 or stats.device != self.device
-                or tuple(stats.shape) != (batch, self.HEADS, tiles, self.D_STATE)):
+                or tuple(stats.shape) != expected):
             raise RuntimeError("Expected codec calibration sum [batch,128,4,128] FP32")
-        hpg = self.HEADS // self.GROUPS
-        totals = stats.reshape(batch, self.GROUPS, hpg, tiles, self.D_STATE).double().sum(dim=(0, 2, 3))
-        if self._sums[index] is None:
-            self._sums[index] = totals
-        else:
-            self._sums[index].add_(totals)
-        self._counts[index] += batch * length * hpg * self.HEADDIM
+        heads_per_group = self.HEADS // self.GROUPS
+        by_group = stats.double().reshape(batch, self.GROUPS, heads_per_group, tiles, self.D_STATE).sum(dim=(0, 2, 3))
+        total = self._stat_sums.get(index)
+        self._stat_sums[index] = by_group if total is None else total.add_(by_group)
+        self._stat_counts[index] += batch * length * heads_per_group * self.HEADDIM
 
     def reset_statistics(self):
-        self._sums = [None] * len(self._mixers)
-        self._counts = [0] * len(self._mixers)
+        self._stat_sums = {}
+        self._stat_counts = [0] * len(self._mixers)
 
     def statistics(self):
         """CPU FP64 sums/means [56,8,128] and sample counts [56]."""
-        if not self.collect_stats or any(value is None for value in self._sums):
+        layers = range(len(self._mixers))
+        if not self.collect_stats or any(i not in self._stat_sums for i in layers):
             raise RuntimeError("Complete S16 calibration is required before collecting statistics")
-        sums = torch.stack(self._sums).detach().cpu()
-        counts = torch.tensor(self._counts, dtype=torch.int64)
+        counts = torch.tensor(self._stat_counts, dtype=torch.int64)
         if bool((counts <= 0).any()):
             raise RuntimeError("Calibration has empty layers")
+        sums = torch.stack([self._stat_sums[i] for i in layers]).detach().cpu()
         return {"sum_abs": sums, "sample_count_per_group": counts, "mean_abs": sums / counts[:, None, None],
                 "semantics": "abs(FP16 stored carry), each token; average over batch, heads within each group, "
                              "P and time"}
@@ -495,19 +559,26 @@ class StateQuant(_MixerController):
                                 collect_stats=self.collect_stats)
 
     def cache_breakdown(self):
-        """Persistent request cache payload (state_quant.py:347-366)."""
-        conv = sum(v.conv.numel() * v.conv.element_size() for v in self._cache)
-        state = sum(int(v.state.nbytes) for v in self._cache)
-        scales = sum(t.numel() * t.element_size() for v in self._cache for k, t in v.state.tensors.items()
-                     if k in ("s4", "s8"))
-        tables = 0 if self.permutations is None else self.permutations.numel() * self.permutations.element_size()
-        statistics = sum(v.numel() * v.element_size() for v in self._sums if v is not None)
-        return {"mode": self.mode, "batch_size": self._batch_size, "allocated_layers": len(self._cache),
-                "conv_fp16_bytes": conv, "ssm_payload_bytes": state - scales, "ssm_scale_bytes": scales,
-                "ssm_total_bytes": state, "permutation_bytes": tables, "total_bytes": conv + state + tables,
-                "calibration_workspace_bytes": statistics, "tokens_per_layer": [v.tokens for v in self._cache],
-                "scope": "Actual persistent request cache plus compact permutation table; weights, activations, "
-                         "registers, allocator reserve and calibration workspace excluded from total_bytes"}
+        """Bytes the request holds per kind of tensor, in the reference's
+        report format (state_quant.py:347-366): windows, packed payload,
+        stored scales, the permutation table and, outside the total, the
+        calibration sums."""
+        def size(t):
+            return t.numel() * t.element_size()
+
+        layers = self._cache
+        conv = sum(size(c.conv) for c in layers)
+        state = sum(int(c.state.nbytes) for c in layers)
+        scales = sum(size(t) for c in layers for k, t in c.state.tensors.items() if k in ("s8", "s4"))
+        tables = 0 if self.permutations is None else size(self.permutations)
+        report = {"mode": self.mode, "batch_size": self._batch_size, "allocated_layers": len(layers)}
+        report.update(conv_fp16_bytes=conv, ssm_payload_bytes=state - scales, ssm_scale_bytes=scales,
+                      ssm_total_bytes=state, permutation_bytes=tables, total_bytes=conv + state + tables,
+                      calibration_workspace_bytes=sum(size(t) for t in self._stat_sums.values()),
+                      tokens_per_layer=[c.tokens for c in layers],
+                      scope="Actual persistent request cache plus compact permutation table; weights, activations, "
+                            "registers, allocator reserve and calibration workspace excluded from total_bytes")
+        return report
 
 
 PackedStateRuntime = StateQuant

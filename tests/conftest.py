@@ -30,3 +30,15 @@ def device():
     if not torch.cuda.is_available():
         pytest.skip("no HIP device")
     return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="session")
+def model(device):
+    """A random-init Mamba-2 8B model of the real geometry on the GPU (built
+    once per session; tests may overwrite its projection weights)."""
+    import torch
+    from mamba2_model import random_model
+    print("[model] building the random 8B model", flush=True)
+    m = random_model(device)
+    torch.cuda.synchronize()
+    return m

@@ -12,6 +12,16 @@ from torch import nn
 import torch.nn.functional as F
 
 
+def _mean_square(v):
+    """Mean of v^2 over the last dimension (a multiple of 64 wide) as two
+    reductions of at most 64 elements per output: each output fits one
+    workgroup, so no reduction splits across workgroups (which would clear
+    semaphores with a memset inside a captured HIP graph)."""
+    n = v.shape[-1]
+    partial = v.pow(2).reshape(*v.shape[:-1], n // 64, 64).sum(-1)
+    return partial.sum(-1, keepdim=True) / n
+
+
 class RMSNorm(nn.Module):
     def __init__(self, d, eps=1e-5):
         super().__init__()
@@ -20,7 +30,7 @@ class RMSNorm(nn.Module):
 
     def forward(self, x):
         v = x.float()
-        v = v * torch.rsqrt(v.pow(2).mean(-1, keepdim=True) + self.eps)
+        v = v * torch.rsqrt(_mean_square(v) + self.eps)
         return (v * self.weight.float()).to(x.dtype)
 
 
@@ -36,7 +46,7 @@ class GatedRMSNorm(nn.Module):
         v = y.float() * F.silu(z.float())
         shape = v.shape
         v = v.reshape(*shape[:-1], shape[-1] // self.group_size, self.group_size)
-        v = v * torch.rsqrt(v.pow(2).mean(-1, keepdim=True) + self.eps)
+        v = v * torch.rsqrt(_mean_square(v) + self.eps)
         return (v.reshape(shape) * self.weight.float()).to(y.dtype)
 
 

@@ -10,21 +10,12 @@ import torch
 import torch.nn.functional as F
 
 import cases
-from mamba2_model import random_model
 
 pytestmark = pytest.mark.gpu
 
 LAYOUTS = ("36_24_68", "16_64_48", "32_32_64", "40_16_72", "16_64_48", "16_64_48", "24_48_56", "32_32_64") * 7
 CACHE_B1 = 28_499_968
 TABLE = 57_344
-
-
-@pytest.fixture(scope="module")
-def model(device):
-    print("[controllers] building the random 8B model", flush=True)
-    m = random_model(device)
-    torch.cuda.synchronize()
-    return m
 
 
 def tables(device, seed=3):
@@ -195,9 +186,13 @@ def test_packed_projections(model, device):
     """use_packed_projections: the one-token in_proj/out_proj as packed FP4
     GEMVs.  Packets whose decode equals the module weights pass verify=True
     (the model's projections are first overwritten by the decode of seeded G16
-    packets); a packet that decodes differently is rejected; a one-token step
-    with the packed projections matches the FP16-module step within the
-    summation-order tolerance; prefill keeps the modules."""
+    packets); a packet that decodes differently is rejected.  A 56-layer
+    one-token step with the packed projections stays close to the FP16-module
+    step: each projection differs only in summation order (within 1e-3,
+    test_packed_projection_outputs_per_layer), but every layer requantizes its
+    state, so a code that sits on a rounding boundary can move by one step and
+    the differences compound over the 56 layers; 2e-2 bounds that drift of
+    the final hidden state."""
     import math
     from mamba2_recall import fp4, ridge_codec
     gen = torch.Generator(device=device).manual_seed(31)
@@ -244,3 +239,185 @@ def test_packed_projections(model, device):
         err = float((hp.float() - h16.float()).norm() / h16.float().norm())
         print(f"[controllers] packed vs FP16 one-token hidden rel L2 {err:.2e}", flush=True)
         assert bool(torch.isfinite(hp).all()) and err < 2e-2
+
+
+class _AdapterHooks:
+    """Hooks shaped like the Resurface adapter's (resurface_native.py:167-170,
+    186-231): a mixer forward pre-hook that takes the mixer input, a norm
+    forward pre-hook that replaces the norm's y with y + scale * [u, u] and
+    marks the input consumed, and an always-call mixer forward hook that
+    raises if the mixer returned without the norm hook having run."""
+
+    def __init__(self, model, scale):
+        self.scale = scale
+        self.calls = [0] * len(model.backbone.layers)
+        self.frames = {}
+        self.handles = []
+        for i, layer in enumerate(model.backbone.layers):
+            mx = layer.mixer
+            self.handles.append(mx.register_forward_pre_hook(self._input(i), with_kwargs=True))
+            self.handles.append(mx.norm.register_forward_pre_hook(self._norm(i), with_kwargs=True))
+            self.handles.append(mx.register_forward_hook(self._end(i), with_kwargs=True, always_call=True))
+
+    def _input(self, i):
+        def hook(module, args, kwargs):
+            u = args[0] if args else kwargs["u"]
+            assert i not in self.frames, "reentrant mixer call"
+            self.frames[i] = {"u": u, "consumed": False}
+        return hook
+
+    def _norm(self, i):
+        def hook(module, args, kwargs):
+            frame = self.frames.get(i)
+            if frame is None or frame["consumed"]:
+                raise RuntimeError("Norm hook has no unique corresponding mixer input")
+            y = args[0]
+            u = frame["u"].reshape(*y.shape[:-1], 4096)
+            frame["consumed"] = True
+            self.calls[i] += 1
+            return (y + self.scale * torch.cat((u, u), dim=-1), *args[1:]), kwargs
+        return hook
+
+    def _end(self, i):
+        def hook(module, args, kwargs, output):
+            frame = self.frames.pop(i, None)
+            if frame is not None and output is not None and not frame["consumed"]:
+                raise RuntimeError("Native mixer bypassed adapter injection")
+        return hook
+
+    def close(self):
+        for h in self.handles:
+            h.remove()
+
+
+def _ridge_statics(seed):
+    rng = np.random.default_rng(seed)
+    bases, scales, preds = [], [], []
+    for layout in LAYOUTS:
+        n8, n4, nz = cases.ridge_counts(layout)
+        s = cases.ridge_statics(rng, 8, n8, n4, nz)
+        bases.append(torch.from_numpy(s["basis"].view(np.float16)))
+        scales.append(torch.from_numpy(s["lscale"].view(np.float16)))
+        preds.append(torch.from_numpy(s["pred"].view(np.float16)))
+    return bases, scales, preds
+
+
+def _g16_packets(model, device, seed):
+    """Seeded G16 packets written into every projection (decoded weights), so
+    the packed GEMVs and the modules hold the same weights."""
+    import math
+    from mamba2_recall import fp4
+    gen = torch.Generator(device=device).manual_seed(seed)
+
+    def packet(w):
+        rows, cols = w.shape
+        packed = torch.randint(0, 256, (rows, cols // 2), generator=gen, device=device, dtype=torch.uint8)
+        s = torch.exp(torch.randn((rows, cols // 16), generator=gen, device=device) * 0.5) / math.sqrt(8.5625 * cols)
+        g = (s.max() / 448.0).float().reshape(1)
+        sb = (s / g).clamp(0, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+        fp4.decode_into(packed, sb, g, w.data, rows=rows, columns=cols, group=16)
+        return packed, sb, g
+
+    return [dict(in_proj=packet(layer.mixer.in_proj.weight), out_proj=packet(layer.mixer.out_proj.weight))
+            for layer in model.backbone.layers]
+
+
+def test_resurface_hooks_under_the_predictor_controller(model, device):
+    """The norm stays a module call under the controller: with the adapter's
+    three hook kinds registered, the norm pre-hook fires exactly once per
+    layer per backbone call (prefill, one-token steps, packed projections),
+    its change reaches the hidden states (a zero change leaves them bit for
+    bit), the end hook never reports a bypass, and a HIP graph captured with
+    the hooks replays the hooked step."""
+    from mamba2_recall import ridge_codec
+    perms = tables(device)
+    bases, scales, preds = _ridge_statics(15)
+    tok = ids(device, 2, 6, seed=41)
+    packets = _g16_packets(model, device, 43)
+    with ridge_codec.PredictorState(model, perms, LAYOUTS, bases, scales, preds) as pq:
+        pq.validate_each_step = False
+
+        def run(hooks_scale, packed=False):
+            hooks = _AdapterHooks(model, hooks_scale) if hooks_scale is not None else None
+            try:
+                pq.use_packed_projections(packets if packed else None)
+                hs = [pq.backbone(tok[:, :4], reset=True)]
+                hs += [pq.backbone(tok[:, t:t + 1]) for t in (4, 5)]
+                torch.cuda.synchronize()
+                return hs, (list(hooks.calls) if hooks else None)
+            finally:
+                pq.use_packed_projections(None)
+                if hooks:
+                    hooks.close()
+
+        print("[controllers] resurface hooks: plain, zero-change and active runs", flush=True)
+        plain, _ = run(None)
+        zero, calls0 = run(0.0)
+        active, calls = run(0.05)
+        assert calls0 == [3] * 56 and calls == [3] * 56
+        assert all(torch.equal(a, b) for a, b in zip(plain, zero))
+        assert all(not torch.equal(a, b) for a, b in zip(plain, active))
+        assert all(bool(torch.isfinite(h).all()) for h in active)
+        print("[controllers] resurface hooks with packed projections", flush=True)
+        packed_plain, _ = run(None, packed=True)
+        packed_active, pcalls = run(0.05, packed=True)
+        assert pcalls == [3] * 56
+        assert torch.equal(packed_active[0], active[0])   # prefill keeps the modules
+        assert all(not torch.equal(a, b) for a, b in zip(packed_plain[1:], packed_active[1:]))
+
+        print("[controllers] resurface hooks captured in a HIP graph", flush=True)
+        hooks = _AdapterHooks(model, 0.05)
+        try:
+            pq.backbone(tok[:, :4], reset=True)
+            snap = [(e.conv.clone(), {k: v.clone() for k, v in e.state.tensors.items()}) for e in pq._cache]
+            static = tok[:, 4:5].clone()
+            eager = pq.backbone(static).clone()
+
+            def restore():
+                for e, (conv, tensors) in zip(pq._cache, snap):
+                    e.conv.copy_(conv)
+                    for k, v in tensors.items():
+                        e.state.tensors[k].copy_(v)
+
+            restore()
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                pq.backbone(static)
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            restore()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                out = pq.backbone(static)
+            for _ in range(3):
+                restore()
+                graph.replay()
+                torch.cuda.synchronize()
+                assert torch.equal(out, eager)
+            assert hooks.calls == [4] * 56   # prefill, eager step, side-stream warm-up, capture
+            del graph
+        finally:
+            hooks.close()
+
+
+def test_packed_projection_outputs_per_layer(model, device):
+    """Each layer's packed FP4 GEMV projections against its FP16 modules on
+    the same inputs (the decoded weights are identical; only the summation
+    order differs): in_proj and out_proj outputs within 1e-3 relative L2, the
+    north-star bar for layer outputs, at batch 1 and 4."""
+    from mamba2_recall import fp4
+    packets = _g16_packets(model, device, 45)
+    gen = torch.Generator(device=device).manual_seed(46)
+    worst = 0.0
+    for batch in (1, 4):
+        for index in (0, 27, 55):
+            mx = model.backbone.layers[index].mixer
+            for name, width in (("in_proj", 4096), ("out_proj", 8192)):
+                u = torch.randn(batch, width, generator=gen, device=device).half()
+                want = getattr(mx, name)(u).float()
+                got = fp4.gemv_g16(*packets[index][name], u).float()
+                err = float((got - want).norm() / want.norm())
+                worst = max(worst, err)
+                assert err <= 1e-3, (batch, index, name, err)
+    print(f"[controllers] packed projections: worst rel L2 {worst:.2e}", flush=True)

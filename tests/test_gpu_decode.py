@@ -1,0 +1,181 @@
+"""greedy decode of a random-init Mamba-2 8B model (d_model
+4096, 56 layers, d_inner 8192, d_conv 4, vocab 256000) with the ridge-latent
+per-token requantize hook on every layer (published layouts, seeded statics),
+the one-token convolution as the HIP update, and the one-token projections as
+FP16 GEMMs or, separately, as packed-resident FP4 G16 GEMVs.
+
+Batch 1 runs 2048 one-token steps; batch 16 runs 512 (a quarter of the
+length keeps the test near a minute: 16 x 512 sequence-steps is four times
+the batch-1 count).  Each decode step (backbone, lm_head, argmax, token
+feedback) is replayed as one captured HIP graph; every 256 steps one step
+runs eagerly with the codec inputs of layers 0 and 55 captured, and the CPU
+oracle, given those inputs and the layer's packed state before the step, must
+produce the packed state after it bit for bit and the readout within 1e-3
+relative L2.  The first 32 greedy ids of the graph-replayed run equal those of
+an all-eager run from the same snapshot, and the cache stays finite.  The
+graph covers the backbone; lm_head, argmax and the token feedback run
+eagerly after each replay (see _next_ids).
+Reference logits are parity-unpinned here: the reference runtime needs
+mamba_ssm, which this image lacks (the model is a stand-in of the same
+geometry, tests/mamba2_model.py)."""
+import time
+
+import numpy as np
+import pytest
+import torch
+
+import cases
+from bench import PUBLISHED_LAYOUTS
+
+pytestmark = pytest.mark.gpu
+
+CHECK_LAYERS = (0, 55)
+CHECK_EVERY = 256
+EAGER_STEPS = 32
+
+
+def _statics(seed):
+    rng = np.random.default_rng(seed)
+    perms = torch.from_numpy(np.stack([rng.permutation(128) for _ in range(56 * 8)]).astype(np.uint8))
+    bases, scales, preds = [], [], []
+    for layout in PUBLISHED_LAYOUTS:
+        n8, n4, nz = cases.ridge_counts(layout)
+        s = cases.ridge_statics(rng, 8, n8, n4, nz)
+        bases.append(torch.from_numpy(s["basis"].view(np.float16)))
+        scales.append(torch.from_numpy(s["lscale"].view(np.float16)))
+        preds.append(torch.from_numpy(s["pred"].view(np.float16)))
+    return perms.reshape(56, 8, 128), bases, scales, preds
+
+
+class _CodecTap:
+    """Wraps a controller's codec call for the listed layers: records the
+    codec inputs, the packed state before the call and after it, and the
+    readout, as numpy arrays."""
+
+    def __init__(self, pq, layers):
+        self.pq, self.layers, self.records = pq, set(layers), {}
+        self.inner = pq._scan_layer
+        pq._scan_layer = self
+
+    def __call__(self, index, mx, x, dt, aa, bm, cm, entry):
+        if index not in self.layers:
+            return self.inner(index, mx, x, dt, aa, bm, cm, entry)
+        before = {k: v.clone() for k, v in entry.state.tensors.items()}
+        y, stats = self.inner(index, mx, x, dt, aa, bm, cm, entry)
+
+        def bits(t):
+            return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+        def raw(t):
+            u8 = t.contiguous().view(torch.uint8).cpu().numpy()
+            return u8.view(np.uint16).reshape(t.shape) if t.element_size() == 2 else u8.reshape(t.shape)
+
+        self.records[index] = dict(
+            x=bits(x), dt=bits(dt), A=aa.contiguous().cpu().numpy(), B=bits(bm), C=bits(cm), D=bits(mx.D),
+            dt_bias=bits(mx.dt_bias), before={k: raw(v) for k, v in before.items()},
+            after={k: raw(v) for k, v in entry.state.tensors.items()}, y=bits(y))
+        return y, stats
+
+    def close(self):
+        del self.pq._scan_layer
+
+
+def _check_against_oracle(oracle, pq, records, step):
+    for index, r in records.items():
+        n8, n4, nz = cases.ridge_counts(PUBLISHED_LAYOUTS[index])
+        state = {k: np.ascontiguousarray(v) for k, v in r["before"].items()}
+        y_ref = oracle.state_step(oracle.MODE_RIDGE, n8, n4, nz, r["x"], r["dt"], r["A"], r["B"], r["C"], r["D"],
+                                  r["dt_bias"], pq.permutations[index].cpu().numpy(),
+                                  pq.bases[index].view(torch.int16).cpu().numpy().view(np.uint16),
+                                  pq.latent_scales[index].view(torch.int16).cpu().numpy().view(np.uint16),
+                                  pq.predictors[index].view(torch.int16).cpu().numpy().view(np.uint16), state)
+        for k, want in state.items():
+            got = r["after"][k]
+            bad = int((got.reshape(-1) != want.reshape(-1)).sum())
+            assert bad == 0, f"step {step} layer {index}: {bad} mismatched {k} elements"
+        err = cases.rel_l2(cases.f16_to_f32(r["y"]), cases.f16_to_f32(y_ref))
+        assert err <= 1e-3, f"step {step} layer {index}: readout rel L2 {err:.2e}"
+
+
+def _next_ids(model, hidden):
+    """Greedy token of the last position: lm_head then argmax over the 256000
+    logits.  Always run eagerly: the argmax is a multi-workgroup torch
+    reduction that clears its semaphores with hipMemsetAsync, and memset
+    nodes in captured graphs are not reliable on replay, so the graphs below
+    capture the backbone only."""
+    return model.lm_head(hidden[:, -1:]).float().argmax(-1)
+
+
+def _decode(model, pq, oracle, batch, steps, device):
+    gen = torch.Generator(device=device).manual_seed(1000 + batch)
+    prompt = torch.randint(0, 256000, (batch, 8), generator=gen, device=device)
+    h = pq.backbone(prompt, reset=True)
+    start = _next_ids(model, h)
+    snap = [(e.conv.clone(), {k: v.clone() for k, v in e.state.tensors.items()}) for e in pq._cache]
+
+    def restore():
+        for e, (conv, tensors) in zip(pq._cache, snap):
+            e.conv.copy_(conv)
+            for k, v in tensors.items():
+                e.state.tensors[k].copy_(v)
+
+    # all-eager reference for the first steps
+    nxt, eager_ids = start.clone(), []
+    for _ in range(EAGER_STEPS):
+        nxt = _next_ids(model, pq.backbone(nxt))
+        eager_ids.append(nxt)
+    restore()
+    static_ids = start.clone()
+    static_hidden = torch.empty(batch, 1, 4096, dtype=torch.float16, device=device)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):   # capture warm-up; the snapshot is restored after it
+        static_hidden.copy_(pq.backbone(static_ids))
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    restore()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_hidden.copy_(pq.backbone(static_ids))
+    ids, checks = [], 0
+    t0 = time.perf_counter()
+    for step in range(steps):
+        if step % CHECK_EVERY == 0:
+            torch.cuda.synchronize()
+            print(f"[decode] batch={batch} step {step}/{steps} {time.perf_counter() - t0:.1f} s", flush=True)
+            tap = _CodecTap(pq, CHECK_LAYERS)
+            try:
+                static_hidden.copy_(pq.backbone(static_ids))
+            finally:
+                tap.close()
+            _check_against_oracle(oracle, pq, tap.records, step)
+            checks += 1
+        else:
+            graph.replay()
+        static_ids.copy_(_next_ids(model, static_hidden))
+        if step < EAGER_STEPS:
+            ids.append(static_ids.clone())
+    torch.cuda.synchronize()
+    del graph
+    assert all(torch.equal(a, b) for a, b in zip(eager_ids, ids)), "graph-replayed ids differ from the eager run"
+    assert pq.assert_finite_cache()
+    assert checks == steps // CHECK_EVERY
+    return static_ids
+
+
+@pytest.mark.parametrize("batch,steps,packed", [(1, 2048, False), (1, 2048, True), (16, 512, False),
+                                                (16, 512, True)])
+def test_greedy_decode_with_requantized_state(model, oracle, device, batch, steps, packed):
+    from mamba2_recall import ridge_codec
+    from test_gpu_controllers import _g16_packets
+    perms, bases, scales, preds = _statics(77)
+    packets = _g16_packets(model, device, 78) if packed else None
+    print(f"[decode] batch={batch} steps={steps} packed={packed}", flush=True)
+    t0 = time.perf_counter()
+    with torch.no_grad(), ridge_codec.PredictorState(model, perms, PUBLISHED_LAYOUTS, bases, scales, preds) as pq:
+        pq.validate_each_step = False
+        if packed:
+            pq.use_packed_projections(packets, verify=(batch == 1))
+        print(f"[decode] set-up {time.perf_counter() - t0:.1f} s", flush=True)
+        last = _decode(model, pq, oracle, batch, steps, device)
+        assert last.shape == (batch, 1) and bool(((last >= 0) & (last < 256000)).all())
