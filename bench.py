@@ -68,10 +68,11 @@ def step_bytes(batch, layouts):
 class RidgeStack:
     """56 layers of resident inputs, statics and packed states."""
 
-    def __init__(self, batch, device, seed=2026):
+    def __init__(self, batch, device, seed=2026, tokens=1):
         from mamba2_recall import _native, ridge_codec
         self.native = _native
         self.batch = batch
+        self.tokens = tokens
         self.device = device
         gen = torch.Generator(device=device).manual_seed(seed)
         f16 = torch.float16
@@ -80,12 +81,12 @@ class RidgeStack:
             n8, n4, nz = ridge_counts(layout)
             F = n8 + n4 + 2
             d = dict(layout=layout, n8=n8, n4=n4, nz=nz)
-            d["x"] = torch.randn((batch, 1, H, P), generator=gen, device=device).to(f16)
-            d["dt"] = torch.randn((batch, 1, H), generator=gen, device=device).to(f16)
+            d["x"] = torch.randn((batch, tokens, H, P), generator=gen, device=device).to(f16)
+            d["dt"] = torch.randn((batch, tokens, H), generator=gen, device=device).to(f16)
             u = torch.rand(H, generator=gen, device=device) * float(np.log(16.0))
             d["A"] = (-torch.exp(u)).float().contiguous()
-            d["B"] = torch.randn((batch, 1, G, NSTATE), generator=gen, device=device).to(f16)
-            d["C"] = torch.randn((batch, 1, G, NSTATE), generator=gen, device=device).to(f16)
+            d["B"] = torch.randn((batch, tokens, G, NSTATE), generator=gen, device=device).to(f16)
+            d["C"] = torch.randn((batch, tokens, G, NSTATE), generator=gen, device=device).to(f16)
             d["D"] = torch.randn(H, generator=gen, device=device).to(f16)
             d["dt_bias"] = torch.zeros(H, device=device, dtype=f16)
             d["perm"] = torch.stack([torch.randperm(NSTATE, generator=gen, device=device)
@@ -98,9 +99,10 @@ class RidgeStack:
             self.layers.append(d)
         # warm the carry from zero with 16 tokens per layer,
         # as 16 one-token steps (equal to one 16-token call; keeps every launch
-        # of the kernel a one-token launch, as in the timed region)
+        # of the kernel a one-token launch, as in the timed region); a
+        # multi-token stack starts from the carry of one pass over its tokens
         for d in self.layers:
-            for t in range(16):
+            for t in range(16 if tokens == 1 else 1):
                 ridge_codec.scan(d["x"], d["dt"], d["A"], d["B"], d["C"], d["D"], d["dt_bias"], d["state"],
                                  d["perm"], d["basis"], d["lscale"], d["pred"], layout=d["layout"], validate=(t == 0))
         torch.cuda.synchronize()
@@ -112,7 +114,7 @@ class RidgeStack:
             self.native.call("m2r_state_step_ridge", p(d["x"]), p(d["dt"]), p(d["A"]), p(d["B"]), p(d["C"]),
                              p(d["D"]), 0, p(d["dt_bias"]), 0, p(d["perm"]), p(d["basis"]), p(d["lscale"]),
                              p(d["pred"]), p(t["lo"]), p(t["hi"]), p(t["q4"]), p(t["latent"]), p(t["s8"]),
-                             p(t["s4"]), p(d["y"]), self.batch, 1, H, P, G, d["n8"], d["n4"], d["nz"],
+                             p(t["s4"]), p(d["y"]), self.batch, self.tokens, H, P, G, d["n8"], d["n4"], d["nz"],
                              stream_handle)
 
     def graph(self):
@@ -128,6 +130,29 @@ class RidgeStack:
             self.launch_all(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
         torch.cuda.synchronize()
         return g
+
+
+def prefill_timing(device, tokens=2048, steps=5, warmup=2):
+    """The reference's perplexity path runs each ~2047-token window through
+    every layer as one multi-token scan (scripts/run_fp4_ridge_resurface_v3.py:
+    102): the 56 published layers at batch 1, each one launch of the
+    runtime-L ridge instance over `tokens` tokens (the state stays in
+    registers and LDS across the tokens), as a graph of 56 launches.
+    Algorithmic bytes per layer: packed state in and out once, the statics,
+    and per token x, y, B, C and dt.  Returns ms per window, µs per token
+    (all 56 layers) and GB/s."""
+    stack = RidgeStack(1, device, seed=2028, tokens=tokens)
+    g = stack.graph()
+    ms, _ = time_graph(g, steps, warmup)
+    del g
+    per_token = 2 * 16384 + 2 * 2048 + 256
+    nbytes = sum(2 * 52 * 8192 + per_token * tokens + (step_bytes(1, (lay,)) - 889_088) for lay in PUBLISHED_LAYOUTS)
+    del stack
+    torch.cuda.empty_cache()
+    return dict(tokens=tokens, ms_per_window=round(ms, 3), us_per_token_56_layers=round(ms * 1e3 / tokens, 3),
+                gbs=round(nbytes / (ms * 1e-3) / 1e9, 1),
+                note="batch 1, published layouts, one launch per layer of the runtime-L ridge step over the "
+                     "whole window (HIP graph of 56 launches)")
 
 
 def layers_one_launch(stack, steps, warmup):
@@ -655,7 +680,7 @@ def cpu_baseline(budget_s=12.0, fp4_budget_s=3.0):
     # block scales + FP16 output
     fp4_bytes, fp4_s, rounds = 0, 0.0, 0
     while fp4_s < fp4_budget_s:
-        for rows, cols in ((18560, 4096), (4096, 8192)):
+        for rows, cols in ((4096, 4096), (1024, 8192)):   # row slices of one in_proj and one out_proj
             codes = rng.integers(0, 256, (rows, cols // 2), dtype=np.uint8)
             blocks = rng.integers(0x30, 0x48, (rows, cols // 16), dtype=np.uint8)
             t0 = time.perf_counter()
@@ -665,12 +690,75 @@ def cpu_baseline(budget_s=12.0, fp4_budget_s=3.0):
                 raise RuntimeError(f"CPU FP4 baseline: decode rejected a valid packet (bits {err})")
             fp4_bytes += rows * cols // 2 + rows * cols // 16 + 2 * rows * cols
         rounds += 1
+    torch_leg = torch_cpu_baseline(cores)
     return dict(value=round(done_bytes / elapsed / 1e9, 4), unit="GB/s", cores=cores, kind="port",
+                cpu_model=cpu_model(),
                 sample=f"C oracle (OpenMP over rows), {layers} published ridge layer steps in order at batch "
                        f"{batch}, 1 token each, {elapsed:.1f} s",
                 fp4_g16_decode=dict(value=round(fp4_bytes / fp4_s / 1e9, 3), unit="GB/s", cores=cores, kind="port",
                                     sample=f"C oracle, {rounds} x (in_proj [18560,4096] + out_proj [4096,8192]), "
-                                           f"{fp4_s:.1f} s"))
+                                           f"{fp4_s:.1f} s"),
+                pytorch_cpu=torch_leg)
+
+
+def cpu_model():
+    """The host CPU's model name (first processor in /proc/cpuinfo)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def torch_cpu_baseline(threads, budget_s=2.0):
+    """The PyTorch-CPU restatements (oracle/torch_cpu.py) with
+    torch.set_num_threads(threads): the FP4 G16 decode of the first 4096 rows
+    of an in_proj and the first 1024 rows of an out_proj per round
+    (algorithmic bytes: codes + block scales + FP16 output), and the packed-row dequantization of one published-layout layer
+    at batch 8 (52-byte rows in, 512 FP32 bytes out per row), each repeated
+    for about `budget_s` seconds."""
+    from oracle import torch_cpu
+    previous = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        gen = torch.Generator().manual_seed(5)
+        mats = []
+        for rows, cols in ((4096, 4096), (1024, 8192)):   # row slices of one in_proj and one out_proj
+            codes = torch.randint(0, 256, (rows, cols // 2), generator=gen, dtype=torch.uint8)
+            blocks = torch.randint(0x30, 0x48, (rows, cols // 16), generator=gen, dtype=torch.uint8)
+            mats.append((codes, blocks, rows * cols // 2 + rows * cols // 16 + 2 * rows * cols))
+        fp4_bytes, fp4_s, rounds = 0, 0.0, 0
+        while fp4_s < budget_s:
+            for codes, blocks, nbytes in mats:
+                t0 = time.perf_counter()
+                torch_cpu.fp4_g16_decode(codes, blocks, 1.0 / 448.0)
+                fp4_s += time.perf_counter() - t0
+                fp4_bytes += nbytes
+            rounds += 1
+        n8, n4, _ = ridge_counts("32_32_64")
+        rows = 8 * H * P
+        st = dict(lo=torch.randint(0, 256, (rows, n8 // 2), generator=gen, dtype=torch.uint8),
+                  hi=torch.randint(0, 256, (rows, n8 // 2), generator=gen, dtype=torch.uint8),
+                  q4=torch.randint(0, 256, (rows, n4 // 2), generator=gen, dtype=torch.uint8),
+                  s8=(torch.rand(rows, generator=gen) * 0.01).half().view(torch.int16),
+                  s4=(torch.rand(rows, generator=gen) * 0.1).half().view(torch.int16))
+        dec_bytes, dec_s, calls = 0, 0.0, 0
+        while dec_s < budget_s:
+            t0 = time.perf_counter()
+            torch_cpu.decode_rows(st["lo"], st["hi"], st["q4"], st["s8"], st["s4"], n8, n4)
+            dec_s += time.perf_counter() - t0
+            dec_bytes += rows * (52 + 512)
+            calls += 1
+    finally:
+        torch.set_num_threads(previous)
+    return dict(fp4_g16_decode=dict(value=round(fp4_bytes / fp4_s / 1e9, 3), unit="GB/s", cores=threads,
+                                    kind="port", sample=f"oracle/torch_cpu.py, {rounds} x (in_proj rows [4096,4096] + "
+                                                        f"out_proj rows [1024,8192]), {fp4_s:.1f} s"),
+                decode_state=dict(value=round(dec_bytes / dec_s / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                                  sample=f"oracle/torch_cpu.py packed-row dequantization, layout 32_32_64, batch 8 "
+                                         f"({rows} rows), {calls} calls, {dec_s:.1f} s"))
 
 
 def main():
@@ -681,7 +769,8 @@ def main():
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--skip-fp4", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=("step", "copy", "codecs", "e2e", "loader", "ceiling", "layers"), default=None)
+    ap.add_argument("--only", choices=("step", "copy", "codecs", "e2e", "loader", "ceiling", "layers", "prefill"),
+                    default=None)
     ap.add_argument("--skip-e2e", action="store_true", help="skip the end-to-end 8B decode (BASELINE config 5)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -704,6 +793,9 @@ def main():
                               bytes_written=a.numel(), launches=args.steps)))
         return
 
+    if args.only == "prefill":
+        print(json.dumps(dict(only="prefill", prefill_b1_2048=prefill_timing(device))))
+        return
     if args.only == "ceiling":
         print(json.dumps(dict(only="ceiling", ceiling=stream_ceiling(device))))
         return
@@ -765,6 +857,7 @@ def main():
                      fp4_g16_frac_of_copy=round(fp4_gbs / copy_gbs, 4),
                      fp4_g16_frac_of_mix_ceiling=round(fp4_gbs / fp4_ceiling, 4))
     extra["other_codecs_b64"] = other_codecs(device)
+    extra["prefill_b1_2048"] = prefill_timing(device)
     if not args.skip_e2e:
         extra["e2e_decode"] = e2e_decode(device, batches=(1, 16))
     line = dict(

@@ -941,3 +941,40 @@ def test_latent_update_is_fused(oracle):
     got, _ = _one_hot_latent_call(oracle, "32_32_64", np.float32([x]), np.uint8([[vb, 0]]), dt=_DT, A=_A,
                                   b=(bv, 0.0), c=(0.0, 0.0), ls=(float(ls), 1.0), d0=0, d1=1, L2=False)
     assert int(got[0, 0]) == int(byte_of(np.array([f]))[0]) != int(byte_of(np.array([s]))[0])
+
+
+# ------------------------------------------------- PyTorch-CPU restatements
+
+def test_torch_cpu_decode_rows_matches_reference_vectors():
+    """oracle/torch_cpu.decode_rows against the reference decode_state's own
+    outputs in packed lane order (sq3p25 16/64/48; arbitrary bytes, zero,
+    negative-zero, subnormal and negative scales), bit for bit."""
+    from pathlib import Path
+    from oracle import torch_cpu
+    g = np.load(Path(__file__).resolve().parent / "golden" / "decode_state_vectors.npz")
+    t = {k: torch.from_numpy(g[f"sq_{k}"]) for k in ("lo", "hi", "q4", "s8", "s4")}
+    out = torch_cpu.decode_rows(t["lo"], t["hi"], t["q4"], t["s8"].view(torch.int16), t["s4"].view(torch.int16), 16, 64)
+    assert np.array_equal(out.numpy().view(np.uint32), g["sq_decode"].view(np.uint32))
+
+
+def test_torch_cpu_fp4_decode_matches_c_oracle(oracle):
+    """oracle/torch_cpu.fp4_g16_decode against the C oracle's G16 decode: all
+    16 codes in every non-NaN block byte (signs included) and random rows,
+    under three global scales, bit for bit."""
+    from oracle import torch_cpu
+    rng = np.random.default_rng(9)
+    # every finite non-negative block byte; a zero block (0x00, 0x80) may
+    # only hold the zero codes 0 and 8 (fp4.py:247), which its row then repeats
+    blocks = np.array([b for b in range(256) if (b & 0x7F) != 0x7F and not (b & 0x80 and b != 0x80)], np.uint8)
+    rows = len(blocks)
+    codes = np.tile(np.arange(16, dtype=np.uint8), (rows, 1))          # one group per row, all codes
+    codes[(blocks & 0x7F) == 0] = np.tile(np.array([0, 8], np.uint8), 8)
+    packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
+    packed = np.concatenate([packed, rng.integers(0, 256, (rows, 56), dtype=np.uint16).astype(np.uint8)], axis=1)
+    nonzero = blocks[(blocks & 0x7F) != 0]
+    sb = np.stack([blocks] + [rng.choice(nonzero, rows) for _ in range(7)], axis=1).astype(np.uint8)
+    for g in (np.float32(1.0), np.float32(0.0123), np.float32(3.1e-5)):
+        want, err = oracle.fp4_decode(16, packed, sb, g, rows, 128)
+        assert err == 0
+        got = torch_cpu.fp4_g16_decode(torch.from_numpy(packed), torch.from_numpy(sb), float(g))
+        assert np.array_equal(got.numpy().view(np.uint16), want)
