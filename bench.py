@@ -205,7 +205,7 @@ def time_graph(g, steps, warmup):
 TRAFFIC_PROFILE = ROOT / "profiles" / "state_step_b64_pmc_traffic.txt"
 
 
-STEP_KERNEL_SOURCES = ("m2r_state.hip", "m2r_device.h", "m2r_tile.h")
+STEP_KERNEL_SOURCES = ("m2r_state.hip", "m2r_step.h", "m2r_device.h", "m2r_tile.h")
 
 
 def step_kernel_digest():

@@ -130,6 +130,7 @@ static int build_table(const m2r_ridge_layer* layers, int nlayers, int64_t batch
   if (batch * nlayers > 65535) return m2r_fail("layers step: batch x layers exceeds the grid limit 65535");
   if ((double)batch * H * P >= 2147483647.0) return m2r_fail("layers step: B*H*P must fit int32");
   if (P % 8) return m2r_fail("layers step: P must be a multiple of 8");
+  if (H % 2) return m2r_fail("layers step: H must be even");
   const int64_t hpg = H / G;
   const int64_t slots = batch * H * ((P + 63) / 64);
   if (hpg % 16 == 0 && slots >= 16LL * 512) { wpb = 4; hpw = 4; }
@@ -148,12 +149,15 @@ static int build_table(const m2r_ridge_layer* layers, int nlayers, int64_t batch
       if (!q || !aligned(q, 4)) return m2r_fail("layers step: B, C and lscale must be 4-byte aligned");
     if (!l.x || !l.dt || !l.A || !l.D || !l.dt_bias || !l.perm || !l.basis || !l.y)
       return m2r_fail("layers step: null pointer");
+    const void* a4s[] = {l.x, l.dt, l.A, l.D, l.dt_bias, l.perm, l.basis};
+    for (const void* q : a4s)
+      if (!aligned(q, 4)) return m2r_fail("layers step: x, dt, A, D, dt_bias, perm and basis must be 4-byte aligned");
     LayerEntry& e = table[(size_t)i];
     e = LayerEntry{};
     e.args = StepArgs{(const uint16_t*)l.x, (const uint16_t*)l.dt, l.A, (const uint16_t*)l.B, (const uint16_t*)l.C,
                       l.D, l.dt_bias, l.perm, (const uint16_t*)l.basis, (const uint16_t*)l.lscale,
                       (const uint16_t*)l.pred, l.lo, l.hi, l.q4, l.latent, (uint16_t*)l.s8, (uint16_t*)l.s4,
-                      (uint16_t*)l.y, (int)batch, 1, (int)H, (int)P, (int)G, l.d_is_f32, l.db_is_f32, 1};
+                      (uint16_t*)l.y, (int)batch, 1, (int)H, (int)P, (int)G, l.d_is_f32, l.db_is_f32, 3};
     e.layout = id;
   }
   return 0;

@@ -17,11 +17,15 @@ namespace m2r {
 // as waves_per_block * 16 + heads_per_wave.
 static std::atomic<int> g_forced_shape{0};
 
+// a.dma_tiles: bit 0 = 16-byte LDS transfers of the state rows; bit 1 = the
+// one-token inputs may be staged by dword transfers (the staged prologue of
+// the one-token instances with an even number of heads per workgroup).
 template <int N8, int N4, int NZ, int MODE, int WPB, int HPW>
 static void launch_shape(const StepArgs& a, dim3 grid, hipStream_t stream) {
-  if (a.dma_tiles && a.L == 1) {
+  constexpr bool staged = StepSmem<N8, N4, NZ, MODE, WPB, HPW, true, true>::STAGED;
+  if ((a.dma_tiles & 1) && a.L == 1 && (!staged || (a.dma_tiles & 2))) {
     hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, WPB, HPW, true, true>), grid, dim3(64 * WPB), 0, stream, a);
-  } else if (a.dma_tiles) {
+  } else if (a.dma_tiles & 1) {
     hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, WPB, HPW, true, false>), grid, dim3(64 * WPB), 0, stream, a);
   } else {
     hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, WPB, HPW, false, false>), grid, dim3(64 * WPB), 0, stream, a);
@@ -105,6 +109,16 @@ static int dma_tiles_ok(int64_t P, std::initializer_list<const void*> align16,
   return 1;
 }
 
+// Staged one-token inputs (bit 1 of StepArgs::dma_tiles): an even number of
+// heads (so that every workgroup's heads start on a dword) and dword-aligned
+// per-head, row and static arrays.
+static int staged_ok(int64_t H, std::initializer_list<const void*> align4) {
+  if (H % 2) return 0;
+  for (const void* f : align4)
+    if (f && ((uintptr_t)f & 3)) return 0;
+  return 2;
+}
+
 static int check_geometry(int64_t batch, int64_t L, int64_t H, int64_t P, int64_t G) {
   if (batch <= 0 || L <= 0 || H <= 0 || P <= 0 || G <= 0) return m2r_fail("state step: non-positive geometry");
   if (H % G) return m2r_fail("state step: heads must be divisible by groups");
@@ -124,7 +138,9 @@ extern "C" int m2r_state_step_ridge(const void* x, const void* dt, const float* 
   d.args = StepArgs{(const uint16_t*)x, (const uint16_t*)dt, A, (const uint16_t*)B, (const uint16_t*)C, D, dt_bias,
                     perm, (const uint16_t*)basis, (const uint16_t*)lscale, (const uint16_t*)pred, lo, hi, q4, latent,
                     (uint16_t*)s8, (uint16_t*)s4, (uint16_t*)y, (int)batch, (int)L, (int)H, (int)P, (int)G,
-                    d_is_f32, db_is_f32, dma_tiles_ok(P, {lo, hi, q4, latent, s8, s4, pred}, {B, C, lscale})};
+                    d_is_f32, db_is_f32,
+                    dma_tiles_ok(P, {lo, hi, q4, latent, s8, s4, pred}, {B, C, lscale}) |
+                        staged_ok(H, {x, dt, A, D, dt_bias, perm, basis})};
   d.n8_ = n8; d.n4_ = n4; d.nz_ = nz;
   hipError_t e = dispatch_ridge(d, stream);
   if (e == hipErrorInvalidValue) return m2r_fail("ridge step: unsupported tier layout");
@@ -141,7 +157,7 @@ extern "C" int m2r_state_step_tier(const void* x, const void* dt, const float* A
   d.args = StepArgs{(const uint16_t*)x, (const uint16_t*)dt, A, (const uint16_t*)B, (const uint16_t*)C, D, dt_bias,
                     perm, nullptr, nullptr, nullptr, lo, hi, q4, nullptr, (uint16_t*)s8, (uint16_t*)s4,
                     (uint16_t*)y, (int)batch, (int)L, (int)H, (int)P, (int)G, d_is_f32, db_is_f32,
-                    dma_tiles_ok(P, {lo, hi, q4, s8, s4}, {B, C})};
+                    dma_tiles_ok(P, {lo, hi, q4, s8, s4}, {B, C}) | staged_ok(H, {x, dt, A, D, dt_bias, perm})};
   d.n8_ = n8; d.n4_ = n4; d.nz_ = nz;
   hipError_t e = dispatch_tier(d, stream);
   if (e == hipErrorInvalidValue) return m2r_fail("tier step: unsupported tier layout");
@@ -169,6 +185,6 @@ extern "C" int m2r_state_step_legacy(const void* x, const void* dt, const float*
   StepArgs args{(const uint16_t*)x, (const uint16_t*)dt, A, (const uint16_t*)B, (const uint16_t*)C, D, dt_bias,
                 perm, nullptr, nullptr, nullptr, lo, hi, q4, nullptr, (uint16_t*)s8, (uint16_t*)s4,
                 (uint16_t*)y, (int)batch, (int)L, (int)H, (int)P, (int)G, d_is_f32, db_is_f32,
-                dma_tiles_ok(P, {lo, hi, q4, s8, s4}, {B, C})};
+                dma_tiles_ok(P, {lo, hi, q4, s8, s4}, {B, C}) | staged_ok(H, {x, dt, A, D, dt_bias, perm})};
   return m2r_check(launch_layout<16, 64, 48, MODE_LEGACY>(args, stream), "legacy step launch");
 }

@@ -54,9 +54,30 @@ struct StepArgs {
   uint16_t* y;             // f16 [B, L, H, P]
   int B, L, H, P, G;
   int d_f32, db_f32;
-  int dma_tiles;           // P % 8 == 0, 16-byte aligned state fields and predictor, 4-byte aligned
-                           // B and C: 16-byte LDS transfers and paired B/C loads
+  int dma_tiles;           // bit 0: P % 8 == 0, 16-byte aligned state fields and predictor, 4-byte
+                           // aligned B and C: 16-byte LDS transfers and paired B/C loads; bit 1: H
+                           // even and 4-byte aligned x, dt, A, D, dt_bias, perm (and basis): the
+                           // one-token instances may stage their inputs by dword transfers
 };
+
+// Loads every field of the arguments into scalar registers at once (one
+// wait) instead of on first use (a wait per field, in series).
+__device__ __forceinline__ void load_args(const StepArgs& a) {
+  asm volatile("" ::"s"(a.x), "s"(a.dt), "s"(a.A), "s"(a.Bm), "s"(a.Cm), "s"(a.D), "s"(a.dt_bias), "s"(a.perm),
+               "s"(a.basis), "s"(a.lscale), "s"(a.pred), "s"(a.lo), "s"(a.hi), "s"(a.q4), "s"(a.latent),
+               "s"(a.s8), "s"(a.s4), "s"(a.y), "s"(a.B), "s"(a.H), "s"(a.P), "s"(a.G), "s"(a.d_f32),
+               "s"(a.db_f32));
+}
+
+// Scalar load of the dword at a wave-uniform address (the inputs are never
+// written by the step kernels: constant address space).
+__device__ __forceinline__ uint32_t scalar_dword(const void* p) {
+  // both halves zero-extended (readfirstlane returns a signed int)
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)p);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uintptr_t)p >> 32));
+  const uintptr_t u = (uintptr_t)lo | ((uintptr_t)hi << 32);
+  return *(const __attribute__((address_space(4))) uint32_t*)u;
+}
 
 // Carried coordinates are held in an internal lane order that makes the
 // conversion between the nibble planes and code bytes two bitfield inserts
@@ -155,6 +176,17 @@ struct GroupToken {
   float tree[4];                  // e0.c, e1.c, e0.b, e1.b
 };
 
+// Token inputs of a one-token workgroup staged in LDS by direct transfers
+// (the staged prologue): the group's B and C rows (f16 pairs) and statics,
+// `stat`: [0, 32) the permutation bytes, [32, 32 + NZ) the dead-tier basis
+// (f16 pairs).
+struct TokenStage {
+  alignas(16) uint32_t b[64];
+  alignas(16) uint32_t c[64];
+  alignas(16) uint32_t stat[128];
+};
+struct NoStage {};
+
 // Inputs of one token that a wave loads one token ahead: its lane's two f16
 // of the group's B and of its C row, x of its rows in every head slot, and
 // for lanes < HPW the dt and dt_bias bits of head slot `lane`.  Nothing is
@@ -219,15 +251,19 @@ __device__ __forceinline__ float2 wave_dt_activation(const WaveRaw<HPW>& r, floa
 // raw indices are pv0 and pv1), B*dt, sum b.c, the readout weights and, for
 // the ridge codec, the correction of the readout weights by the static
 // predictor and the dead-tier dot products.  `first`: the first token, whose
-// ridge correction waits for the workgroup's predictor transfer.
-template <int N8, int N4, int NZ, int MODE, int WPB, int HPW>
+// ridge correction waits for the workgroup's predictor transfer.  STAGED:
+// x already sits in wt.x (transferred there by the staged prologue, which
+// also waited for the predictor).
+template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool STAGED = false>
 __device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, GroupToken<N8 + N4>& gt,
                                                  const WaveRaw<HPW>& r, float2 act, int pv0, int pv1,
                                                  const float (&e0v)[2], const float (&e1v)[2],
                                                  const uint16_t* s_pred, bool first, int lane, int wave) {
   constexpr int NL = N8 + N4, F = NL + 2, RZ = next_pow2(NZ);
+  if constexpr (!STAGED) {
 #pragma unroll
-  for (int k = 0; k < HPW; ++k) wt.x[k][lane] = r.xv[k];
+    for (int k = 0; k < HPW; ++k) wt.x[k][lane] = r.xv[k];
+  }
   const float dtv = act.x;
   // gather: raw element i of the B (C) row is half i & 1 of lane i >> 1's pair
   const int braw = (int)((uint32_t)r.bc[0] | ((uint32_t)r.bc[1] << 16));
@@ -265,7 +301,7 @@ __device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, Gro
     if (64 + lane < NL) wt.cw[64 + lane] = c1;
   } else {
     wave_sync();                 // the dead-tier c and b are read across lanes below
-    if (first) __syncthreads();  // every wave's share of the predictor transfer has landed
+    if (!STAGED && first) __syncthreads();  // every wave's share of the predictor transfer has landed
     if constexpr (WPB >= 4) {
       // Split across the workgroup: wave w computes the corrections of
       // internal outputs [w FW, (w + 1) FW), lanes l and l + 32 the two halves
@@ -561,6 +597,9 @@ template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE
 struct StepSmem {
   static constexpr int NL = N8 + N4, F = NL + 2, NH = WPB * HPW;
   static constexpr bool RIDGE = MODE == MODE_RIDGE, SPLIT = RIDGE && WPB >= 4;
+  // one-token instances with an even number of heads per workgroup stage
+  // their token inputs in LDS by direct transfers
+  static constexpr bool STAGED = DMA && ONE && NH % 2 == 0 && NH <= 16;
   // slot tile: lo, hi, q4, s8, s4 (and latent) fields of 64 rows, 16 bytes of slack
   static constexpr int TILE = 128 * (N8 / 2) + 64 * (N4 / 2) + 256 + (RIDGE ? 128 : 0) + 16;
   static constexpr int PRED_DW = RIDGE ? F * NZ / 2 : 1;
@@ -570,6 +609,7 @@ struct StepSmem {
   // token t + 1 while another still reads token t)
   alignas(16) GroupToken<NL> gt[SPLIT && !ONE ? 2 : 1];
   alignas(16) uint32_t pred32[PRED_WORDS];
+  alignas(16) std::conditional_t<STAGED, TokenStage, NoStage> stage;
   alignas(16) uint8_t tile[NH][TILE];
 };
 
@@ -692,55 +732,161 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a, StepSmem<N8, 
     if constexpr (RIDGE) wave_copy_out<2>(a.latent, t + O_LAT, row0, nvalid, lane);
   };
 
-  // ---- prologue: the wave's share of the predictor's LDS transfer, then the
-  // register loads of the first token and the statics (one wait covers both),
-  // then the LDS transfer of the wave's first slot, which lands while the
-  // token is built; each later slot is fetched while the previous computes --
-  // (order: the dt inputs, the predictor transfer, then the rest; the dt
-  // activation's wait for its inputs thus covers only the first two)
   WaveRaw<HPW> raw;
-  wave_load_dt<WPB, HPW>(a, raw, b * L, h0, lane, wave);
-  const int hl = h0 + min(lane, HPW - 1) * WPB + wave;   // head of slot `lane` (lanes < HPW)
-  const float Ah = a.A[hl];
-  if constexpr (RIDGE) {
-    const uint8_t* pg = (const uint8_t*)(a.pred + (size_t)g * F * NZ);
-    if constexpr (DMA) {   // 16-byte chunks; lanes past the end re-read the last one
-      for (int j = wave; j < PRED_OPS16; j += WPB)
-        lds_dma_b128(pg + 16 * min(j * 64 + lane, PRED_DW / 4 - 1), lds_address(s_pred32 + 256 * j));
-    } else {
-      for (int j = wave; j < PRED_OPS; j += WPB)
-        lds_dma_b32(pg + 4 * min(j * 64 + lane, PRED_DW - 1), lds_address(s_pred32 + 64 * j));
-    }
-  }
-  wave_load_rest<WPB, HPW, DMA>(a, raw, b * L, g, h0, pbase, lane, wave);
-  // statics, kept as loaded bits until the first token's full wait (a
-  // conversion here would make the compiler wait for them before the dt
-  // activation)
-  const uint32_t d_bits = a.d_f32 ? ((const uint32_t*)a.D)[hl] : (uint32_t)((const uint16_t*)a.D)[hl];
-  const uint32_t perm0 = a.perm[g * 128 + packed_lane<N8, N4>(lane)];
-  const uint32_t perm1 = a.perm[g * 128 + packed_lane<N8, N4>(64 + lane)];
+  float Ah;
+  uint32_t d_bits, perm0, perm1;
   uint32_t basis_w[2] = {0u, 0u};
   uint32_t ls_w = 0u;
-  if constexpr (RIDGE) {
+  float2 act;
+  if constexpr (Smem::STAGED) {
+    // ---- staged prologue (one token, LDS transfers): the vector inputs of
+    // the token and the statics travel by direct transfers into LDS together
+    // with the predictor and the wave's first slot, and the per-head scalars
+    // by scalar loads, so that no compiler-visible vector load is
+    // outstanding.  The dt activation runs while the transfers are in flight;
+    // the wave then waits once for everything but its slot transfers (which
+    // keep landing while the token is built), and the workgroup barrier
+    // publishes every wave's share.  Shared transfers (B row, C row,
+    // permutation and basis) are spread over the waves; each wave transfers x
+    // of its own head slots straight into its token record.
+    TokenStage& st = sm.stage;
+    const int bt = b;   // b * L with L == 1
+    load_args(a);
+    // the dwords holding the per-head scalars of the wave's head slots, all
+    // loads issued before the first wait (H is even: no dword of a per-head
+    // array reaches past its end)
+    uint32_t sdt[HPW], sdb[HPW], sA[HPW], sD[HPW];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int d0 = (RZ == 128) ? 2 * lane + j : lane;
-      basis_w[j] = ((const uint32_t*)a.basis)[g * NZ + min(d0, NZ - 1)];   // unused past NZ
+    for (int k = 0; k < HPW; ++k) {
+      const int h = h0 + k * WPB + wave, he = h & ~1;
+      sdt[k] = scalar_dword(a.dt + ((size_t)bt * H + he));
+      sdb[k] = scalar_dword(a.db_f32 ? (const void*)((const uint32_t*)a.dt_bias + h)
+                                     : (const void*)((const uint16_t*)a.dt_bias + he));
+      sA[k] = scalar_dword(a.A + h);
+      sD[k] = scalar_dword(a.d_f32 ? (const void*)((const uint32_t*)a.D + h) : (const void*)((const uint16_t*)a.D + he));
     }
-    ls_w = DMA ? *(const uint32_t*)(a.lscale + g * 2)
-               : (uint32_t)a.lscale[g * 2] | ((uint32_t)a.lscale[g * 2 + 1] << 16);
-  }
-  // dt activation of the first token while the other loads are in flight
-  float2 act = wave_dt_activation<HPW>(raw, Ah, a.db_f32);
-  // the predictor transfer and the register loads complete before any slot
-  // transfer is issued (the compiler's own waits for the register loads then
-  // never cover a slot transfer; no load may be scheduled past this wait)
-  __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-  __builtin_amdgcn_sched_barrier(0);
-  if constexpr (dma_tiles) slot_dma(wave);
-  else {
-    for (int k = 0; k < HPW; ++k) slot_copy_in(k * WPB + wave);
+    if constexpr (RIDGE) ls_w = scalar_dword(a.lscale + 2 * g);
+    constexpr int SHARED_OPS = RIDGE ? 4 : 3;
+    for (int j = wave; j < SHARED_OPS; j += WPB) {
+      const void* src;
+      uint32_t* dst;
+      if (j == 0) {
+        src = a.Bm + ((size_t)bt * a.G + g) * 128 + 2 * lane;
+        dst = st.b;
+      } else if (j == 1) {
+        src = a.Cm + ((size_t)bt * a.G + g) * 128 + 2 * lane;
+        dst = st.c;
+      } else if (j == 2) {   // permutation bytes, then the first 32 basis pairs
+        if (lane < 32 || !RIDGE) src = a.perm + (size_t)g * 128 + 4 * (lane & 31);
+        else src = (const uint32_t*)a.basis + (size_t)g * NZ + min(lane - 32, NZ - 1);
+        dst = st.stat;
+      } else {               // basis pairs 32 .. NZ - 1
+        src = (const uint32_t*)a.basis + (size_t)g * NZ + min(32 + lane, NZ - 1);
+        dst = st.stat + 64;
+      }
+      lds_dma_b32(src, lds_address(dst));
+    }
+    if constexpr (RIDGE) {   // the predictor: 16-byte chunks; lanes past the end re-read the last one
+      const uint8_t* pg = (const uint8_t*)(a.pred + (size_t)g * F * NZ);
+      for (int j = wave; j < PRED_OPS16; j += WPB)
+        lds_dma_b128(pg + 16 * min(j * 64 + lane, PRED_DW / 4 - 1), lds_address(s_pred32 + 256 * j));
+    }
+#pragma unroll
+    for (int j = 0; j < (HPW + 1) / 2; ++j) {   // x of head slots 2j (lanes < 32) and 2j + 1
+      const int k = 2 * j + (lane >> 5);
+      const int hk = h0 + min(k, HPW - 1) * WPB + wave;
+      const uint16_t* src = a.x + ((size_t)bt * H + hk) * P + pbase + 2 * min(lane & 31, nvalid / 2 - 1);
+      if (HPW % 2 == 0 || k < HPW) lds_dma_b32(src, lds_address(&wt.x[2 * j][0]));
+    }
+    slot_dma(wave);
+    // the binary16 halves, then head slot `lane`'s scalars (lanes < HPW; the
+    // others take the last slot's)
+#pragma unroll
+    for (int k = 0; k < HPW; ++k) {
+      const int odd = (h0 + k * WPB + wave) & 1;   // H even: the head's parity is its element's
+      sdt[k] = odd ? sdt[k] >> 16 : sdt[k] & 0xFFFFu;
+      if (!a.db_f32) sdb[k] = odd ? sdb[k] >> 16 : sdb[k] & 0xFFFFu;
+      if (!a.d_f32) sD[k] = odd ? sD[k] >> 16 : sD[k] & 0xFFFFu;
+    }
+    uint32_t vdt = sdt[HPW - 1], vdb = sdb[HPW - 1], vA = sA[HPW - 1], vD = sD[HPW - 1];
+#pragma unroll
+    for (int k = HPW - 2; k >= 0; --k) {
+      vdt = lane == k ? sdt[k] : vdt;
+      vdb = lane == k ? sdb[k] : vdb;
+      vA = lane == k ? sA[k] : vA;
+      vD = lane == k ? sD[k] : vD;
+    }
+    raw.dt = (uint16_t)vdt;
+    raw.db_lo = (uint16_t)vdb;
+    raw.db_hi = a.db_f32 ? (uint16_t)(vdb >> 16) : (uint16_t)vdb;
+    Ah = __builtin_bit_cast(float, vA);
+    d_bits = vD;
+    act = wave_dt_activation<HPW>(raw, Ah, a.db_f32);
+    wait_vmcnt<SLOT_DMA>();   // this wave's token, statics and predictor transfers have landed
+    __syncthreads();          // ... and every other wave's
+    const uint32_t bw = st.b[lane], cw = st.c[lane];
+    raw.bc[0] = (uint16_t)bw;
+    raw.bc[1] = (uint16_t)(bw >> 16);
+    raw.bc[2] = (uint16_t)cw;
+    raw.bc[3] = (uint16_t)(cw >> 16);
+    const uint8_t* p8 = (const uint8_t*)st.stat;
+    perm0 = p8[packed_lane<N8, N4>(lane)];
+    perm1 = p8[packed_lane<N8, N4>(64 + lane)];
+    if constexpr (RIDGE) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int d0 = (RZ == 128) ? 2 * lane + j : lane;
+        basis_w[j] = st.stat[32 + min(d0, NZ - 1)];   // unused past NZ
+      }
+    }
+  } else {
+    // ---- prologue: the wave's share of the predictor's LDS transfer, then the
+    // register loads of the first token and the statics (one wait covers both),
+    // then the LDS transfer of the wave's first slot, which lands while the
+    // token is built; each later slot is fetched while the previous computes --
+    // (order: the dt inputs, the predictor transfer, then the rest; the dt
+    // activation's wait for its inputs thus covers only the first two)
+    wave_load_dt<WPB, HPW>(a, raw, b * L, h0, lane, wave);
+    const int hl = h0 + min(lane, HPW - 1) * WPB + wave;   // head of slot `lane` (lanes < HPW)
+    Ah = a.A[hl];
+    if constexpr (RIDGE) {
+      const uint8_t* pg = (const uint8_t*)(a.pred + (size_t)g * F * NZ);
+      if constexpr (DMA) {   // 16-byte chunks; lanes past the end re-read the last one
+        for (int j = wave; j < PRED_OPS16; j += WPB)
+          lds_dma_b128(pg + 16 * min(j * 64 + lane, PRED_DW / 4 - 1), lds_address(s_pred32 + 256 * j));
+      } else {
+        for (int j = wave; j < PRED_OPS; j += WPB)
+          lds_dma_b32(pg + 4 * min(j * 64 + lane, PRED_DW - 1), lds_address(s_pred32 + 64 * j));
+      }
+    }
+    wave_load_rest<WPB, HPW, DMA>(a, raw, b * L, g, h0, pbase, lane, wave);
+    // statics, kept as loaded bits until the first token's full wait (a
+    // conversion here would make the compiler wait for them before the dt
+    // activation)
+    d_bits = a.d_f32 ? ((const uint32_t*)a.D)[hl] : (uint32_t)((const uint16_t*)a.D)[hl];
+    perm0 = a.perm[g * 128 + packed_lane<N8, N4>(lane)];
+    perm1 = a.perm[g * 128 + packed_lane<N8, N4>(64 + lane)];
+    if constexpr (RIDGE) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int d0 = (RZ == 128) ? 2 * lane + j : lane;
+        basis_w[j] = ((const uint32_t*)a.basis)[g * NZ + min(d0, NZ - 1)];   // unused past NZ
+      }
+      ls_w = DMA ? *(const uint32_t*)(a.lscale + g * 2)
+                 : (uint32_t)a.lscale[g * 2] | ((uint32_t)a.lscale[g * 2 + 1] << 16);
+    }
+    // dt activation of the first token while the other loads are in flight
+    act = wave_dt_activation<HPW>(raw, Ah, a.db_f32);
+    // the predictor transfer and the register loads complete before any slot
+    // transfer is issued (the compiler's own waits for the register loads then
+    // never cover a slot transfer; no load may be scheduled past this wait)
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (dma_tiles) slot_dma(wave);
+    else {
+      for (int k = 0; k < HPW; ++k) slot_copy_in(k * WPB + wave);
+    }
   }
   if (lane < HPW) wt.D[lane] = a.d_f32 ? __builtin_bit_cast(float, d_bits) : h2f((uint16_t)d_bits);
   const int pv0 = perm0 & 127, pv1 = perm1 & 127;   // raw B/C index of internal positions lane, lane + 64
@@ -768,7 +914,8 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a, StepSmem<N8, 
       wave_load_rest<WPB, HPW, DMA>(a, raw, bt + 1, g, h0, pbase, lane, wave);
     }
     GroupToken<NL>& gt = s_gt[SPLIT && !ONE ? (t & 1) : 0];
-    wave_token_build<N8, N4, NZ, MODE, WPB, HPW>(wt, gt, cur, act, pv0, pv1, e0v, e1v, s_pred, t == 0, lane, wave);
+    wave_token_build<N8, N4, NZ, MODE, WPB, HPW, Smem::STAGED>(wt, gt, cur, act, pv0, pv1, e0v, e1v, s_pred, t == 0,
+                                                              lane, wave);
     // readout weights and dead-tier dot products of this token
     const float* cwt = SPLIT ? gt.cw : wt.cw;
     const float dot1 = SPLIT ? gt.tree[0] + gt.cw[NL] : wt.dots[1];

@@ -27,6 +27,19 @@ def devp(a, device):
     return torch.from_numpy(np.ascontiguousarray(a)).to(device)
 
 
+def devp_shifted(a, device):
+    """devp(a) at an address one element past an allocation's start: f16
+    inputs then start on an odd multiple of 2 bytes."""
+    t = devp(a, device)
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=device)
+    buf[1:].copy_(t.reshape(-1))
+    return buf[1:].view(t.shape)
+
+
+def device_inputs(inp, device, shifted=()):
+    return {k: (devp_shifted if k in shifted else devp)(v, device) for k, v in inp.items() if k != "perm"}
+
+
 def to_state(np_state, state, device):
     for k, v in np_state.items():
         t = state.tensors[k]
@@ -84,7 +97,7 @@ NONFINITE_SCALES = [0x7C00, 0xFC00, 0x7E00, 0x7C00, 0xFE00, 0x7C00]
 
 
 def run_ridge(oracle, device, layout, batch, L, H, P, G, seed, *, random_state=True, d_f32=False, db_f32=False,
-              dt_bias_zero=True, x_scale=1.0, scale_mu=-4.0, special_scales=None):
+              dt_bias_zero=True, x_scale=1.0, scale_mu=-4.0, special_scales=None, shifted=()):
     from mamba2_recall import ridge_codec
     n8, n4, nz = ridge_counts(layout)
     rng = np.random.default_rng(seed)
@@ -102,7 +115,7 @@ def run_ridge(oracle, device, layout, batch, L, H, P, G, seed, *, random_state=T
                               ref_state)
     state = ridge_codec.allocate_state(batch, H, P, 128, device, layout=layout)
     to_state(st0, state, device)
-    t = {k: devp(v, device) for k, v in inp.items() if k != "perm"}
+    t = device_inputs(inp, device, shifted)
     perm = torch.from_numpy(inp["perm"]).to(device)
     basis, ls, pred = (dev16(sta[k], device) for k in ("basis", "lscale", "pred"))
     y, _ = ridge_codec.scan(t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["dt_bias"], state, perm, basis, ls,
@@ -115,7 +128,7 @@ def run_ridge(oracle, device, layout, batch, L, H, P, G, seed, *, random_state=T
 
 
 def run_tier(oracle, device, kind, layout, batch, L, H, P, G, seed, *, random_state=True, d_f32=False,
-             db_f32=False, dt_bias_zero=True, x_scale=1.0, scale_mu=-4.0, special_scales=None):
+             db_f32=False, dt_bias_zero=True, x_scale=1.0, scale_mu=-4.0, special_scales=None, shifted=()):
     from mamba2_recall import state_codec, tier_codec
     n8, n4, nz = tier_counts(layout)
     rng = np.random.default_rng(seed)
@@ -130,7 +143,7 @@ def run_tier(oracle, device, kind, layout, batch, L, H, P, G, seed, *, random_st
     mode = oracle.MODE_LEGACY if kind == "legacy" else oracle.MODE_STORED
     y_ref = oracle.state_step(mode, n8, n4, nz, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"],
                               inp["dt_bias"], inp["perm"], None, None, None, ref_state)
-    t = {k: devp(v, device) for k, v in inp.items() if k != "perm"}
+    t = device_inputs(inp, device, shifted)
     perm = torch.from_numpy(inp["perm"]).to(device)
     if kind == "legacy":
         state = state_codec.allocate_state(batch, H, P, 128, "sq3p25", device)
@@ -250,6 +263,35 @@ def test_ridge_every_workgroup_shape(oracle, device, forced_shape):
     run_ridge(oracle, device, "32_32_64", batch=2, L=3, H=32, P=80, G=2, seed=61)
     run_ridge(oracle, device, "8_80_40", batch=1, L=2, H=16, P=48, G=1, seed=62)
     run_ridge(oracle, device, "44_8_76", batch=3, L=1, H=16, P=64, G=1, seed=63, random_state=False)
+
+
+@pytest.mark.parametrize("forced_shape", SHAPES, indirect=True, ids=lambda s: f"w{s[0]}h{s[1]}")
+def test_one_token_staged_inputs_every_workgroup_shape(oracle, device, forced_shape):
+    """One-token steps, whose instances with an even number of heads per
+    workgroup stage x, dt, dt_bias, A, D, B, C and the statics in LDS by
+    dword transfers: f16 and f32 D and dt_bias (nonzero), ragged P (second
+    P block of 16 rows), one group and several, every packed format."""
+    run_ridge(oracle, device, "32_32_64", batch=2, L=1, H=32, P=80, G=2, seed=66, d_f32=True, db_f32=True,
+              dt_bias_zero=False)
+    run_ridge(oracle, device, "8_80_40", batch=3, L=1, H=16, P=64, G=1, seed=67, dt_bias_zero=False)
+    run_tier(oracle, device, "tier", "40_16_72", batch=2, L=1, H=32, P=80, G=2, seed=68, d_f32=True,
+             dt_bias_zero=False)
+    run_tier(oracle, device, "legacy", "16_64_48", batch=2, L=1, H=16, P=64, G=1, seed=69, db_f32=True,
+             dt_bias_zero=False)
+
+
+@pytest.mark.parametrize("kind", ["ridge", "tier"])
+def test_one_token_unaligned_inputs_take_the_register_prologue(oracle, device, kind):
+    """f16 inputs that start 2 bytes past a dword (views one element into
+    their allocations) cannot be staged by dword transfers: the one-token
+    step then loads them into registers, with the same results."""
+    shifted = ("x", "dt", "D", "dt_bias")
+    if kind == "ridge":
+        run_ridge(oracle, device, "24_48_56", batch=64, L=1, H=128, P=64, G=8, seed=70, dt_bias_zero=False,
+                  shifted=shifted)
+    else:
+        run_tier(oracle, device, "tier", "32_32_64", batch=64, L=1, H=128, P=64, G=8, seed=71,
+                 dt_bias_zero=False, shifted=shifted)
 
 
 @pytest.mark.parametrize("forced_shape", SHAPES, indirect=True, ids=lambda s: f"w{s[0]}h{s[1]}")
