@@ -767,6 +767,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--step-shape", default=None, metavar="WAVES,HEADS",
+                    help="with --only step: force the step kernel's workgroup shape (m2r_set_step_shape), "
+                         "for counter runs that compare shapes")
     ap.add_argument("--skip-fp4", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", choices=("step", "copy", "codecs", "e2e", "loader", "ceiling", "layers", "prefill"),
@@ -815,6 +818,11 @@ def main():
         print(json.dumps(dict(only="layers", batch=args.batch, ms_per_step=round(ms, 5))))
         return
     stack = RidgeStack(args.batch, device)
+    if args.step_shape:
+        if args.only != "step":
+            raise SystemExit("--step-shape applies to --only step")
+        from mamba2_recall import _native
+        _native.call("m2r_set_step_shape", *(int(v) for v in args.step_shape.split(",")))
     g = stack.graph()
     ms, wall_ms = time_graph(g, args.steps, args.warmup)
     nbytes = step_bytes(args.batch, PUBLISHED_LAYOUTS)
@@ -827,7 +835,8 @@ def main():
     del g, stack
     torch.cuda.empty_cache()
     if args.only == "step":
-        print(json.dumps(dict(only="step", batch=args.batch, ms_per_step=round(ms, 5), avg_launch_us=round(kern_us, 3))))
+        print(json.dumps(dict(only="step", batch=args.batch, step_shape=args.step_shape, ms_per_step=round(ms, 5),
+                              avg_launch_us=round(kern_us, 3))))
         return
 
     stack1 = RidgeStack(1, device, seed=2027)
