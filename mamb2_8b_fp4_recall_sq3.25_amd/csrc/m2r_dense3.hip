@@ -798,7 +798,7 @@ extern "C" int m2r_state_step_dense3(const void* x, const void* dt, const float*
     const long long slots = (long long)batch * H * pblocks;
     int wpb = 1, hpw = 1;
     const int forced = m2r_forced_step_shape();
-    if (forced && hpg % ((forced >> 4) * (forced & 15)) == 0 && (forced >> 4) != 8) {
+    if (forced && (forced & 15) && hpg % ((forced >> 4) * (forced & 15)) == 0 && (forced >> 4) != 8) {
       wpb = forced >> 4;
       hpw = forced & 15;
     } else if (hpg % 16 == 0 && slots >= 16LL * 512) {

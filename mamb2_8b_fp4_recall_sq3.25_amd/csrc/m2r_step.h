@@ -202,17 +202,19 @@ struct WaveRaw {
 // starts as soon as they land, while the other loads are still in flight.
 // Every load here is unconditional, with clamped indices (a conditional load
 // makes the compiler wait for it at the end of its branch).
-template <int WPB, int HPW>
+// PAIR: two waves per head (one per tier), a wave's only slot is head wave / 2.
+template <int WPB, int HPW, bool PAIR = false>
 __device__ __forceinline__ void wave_load_dt(const StepArgs& a, WaveRaw<HPW>& r, int bt, int h0, int lane,
                                              int wave) {
-  const int h = h0 + min(lane, HPW - 1) * WPB + wave;   // lanes >= HPW repeat the last slot
+  // lanes >= HPW repeat the last slot
+  const int h = h0 + (PAIR ? (wave >> 1) : min(lane, HPW - 1) * WPB + wave);
   const uint16_t* db = (const uint16_t*)a.dt_bias;
   r.dt = a.dt[(size_t)bt * a.H + h];
   r.db_lo = db[a.db_f32 ? 2 * h : h];
   r.db_hi = db[a.db_f32 ? 2 * h + 1 : h];
 }
 // ALIGNED: B and C are 4-byte aligned, so a lane's pair is one load each.
-template <int WPB, int HPW, bool ALIGNED>
+template <int WPB, int HPW, bool ALIGNED, bool PAIR = false>
 __device__ __forceinline__ void wave_load_rest(const StepArgs& a, WaveRaw<HPW>& r, int bt, int g, int h0,
                                                int pbase, int lane, int wave) {
   const size_t row = ((size_t)bt * a.G + g) * 128 + 2 * lane;
@@ -231,7 +233,7 @@ __device__ __forceinline__ void wave_load_rest(const StepArgs& a, WaveRaw<HPW>& 
   const int p = min(pbase + lane, a.P - 1);   // rows past P read row P-1 (never stored)
 #pragma unroll
   for (int k = 0; k < HPW; ++k) {
-    const int h = h0 + k * WPB + wave;
+    const int h = h0 + (PAIR ? (wave >> 1) : k * WPB + wave);
     r.xv[k] = a.x[((size_t)bt * a.H + h) * a.P + p];
   }
 }
@@ -593,9 +595,15 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
 // publishes the ridge predictor (staged once, shared by all waves).
 // LDS of one workgroup: the waves' token records, the shared ridge-correction
 // record(s), the staged predictor and the slot tiles.
-template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE>
+// PAIR: the small-batch layout, two waves per head slot (HPW == 1): the even
+// wave carries the INT8 tier, the odd wave the INT4 tier, the latent
+// coefficients and the readout, so that each slot's serial chain is about
+// half as long; `pacc` passes the INT8 tier's readout partial sums (one
+// buffer per token parity).
+template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE, bool PAIR = false>
 struct StepSmem {
-  static constexpr int NL = N8 + N4, F = NL + 2, NH = WPB * HPW;
+  static_assert(!PAIR || (HPW == 1 && WPB % 2 == 0), "two waves per head slot, one slot each");
+  static constexpr int NL = N8 + N4, F = NL + 2, NH = PAIR ? WPB / 2 : WPB * HPW;
   static constexpr bool RIDGE = MODE == MODE_RIDGE, SPLIT = RIDGE && WPB >= 4;
   // one-token instances with an even number of heads per workgroup stage
   // their token inputs in LDS by direct transfers
@@ -610,20 +618,22 @@ struct StepSmem {
   alignas(16) GroupToken<NL> gt[SPLIT && !ONE ? 2 : 1];
   alignas(16) uint32_t pred32[PRED_WORDS];
   alignas(16) std::conditional_t<STAGED, TokenStage, NoStage> stage;
+  alignas(16) float pacc[PAIR ? 2 : 1][PAIR ? NH : 1][PAIR ? 64 : 1];
   alignas(16) uint8_t tile[NH][TILE];
 };
 
 // The step of one workgroup: block coordinates (bx, by) and batch row b,
 // arguments `a`, LDS `sm`.  k_state_step runs it on its own grid; the
 // multi-layer kernel runs it with arguments read from a table of layers.
-template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE>
-__device__ __forceinline__ void state_step_body(const StepArgs& a, StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE>& sm,
-                                                int bx, int by, int b) {
+template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE, bool PAIR = false>
+__device__ __forceinline__ void state_step_body(const StepArgs& a,
+                                                StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, PAIR>& sm, int bx,
+                                                int by, int b) {
   constexpr int W8 = N8 / 2;          // bytes per row of lo and of hi
   constexpr int W4 = N4 / 2;          // bytes per row of q4
   constexpr int NL = N8 + N4;         // carried coordinates
   constexpr int F = NL + 2;           // ridge predictor features
-  constexpr int NH = WPB * HPW;
+  constexpr int NH = PAIR ? WPB / 2 : WPB * HPW;
   constexpr int RZ = next_pow2(NZ);
   constexpr bool RIDGE = MODE == MODE_RIDGE;
   constexpr int O_LO = 0, O_HI = 64 * W8, O_Q4 = 128 * W8, O_S8 = O_Q4 + 64 * W4, O_S4 = O_S8 + 128;
@@ -639,7 +649,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a, StepSmem<N8, 
   static_assert(!RIDGE || (F * NZ) % 2 == 0, "predictor staged as dwords");
   static_assert(TILE % 16 == 0, "tiles stay 16-byte aligned");
 
-  using Smem = StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE>;
+  using Smem = StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, PAIR>;
   static_assert(Smem::TILE == TILE && Smem::PRED_WORDS == (DMA ? PRED_OPS16 * 256 : PRED_OPS * 64), "LDS layout");
   constexpr bool SPLIT = Smem::SPLIT;
   auto& s_wt = sm.wt;
@@ -650,6 +660,10 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a, StepSmem<N8, 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: per-wave values in SGPRs
+  // PAIR: tier role of the wave (0: INT8 tier; 1: INT4 tier, latent, readout)
+  const int role = PAIR ? (wave & 1) : 0;
+  // workgroup-local head of the wave's slot k
+  auto head_slot = [&](int k) { return PAIR ? (wave >> 1) : k * WPB + wave; };
   const int h0 = by * NH;
   const int H = a.H, P = a.P;
   // ONE: the one-token (decode) instance, with a compile-time token count:
@@ -663,19 +677,28 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a, StepSmem<N8, 
   const uint16_t* s_pred = (const uint16_t*)s_pred32;
   WaveToken<N8, N4, HPW>& wt = s_wt[wave];
 
-  // vector memory operations per slot transfer (and per state copy-out)
-  constexpr int SLOT_DMA = 2 * chunk_ops(W8) + chunk_ops(W4) + chunk_ops(2) * (RIDGE ? 3 : 2);
+  // vector memory operations per slot transfer (and per state copy-out); in
+  // PAIR mode a wave transfers its tier's fields only: the INT8 wave lo, hi
+  // and s8 (OPS8), the INT4 wave q4, s4 and the latent bytes (OPS4)
+  constexpr int OPS8 = 2 * chunk_ops(W8) + chunk_ops(2);
+  constexpr int OPS4 = chunk_ops(W4) + chunk_ops(2) * (RIDGE ? 2 : 1);
+  constexpr int SLOT_DMA = OPS8 + OPS4;
   static_assert(SLOT_DMA <= 63, "a slot's transfers must fit the vmcnt range");
+  const bool own8 = !PAIR || role == 0, own4 = !PAIR || role == 1;   // the fields this wave moves
   auto slot_row0 = [&](int hh) { return (b * H + h0 + hh) * P + pbase; };
   auto slot_dma = [&](int hh) {   // direct global -> LDS transfers
     const int row0 = slot_row0(hh);
     uint8_t* t = s_tile[hh];
-    field_dma16<W8>(t + O_LO, a.lo, row0, nvalid, lane);
-    field_dma16<W8>(t + O_HI, a.hi, row0, nvalid, lane);
-    field_dma16<W4>(t + O_Q4, a.q4, row0, nvalid, lane);
-    field_dma16<2>(t + O_S8, (const uint8_t*)a.s8, row0, nvalid, lane);
-    field_dma16<2>(t + O_S4, (const uint8_t*)a.s4, row0, nvalid, lane);
-    if constexpr (RIDGE) field_dma16<2>(t + O_LAT, a.latent, row0, nvalid, lane);
+    if (own8) {
+      field_dma16<W8>(t + O_LO, a.lo, row0, nvalid, lane);
+      field_dma16<W8>(t + O_HI, a.hi, row0, nvalid, lane);
+    }
+    if (own4) field_dma16<W4>(t + O_Q4, a.q4, row0, nvalid, lane);
+    if (own8) field_dma16<2>(t + O_S8, (const uint8_t*)a.s8, row0, nvalid, lane);
+    if (own4) {
+      field_dma16<2>(t + O_S4, (const uint8_t*)a.s4, row0, nvalid, lane);
+      if constexpr (RIDGE) field_dma16<2>(t + O_LAT, a.latent, row0, nvalid, lane);
+    }
   };
   constexpr int COPY_OPS = SLOT_DMA;   // one store instruction per transfer chunk
   static_assert(SLOT_DMA + COPY_OPS + 1 <= 63, "vmcnt range");
@@ -697,17 +720,40 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a, StepSmem<N8, 
   auto slot_copy_in = [&](int hh) {   // other geometries: 16-bit transfers through VGPRs
     const int row0 = slot_row0(hh);
     uint8_t* t = s_tile[hh];
-    wave_copy_in<W8>(t + O_LO, a.lo, row0, nvalid, lane);
-    wave_copy_in<W8>(t + O_HI, a.hi, row0, nvalid, lane);
-    wave_copy_in<W4>(t + O_Q4, a.q4, row0, nvalid, lane);
-    wave_copy_in<2>(t + O_S8, (const uint8_t*)a.s8, row0, nvalid, lane);
-    wave_copy_in<2>(t + O_S4, (const uint8_t*)a.s4, row0, nvalid, lane);
-    if constexpr (RIDGE) wave_copy_in<2>(t + O_LAT, a.latent, row0, nvalid, lane);
+    if (own8) {
+      wave_copy_in<W8>(t + O_LO, a.lo, row0, nvalid, lane);
+      wave_copy_in<W8>(t + O_HI, a.hi, row0, nvalid, lane);
+      wave_copy_in<2>(t + O_S8, (const uint8_t*)a.s8, row0, nvalid, lane);
+    }
+    if (own4) {
+      wave_copy_in<W4>(t + O_Q4, a.q4, row0, nvalid, lane);
+      wave_copy_in<2>(t + O_S4, (const uint8_t*)a.s4, row0, nvalid, lane);
+      if constexpr (RIDGE) wave_copy_in<2>(t + O_LAT, a.latent, row0, nvalid, lane);
+    }
   };
   auto slot_copy_out = [&](int hh) {
     const int row0 = slot_row0(hh);
     const uint8_t* t = s_tile[hh];
-    if constexpr (dma_tiles) {   // every LDS read of the slot, then its stores
+    if constexpr (dma_tiles && PAIR) {   // this wave's fields: every LDS read, then the stores
+      constexpr int C8W = chunk_ops(W8), C4W = chunk_ops(W4), C2 = chunk_ops(2);
+      u32x4 v[OPS8 > OPS4 ? OPS8 : OPS4];
+      if (own8) {
+        field_read16<W8>(t + O_LO, lane, v);
+        field_read16<W8>(t + O_HI, lane, v + C8W);
+        field_read16<2>(t + O_S8, lane, v + 2 * C8W);
+        field_write16<W8>(a.lo, v, row0, nvalid, lane);
+        field_write16<W8>(a.hi, v + C8W, row0, nvalid, lane);
+        field_write16<2>((uint8_t*)a.s8, v + 2 * C8W, row0, nvalid, lane);
+      } else {
+        field_read16<W4>(t + O_Q4, lane, v);
+        field_read16<2>(t + O_S4, lane, v + C4W);
+        if constexpr (RIDGE) field_read16<2>(t + O_LAT, lane, v + C4W + C2);
+        field_write16<W4>(a.q4, v, row0, nvalid, lane);
+        field_write16<2>((uint8_t*)a.s4, v + C4W, row0, nvalid, lane);
+        if constexpr (RIDGE) field_write16<2>(a.latent, v + C4W + C2, row0, nvalid, lane);
+      }
+      return;
+    } else if constexpr (dma_tiles) {   // every LDS read of the slot, then its stores
       constexpr int C8W = chunk_ops(W8), C4W = chunk_ops(W4), C2 = chunk_ops(2);
       u32x4 v[SLOT_DMA];
       field_read16<W8>(t + O_LO, lane, v);
@@ -724,12 +770,16 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a, StepSmem<N8, 
       if constexpr (RIDGE) field_write16<2>(a.latent, v + 2 * C8W + C4W + 2 * C2, row0, nvalid, lane);
       return;
     }
-    wave_copy_out<W8>(a.lo, t + O_LO, row0, nvalid, lane);
-    wave_copy_out<W8>(a.hi, t + O_HI, row0, nvalid, lane);
-    wave_copy_out<W4>(a.q4, t + O_Q4, row0, nvalid, lane);
-    wave_copy_out<2>((uint8_t*)a.s8, t + O_S8, row0, nvalid, lane);
-    wave_copy_out<2>((uint8_t*)a.s4, t + O_S4, row0, nvalid, lane);
-    if constexpr (RIDGE) wave_copy_out<2>(a.latent, t + O_LAT, row0, nvalid, lane);
+    if (own8) {
+      wave_copy_out<W8>(a.lo, t + O_LO, row0, nvalid, lane);
+      wave_copy_out<W8>(a.hi, t + O_HI, row0, nvalid, lane);
+      wave_copy_out<2>((uint8_t*)a.s8, t + O_S8, row0, nvalid, lane);
+    }
+    if (own4) {
+      wave_copy_out<W4>(a.q4, t + O_Q4, row0, nvalid, lane);
+      wave_copy_out<2>((uint8_t*)a.s4, t + O_S4, row0, nvalid, lane);
+      if constexpr (RIDGE) wave_copy_out<2>(a.latent, t + O_LAT, row0, nvalid, lane);
+    }
   };
 
   WaveRaw<HPW> raw;
@@ -758,7 +808,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a, StepSmem<N8, 
     uint32_t sdt[HPW], sdb[HPW], sA[HPW], sD[HPW];
 #pragma unroll
     for (int k = 0; k < HPW; ++k) {
-      const int h = h0 + k * WPB + wave, he = h & ~1;
+      const int h = h0 + head_slot(k), he = h & ~1;
       sdt[k] = scalar_dword(a.dt + ((size_t)bt * H + he));
       sdb[k] = scalar_dword(a.db_f32 ? (const void*)((const uint32_t*)a.dt_bias + h)
                                      : (const void*)((const uint16_t*)a.dt_bias + he));
@@ -794,16 +844,16 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a, StepSmem<N8, 
 #pragma unroll
     for (int j = 0; j < (HPW + 1) / 2; ++j) {   // x of head slots 2j (lanes < 32) and 2j + 1
       const int k = 2 * j + (lane >> 5);
-      const int hk = h0 + min(k, HPW - 1) * WPB + wave;
+      const int hk = h0 + head_slot(min(k, HPW - 1));
       const uint16_t* src = a.x + ((size_t)bt * H + hk) * P + pbase + 2 * min(lane & 31, nvalid / 2 - 1);
       if (HPW % 2 == 0 || k < HPW) lds_dma_b32(src, lds_address(&wt.x[2 * j][0]));
     }
-    slot_dma(wave);
+    slot_dma(head_slot(0));
     // the binary16 halves, then head slot `lane`'s scalars (lanes < HPW; the
     // others take the last slot's)
 #pragma unroll
     for (int k = 0; k < HPW; ++k) {
-      const int odd = (h0 + k * WPB + wave) & 1;   // H even: the head's parity is its element's
+      const int odd = (h0 + head_slot(k)) & 1;   // H even: the head's parity is its element's
       sdt[k] = odd ? sdt[k] >> 16 : sdt[k] & 0xFFFFu;
       if (!a.db_f32) sdb[k] = odd ? sdb[k] >> 16 : sdb[k] & 0xFFFFu;
       if (!a.d_f32) sD[k] = odd ? sD[k] >> 16 : sD[k] & 0xFFFFu;
@@ -822,7 +872,10 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a, StepSmem<N8, 
     Ah = __builtin_bit_cast(float, vA);
     d_bits = vD;
     act = wave_dt_activation<HPW>(raw, Ah, a.db_f32);
-    wait_vmcnt<SLOT_DMA>();   // this wave's token, statics and predictor transfers have landed
+    // this wave's token, statics and predictor transfers have landed
+    if (!PAIR) wait_vmcnt<SLOT_DMA>();
+    else if (role == 0) wait_vmcnt<OPS8>();
+    else wait_vmcnt<OPS4>();
     __syncthreads();          // ... and every other wave's
     const uint32_t bw = st.b[lane], cw = st.c[lane];
     raw.bc[0] = (uint16_t)bw;
@@ -846,8 +899,8 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a, StepSmem<N8, 
     // token is built; each later slot is fetched while the previous computes --
     // (order: the dt inputs, the predictor transfer, then the rest; the dt
     // activation's wait for its inputs thus covers only the first two)
-    wave_load_dt<WPB, HPW>(a, raw, b * L, h0, lane, wave);
-    const int hl = h0 + min(lane, HPW - 1) * WPB + wave;   // head of slot `lane` (lanes < HPW)
+    wave_load_dt<WPB, HPW, PAIR>(a, raw, b * L, h0, lane, wave);
+    const int hl = h0 + head_slot(min(lane, HPW - 1));   // head of slot `lane` (lanes < HPW)
     Ah = a.A[hl];
     if constexpr (RIDGE) {
       const uint8_t* pg = (const uint8_t*)(a.pred + (size_t)g * F * NZ);
@@ -859,7 +912,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a, StepSmem<N8, 
           lds_dma_b32(pg + 4 * min(j * 64 + lane, PRED_DW - 1), lds_address(s_pred32 + 64 * j));
       }
     }
-    wave_load_rest<WPB, HPW, DMA>(a, raw, b * L, g, h0, pbase, lane, wave);
+    wave_load_rest<WPB, HPW, DMA, PAIR>(a, raw, b * L, g, h0, pbase, lane, wave);
     // statics, kept as loaded bits until the first token's full wait (a
     // conversion here would make the compiler wait for them before the dt
     // activation)
@@ -883,9 +936,9 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a, StepSmem<N8, 
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (dma_tiles) slot_dma(wave);
+    if constexpr (dma_tiles) slot_dma(head_slot(0));
     else {
-      for (int k = 0; k < HPW; ++k) slot_copy_in(k * WPB + wave);
+      for (int k = 0; k < HPW; ++k) slot_copy_in(head_slot(k));
     }
   }
   if (lane < HPW) wt.D[lane] = a.d_f32 ? __builtin_bit_cast(float, d_bits) : h2f((uint16_t)d_bits);
@@ -910,8 +963,8 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a, StepSmem<N8, 
     const int bt = b * L + t;
     const WaveRaw<HPW> cur = raw;
     if (t + 1 < L) {   // prefetch
-      wave_load_dt<WPB, HPW>(a, raw, bt + 1, h0, lane, wave);
-      wave_load_rest<WPB, HPW, DMA>(a, raw, bt + 1, g, h0, pbase, lane, wave);
+      wave_load_dt<WPB, HPW, PAIR>(a, raw, bt + 1, h0, lane, wave);
+      wave_load_rest<WPB, HPW, DMA, PAIR>(a, raw, bt + 1, g, h0, pbase, lane, wave);
     }
     GroupToken<NL>& gt = s_gt[SPLIT && !ONE ? (t & 1) : 0];
     wave_token_build<N8, N4, NZ, MODE, WPB, HPW, Smem::STAGED>(wt, gt, cur, act, pv0, pv1, e0v, e1v, s_pred, t == 0,
@@ -929,7 +982,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a, StepSmem<N8, 
       // work overlaps the other waves' vector work, instead of being hoisted
       // out of the token loop for all slots at once (more scalar registers
       // than exist: spills, and a long serial setup before the first token).
-      int hh = k * WPB + wave;
+      int hh = head_slot(k);
       asm volatile("" : "+s"(hh));
       const int h = h0 + hh;
       wave_priority_by_slots_left(HPW - k);
@@ -937,110 +990,206 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a, StepSmem<N8, 
       uint8_t* tile = s_tile[hh];
       uint16_t* t16 = (uint16_t*)tile;
 
-      // ---- unpack the slot: carried codes, internal lane order ------------------
-      // byte k of c8[i] is q8 + 128 of internal coordinate 4i+k, of c4[i] q4 + 8
-      uint32_t c8[C8], c4[C4];
-      {
-        uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4], wq[(W4 + 3) / 4];
-        lds_read_row<W8>(tile + O_LO, lane * W8, wl);
-        lds_read_row<W8>(tile + O_HI, lane * W8, wh);
-        planes_to_bytes8<N8>(wl, wh, c8);
-        lds_read_row<W4>(tile + O_Q4, lane * W4, wq);
-        plane_to_bytes4<N4>(wq, c4);
-      }
-      float sc8 = h2f(t16[O_S8 / 2 + lane]);
-      float sc4 = h2f(t16[O_S4 / 2 + lane]);
-      float z0 = 0.f, z1 = 0.f;
-      if constexpr (RIDGE) {
-        const uint32_t lat = t16[O_LAT / 2 + lane];
-        z0 = e4m3_byte_to_f32<0>(lat) * ls0;
-        z1 = e4m3_byte_to_f32<1>(lat) * ls1;
-      }
-      if (!valid) {   // rows past P: finite placeholders, never stored
+      if constexpr (PAIR) {
+        // ---- one tier per wave (PAIR): the even wave updates and requantizes
+        // the INT8 tier, the odd wave the INT4 tier and the latent
+        // coefficients, then reads out the row with the INT8 wave's partial
+        // sum (published through LDS behind the workgroup barrier) -----------
+        const float x = h2f(wt.x[0][lane]);
+        const float decay = wt.decay[0];
+        const float dtv = wt.dtv[0];
+        const bool base_ok = wt.bounded[0] != 0 && __builtin_fabsf(x) <= 65504.f;
+        const f32x4* bdt4 = (const f32x4*)wt.bdt[0];
+        const f32x4* cw4 = (const f32x4*)cwt;
+        float(&pacc)[64] = sm.pacc[t & 1][hh];
+        float acc = 0.f, z0 = 0.f, z1 = 0.f;
+        if (role == 0) {
+          uint32_t c8[C8];
+          {
+            uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4];
+            lds_read_row<W8>(tile + O_LO, lane * W8, wl);
+            lds_read_row<W8>(tile + O_HI, lane * W8, wh);
+            planes_to_bytes8<N8>(wl, wh, c8);
+          }
+          float sc8 = h2f(t16[O_S8 / 2 + lane]);
+          if (!valid) {   // rows past P: finite placeholders, never stored
 #pragma unroll
-        for (int i = 0; i < C8; ++i) c8[i] = 0x80808080u;
+            for (int i = 0; i < C8; ++i) c8[i] = 0x80808080u;
+            sc8 = 0.f;
+          }
+          const bool fin8 = __builtin_fabsf(sc8) <= 65504.f;
+          if (__builtin_amdgcn_ballot_w64(!fin8) == 0)
+            sc8 = tier_step<N8, true, MODE, false>(c8, sc8, decay, x, bdt4, cw4, acc, base_ok);
+          else
+            sc8 = tier_step<N8, true, MODE, true>(c8, sc8, decay, x, bdt4, cw4, acc, base_ok && fin8);
+          pacc[lane] = acc;
+          if (valid) {
+            uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4];
+            bytes_to_planes8<N8>(c8, wl, wh);
+            lds_write_row<W8>(tile + O_LO, lane * W8, wl);
+            lds_write_row<W8>(tile + O_HI, lane * W8, wh);
+            t16[O_S8 / 2 + lane] = f2h(sc8);
+          }
+        } else {
+          uint32_t c4[C4];
+          {
+            uint32_t wq[(W4 + 3) / 4];
+            lds_read_row<W4>(tile + O_Q4, lane * W4, wq);
+            plane_to_bytes4<N4>(wq, c4);
+          }
+          float sc4 = h2f(t16[O_S4 / 2 + lane]);
+          if constexpr (RIDGE) {
+            const uint32_t lat = t16[O_LAT / 2 + lane];
+            z0 = e4m3_byte_to_f32<0>(lat) * ls0;
+            z1 = e4m3_byte_to_f32<1>(lat) * ls1;
+          }
+          if (!valid) {
 #pragma unroll
-        for (int i = 0; i < C4; ++i) c4[i] = 0x08080808u;
-        sc8 = sc4 = z0 = z1 = 0.f;
-      }
-      const float x = h2f(wt.x[k][lane]);
-      const float decay = wt.decay[k];
-      const float dtv = wt.dtv[k];
-      const bool base_ok = wt.bounded[k] != 0 && __builtin_fabsf(x) <= 65504.f;
-
-      // ---- per tier: update, readout accumulation, requantization ---------------
-      // (each tier is requantized before the next is updated, so only one
-      // tier's updated values are live at a time)
-      const f32x4* bdt4 = (const f32x4*)wt.bdt[k];
-      const f32x4* cw4 = (const f32x4*)cwt;
-      float acc = 0.f;
-      const bool fin8 = __builtin_fabsf(sc8) <= 65504.f, fin4 = __builtin_fabsf(sc4) <= 65504.f;
-      const bool ok8 = base_ok && fin8;
-      const bool ok4 = base_ok && fin4;
-      // one wave-uniform choice per slot between two copies of the tier code:
-      // the fused dequantization when every scale of the wave is finite, the
-      // exact products otherwise (non-finite scales are rare: the reference's
-      // controllers reject such states)
-      auto tiers = [&](auto exact) {
-        constexpr bool EX = decltype(exact)::value;
-        sc8 = tier_step<N8, true, MODE, EX>(c8, sc8, decay, x, bdt4, cw4, acc, ok8);
-        __builtin_amdgcn_sched_barrier(0);
-        // the next slot's transfers and the previous slot's copy-out are
-        // issued between the tiers, where the other waves' arithmetic covers
-        // their issue time
-        if (dma_tiles && t == 0 && k + 1 < HPW) slot_dma(hh + WPB);
-        sc4 = tier_step<N4, false, MODE, EX>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc, ok4);
-        __builtin_amdgcn_sched_barrier(0);
-        if (t == L - 1 && k > 0) slot_copy_out(hh - WPB);   // the previous slot's state
-        __builtin_amdgcn_sched_barrier(0);
-      };
-      if (__builtin_amdgcn_ballot_w64(!(fin8 && fin4)) == 0) tiers(std::false_type{});
-      else tiers(std::true_type{});
-      // readout: sum_i u_i c_i + corrections = decay * (sum_i prior_i (c_i +
-      // corr_i) + latent terms) + x * (dt * sum_all b c + D)
-      float out;
-      uint32_t qz = 0;
-      if constexpr (RIDGE) {
-        out = decay * (acc + z0 * dot1 + z1 * dot2) + x * (dtv * wt.dots[0] + wt.D[k]);
-        // latent step (bit-exact): z <- fma(z, decay, (x * dt) * (e . b_dead)), requantized
-        const float xdt = x * dtv;
-        const float zn0 = state_update(z0, decay, xdt * dot3);
-        const float zn1 = state_update(z1, decay, xdt * dot4);
-        const float q0 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn0, ls0, rls0), -448.f), 448.f);
-        const float q1 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn1, ls1, rls1), -448.f), 448.f);
-        qz = f32x2_to_e4m3(q0, q1);   // q0, q1 are clamped, never NaN (maxNum drops a NaN)
+            for (int i = 0; i < C4; ++i) c4[i] = 0x08080808u;
+            sc4 = z0 = z1 = 0.f;
+          }
+          const bool fin4 = __builtin_fabsf(sc4) <= 65504.f;
+          if (__builtin_amdgcn_ballot_w64(!fin4) == 0)
+            sc4 = tier_step<N4, false, MODE, false>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc, base_ok);
+          else
+            sc4 = tier_step<N4, false, MODE, true>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc,
+                                                   base_ok && fin4);
+          uint32_t qz = 0;
+          if constexpr (RIDGE) {   // latent step (bit-exact), as in the one-wave slot below
+            const float xdt = x * dtv;
+            const float zn0 = state_update(z0, decay, xdt * dot3);
+            const float zn1 = state_update(z1, decay, xdt * dot4);
+            const float q0 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn0, ls0, rls0), -448.f), 448.f);
+            const float q1 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn1, ls1, rls1), -448.f), 448.f);
+            qz = f32x2_to_e4m3(q0, q1);
+          }
+          if (valid) {
+            uint32_t wq[(W4 + 3) / 4];
+            bytes_to_plane4<N4>(c4, wq);
+            lds_write_row<W4>(tile + O_Q4, lane * W4, wq);
+            t16[O_S4 / 2 + lane] = f2h(sc4);
+            if constexpr (RIDGE) t16[O_LAT / 2 + lane] = (uint16_t)qz;
+          }
+        }
+        __syncthreads();   // the INT8 waves' partial readouts are published
+        if (role == 1) {
+          const float acc8 = pacc[lane];
+          float out;
+          if constexpr (RIDGE) out = decay * ((acc8 + acc) + z0 * dot1 + z1 * dot2) + x * (dtv * wt.dots[0] + wt.D[0]);
+          else out = decay * (acc8 + acc) + x * (dtv * wt.dots[0] + wt.D[0]);
+          const __amdgpu_buffer_rsrc_t ry = raw_buffer(a.y + ((size_t)bt * H + h) * P + pbase, 2 * nvalid);
+          __builtin_amdgcn_raw_buffer_store_b16(f2h(out), ry, 2 * lane, 0, STORE_THROUGH);
+        }
       } else {
-        out = decay * acc + x * (dtv * wt.dots[0] + wt.D[k]);
-      }
-      {   // one unguarded store instruction: the range check drops rows past P
-        const __amdgpu_buffer_rsrc_t ry = raw_buffer(a.y + ((size_t)bt * H + h) * P + pbase, 2 * nvalid);
-        __builtin_amdgcn_raw_buffer_store_b16(f2h(out), ry, 2 * lane, 0, STORE_THROUGH);
-      }
 
-      // ---- repack the slot row into the tile ---------------------------------------
-      if (valid) {
-        uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4], wq[(W4 + 3) / 4];
-        bytes_to_planes8<N8>(c8, wl, wh);
-        lds_write_row<W8>(tile + O_LO, lane * W8, wl);
-        lds_write_row<W8>(tile + O_HI, lane * W8, wh);
-        bytes_to_plane4<N4>(c4, wq);
-        lds_write_row<W4>(tile + O_Q4, lane * W4, wq);
-        t16[O_S8 / 2 + lane] = f2h(sc8);
-        t16[O_S4 / 2 + lane] = f2h(sc4);
-        if constexpr (RIDGE) t16[O_LAT / 2 + lane] = (uint16_t)qz;
+        // ---- unpack the slot: carried codes, internal lane order ------------------
+        // byte k of c8[i] is q8 + 128 of internal coordinate 4i+k, of c4[i] q4 + 8
+        uint32_t c8[C8], c4[C4];
+        {
+          uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4], wq[(W4 + 3) / 4];
+          lds_read_row<W8>(tile + O_LO, lane * W8, wl);
+          lds_read_row<W8>(tile + O_HI, lane * W8, wh);
+          planes_to_bytes8<N8>(wl, wh, c8);
+          lds_read_row<W4>(tile + O_Q4, lane * W4, wq);
+          plane_to_bytes4<N4>(wq, c4);
+        }
+        float sc8 = h2f(t16[O_S8 / 2 + lane]);
+        float sc4 = h2f(t16[O_S4 / 2 + lane]);
+        float z0 = 0.f, z1 = 0.f;
+        if constexpr (RIDGE) {
+          const uint32_t lat = t16[O_LAT / 2 + lane];
+          z0 = e4m3_byte_to_f32<0>(lat) * ls0;
+          z1 = e4m3_byte_to_f32<1>(lat) * ls1;
+        }
+        if (!valid) {   // rows past P: finite placeholders, never stored
+  #pragma unroll
+          for (int i = 0; i < C8; ++i) c8[i] = 0x80808080u;
+  #pragma unroll
+          for (int i = 0; i < C4; ++i) c4[i] = 0x08080808u;
+          sc8 = sc4 = z0 = z1 = 0.f;
+        }
+        const float x = h2f(wt.x[k][lane]);
+        const float decay = wt.decay[k];
+        const float dtv = wt.dtv[k];
+        const bool base_ok = wt.bounded[k] != 0 && __builtin_fabsf(x) <= 65504.f;
+
+        // ---- per tier: update, readout accumulation, requantization ---------------
+        // (each tier is requantized before the next is updated, so only one
+        // tier's updated values are live at a time)
+        const f32x4* bdt4 = (const f32x4*)wt.bdt[k];
+        const f32x4* cw4 = (const f32x4*)cwt;
+        // the readout's partial sums per tier, added after both (the same order
+        // as the two-wave slot, whose tiers run on different waves)
+        float acc8 = 0.f, acc4 = 0.f;
+        const bool fin8 = __builtin_fabsf(sc8) <= 65504.f, fin4 = __builtin_fabsf(sc4) <= 65504.f;
+        const bool ok8 = base_ok && fin8;
+        const bool ok4 = base_ok && fin4;
+        // one wave-uniform choice per slot between two copies of the tier code:
+        // the fused dequantization when every scale of the wave is finite, the
+        // exact products otherwise (non-finite scales are rare: the reference's
+        // controllers reject such states)
+        auto tiers = [&](auto exact) {
+          constexpr bool EX = decltype(exact)::value;
+          sc8 = tier_step<N8, true, MODE, EX>(c8, sc8, decay, x, bdt4, cw4, acc8, ok8);
+          __builtin_amdgcn_sched_barrier(0);
+          // the next slot's transfers and the previous slot's copy-out are
+          // issued between the tiers, where the other waves' arithmetic covers
+          // their issue time
+          if (dma_tiles && t == 0 && k + 1 < HPW) slot_dma(hh + WPB);
+          sc4 = tier_step<N4, false, MODE, EX>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc4, ok4);
+          __builtin_amdgcn_sched_barrier(0);
+          if (t == L - 1 && k > 0) slot_copy_out(hh - WPB);   // the previous slot's state
+          __builtin_amdgcn_sched_barrier(0);
+        };
+        if (__builtin_amdgcn_ballot_w64(!(fin8 && fin4)) == 0) tiers(std::false_type{});
+        else tiers(std::true_type{});
+        const float acc = acc8 + acc4;
+        // readout: sum_i u_i c_i + corrections = decay * (sum_i prior_i (c_i +
+        // corr_i) + latent terms) + x * (dt * sum_all b c + D)
+        float out;
+        uint32_t qz = 0;
+        if constexpr (RIDGE) {
+          out = decay * (acc + z0 * dot1 + z1 * dot2) + x * (dtv * wt.dots[0] + wt.D[k]);
+          // latent step (bit-exact): z <- fma(z, decay, (x * dt) * (e . b_dead)), requantized
+          const float xdt = x * dtv;
+          const float zn0 = state_update(z0, decay, xdt * dot3);
+          const float zn1 = state_update(z1, decay, xdt * dot4);
+          const float q0 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn0, ls0, rls0), -448.f), 448.f);
+          const float q1 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn1, ls1, rls1), -448.f), 448.f);
+          qz = f32x2_to_e4m3(q0, q1);   // q0, q1 are clamped, never NaN (maxNum drops a NaN)
+        } else {
+          out = decay * acc + x * (dtv * wt.dots[0] + wt.D[k]);
+        }
+        {   // one unguarded store instruction: the range check drops rows past P
+          const __amdgpu_buffer_rsrc_t ry = raw_buffer(a.y + ((size_t)bt * H + h) * P + pbase, 2 * nvalid);
+          __builtin_amdgcn_raw_buffer_store_b16(f2h(out), ry, 2 * lane, 0, STORE_THROUGH);
+        }
+
+        // ---- repack the slot row into the tile ---------------------------------------
+        if (valid) {
+          uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4], wq[(W4 + 3) / 4];
+          bytes_to_planes8<N8>(c8, wl, wh);
+          lds_write_row<W8>(tile + O_LO, lane * W8, wl);
+          lds_write_row<W8>(tile + O_HI, lane * W8, wh);
+          bytes_to_plane4<N4>(c4, wq);
+          lds_write_row<W4>(tile + O_Q4, lane * W4, wq);
+          t16[O_S8 / 2 + lane] = f2h(sc8);
+          t16[O_S4 / 2 + lane] = f2h(sc4);
+          if constexpr (RIDGE) t16[O_LAT / 2 + lane] = (uint16_t)qz;
+        }
       }
       wave_sync();
     }
-    if (t == L - 1) slot_copy_out((HPW - 1) * WPB + wave);
+    if (t == L - 1) slot_copy_out(head_slot(HPW - 1));
     if (t + 1 < L) act = wave_dt_activation<HPW>(raw, Ah, a.db_f32);
   }
 }
 
-template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE>
-__global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(WPB == 8 ? 4 : 2, 8)))
+template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE, bool PAIR = false>
+__global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(WPB == 8 && !PAIR ? 4 : 2, 8)))
 void k_state_step(StepArgs a) {
-  __shared__ StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE> sm;
-  state_step_body<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE>(a, sm, blockIdx.x, blockIdx.y, blockIdx.z);
+  __shared__ StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, PAIR> sm;
+  state_step_body<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, PAIR>(a, sm, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 }  // namespace m2r
