@@ -11,11 +11,12 @@ bandwidth, a live roofline for the dominant kernel, and the CPU oracle
 timed on a bounded sample (state step and FP4 decode) as a baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-fp4] [--skip-cpu] [--skip-e2e]
-       python bench.py --only step|copy|codecs|layers|ceiling|e2e|loader
+       python bench.py --only step|copy|codecs|layers|ceiling|e2e|loader|prefill|fp4
        (profiling runs: only the step graph at --batch, only a 256 MiB copy
        used to calibrate counters, only the other codecs' batch-64 graphs,
        only the one-launch multi-layer step at --batch, only the HBM
-       ceilings, only the end-to-end decode, only the checkpoint loader)
+       ceilings, only the end-to-end decode, only the checkpoint loader,
+       only the batch-1 prefill, only the FP4 full decode)
 """
 from __future__ import annotations
 
@@ -772,7 +773,7 @@ def main():
                          "for counter runs that compare shapes")
     ap.add_argument("--skip-fp4", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=("step", "copy", "codecs", "e2e", "loader", "ceiling", "layers", "prefill"),
+    ap.add_argument("--only", choices=("step", "copy", "codecs", "e2e", "loader", "ceiling", "layers", "prefill", "fp4"),
                     default=None)
     ap.add_argument("--skip-e2e", action="store_true", help="skip the end-to-end 8B decode (BASELINE config 5)")
     args = ap.parse_args()
@@ -807,6 +808,10 @@ def main():
         return
     if args.only == "e2e":
         print(json.dumps(dict(only="e2e", e2e_decode=e2e_decode(device))))
+        return
+    if args.only == "fp4":   # the FP4 G16 full 8B decode alone (profiling runs)
+        fp4_ms, fp4_gbs = fp4_full_decode(device, steps=args.steps)
+        print(json.dumps(dict(only="fp4", fp4_g16_full_decode_ms=round(fp4_ms, 3), fp4_g16_full_decode_gbs=round(fp4_gbs, 1))))
         return
     if args.only == "codecs":
         print(json.dumps(dict(only="codecs", other_codecs_b64=other_codecs(device, steps=args.steps))))

@@ -113,6 +113,42 @@ __global__ __launch_bounds__(256) void k_fp4_g16(const uint32_t* __restrict__ co
   report(err, flag);
 }
 
+// G16 over whole blocks of 1024 units, wide loads: thread t of workgroup w
+// decodes the four consecutive units 4(256 w + t) .. +3 from one 16-byte code
+// load and one 2-byte load of their two block scales, stages the four 16-byte
+// results in LDS and stores them transposed, so that every store instruction
+// of a wave is again a contiguous 1 KiB (four units per lane stored directly
+// would leave each instruction a 16-byte stripe every 64 bytes: partial-line
+// writes, several times slower).  Needs 16-byte aligned codes and 2-byte
+// aligned scales; the same values and error bits as k_fp4_g16.
+__global__ __launch_bounds__(256) void k_fp4_g16_wide(const u32x4* __restrict__ codes,
+                                                      const uint16_t* __restrict__ scales,
+                                                      const float* __restrict__ global_scale,
+                                                      u32x4* __restrict__ out, uint32_t* flag) {
+  __shared__ u32x4 stage[1024];
+  const float gl = *global_scale;
+  uint32_t err = (gl > 0.f && gl < __builtin_inff()) ? 0u : FP4_ERR_GLOBAL;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const u32x4 c4 = __builtin_nontemporal_load(codes + t);
+  const uint32_t s2 = scales[t];   // block scales of units 4t, 4t+1 (low byte) and 4t+2, 4t+3
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t cw = c4[k], s = (s2 >> (8 * (k >> 1))) & 0xFFu;
+    const uint32_t mag = s & 0x7Fu;
+    err |= (mag == 0x7Fu) ? FP4_ERR_SCALE_NONFINITE : 0u;
+    err |= ((s & 0x80u) && mag != 0u) ? FP4_ERR_SCALE_NEGATIVE : 0u;
+    err |= (mag == 0u && (cw & 0x77777777u) != 0u) ? FP4_ERR_ZERO_SCALE_CODE : 0u;
+    const float hb = e4m3_byte_to_f32<0>(mag) * 0.5f;
+    stage[4 * threadIdx.x + k] = decode8<true>(cw, hb, gl, s >> 7, err);
+  }
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * 1024;
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    __builtin_nontemporal_store(stage[k * 256 + threadIdx.x], out + base + k * 256 + threadIdx.x);
+  report(err, flag);
+}
+
 // G64, cols % 64 == 0: unit u uses the FP16 scale u/8; one rounding.
 template <int UPT>
 __global__ __launch_bounds__(256) void k_fp4_g64(const uint32_t* __restrict__ codes,
@@ -228,18 +264,31 @@ extern "C" int m2r_fp4_decode_g16(const uint8_t* packed, const uint8_t* e4m3_sca
     const int64_t n_units = rows * cols / 8;
     const int forced = g_fp4_upt.load(std::memory_order_relaxed);
     const int upt = forced ? forced : 4;
-    // automatic: four units per thread, one pass (no grid cap), non-temporal
-    // stores: the fastest of 1/2/4/8 units x caps 2048/4096/16384/none x
-    // store policies on the full 8B weight set
+    // per-unit kernel: four units per thread, one pass (no grid cap),
+    // non-temporal stores: the fastest of 1/2/4/8 units x caps
+    // 2048/4096/16384/none x store policies on the full 8B weight set
     const int64_t cap = forced ? g_fp4_cap.load(std::memory_order_relaxed) : 0;
     const bool nt = forced ? g_fp4_nt.load(std::memory_order_relaxed) != 0 : true;
-    const dim3 grid(grid_for(n_units, upt, cap));
     const uint32_t* codes = (const uint32_t*)packed;
     u32x4* out = (u32x4*)out_f16;
-    if (upt == 1) launch_g16<1>(nt, grid, stream, codes, e4m3_scales, global_scale, out, n_units, err_flag);
-    else if (upt == 2) launch_g16<2>(nt, grid, stream, codes, e4m3_scales, global_scale, out, n_units, err_flag);
-    else if (upt == 8) launch_g16<8>(nt, grid, stream, codes, e4m3_scales, global_scale, out, n_units, err_flag);
-    else launch_g16<4>(nt, grid, stream, codes, e4m3_scales, global_scale, out, n_units, err_flag);
+    // automatic: whole blocks of 1024 units with the wide-load kernel, the
+    // rest (fewer than 1024 units) with the per-unit kernel
+    const int64_t n_wide = forced || ((uintptr_t)packed & 15) || ((uintptr_t)e4m3_scales & 1) ? 0 : n_units / 1024 * 1024;
+    if (n_wide > 0) {
+      if (n_wide / 1024 > 0x7FFFFFFF) return m2r_fail("fp4 g16: matrix too large");
+      hipLaunchKernelGGL(k_fp4_g16_wide, dim3((unsigned)(n_wide / 1024)), dim3(256), 0, stream, (const u32x4*)packed,
+                         (const uint16_t*)e4m3_scales, global_scale, out, err_flag);
+      if (n_wide == n_units) return m2r_check(hipGetLastError(), "fp4 g16 launch");
+      codes += n_wide;
+      e4m3_scales += n_wide / 2;
+      out += n_wide;
+    }
+    const int64_t n_rest = n_units - n_wide;
+    const dim3 grid(grid_for(n_rest, upt, cap));
+    if (upt == 1) launch_g16<1>(nt, grid, stream, codes, e4m3_scales, global_scale, out, n_rest, err_flag);
+    else if (upt == 2) launch_g16<2>(nt, grid, stream, codes, e4m3_scales, global_scale, out, n_rest, err_flag);
+    else if (upt == 8) launch_g16<8>(nt, grid, stream, codes, e4m3_scales, global_scale, out, n_rest, err_flag);
+    else launch_g16<4>(nt, grid, stream, codes, e4m3_scales, global_scale, out, n_rest, err_flag);
   } else {
     int64_t groups = (cols + 15) / 16;
     int64_t n = rows * groups;
