@@ -149,6 +149,34 @@ __global__ __launch_bounds__(256) void k_fp4_g16_wide(const u32x4* __restrict__ 
   report(err, flag);
 }
 
+// G64 over whole blocks of 1024 units, the layout of k_fp4_g16_wide: the four
+// units of a thread share one FP16 scale (64 weights = 8 units); 16-byte
+// aligned codes, 2-byte aligned scales.
+__global__ __launch_bounds__(256) void k_fp4_g64_wide(const u32x4* __restrict__ codes,
+                                                      const uint16_t* __restrict__ scales, u32x4* __restrict__ out,
+                                                      uint32_t* flag) {
+  __shared__ u32x4 stage[1024];
+  uint32_t err = 0u;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const u32x4 c4 = __builtin_nontemporal_load(codes + t);
+  const uint32_t s = scales[t >> 1];
+  const uint32_t mag = s & 0x7FFFu;
+  err |= (mag >= 0x7C00u) ? FP4_ERR_SCALE_NONFINITE : 0u;
+  err |= ((s & 0x8000u) && mag != 0u) ? FP4_ERR_SCALE_NEGATIVE : 0u;
+  const float hb = h2f((uint16_t)mag) * 0.5f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    err |= (mag == 0u && (c4[k] & 0x77777777u) != 0u) ? FP4_ERR_ZERO_SCALE_CODE : 0u;
+    stage[4 * threadIdx.x + k] = decode8<false>(c4[k], hb, 1.0f, s >> 15, err);
+  }
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * 1024;
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    __builtin_nontemporal_store(stage[k * 256 + threadIdx.x], out + base + k * 256 + threadIdx.x);
+  report(err, flag);
+}
+
 // G64, cols % 64 == 0: unit u uses the FP16 scale u/8; one rounding.
 template <int UPT>
 __global__ __launch_bounds__(256) void k_fp4_g64(const uint32_t* __restrict__ codes,
@@ -302,11 +330,27 @@ extern "C" int m2r_fp4_decode_g64(const uint8_t* packed, const void* f16_scales,
                                   int64_t cols, uint32_t* err_flag, hipStream_t stream) {
   if (rows <= 0 || cols <= 0) return m2r_fail("fp4 g64: non-positive shape");
   if (cols % 64 == 0) {
-    int64_t n_units = rows * cols / 8;
+    const int64_t n_units = rows * cols / 8;
     constexpr int UPT = 4;
-    const int64_t cap = g_fp4_upt.load(std::memory_order_relaxed) ? g_fp4_cap.load(std::memory_order_relaxed) : 0;
-    hipLaunchKernelGGL((k_fp4_g64<UPT>), dim3(grid_for(n_units, UPT, cap)), dim3(256), 0, stream,
-                       (const uint32_t*)packed, (const uint16_t*)f16_scales, (u32x4*)out_f16, n_units, err_flag);
+    const bool forced = g_fp4_upt.load(std::memory_order_relaxed) != 0;
+    const int64_t cap = forced ? g_fp4_cap.load(std::memory_order_relaxed) : 0;
+    const uint32_t* codes = (const uint32_t*)packed;
+    const uint16_t* sc = (const uint16_t*)f16_scales;
+    u32x4* out = (u32x4*)out_f16;
+    // automatic: whole blocks of 1024 units with the wide-load kernel, the rest per unit
+    const int64_t n_wide = forced || ((uintptr_t)packed & 15) || ((uintptr_t)f16_scales & 1) ? 0 : n_units / 1024 * 1024;
+    if (n_wide > 0) {
+      if (n_wide / 1024 > 0x7FFFFFFF) return m2r_fail("fp4 g64: matrix too large");
+      hipLaunchKernelGGL(k_fp4_g64_wide, dim3((unsigned)(n_wide / 1024)), dim3(256), 0, stream, (const u32x4*)packed,
+                         sc, out, err_flag);
+      if (n_wide == n_units) return m2r_check(hipGetLastError(), "fp4 g64 launch");
+      codes += n_wide;
+      sc += n_wide / 8;
+      out += n_wide;
+    }
+    const int64_t n_rest = n_units - n_wide;
+    hipLaunchKernelGGL((k_fp4_g64<UPT>), dim3(grid_for(n_rest, UPT, cap)), dim3(256), 0, stream, codes, sc, out, n_rest,
+                       err_flag);
   } else {
     int64_t groups = (cols + 63) / 64;
     int64_t n = rows * groups;

@@ -39,7 +39,8 @@ def decode_dev(packed, scales_u8, g, rows, cols, device, group=16):
     return fp4.decode_packet(packet)
 
 
-@pytest.mark.parametrize("rows,cols", [(512, 4096), (37, 8192), (3, 48), (5, 40)])
+# (33, 4112): 16 whole blocks of 1024 units for the wide-load kernel and 578 units for the per-unit one
+@pytest.mark.parametrize("rows,cols", [(512, 4096), (37, 8192), (33, 4112), (3, 48), (5, 40)])
 def test_g16_random_bit_exact(oracle, device, rows, cols):
     rng = np.random.default_rng(rows * 7 + cols)
     packed, sb, g = g16_packet(rng, rows, cols, device)
@@ -157,7 +158,8 @@ def test_g64_grid_stride_sweeps(oracle, device):
     _assert_equal_in_chunks(decode_dev(packed, sc, None, rows, cols, device, group=64), want)
 
 
-@pytest.mark.parametrize("rows,cols", [(64, 4096), (7, 192), (3, 100)])
+# (19, 8256): 19 whole blocks of 1024 units for the wide-load kernel and 152 units for the per-unit one
+@pytest.mark.parametrize("rows,cols", [(64, 4096), (19, 8256), (7, 192), (3, 100)])
 def test_g64_random_bit_exact(oracle, device, rows, cols):
     rng = np.random.default_rng(rows + cols)
     groups = (cols + 63) // 64
