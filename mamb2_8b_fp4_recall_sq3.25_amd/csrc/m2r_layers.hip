@@ -158,6 +158,7 @@ static int build_table(const m2r_ridge_layer* layers, int nlayers, int64_t batch
                       l.D, l.dt_bias, l.perm, (const uint16_t*)l.basis, (const uint16_t*)l.lscale,
                       (const uint16_t*)l.pred, l.lo, l.hi, l.q4, l.latent, (uint16_t*)l.s8, (uint16_t*)l.s4,
                       (uint16_t*)l.y, (int)batch, 1, (int)H, (int)P, (int)G, l.d_is_f32, l.db_is_f32, 3};
+    e.args.rhpg = 1.0f / (float)hpg;
     e.layout = id;
   }
   return 0;

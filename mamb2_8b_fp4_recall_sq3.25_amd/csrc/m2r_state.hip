@@ -38,7 +38,9 @@ static void launch_shape(const StepArgs& a, dim3 grid, hipStream_t stream) {
 }
 
 template <int N8, int N4, int NZ, int MODE>
-static hipError_t launch_layout(const StepArgs& a, hipStream_t stream) {
+static hipError_t launch_layout(const StepArgs& args, hipStream_t stream) {
+  StepArgs a = args;
+  a.rhpg = 1.0f / (float)(a.H / a.G);
   const int pblocks = (a.P + 63) / 64;
   const int hpg = a.H / a.G;
   const long long slots = (long long)a.B * a.H * pblocks;

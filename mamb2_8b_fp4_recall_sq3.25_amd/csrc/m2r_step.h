@@ -58,6 +58,7 @@ struct StepArgs {
                            // aligned B and C: 16-byte LDS transfers and paired B/C loads; bit 1: H
                            // even and 4-byte aligned x, dt, A, D, dt_bias, perm (and basis): the
                            // one-token instances may stage their inputs by dword transfers
+  float rhpg;              // 1 / (H / G) rounded to binary32: group of head h = (int)((h + 0.5) * rhpg)
 };
 
 // Loads every field of the arguments into scalar registers at once (one
@@ -66,7 +67,16 @@ __device__ __forceinline__ void load_args(const StepArgs& a) {
   asm volatile("" ::"s"(a.x), "s"(a.dt), "s"(a.A), "s"(a.Bm), "s"(a.Cm), "s"(a.D), "s"(a.dt_bias), "s"(a.perm),
                "s"(a.basis), "s"(a.lscale), "s"(a.pred), "s"(a.lo), "s"(a.hi), "s"(a.q4), "s"(a.latent),
                "s"(a.s8), "s"(a.s4), "s"(a.y), "s"(a.B), "s"(a.H), "s"(a.P), "s"(a.G), "s"(a.d_f32),
-               "s"(a.db_f32));
+               "s"(a.db_f32), "s"(a.rhpg));
+  // nothing is scheduled above this point, so no field is loaded later
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Group of head h (wave-uniform): floor(h / hpg) as (int)((h + 0.5) * rhpg).
+// Exact for H < 2^22: the float product is within G * 2^-23 of
+// (h + 0.5) / hpg, whose distance to the integers is at least 0.5 / hpg.
+__device__ __forceinline__ int group_of_head(int h, float rhpg) {
+  return __builtin_amdgcn_readfirstlane((int)(((float)h + 0.5f) * rhpg));
 }
 
 // Scalar load of the dword at a wave-uniform address (the inputs are never
@@ -77,6 +87,21 @@ __device__ __forceinline__ uint32_t scalar_dword(const void* p) {
   const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uintptr_t)p >> 32));
   const uintptr_t u = (uintptr_t)lo | ((uintptr_t)hi << 32);
   return *(const __attribute__((address_space(4))) uint32_t*)u;
+}
+// N consecutive dwords at a wave-uniform, dword-aligned address: one scalar load.
+template <int N>
+__device__ __forceinline__ void scalar_dwords(const void* p, uint32_t* out) {
+  if constexpr (N == 1) {
+    out[0] = scalar_dword(p);
+  } else {
+    typedef uint32_t vec __attribute__((ext_vector_type(N), aligned(4)));
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)p);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uintptr_t)p >> 32));
+    const uintptr_t u = (uintptr_t)lo | ((uintptr_t)hi << 32);
+    const vec v = *(const __attribute__((address_space(4))) vec*)u;
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = v[i];
+  }
 }
 
 // Carried coordinates are held in an internal lane order that makes the
@@ -202,12 +227,14 @@ struct WaveRaw {
 // starts as soon as they land, while the other loads are still in flight.
 // Every load here is unconditional, with clamped indices (a conditional load
 // makes the compiler wait for it at the end of its branch).
-// PAIR: two waves per head (one per tier), a wave's only slot is head wave / 2.
+// A wave's head slots are HPW consecutive heads (slot k of wave w is
+// workgroup head w * HPW + k); PAIR: two waves per head (one per tier), a
+// wave's only slot is head wave / 2.
 template <int WPB, int HPW, bool PAIR = false>
 __device__ __forceinline__ void wave_load_dt(const StepArgs& a, WaveRaw<HPW>& r, int bt, int h0, int lane,
                                              int wave) {
   // lanes >= HPW repeat the last slot
-  const int h = h0 + (PAIR ? (wave >> 1) : min(lane, HPW - 1) * WPB + wave);
+  const int h = h0 + (PAIR ? (wave >> 1) : wave * HPW + min(lane, HPW - 1));
   const uint16_t* db = (const uint16_t*)a.dt_bias;
   r.dt = a.dt[(size_t)bt * a.H + h];
   r.db_lo = db[a.db_f32 ? 2 * h : h];
@@ -233,7 +260,7 @@ __device__ __forceinline__ void wave_load_rest(const StepArgs& a, WaveRaw<HPW>& 
   const int p = min(pbase + lane, a.P - 1);   // rows past P read row P-1 (never stored)
 #pragma unroll
   for (int k = 0; k < HPW; ++k) {
-    const int h = h0 + (PAIR ? (wave >> 1) : k * WPB + wave);
+    const int h = h0 + (PAIR ? (wave >> 1) : wave * HPW + k);
     r.xv[k] = a.x[((size_t)bt * a.H + h) * a.P + p];
   }
 }
@@ -663,13 +690,13 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   // PAIR: tier role of the wave (0: INT8 tier; 1: INT4 tier, latent, readout)
   const int role = PAIR ? (wave & 1) : 0;
   // workgroup-local head of the wave's slot k
-  auto head_slot = [&](int k) { return PAIR ? (wave >> 1) : k * WPB + wave; };
+  auto head_slot = [&](int k) { return PAIR ? (wave >> 1) : wave * HPW + k; };
   const int h0 = by * NH;
   const int H = a.H, P = a.P;
   // ONE: the one-token (decode) instance, with a compile-time token count:
   // no token loop, prefetch or loop-carried state
   const int L = ONE ? 1 : a.L;
-  const int g = h0 / (H / a.G);
+  const int g = group_of_head(h0, a.rhpg);
   const int pbase = bx * 64;
   const int nvalid = min(64, P - pbase);
   const bool valid = lane < nvalid;
@@ -689,13 +716,15 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   auto slot_dma = [&](int hh) {   // direct global -> LDS transfers
     const int row0 = slot_row0(hh);
     uint8_t* t = s_tile[hh];
+    // the INT8 tier's fields first: the first slot's INT8 tier starts when
+    // they have landed
     if (own8) {
       field_dma16<W8>(t + O_LO, a.lo, row0, nvalid, lane);
       field_dma16<W8>(t + O_HI, a.hi, row0, nvalid, lane);
+      field_dma16<2>(t + O_S8, (const uint8_t*)a.s8, row0, nvalid, lane);
     }
-    if (own4) field_dma16<W4>(t + O_Q4, a.q4, row0, nvalid, lane);
-    if (own8) field_dma16<2>(t + O_S8, (const uint8_t*)a.s8, row0, nvalid, lane);
     if (own4) {
+      field_dma16<W4>(t + O_Q4, a.q4, row0, nvalid, lane);
       field_dma16<2>(t + O_S4, (const uint8_t*)a.s4, row0, nvalid, lane);
       if constexpr (RIDGE) field_dma16<2>(t + O_LAT, a.latent, row0, nvalid, lane);
     }
@@ -711,9 +740,14 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   // slot, also issued mid-slot) and slot k-1's y store (one store
   // instruction).  (Loads the compiler issues in between, the next token's
   // prefetch, only make a wait longer.)
+  // (The one-wave slot waits at slot 0 only for the INT8 fields, issued
+  // first; it waits for the INT4 fields after the INT8 tier.)
   auto slot_wait = [&](int k) {
     const bool copy = L == 1 && k >= 2;
-    if (k == 0) wait_vmcnt<0>();
+    if (k == 0) {
+      if (dma_tiles && !PAIR) wait_vmcnt<OPS4>();
+      else wait_vmcnt<0>();
+    }
     else if (copy) wait_vmcnt<COPY_OPS + 1>();
     else wait_vmcnt<1>();
   };
@@ -802,18 +836,26 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     TokenStage& st = sm.stage;
     const int bt = b;   // b * L with L == 1
     load_args(a);
-    // the dwords holding the per-head scalars of the wave's head slots, all
-    // loads issued before the first wait (H is even: no dword of a per-head
-    // array reaches past its end)
-    uint32_t sdt[HPW], sdb[HPW], sA[HPW], sD[HPW];
-#pragma unroll
-    for (int k = 0; k < HPW; ++k) {
-      const int h = h0 + head_slot(k), he = h & ~1;
-      sdt[k] = scalar_dword(a.dt + ((size_t)bt * H + he));
-      sdb[k] = scalar_dword(a.db_f32 ? (const void*)((const uint32_t*)a.dt_bias + h)
-                                     : (const void*)((const uint16_t*)a.dt_bias + he));
-      sA[k] = scalar_dword(a.A + h);
-      sD[k] = scalar_dword(a.d_f32 ? (const void*)((const uint32_t*)a.D + h) : (const void*)((const uint16_t*)a.D + he));
+    // the per-head scalars of the wave's head slots, heads hf .. hf + HPW - 1
+    // (one when HPW == 1; hf is even when HPW > 1, as h0 is): per array the
+    // dwords holding them, by at most two scalar loads, all issued before the
+    // first wait.  An array of binary16 or binary32 values (D, dt_bias) is
+    // read as DW dwords, then DW more that only the binary32 case uses (the
+    // binary16 case re-reads the first ones: nothing past the wave's heads
+    // is read).
+    constexpr int DW = (HPW + 1) / 2;   // dwords holding HPW binary16 values
+    const int hf = h0 + head_slot(0), he = hf & ~1;
+    uint32_t wdt[DW], wA[HPW], wD[2 * DW], wdb[2 * DW];
+    scalar_dwords<DW>(a.dt + ((size_t)bt * H + he), wdt);
+    scalar_dwords<HPW>(a.A + hf, wA);
+    {
+      const uint8_t* pd = a.d_f32 ? (const uint8_t*)((const uint32_t*)a.D + hf) : (const uint8_t*)((const uint16_t*)a.D + he);
+      const uint8_t* pb = a.db_f32 ? (const uint8_t*)((const uint32_t*)a.dt_bias + hf)
+                                   : (const uint8_t*)((const uint16_t*)a.dt_bias + he);
+      scalar_dwords<DW>(pd, wD);
+      scalar_dwords<DW>(a.d_f32 && HPW > 1 ? pd + 4 * DW : pd, wD + DW);
+      scalar_dwords<DW>(pb, wdb);
+      scalar_dwords<DW>(a.db_f32 && HPW > 1 ? pb + 4 * DW : pb, wdb + DW);
     }
     if constexpr (RIDGE) ls_w = scalar_dword(a.lscale + 2 * g);
     constexpr int SHARED_OPS = RIDGE ? 4 : 3;
@@ -849,14 +891,17 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
       if (HPW % 2 == 0 || k < HPW) lds_dma_b32(src, lds_address(&wt.x[2 * j][0]));
     }
     slot_dma(head_slot(0));
-    // the binary16 halves, then head slot `lane`'s scalars (lanes < HPW; the
-    // others take the last slot's)
+    // head slot k's values (binary16 bits, or binary32 bits of D and
+    // dt_bias), then head slot `lane`'s in lanes < HPW (the others take the
+    // last slot's)
+    uint32_t sdt[HPW], sdb[HPW], sA[HPW], sD[HPW];
 #pragma unroll
     for (int k = 0; k < HPW; ++k) {
-      const int odd = (h0 + head_slot(k)) & 1;   // H even: the head's parity is its element's
-      sdt[k] = odd ? sdt[k] >> 16 : sdt[k] & 0xFFFFu;
-      if (!a.db_f32) sdb[k] = odd ? sdb[k] >> 16 : sdb[k] & 0xFFFFu;
-      if (!a.d_f32) sD[k] = odd ? sD[k] >> 16 : sD[k] & 0xFFFFu;
+      const int hsh = HPW > 1 ? 16 * (k & 1) : 16 * (hf & 1);   // the head's half of its dword
+      sdt[k] = (wdt[k / 2] >> hsh) & 0xFFFFu;
+      sA[k] = wA[k];
+      sD[k] = a.d_f32 ? wD[k] : (wD[k / 2] >> hsh) & 0xFFFFu;
+      sdb[k] = a.db_f32 ? wdb[k] : (wdb[k / 2] >> hsh) & 0xFFFFu;
     }
     uint32_t vdt = sdt[HPW - 1], vdb = sdb[HPW - 1], vA = sA[HPW - 1], vD = sD[HPW - 1];
 #pragma unroll
@@ -1081,19 +1126,70 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           __builtin_amdgcn_raw_buffer_store_b16(f2h(out), ry, 2 * lane, 0, STORE_THROUGH);
         }
       } else {
+        const float x = h2f(wt.x[k][lane]);
+        const float decay = wt.decay[k];
+        const float dtv = wt.dtv[k];
+        const bool base_ok = wt.bounded[k] != 0 && __builtin_fabsf(x) <= 65504.f;
+        const f32x4* bdt4 = (const f32x4*)wt.bdt[k];
+        const f32x4* cw4 = (const f32x4*)cwt;
+        // the readout's partial sums per tier, added after both (the same order
+        // as the two-wave slot, whose tiers run on different waves)
+        float acc8 = 0.f, acc4 = 0.f;
 
-        // ---- unpack the slot: carried codes, internal lane order ------------------
-        // byte k of c8[i] is q8 + 128 of internal coordinate 4i+k, of c4[i] q4 + 8
-        uint32_t c8[C8], c4[C4];
+        // ---- INT8 tier: unpack (byte k of c8[i] is q8 + 128 of internal
+        // coordinate 4i+k), update with readout accumulation, requantize and
+        // repack into the tile; each tier is done before the next is read, so
+        // only one tier's values are live at a time.  Per tier, a wave-uniform
+        // choice between two copies of the tier code: the fused
+        // dequantization when every scale of the wave is finite, the exact
+        // products otherwise (non-finite scales are rare: the reference's
+        // controllers reject such states).
         {
-          uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4], wq[(W4 + 3) / 4];
-          lds_read_row<W8>(tile + O_LO, lane * W8, wl);
-          lds_read_row<W8>(tile + O_HI, lane * W8, wh);
-          planes_to_bytes8<N8>(wl, wh, c8);
+          uint32_t c8[C8];
+          {
+            uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4];
+            lds_read_row<W8>(tile + O_LO, lane * W8, wl);
+            lds_read_row<W8>(tile + O_HI, lane * W8, wh);
+            planes_to_bytes8<N8>(wl, wh, c8);
+          }
+          float sc8 = h2f(t16[O_S8 / 2 + lane]);
+          if (!valid) {   // rows past P: finite placeholders, never stored
+#pragma unroll
+            for (int i = 0; i < C8; ++i) c8[i] = 0x80808080u;
+            sc8 = 0.f;
+          }
+          const bool fin8 = __builtin_fabsf(sc8) <= 65504.f;
+          if (__builtin_amdgcn_ballot_w64(!fin8) == 0)
+            sc8 = tier_step<N8, true, MODE, false>(c8, sc8, decay, x, bdt4, cw4, acc8, base_ok);
+          else
+            sc8 = tier_step<N8, true, MODE, true>(c8, sc8, decay, x, bdt4, cw4, acc8, base_ok && fin8);
+          if (valid) {
+            uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4];
+            bytes_to_planes8<N8>(c8, wl, wh);
+            lds_write_row<W8>(tile + O_LO, lane * W8, wl);
+            lds_write_row<W8>(tile + O_HI, lane * W8, wh);
+            t16[O_S8 / 2 + lane] = f2h(sc8);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // the next slot's transfers are issued between the tiers, where the
+        // other waves' arithmetic covers their issue time
+        if (dma_tiles && t == 0 && k + 1 < HPW) slot_dma(hh + 1);   // head_slot(k + 1)
+        // first slot, first token: its INT4 fields (transferred after the
+        // INT8 ones) are waited for only now; later only the next slot's
+        // transfers may be outstanding
+        if (dma_tiles && t == 0 && k == 0) {
+          if (HPW > 1) wait_vmcnt<SLOT_DMA>();
+          else wait_vmcnt<0>();
+        }
+
+        // ---- INT4 tier and the latent coefficients ------------------------------
+        uint32_t c4[C4];
+        {
+          uint32_t wq[(W4 + 3) / 4];
           lds_read_row<W4>(tile + O_Q4, lane * W4, wq);
           plane_to_bytes4<N4>(wq, c4);
         }
-        float sc8 = h2f(t16[O_S8 / 2 + lane]);
         float sc4 = h2f(t16[O_S4 / 2 + lane]);
         float z0 = 0.f, z1 = 0.f;
         if constexpr (RIDGE) {
@@ -1101,48 +1197,20 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           z0 = e4m3_byte_to_f32<0>(lat) * ls0;
           z1 = e4m3_byte_to_f32<1>(lat) * ls1;
         }
-        if (!valid) {   // rows past P: finite placeholders, never stored
-  #pragma unroll
-          for (int i = 0; i < C8; ++i) c8[i] = 0x80808080u;
-  #pragma unroll
+        if (!valid) {
+#pragma unroll
           for (int i = 0; i < C4; ++i) c4[i] = 0x08080808u;
-          sc8 = sc4 = z0 = z1 = 0.f;
+          sc4 = z0 = z1 = 0.f;
         }
-        const float x = h2f(wt.x[k][lane]);
-        const float decay = wt.decay[k];
-        const float dtv = wt.dtv[k];
-        const bool base_ok = wt.bounded[k] != 0 && __builtin_fabsf(x) <= 65504.f;
-
-        // ---- per tier: update, readout accumulation, requantization ---------------
-        // (each tier is requantized before the next is updated, so only one
-        // tier's updated values are live at a time)
-        const f32x4* bdt4 = (const f32x4*)wt.bdt[k];
-        const f32x4* cw4 = (const f32x4*)cwt;
-        // the readout's partial sums per tier, added after both (the same order
-        // as the two-wave slot, whose tiers run on different waves)
-        float acc8 = 0.f, acc4 = 0.f;
-        const bool fin8 = __builtin_fabsf(sc8) <= 65504.f, fin4 = __builtin_fabsf(sc4) <= 65504.f;
-        const bool ok8 = base_ok && fin8;
-        const bool ok4 = base_ok && fin4;
-        // one wave-uniform choice per slot between two copies of the tier code:
-        // the fused dequantization when every scale of the wave is finite, the
-        // exact products otherwise (non-finite scales are rare: the reference's
-        // controllers reject such states)
-        auto tiers = [&](auto exact) {
-          constexpr bool EX = decltype(exact)::value;
-          sc8 = tier_step<N8, true, MODE, EX>(c8, sc8, decay, x, bdt4, cw4, acc8, ok8);
-          __builtin_amdgcn_sched_barrier(0);
-          // the next slot's transfers and the previous slot's copy-out are
-          // issued between the tiers, where the other waves' arithmetic covers
-          // their issue time
-          if (dma_tiles && t == 0 && k + 1 < HPW) slot_dma(hh + WPB);
-          sc4 = tier_step<N4, false, MODE, EX>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc4, ok4);
-          __builtin_amdgcn_sched_barrier(0);
-          if (t == L - 1 && k > 0) slot_copy_out(hh - WPB);   // the previous slot's state
-          __builtin_amdgcn_sched_barrier(0);
-        };
-        if (__builtin_amdgcn_ballot_w64(!(fin8 && fin4)) == 0) tiers(std::false_type{});
-        else tiers(std::true_type{});
+        const bool fin4 = __builtin_fabsf(sc4) <= 65504.f;
+        if (__builtin_amdgcn_ballot_w64(!fin4) == 0)
+          sc4 = tier_step<N4, false, MODE, false>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc4, base_ok);
+        else
+          sc4 = tier_step<N4, false, MODE, true>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc4,
+                                                 base_ok && fin4);
+        __builtin_amdgcn_sched_barrier(0);
+        if (t == L - 1 && k > 0) slot_copy_out(hh - 1);   // the previous slot's state (head_slot(k - 1))
+        __builtin_amdgcn_sched_barrier(0);
         const float acc = acc8 + acc4;
         // readout: sum_i u_i c_i + corrections = decay * (sum_i prior_i (c_i +
         // corr_i) + latent terms) + x * (dt * sum_all b c + D)
@@ -1165,15 +1233,11 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           __builtin_amdgcn_raw_buffer_store_b16(f2h(out), ry, 2 * lane, 0, STORE_THROUGH);
         }
 
-        // ---- repack the slot row into the tile ---------------------------------------
+        // ---- repack the INT4 tier and the latent bytes into the tile ------------------
         if (valid) {
-          uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4], wq[(W4 + 3) / 4];
-          bytes_to_planes8<N8>(c8, wl, wh);
-          lds_write_row<W8>(tile + O_LO, lane * W8, wl);
-          lds_write_row<W8>(tile + O_HI, lane * W8, wh);
+          uint32_t wq[(W4 + 3) / 4];
           bytes_to_plane4<N4>(c4, wq);
           lds_write_row<W4>(tile + O_Q4, lane * W4, wq);
-          t16[O_S8 / 2 + lane] = f2h(sc8);
           t16[O_S4 / 2 + lane] = f2h(sc4);
           if constexpr (RIDGE) t16[O_LAT / 2 + lane] = (uint16_t)qz;
         }

@@ -100,8 +100,11 @@ __device__ __forceinline__ void tile_store_lds(const TileRegs<W>& t, uint8_t* ld
 // and (2) wait with wait_vmcnt before reading the destination.  M0, which
 // carries the LDS address (wave-uniform by contract), is saved and restored
 // around the instruction.
+// The LDS address of a generic pointer into LDS is its low 32 bits (the
+// high half is the shared aperture's base), taken here without the
+// address-space cast's null test.
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
-  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+  return (uint32_t)(uintptr_t)p;
 }
 __device__ __forceinline__ void lds_dma_b32(const void* g, uint32_t lds) {
   uint32_t saved;
