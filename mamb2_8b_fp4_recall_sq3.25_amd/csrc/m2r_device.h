@@ -223,85 +223,114 @@ __device__ __forceinline__ float state_update(float state, float decay, float in
 //
 // A binary64 constant passed through an empty volatile asm: the value is
 // unchanged, but the compiler can no longer hoist its materialization out of
-// loops (keeping ~20 such constants in registers for a whole kernel).
+// loops (keeping ~20 such constants in registers for a whole kernel).  VREG
+// materializes it in vector registers instead of scalar ones (for code whose
+// scalar issue is the bottleneck).
+template <bool VREG = false>
 __device__ __forceinline__ double kconst(double v) {
-  asm volatile("" : "+s"(v));
+  if constexpr (VREG) asm volatile("" : "+v"(v));
+  else asm volatile("" : "+s"(v));
   return v;
 }
 
+// VREG: branch-free, the out-of-range cases selected at the end (the
+// polynomial then runs on an in-range stand-in argument); otherwise early
+// returns.  Both give the same bits.
+template <bool VREG = false>
 __device__ __forceinline__ double xexp_d(double x) {
-  if (x > kconst(100.0)) return __builtin_inf();
-  if (x < -kconst(110.0)) return kconst(0.0);
-  const double inv_ln2 = kconst(1.4426950408889634);           // 1/ln2
-  const double ln2_hi = kconst(6.93147180369123816490e-01);    // high 32 bits of ln2
-  const double ln2_lo = kconst(1.90821492927058770002e-10);    // ln2 - ln2_hi
-  const double magic = kconst(6755399441055744.0);             // 1.5 * 2^52
-  double kd = (x * inv_ln2 + magic) - magic;           // rint(x/ln2)
-  double r = (x - kd * ln2_hi) - kd * ln2_lo;
-  double p = kconst(1.0 / 6227020800.0);                       // 1/13!
-  p = __builtin_fma(p, r, kconst(1.0 / 479001600.0));
-  p = __builtin_fma(p, r, kconst(1.0 / 39916800.0));
-  p = __builtin_fma(p, r, kconst(1.0 / 3628800.0));
-  p = __builtin_fma(p, r, kconst(1.0 / 362880.0));
-  p = __builtin_fma(p, r, kconst(1.0 / 40320.0));
-  p = __builtin_fma(p, r, kconst(1.0 / 5040.0));
-  p = __builtin_fma(p, r, kconst(1.0 / 720.0));
-  p = __builtin_fma(p, r, kconst(1.0 / 120.0));
-  p = __builtin_fma(p, r, kconst(1.0 / 24.0));
-  p = __builtin_fma(p, r, kconst(1.0 / 6.0));
-  p = __builtin_fma(p, r, kconst(0.5));
-  p = __builtin_fma(p, r, kconst(1.0));
-  p = __builtin_fma(p, r, kconst(1.0));
+  if constexpr (!VREG) {
+    if (x > kconst(100.0)) return __builtin_inf();
+    if (x < -kconst(110.0)) return kconst(0.0);
+  }
+  const bool big = VREG && x > kconst<VREG>(100.0), tiny = VREG && x < -kconst<VREG>(110.0);
+  const double xr = (big || tiny) ? 0.0 : x;
+  const double inv_ln2 = kconst<VREG>(1.4426950408889634);           // 1/ln2
+  const double ln2_hi = kconst<VREG>(6.93147180369123816490e-01);    // high 32 bits of ln2
+  const double ln2_lo = kconst<VREG>(1.90821492927058770002e-10);    // ln2 - ln2_hi
+  const double magic = kconst<VREG>(6755399441055744.0);             // 1.5 * 2^52
+  double kd = (xr * inv_ln2 + magic) - magic;           // rint(x/ln2)
+  double r = (xr - kd * ln2_hi) - kd * ln2_lo;
+  double p = kconst<VREG>(1.0 / 6227020800.0);                       // 1/13!
+  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 479001600.0));
+  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 39916800.0));
+  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 3628800.0));
+  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 362880.0));
+  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 40320.0));
+  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 5040.0));
+  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 720.0));
+  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 120.0));
+  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 24.0));
+  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 6.0));
+  p = __builtin_fma(p, r, kconst<VREG>(0.5));
+  p = __builtin_fma(p, r, kconst<VREG>(1.0));
+  p = __builtin_fma(p, r, kconst<VREG>(1.0));
   int64_t k = (int64_t)kd;
   double scale = __builtin_bit_cast(double, (uint64_t)(k + 1023) << 52);
-  return p * scale;
+  const double y = p * scale;
+  return big ? __builtin_inf() : (tiny ? 0.0 : y);
 }
 
+template <bool VREG = false>
 __device__ __forceinline__ double xlog_d(double x) {
   // Domain used by the codec: finite x >= 1 (softplus argument exp(d)+1).
   uint64_t u = __builtin_bit_cast(uint64_t, x);
   int64_t e = (int64_t)((u >> 52) & 0x7FF) - 1023;
   double m = __builtin_bit_cast(double, (u & 0x000FFFFFFFFFFFFFull) | 0x3FF0000000000000ull);
-  if (m > kconst(1.4142135623730951)) { m = m * kconst(0.5); e += 1; }
-  double s = (m - kconst(1.0)) / (m + kconst(1.0));
+  if constexpr (VREG) {
+    const bool upper = m > kconst<VREG>(1.4142135623730951);
+    m = upper ? m * kconst<VREG>(0.5) : m;
+    e += upper ? 1 : 0;
+  } else if (m > kconst(1.4142135623730951)) {
+    m = m * kconst(0.5);
+    e += 1;
+  }
+  double s = (m - kconst<VREG>(1.0)) / (m + kconst<VREG>(1.0));
   double s2 = s * s;
-  double p = kconst(1.0 / 23.0);
-  p = __builtin_fma(p, s2, kconst(1.0 / 21.0));
-  p = __builtin_fma(p, s2, kconst(1.0 / 19.0));
-  p = __builtin_fma(p, s2, kconst(1.0 / 17.0));
-  p = __builtin_fma(p, s2, kconst(1.0 / 15.0));
-  p = __builtin_fma(p, s2, kconst(1.0 / 13.0));
-  p = __builtin_fma(p, s2, kconst(1.0 / 11.0));
-  p = __builtin_fma(p, s2, kconst(1.0 / 9.0));
-  p = __builtin_fma(p, s2, kconst(1.0 / 7.0));
-  p = __builtin_fma(p, s2, kconst(1.0 / 5.0));
-  p = __builtin_fma(p, s2, kconst(1.0 / 3.0));
-  p = __builtin_fma(p, s2, kconst(1.0));
-  double logm = kconst(2.0) * s * p;
+  double p = kconst<VREG>(1.0 / 23.0);
+  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 21.0));
+  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 19.0));
+  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 17.0));
+  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 15.0));
+  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 13.0));
+  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 11.0));
+  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 9.0));
+  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 7.0));
+  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 5.0));
+  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 3.0));
+  p = __builtin_fma(p, s2, kconst<VREG>(1.0));
+  double logm = kconst<VREG>(2.0) * s * p;
   double ed = (double)e;
-  const double ln2_hi = kconst(6.93147180369123816490e-01);
-  const double ln2_lo = kconst(1.90821492927058770002e-10);
+  const double ln2_hi = kconst<VREG>(6.93147180369123816490e-01);
+  const double ln2_lo = kconst<VREG>(1.90821492927058770002e-10);
   return (ed * ln2_hi + logm) + ed * ln2_lo;
 }
 
-__device__ __forceinline__ float xexpf(float x) { return (float)xexp_d((double)x); }
-__device__ __forceinline__ float xlogf(float x) { return (float)xlog_d((double)x); }
+template <bool VREG = false>
+__device__ __forceinline__ float xexpf(float x) { return (float)xexp_d<VREG>((double)x); }
+template <bool VREG = false>
+__device__ __forceinline__ float xlogf(float x) { return (float)xlog_d<VREG>((double)x); }
 
 // Mamba-2 dt activation of the codec kernels: v = dt + dt_bias;
-// v <= 20 ? log(exp(v) + 1) : v, with the inner +1 rounded in binary32.
+// v <= 20 ? log(exp(v) + 1) : v, with the inner +1 rounded in binary32
+// (VREG: branch-free, arguments above 20, and NaN, select v itself).
+template <bool VREG = false>
 __device__ __forceinline__ float softplus_dt(float v) {
-  if (v <= 20.0f) {
-    float e = xexpf(v);
-    return xlogf(e + 1.0f);
+  if constexpr (!VREG) {
+    if (v <= 20.0f) return xlogf(xexpf(v) + 1.0f);
+    return v;
   }
-  return v;
+  const bool soft = v <= 20.0f;
+  const float e = xexpf<VREG>(soft ? v : 0.0f);
+  const float l = xlogf<VREG>(e + 1.0f);
+  return soft ? l : v;
 }
 
 // dt activation and decay for one head (inline; its binary64 constants are
 // rematerialized at each use, see kconst).
+template <bool VREG = false>
 __device__ __forceinline__ float2 dt_activation(float dt_plus_bias, float A) {
-  const float dtv = softplus_dt(dt_plus_bias);
-  return make_float2(dtv, xexpf(A * dtv));
+  const float dtv = softplus_dt<VREG>(dt_plus_bias);
+  return make_float2(dtv, xexpf<VREG>(A * dtv));
 }
 
 }  // namespace m2r

@@ -206,10 +206,11 @@ struct GroupToken {
 // `stat`: [0, 32) the permutation bytes, [32, 32 + NZ) the dead-tier basis
 // (f16 pairs).
 struct TokenStage {
-  alignas(16) uint32_t b[64];
-  alignas(16) uint32_t c[64];
-  alignas(16) uint32_t stat[128];
+  alignas(16) uint32_t b[64];      // shared transfer 0
+  alignas(16) uint32_t c[64];      // shared transfer 1
+  alignas(16) uint32_t stat[128];  // shared transfers 2 and 3
 };
+static_assert(sizeof(TokenStage) == 1024, "shared transfer j lands at dword 64 j");
 struct NoStage {};
 
 // Inputs of one token that a wave loads one token ahead: its lane's two f16
@@ -267,10 +268,10 @@ __device__ __forceinline__ void wave_load_rest(const StepArgs& a, WaveRaw<HPW>& 
 
 // dt activation of head slot `lane` (lanes < HPW; the others compute a copy
 // of the last slot's, unused).
-template <int HPW>
+template <int HPW, bool VREG = false>
 __device__ __forceinline__ float2 wave_dt_activation(const WaveRaw<HPW>& r, float Ah, int db_f32) {
   const float db = db_f32 ? __builtin_bit_cast(float, (uint32_t)r.db_lo | ((uint32_t)r.db_hi << 16)) : h2f(r.db_lo);
-  return dt_activation(h2f(r.dt) + db, Ah);
+  return dt_activation<VREG>(h2f(r.dt) + db, Ah);
 }
 
 // Builds the wave's token values from its landed raw inputs and the dt
@@ -707,29 +708,40 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   // vector memory operations per slot transfer (and per state copy-out); in
   // PAIR mode a wave transfers its tier's fields only: the INT8 wave lo, hi
   // and s8 (OPS8), the INT4 wave q4, s4 and the latent bytes (OPS4)
-  constexpr int OPS8 = 2 * chunk_ops(W8) + chunk_ops(2);
-  constexpr int OPS4 = chunk_ops(W4) + chunk_ops(2) * (RIDGE ? 2 : 1);
-  constexpr int SLOT_DMA = OPS8 + OPS4;
+  // (the two-byte fields of a transfer go in one operation: s8, s4 and the
+  // latent bytes of a one-wave slot; s8, or s4 and the latent bytes, in
+  // PAIR mode)
+  constexpr int C8W = chunk_ops(W8), C4W = chunk_ops(W4);
+  constexpr int OPS8 = 2 * C8W + 1;
+  constexpr int OPS4 = C4W + 1;
+  constexpr int SLOT_DMA = PAIR ? OPS8 + OPS4 : 2 * C8W + 1 + C4W;
   static_assert(SLOT_DMA <= 63, "a slot's transfers must fit the vmcnt range");
+  static_assert(O_S4 == O_S8 + 128 && O_LAT == O_S4 + 128, "two-byte fields back to back in the tile");
   const bool own8 = !PAIR || role == 0, own4 = !PAIR || role == 1;   // the fields this wave moves
   auto slot_row0 = [&](int hh) { return (b * H + h0 + hh) * P + pbase; };
   auto slot_dma = [&](int hh) {   // direct global -> LDS transfers
     const int row0 = slot_row0(hh);
     uint8_t* t = s_tile[hh];
-    // the INT8 tier's fields first: the first slot's INT8 tier starts when
-    // they have landed
-    if (own8) {
-      field_dma16<W8>(t + O_LO, a.lo, row0, nvalid, lane);
-      field_dma16<W8>(t + O_HI, a.hi, row0, nvalid, lane);
-      field_dma16<2>(t + O_S8, (const uint8_t*)a.s8, row0, nvalid, lane);
-    }
-    if (own4) {
-      field_dma16<W4>(t + O_Q4, a.q4, row0, nvalid, lane);
-      field_dma16<2>(t + O_S4, (const uint8_t*)a.s4, row0, nvalid, lane);
-      if constexpr (RIDGE) field_dma16<2>(t + O_LAT, a.latent, row0, nvalid, lane);
+    // the INT8 tier's fields first (with all two-byte fields in a one-wave
+    // slot): the first slot's INT8 tier starts when they have landed
+    const uint32_t tl = lds_address(t);
+    const uint8_t *s8 = (const uint8_t*)a.s8, *s4 = (const uint8_t*)a.s4;
+    if constexpr (!PAIR) {
+      field_dma16_tile<W8, O_LO>(tl, a.lo, row0, nvalid, lane);
+      field_dma16_tile<W8, O_HI>(tl, a.hi, row0, nvalid, lane);
+      scale_fields_dma16_tile<RIDGE ? 3 : 2, O_S8>(tl, s8, s4, RIDGE ? a.latent : s4, row0, nvalid, lane);
+      field_dma16_tile<W4, O_Q4>(tl, a.q4, row0, nvalid, lane);
+    } else if (own8) {
+      field_dma16_tile<W8, O_LO>(tl, a.lo, row0, nvalid, lane);
+      field_dma16_tile<W8, O_HI>(tl, a.hi, row0, nvalid, lane);
+      scale_fields_dma16_tile<1, O_S8>(tl, s8, s8, s8, row0, nvalid, lane);
+    } else {
+      field_dma16_tile<W4, O_Q4>(tl, a.q4, row0, nvalid, lane);
+      scale_fields_dma16_tile<RIDGE ? 2 : 1, O_S4>(tl, s4, RIDGE ? a.latent : s4, s4, row0, nvalid, lane);
     }
   };
-  constexpr int COPY_OPS = SLOT_DMA;   // one store instruction per transfer chunk
+  // store instructions of a slot's copy-out (one per 1 KiB chunk of a field)
+  constexpr int COPY_OPS = 2 * C8W + C4W + (RIDGE ? 3 : 2);
   static_assert(SLOT_DMA + COPY_OPS + 1 <= 63, "vmcnt range");
   // At the first token, before slot k is read: wait until only the
   // operations issued after slot k's transfers are outstanding (vector memory
@@ -745,7 +757,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   auto slot_wait = [&](int k) {
     const bool copy = L == 1 && k >= 2;
     if (k == 0) {
-      if (dma_tiles && !PAIR) wait_vmcnt<OPS4>();
+      if (dma_tiles && !PAIR) wait_vmcnt<C4W>();
       else wait_vmcnt<0>();
     }
     else if (copy) wait_vmcnt<COPY_OPS + 1>();
@@ -770,7 +782,9 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     const uint8_t* t = s_tile[hh];
     if constexpr (dma_tiles && PAIR) {   // this wave's fields: every LDS read, then the stores
       constexpr int C8W = chunk_ops(W8), C4W = chunk_ops(W4), C2 = chunk_ops(2);
-      u32x4 v[OPS8 > OPS4 ? OPS8 : OPS4];
+      // store chunks per role: lo, hi and s8; q4, s4 (and the latent bytes)
+      constexpr int COPY8 = 2 * C8W + 1, COPY4 = C4W + (RIDGE ? 2 : 1);
+      u32x4 v[COPY8 > COPY4 ? COPY8 : COPY4];
       if (own8) {
         field_read16<W8>(t + O_LO, lane, v);
         field_read16<W8>(t + O_HI, lane, v + C8W);
@@ -789,7 +803,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
       return;
     } else if constexpr (dma_tiles) {   // every LDS read of the slot, then its stores
       constexpr int C8W = chunk_ops(W8), C4W = chunk_ops(W4), C2 = chunk_ops(2);
-      u32x4 v[SLOT_DMA];
+      u32x4 v[COPY_OPS];
       field_read16<W8>(t + O_LO, lane, v);
       field_read16<W8>(t + O_HI, lane, v + C8W);
       field_read16<W4>(t + O_Q4, lane, v + 2 * C8W);
@@ -858,25 +872,19 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
       scalar_dwords<DW>(a.db_f32 && HPW > 1 ? pb + 4 * DW : pb, wdb + DW);
     }
     if constexpr (RIDGE) ls_w = scalar_dword(a.lscale + 2 * g);
+    // shared transfer j by wave j, branch-free: the B row (0), the C row (1),
+    // the permutation bytes and the first 32 basis pairs (2), basis pairs
+    // 32 .. NZ - 1 (3)
     constexpr int SHARED_OPS = RIDGE ? 4 : 3;
-    for (int j = wave; j < SHARED_OPS; j += WPB) {
-      const void* src;
-      uint32_t* dst;
-      if (j == 0) {
-        src = a.Bm + ((size_t)bt * a.G + g) * 128 + 2 * lane;
-        dst = st.b;
-      } else if (j == 1) {
-        src = a.Cm + ((size_t)bt * a.G + g) * 128 + 2 * lane;
-        dst = st.c;
-      } else if (j == 2) {   // permutation bytes, then the first 32 basis pairs
-        if (lane < 32 || !RIDGE) src = a.perm + (size_t)g * 128 + 4 * (lane & 31);
-        else src = (const uint32_t*)a.basis + (size_t)g * NZ + min(lane - 32, NZ - 1);
-        dst = st.stat;
-      } else {               // basis pairs 32 .. NZ - 1
-        src = (const uint32_t*)a.basis + (size_t)g * NZ + min(32 + lane, NZ - 1);
-        dst = st.stat + 64;
-      }
-      lds_dma_b32(src, lds_address(dst));
+    static_assert(WPB >= SHARED_OPS, "at most one shared transfer per wave");
+    if (wave < SHARED_OPS) {
+      const uint8_t* bc = (const uint8_t*)(wave == 0 ? a.Bm : a.Cm) + ((size_t)bt * a.G + g) * 256;
+      const uint8_t* prm = a.perm + (size_t)g * 128;
+      const uint8_t* bas = RIDGE ? (const uint8_t*)a.basis + (size_t)g * NZ * 4 : prm;
+      const int bi = wave == 2 ? lane - 32 : lane + 32;   // basis pair of this lane (waves 2 and 3)
+      const uint8_t* src = wave < 2 ? bc + 4 * lane
+                           : ((wave == 2 && (lane < 32 || !RIDGE)) ? prm + 4 * (lane & 31) : bas + 4 * min(bi, NZ - 1));
+      lds_dma_b32(src, lds_address(st.b + 64 * wave));
     }
     if constexpr (RIDGE) {   // the predictor: 16-byte chunks; lanes past the end re-read the last one
       const uint8_t* pg = (const uint8_t*)(a.pred + (size_t)g * F * NZ);
@@ -916,7 +924,10 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     raw.db_hi = a.db_f32 ? (uint16_t)(vdb >> 16) : (uint16_t)vdb;
     Ah = __builtin_bit_cast(float, vA);
     d_bits = vD;
-    act = wave_dt_activation<HPW>(raw, Ah, a.db_f32);
+    // (with two waves per SIMD the prologue's scalar issue is its
+    // bottleneck: the binary64 constants go in vector registers; the
+    // two-wave slots, one wave per SIMD, keep them in scalar ones)
+    act = wave_dt_activation<HPW, !PAIR>(raw, Ah, a.db_f32);
     // this wave's token, statics and predictor transfers have landed
     if (!PAIR) wait_vmcnt<SLOT_DMA>();
     else if (role == 0) wait_vmcnt<OPS8>();

@@ -98,8 +98,10 @@ __device__ __forceinline__ void tile_store_lds(const TileRegs<W>& t, uint8_t* ld
 // compiler-visible global load complete before issuing transfers (otherwise
 // the compiler's wait for such a load would also wait for the transfers),
 // and (2) wait with wait_vmcnt before reading the destination.  M0, which
-// carries the LDS address (wave-uniform by contract), is saved and restored
-// around the instruction.
+// carries the LDS address (wave-uniform by contract), is an operand of the
+// statement: the compiler writes it (once for a run of transfers with the
+// same base) and knows it changed.  The leading s_nop is the wait state
+// between an M0 write and an LDS transfer that reads it.
 // The LDS address of a generic pointer into LDS is its low 32 bits (the
 // high half is the shared aperture's base), taken here without the
 // address-space cast's null test.
@@ -107,9 +109,8 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return (uint32_t)(uintptr_t)p;
 }
 __device__ __forceinline__ void lds_dma_b32(const void* g, uint32_t lds) {
-  uint32_t saved;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
-               : "=&s"(saved) : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
 }
 
 // Raw buffer resource over `bytes` bytes at `base` (gfx9-family dword 3:
@@ -122,9 +123,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_buffer(const void* base, i
 // The 16-byte form: lane l's 16 bytes at g land at M0 + 16 l.  Marked
 // non-temporal: every state byte is read once per launch.
 __device__ __forceinline__ void lds_dma_b128(const void* g, uint32_t lds) {
-  uint32_t saved;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off nt\n\ts_mov_b32 m0, %0"
-               : "=&s"(saved) : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+// The same with an instruction offset, which moves the global and the LDS
+// address alike: lane l's 16 bytes at g + IMM land at lds + IMM + 16 l, so
+// transfers into one tile share M0.
+template <int IMM>
+__device__ __forceinline__ void lds_dma_b128_imm(const void* g, uint32_t lds) {
+  static_assert(IMM >= 0 && IMM < 4096, "instruction offset range");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off offset:%2 nt" ::"v"(g),
+               "{m0}"(__builtin_amdgcn_readfirstlane(lds)), "n"(IMM)
+               : "memory");
 }
 
 // 16-byte transfers of one SoA field of a 64-row slot (64 * W bytes at
@@ -159,6 +169,34 @@ __device__ __forceinline__ void field_dma16(uint8_t* lds, const uint8_t* g, int 
     const int o = k * 1024 + 16 * lane;
     if (k * 1024 + 1024 <= FB || o < FB) lds_dma_b128(base + min(o, last), l0 + 1024 * k);
   }
+}
+
+// The same transfers into a slot tile whose LDS base `tile` is M0 for every
+// field of the slot: the field sits at tile byte offset O and chunk k goes
+// by instruction offset O + 1024 k.
+template <int W, int O, int K = 0>
+__device__ __forceinline__ void field_dma16_tile(uint32_t tile, const uint8_t* g, int row0, int nvalid, int lane) {
+  static_assert(chunk_ops(W) <= 4, "fields of at most 4 KiB per slot");
+  if constexpr (K < chunk_ops(W)) {
+    constexpr int FB = 64 * W, IMM = O + 1024 * K;
+    const uint8_t* base = g + (size_t)row0 * W;
+    const int o = K * 1024 + 16 * lane;
+    if (K * 1024 + 1024 <= FB || o < FB) lds_dma_b128_imm<IMM>(base + (min(o, nvalid * W - 16) - IMM), tile);
+    field_dma16_tile<W, O, K + 1>(tile, g, row0, nvalid, lane);
+  }
+}
+// NF two-byte fields of a slot (128 bytes each: f0, f1, f2), which sit back
+// to back in the tile from byte offset O, in one transfer: lane l moves
+// 16 bytes of field l / 8 (lanes past the nvalid valid rows re-read the
+// field's last valid chunk, which lands in rows nobody reads).  Requires
+// nvalid % 8 == 0.
+template <int NF, int O>
+__device__ __forceinline__ void scale_fields_dma16_tile(uint32_t tile, const uint8_t* f0, const uint8_t* f1,
+                                                        const uint8_t* f2, int row0, int nvalid, int lane) {
+  static_assert(NF >= 1 && NF <= 3, "one to three fields");
+  const int f = lane >> 3, c = min(lane & 7, nvalid / 8 - 1);
+  const uint8_t* fb = f == 0 ? f0 : (f == 1 ? f1 : f2);
+  if (lane < 8 * NF) lds_dma_b128_imm<O>(fb + (size_t)row0 * 2 + (16 * c - O), tile);
 }
 
 // Cache policy of the state and output stores: device scope (sc1) and
@@ -207,9 +245,8 @@ constexpr int dma_ops(int W) { return W / 4 + (W % 4 ? 1 : 0); }
 template <int IMM>
 __device__ __forceinline__ void lds_dma_b32_sbase(uint32_t voff, const void* sbase, uint32_t lds) {
   static_assert(IMM >= 0 && IMM < 4096, "instruction offset range");
-  uint32_t saved;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\tglobal_load_lds_dword %1, %2 offset:%4\n\ts_mov_b32 m0, %0"
-               : "=&s"(saved) : "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds)), "n"(IMM)
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1 offset:%3" ::"v"(voff), "s"(sbase),
+               "{m0}"(__builtin_amdgcn_readfirstlane(lds)), "n"(IMM)
                : "memory");
 }
 
