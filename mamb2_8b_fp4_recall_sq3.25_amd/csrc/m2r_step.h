@@ -701,6 +701,11 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   const int pbase = bx * 64;
   const int nvalid = min(64, P - pbase);
   const bool valid = lane < nvalid;
+  // Rows past P need finite placeholders only when their tile rows hold
+  // stale LDS: the 16-byte transfers fill them with copies of the last
+  // valid chunk (finite codes and scales, stepped like any row and never
+  // stored), the register copies leave them as they were.
+  constexpr bool PLACEHOLDERS = !DMA;
   constexpr bool dma_tiles = DMA;   // a.dma_tiles: 16-byte LDS transfers, else staging through VGPRs
   const uint16_t* s_pred = (const uint16_t*)s_pred32;
   WaveToken<N8, N4, HPW>& wt = s_wt[wave];
@@ -1068,7 +1073,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
             planes_to_bytes8<N8>(wl, wh, c8);
           }
           float sc8 = h2f(t16[O_S8 / 2 + lane]);
-          if (!valid) {   // rows past P: finite placeholders, never stored
+          if (PLACEHOLDERS && !valid) {   // rows past P: finite placeholders, never stored
 #pragma unroll
             for (int i = 0; i < C8; ++i) c8[i] = 0x80808080u;
             sc8 = 0.f;
@@ -1099,7 +1104,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
             z0 = e4m3_byte_to_f32<0>(lat) * ls0;
             z1 = e4m3_byte_to_f32<1>(lat) * ls1;
           }
-          if (!valid) {
+          if (PLACEHOLDERS && !valid) {
 #pragma unroll
             for (int i = 0; i < C4; ++i) c4[i] = 0x08080808u;
             sc4 = z0 = z1 = 0.f;
@@ -1164,7 +1169,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
             planes_to_bytes8<N8>(wl, wh, c8);
           }
           float sc8 = h2f(t16[O_S8 / 2 + lane]);
-          if (!valid) {   // rows past P: finite placeholders, never stored
+          if (PLACEHOLDERS && !valid) {   // rows past P: finite placeholders, never stored
 #pragma unroll
             for (int i = 0; i < C8; ++i) c8[i] = 0x80808080u;
             sc8 = 0.f;
@@ -1208,7 +1213,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           z0 = e4m3_byte_to_f32<0>(lat) * ls0;
           z1 = e4m3_byte_to_f32<1>(lat) * ls1;
         }
-        if (!valid) {
+        if (PLACEHOLDERS && !valid) {
 #pragma unroll
           for (int i = 0; i < C4; ++i) c4[i] = 0x08080808u;
           sc4 = z0 = z1 = 0.f;
