@@ -855,6 +855,21 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     TokenStage& st = sm.stage;
     const int bt = b;   // b * L with L == 1
     load_args(a);
+    // shared transfer j by wave j, branch-free: the B row (0), the C row (1),
+    // the permutation bytes and the first 32 basis pairs (2), basis pairs
+    // 32 .. NZ - 1 (3)
+    constexpr int SHARED_OPS = RIDGE ? 4 : 3;
+    static_assert(WPB >= SHARED_OPS, "at most one shared transfer per wave");
+    if (wave < SHARED_OPS) {
+      const uint8_t* bc = (const uint8_t*)(wave == 0 ? a.Bm : a.Cm) + ((size_t)bt * a.G + g) * 256;
+      const uint8_t* prm = a.perm + (size_t)g * 128;
+      const uint8_t* bas = RIDGE ? (const uint8_t*)a.basis + (size_t)g * NZ * 4 : prm;
+      const int bi = wave == 2 ? lane - 32 : lane + 32;   // basis pair of this lane (waves 2 and 3)
+      const uint8_t* src = wave < 2 ? bc + 4 * lane
+                           : ((wave == 2 && (lane < 32 || !RIDGE)) ? prm + 4 * (lane & 31) : bas + 4 * min(bi, NZ - 1));
+      lds_dma_b32(src, lds_address(st.b + 64 * wave));
+    }
+    // (after the shared transfers, which the token build waits for first)
     // the per-head scalars of the wave's head slots, heads hf .. hf + HPW - 1
     // (one when HPW == 1; hf is even when HPW > 1, as h0 is): per array the
     // dwords holding them, by at most two scalar loads, all issued before the
@@ -877,20 +892,6 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
       scalar_dwords<DW>(a.db_f32 && HPW > 1 ? pb + 4 * DW : pb, wdb + DW);
     }
     if constexpr (RIDGE) ls_w = scalar_dword(a.lscale + 2 * g);
-    // shared transfer j by wave j, branch-free: the B row (0), the C row (1),
-    // the permutation bytes and the first 32 basis pairs (2), basis pairs
-    // 32 .. NZ - 1 (3)
-    constexpr int SHARED_OPS = RIDGE ? 4 : 3;
-    static_assert(WPB >= SHARED_OPS, "at most one shared transfer per wave");
-    if (wave < SHARED_OPS) {
-      const uint8_t* bc = (const uint8_t*)(wave == 0 ? a.Bm : a.Cm) + ((size_t)bt * a.G + g) * 256;
-      const uint8_t* prm = a.perm + (size_t)g * 128;
-      const uint8_t* bas = RIDGE ? (const uint8_t*)a.basis + (size_t)g * NZ * 4 : prm;
-      const int bi = wave == 2 ? lane - 32 : lane + 32;   // basis pair of this lane (waves 2 and 3)
-      const uint8_t* src = wave < 2 ? bc + 4 * lane
-                           : ((wave == 2 && (lane < 32 || !RIDGE)) ? prm + 4 * (lane & 31) : bas + 4 * min(bi, NZ - 1));
-      lds_dma_b32(src, lds_address(st.b + 64 * wave));
-    }
     if constexpr (RIDGE) {   // the predictor: 16-byte chunks; lanes past the end re-read the last one
       const uint8_t* pg = (const uint8_t*)(a.pred + (size_t)g * F * NZ);
       for (int j = wave; j < PRED_OPS16; j += WPB)
