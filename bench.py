@@ -593,8 +593,8 @@ def e2e_decode(device, batches=(1, 4, 16), prefill=8, tokens=256, eager_tokens=6
                    f"{prefill}; {eager_tokens} eager greedy tokens (the reference the graph replays are checked "
                    f"against, token by token and on layer 0's packed state) and {tokens} timed greedy tokens, each "
                    f"one replay of the captured backbone graph plus the eager lm_head, argmax and token "
-                   f"feedback; PyTorch mixer (GEMMs, gated norm) around the HIP "
-                   f"codec and convolution-update kernels; packed_fp4: the one-token in_proj/out_proj as "
+                   f"feedback; PyTorch GEMMs around the HIP codec, convolution-update and "
+                   f"gated-norm kernels; packed_fp4: the one-token in_proj/out_proj as "
                    f"packed-resident FP4 G16 GEMVs")
     return out
 

@@ -260,6 +260,24 @@ int m2r_causal_conv_update(void* window, int64_t ws_b, int64_t ws_c, int64_t ws_
                            int width, int silu, hipStream_t stream);
 
 /*
+ * Gated RMS norm of the Mamba-2 mixer, norm_before_gate = False: per group of
+ * group_size channels of each row, v = y * (z * sigmoid(z)) in binary32,
+ * out = half((v / sqrt(mean(v^2) + eps)) * weight).  Replaces the gated norm
+ * module the reference's controllers call as mx.norm(y, z)
+ * (mamba2_recall/state_quant.py:298-300; mamba_ssm's RMSNormGated, a
+ * third-party Triton kernel).  The sum of squares is a fixed tree, so the
+ * results are deterministic; they agree with a binary32/binary64
+ * restatement of the formula to one binary16 rounding.
+ *   y, z f16 rows of `channels` with element row strides y_stride, z_stride;
+ *   weight f16 [channels]; out f16 rows with stride out_stride.  Pointers
+ *   8-byte aligned, strides multiples of 4 elements; group_size a multiple
+ *   of 4, at most 4096, dividing channels; rows and groups at most 65535.
+ */
+int m2r_gated_rmsnorm(const void* y, int64_t y_stride, const void* z, int64_t z_stride, const void* weight, void* out,
+                      int64_t out_stride, int64_t rows, int64_t channels, int64_t group_size, float eps,
+                      hipStream_t stream);
+
+/*
  * Packed-resident FP4 G16 matrix-vector product: y[m, n] = sum_k u[m, k] *
  * w[n, k] with W read directly in the checkpoint's packed format.  Every
  * weight is the binary16 value m2r_fp4_decode_g16 produces; products

@@ -17,6 +17,7 @@ LIB_PATH = PKG_ROOT / "lib" / "libm2r_hip.so"
 _lib = None
 
 P, I, I64, U32P = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
+F32 = ctypes.c_float
 
 _SIGNATURES = {
     "m2r_abi_version": ([], I),
@@ -38,6 +39,7 @@ _SIGNATURES = {
     "m2r_probe_butterfly": ([P, P, P], I),
     "m2r_set_step_shape": ([I, I], I),
     "m2r_causal_conv_update": ([P, I64, I64, I64, P, I64, P, P, P, I64, I64, I, I, P], I),
+    "m2r_gated_rmsnorm": ([P, I64, P, I64, P, P, I64, I64, I64, I64, F32, P], I),
     "m2r_fp4_gemv_g16": ([P, P, P, P, I64, P, I64, I64, I64, I64, P], I),
     "m2r_state_step_ridge_layers_workspace": ([I], I64),
     "m2r_state_step_ridge_layers": ([P, I, I64, I64, I64, I64, P, I64, P], I),

@@ -90,6 +90,81 @@ def conv_update(window, value, weight, bias, *, silu=True):
     return out
 
 
+def _row_view(t, channels):
+    """(rows, row stride) of `t` [..., channels] when its leading dimensions
+    collapse into rows of one stride with unit channel stride, else None."""
+    if t.dim() < 1 or t.shape[-1] != channels or t.stride(-1) != 1:
+        return None
+    lead = [(t.shape[i], t.stride(i)) for i in range(t.dim() - 1) if t.shape[i] > 1]
+    if not lead:
+        return 1, channels
+    for (_, s_outer), (n_inner, s_inner) in zip(lead, lead[1:]):
+        if s_outer != s_inner * n_inner:
+            return None
+    return t.numel() // channels, lead[-1][1]
+
+
+def gated_rmsnorm(y, z, weight, eps, group_size):
+    """The mixer's gated RMS norm (norm_before_gate False) on the device:
+    per group of `group_size` channels, v = y * z * sigmoid(z) in FP32,
+    out = FP16((v / sqrt(mean(v^2) + eps)) * weight); the computation of
+    mamba_ssm's RMSNormGated, which the reference's controllers call as
+    mx.norm(y, z) (state_quant.py:298-300), in one HIP kernel (fixed
+    reduction tree, deterministic).  y, z: FP16 [..., C] with unit channel
+    stride and leading dimensions of one row stride; returns a new FP16
+    tensor of y's shape."""
+    channels = y.shape[-1]
+    if (y.dtype != torch.float16 or z.dtype != torch.float16 or weight.dtype != torch.float16
+            or tuple(z.shape) != tuple(y.shape) or tuple(weight.shape) != (channels,) or not weight.is_contiguous()):
+        raise ValueError("Gated norm expects FP16 y and z of one shape and an FP16 weight [C]")
+    ry, rz = _row_view(y, channels), _row_view(z, channels)
+    if ry is None or rz is None:
+        raise ValueError("Gated norm operands need unit channel stride and one row stride")
+    for t in (y, z, weight):
+        _native.require_device(t, "gated norm operand")
+    rows = ry[0]
+    out = torch.empty(y.shape, dtype=torch.float16, device=y.device)
+    stream = _native.stream_of(y)
+    for r0 in range(0, rows, 65535):   # the grid's row limit
+        n = min(65535, rows - r0)
+        _native.call("m2r_gated_rmsnorm", y.data_ptr() + 2 * r0 * ry[1], ry[1], z.data_ptr() + 2 * r0 * rz[1],
+                     rz[1], _native.ptr(weight), out.data_ptr() + 2 * r0 * channels, channels, n, channels,
+                     group_size, float(eps), stream)
+    return out
+
+
+class _NormHook:
+    """Installed as a mixer's gated-norm `forward` while a controller owns the
+    model: module hooks on the norm (the Resurface adapter's pre-hook among
+    them) still run around it.  Calls the native kernel for a gate z whose
+    operands it supports, else the forward it shadows."""
+
+    __slots__ = ("module", "fallback")
+
+    def __init__(self, module, fallback):
+        self.module, self.fallback = module, fallback
+
+    def __call__(self, x, z=None):
+        m = self.module
+        if (z is not None and x.dtype == torch.float16 and z.dtype == torch.float16 and x.shape == z.shape
+                and _row_view(x, x.shape[-1]) is not None and _row_view(z, z.shape[-1]) is not None
+                and x.data_ptr() % 8 == 0 and z.data_ptr() % 8 == 0 and all(
+                    v[1] % 4 == 0 for v in (_row_view(x, x.shape[-1]), _row_view(z, z.shape[-1])))):
+            return gated_rmsnorm(x, z, m.weight, m.eps, m.group_size)
+        return self.fallback(x, z)
+
+
+def native_norm_compatible(norm, channels, group_size):
+    """True when `norm` is a gated RMS norm the native kernel computes:
+    gate applied before the norm, FP16 weight [channels], no bias, groups of
+    `group_size` (a multiple of 4, at most 4096)."""
+    w = getattr(norm, "weight", None)
+    return (isinstance(w, torch.Tensor) and w.dtype == torch.float16 and tuple(w.shape) == (channels,)
+            and w.is_contiguous() and w.data_ptr() % 8 == 0 and getattr(norm, "bias", None) is None
+            and not getattr(norm, "norm_before_gate", False) and getattr(norm, "group_size", None) == group_size
+            and isinstance(getattr(norm, "eps", None), float) and group_size % 4 == 0 and group_size <= 4096)
+
+
 def _native_conv_ops():
     """mamba_ssm's fused causal-conv kernels when that package is present,
     else (None, None) and the PyTorch arithmetic below is used."""
@@ -108,6 +183,9 @@ class _MixerController:
     subclass supplies `_new_state`, `_scan_layer` and `cache_breakdown`."""
 
     LAYERS, D_MODEL, HEADS, HEADDIM, D_STATE, GROUPS, D_CONV, D_INNER = 56, 4096, 128, 64, 128, 8, 4, 8192
+    # the mixers' gated norms run on the native kernel while installed (their
+    # module hooks still run); False keeps the model's own norm computation
+    native_norm = True
     PARAMETER_TENSORS, PARAMETER_COUNT = 507, 8_236_999_680
     TABLE_SHAPE = (56, 8, 128)
 
@@ -128,6 +206,7 @@ class _MixerController:
         self._conv_sizes = (self.D_INNER, bc, bc)
         self._request: Optional[_Request] = None
         self._hooks = {}          # mixer index -> (module, forward it shadowed or _MISSING)
+        self._norm_hooks = {}     # mixer index -> (gated norm module, forward it shadowed or _MISSING)
         self._running = False     # inside backbone()
         self._rates = {}
         self._packed = None
@@ -214,6 +293,15 @@ class _MixerController:
             for index, mx in enumerate(self._mixers):
                 self._hooks[index] = (mx, mx.__dict__.get("forward", _MISSING))
                 mx.forward = _LayerHook(self, index, mx)
+            if self.native_norm:
+                # the gated norm stays a module call (its hooks run); its
+                # computation moves to the native kernel while installed
+                for index, mx in enumerate(self._mixers):
+                    norm = mx.norm
+                    if native_norm_compatible(norm, self.D_INNER, self.D_INNER // self.GROUPS):
+                        shadowed = norm.__dict__.get("forward", _MISSING)
+                        self._norm_hooks[index] = (norm, shadowed)
+                        norm.forward = _NormHook(norm, norm.forward)
         except Exception:
             self.close()
             raise
@@ -229,6 +317,12 @@ class _MixerController:
     def close(self):
         """Remove the hooks (restoring whatever forward each mixer had),
         release the model and drop the request caches."""
+        while self._norm_hooks:
+            _, (norm, shadowed) = self._norm_hooks.popitem()
+            if shadowed is _MISSING:
+                norm.__dict__.pop("forward", None)
+            else:
+                norm.forward = shadowed
         while self._hooks:
             _, (mx, shadowed) = self._hooks.popitem()
             if shadowed is _MISSING:

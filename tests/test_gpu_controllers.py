@@ -421,3 +421,30 @@ def test_packed_projection_outputs_per_layer(model, device):
                 worst = max(worst, err)
                 assert err <= 1e-3, (batch, index, name, err)
     print(f"[controllers] packed projections: worst rel L2 {worst:.2e}", flush=True)
+
+
+def test_native_gated_norm_installed_and_restored(model, device):
+    """While a controller owns the model, every mixer's gated norm is still a
+    module call whose computation is the native kernel; close() restores the
+    module's own forward.  With native_norm False the module keeps it, and
+    the one-token output agrees with the native one within the norm's
+    binary16 rounding propagated through the stack."""
+    from mamba2_recall import state_quant
+    from mamba2_recall.state_quant import StateQuant
+    mixers = [layer.mixer for layer in model.backbone.layers]
+    tok = ids(device, 1, 3, seed=31)
+    print("[controllers] native gated norm install / restore", flush=True)
+    with StateQuant(model, mode="s16") as sq:
+        assert all(isinstance(mx.norm.__dict__.get("forward"), state_quant._NormHook) for mx in mixers)
+        h_native = sq.backbone(tok)
+    assert all("forward" not in mx.norm.__dict__ for mx in mixers)
+
+    class Plain(StateQuant):
+        native_norm = False
+    with Plain(model, mode="s16") as sq:
+        assert all("forward" not in mx.norm.__dict__ for mx in mixers)
+        h_module = sq.backbone(tok)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(h_native).all()) and bool(torch.isfinite(h_module).all())
+    rel = float((h_native.float() - h_module.float()).norm() / h_module.float().norm())
+    assert rel < 2e-2, rel
