@@ -837,6 +837,33 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
 
   WaveRaw<HPW> raw;
   float Ah;
+  // Multi-token instances compute the dt activation 64 tokens at a time:
+  // lane j of act64[k] holds (dtv, decay) of token t0 + j for head slot k
+  // (one binary64 chain per 64 tokens instead of one per token); each
+  // token's values are read back with v_readlane.  Same arithmetic as
+  // wave_dt_activation, so the same bits.
+  float2 act64[ONE ? 1 : HPW];
+  auto batch_activation = [&](int t0) {
+    const int tt = min(t0 + lane, L - 1);
+#pragma unroll
+    for (int k = 0; k < HPW; ++k) {
+      const int h = h0 + head_slot(k);
+      const float dtf = h2f(a.dt[((size_t)b * L + tt) * H + h]);
+      const float db = a.db_f32 ? ((const float*)a.dt_bias)[h] : h2f(((const uint16_t*)a.dt_bias)[h]);
+      act64[k] = dt_activation<true>(dtf + db, a.A[h]);   // (rare: constants in vector registers)
+    }
+  };
+  auto token_act = [&](int t) {   // lane k < HPW: head slot k's values of token t
+    const int j = t & 63;
+    float2 r = make_float2(0.f, 0.f);
+#pragma unroll
+    for (int k = HPW - 1; k >= 0; --k) {
+      const float x = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, act64[k].x), j));
+      const float y = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, act64[k].y), j));
+      if (k == HPW - 1 || lane == k) r = make_float2(x, y);
+    }
+    return r;
+  };
   uint32_t d_bits, perm0, perm1;
   uint32_t basis_w[2] = {0u, 0u};
   uint32_t ls_w = 0u;
@@ -990,8 +1017,14 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
       ls_w = DMA ? *(const uint32_t*)(a.lscale + g * 2)
                  : (uint32_t)a.lscale[g * 2] | ((uint32_t)a.lscale[g * 2 + 1] << 16);
     }
-    // dt activation of the first token while the other loads are in flight
-    act = wave_dt_activation<HPW>(raw, Ah, a.db_f32);
+    // dt activation of the first token (multi-token: of the first 64) while
+    // the other loads are in flight
+    if constexpr (ONE) {
+      act = wave_dt_activation<HPW>(raw, Ah, a.db_f32);
+    } else {
+      batch_activation(0);
+      act = token_act(0);
+    }
     // the predictor transfer and the register loads complete before any slot
     // transfer is issued (the compiler's own waits for the register loads then
     // never cover a slot transfer; no load may be scheduled past this wait)
@@ -1262,7 +1295,10 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
       wave_sync();
     }
     if (t == L - 1) slot_copy_out(head_slot(HPW - 1));
-    if (t + 1 < L) act = wave_dt_activation<HPW>(raw, Ah, a.db_f32);
+    if (t + 1 < L) {
+      if (((t + 1) & 63) == 0) batch_activation(t + 1);
+      act = token_act(t + 1);
+    }
   }
 }
 
