@@ -115,6 +115,15 @@ constexpr int tier_packed_of(int j, int T) {
   if (g * 8 + 8 <= T) return g * 8 + (k < 4 ? 2 * k : 2 * (k - 4) + 1);
   return g * 8 + (k < 2 ? 2 * k : 2 * (k - 2) + 1);
 }
+// A two-wave slot steps the INT4 coordinates [0, pair_split(n8, n4)) on the
+// INT8 tier's wave: whole nibble-plane words (a multiple of 8), the split
+// that brings the two waves' coordinate counts closest (none when the INT8
+// tier is the wider one).
+constexpr int pair_split(int n8, int n4) { return n4 > n8 ? 8 * ((n4 - n8 + 7) / 16) : 0; }
+static_assert(pair_split(8, 76) == 32 && pair_split(16, 60) == 24 && pair_split(24, 44) == 8 &&
+                  pair_split(32, 28) == 0 && pair_split(8, 80) == 32,
+              "two-wave INT4 split");
+
 template <int N8, int N4>
 __device__ __forceinline__ int packed_lane(int j) {
   return j < N8 ? tier_packed_of(j, N8) : (j < N8 + N4 ? N8 + tier_packed_of(j - N8, N4) : j);
@@ -487,16 +496,19 @@ __device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, Gro
 // q * s as a packed binary16 subtraction and a product, which is also the
 // IEEE product for infinite and NaN scales (where the fused form gives
 // inf - inf).
-template <int N, bool INT8, int MODE, bool EXACT>
-__device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, float x, const f32x4* bdt4,
-                                           const f32x4* cw4, float& acc, bool finite_in) {
+//
+// tier_update is the first half (dequantization, readout, update and the
+// maximum of |update|; coordinates [0, SA) accumulate the readout into acc,
+// [SA, N) into acc2), tier_requant the second (the new scale and codes from
+// the maximum over the whole tier): a tier split between two waves runs the
+// halves on its parts with the two parts' maxima combined in between.
+template <int N, bool INT8, bool EXACT, int SA = N>
+__device__ __forceinline__ float tier_update(const uint32_t* c, float sc, float decay, float x, const f32x4* bdt4,
+                                             const f32x4* cw4, float& acc, float& acc2, float (&v)[N]) {
   constexpr float BIAS = INT8 ? 128.0f : 8.0f;
-  constexpr float LIM = INT8 ? 127.0f : 7.0f;
-  constexpr float TOP = INT8 ? QTOP127 : QTOP7;
   const float nb = -(1024.0f + BIAS) * sc;
   const f16x2 nbias = {(_Float16)(-(1024.0f + BIAS)), (_Float16)(-(1024.0f + BIAS))};
   const float mz = EXACT ? opaque_neg_zero() : 0.f;
-  float v[N];
   float amax = 0.f;
   // the shared operands of chunk i+1 are read while chunk i computes
   f32x4 cb_next = bdt4[0], cw_next = cw4[0];
@@ -523,7 +535,8 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float prior = pr[j];
-      acc = __builtin_fmaf(prior, cw[j], acc);
+      if (i0 < SA) acc = __builtin_fmaf(prior, cw[j], acc);
+      else acc2 = __builtin_fmaf(prior, cw[j], acc2);
       float u = state_update(prior, decay, cb[j] * x);
       // ordered pin: chunk by chunk, each prior dies as soon as it is used
       asm volatile("" : "+v"(u));
@@ -536,7 +549,17 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
   // Materialize the accumulator and the maximum here: otherwise the compiler
   // sinks their chains (and every update behind the maximum) into the
   // requantization, which keeps every prior and LDS operand live at once.
-  asm volatile("" : "+v"(acc), "+v"(amax));
+  if constexpr (SA > 0 && SA < N) asm volatile("" : "+v"(acc), "+v"(acc2), "+v"(amax));
+  else if constexpr (SA > 0) asm volatile("" : "+v"(acc), "+v"(amax));
+  else asm volatile("" : "+v"(acc2), "+v"(amax));
+  return amax;
+}
+
+template <int N, bool INT8, int MODE>
+__device__ __forceinline__ float tier_requant(const float (&v)[N], uint32_t* c, float amax, bool finite_in) {
+  constexpr float BIAS = INT8 ? 128.0f : 8.0f;
+  constexpr float LIM = INT8 ? 127.0f : 7.0f;
+  constexpr float TOP = INT8 ? QTOP127 : QTOP7;
   const float den = requant_den(amax, LIM, 1.0f / LIM);
   const float stored = round_to_half(den);
   float d, r;
@@ -613,6 +636,22 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
   return stored;
 }
 
+// The whole tier on one wave; SA < N: the readout of coordinates [SA, N)
+// accumulates into acc2 (the order of the two-wave slot, which splits the
+// INT4 tier there).
+template <int N, bool INT8, int MODE, bool EXACT, int SA = N>
+__device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, float x, const f32x4* bdt4,
+                                           const f32x4* cw4, float& acc, float& acc2, bool finite_in) {
+  float v[N];
+  const float amax = tier_update<N, INT8, EXACT, SA>(c, sc, decay, x, bdt4, cw4, acc, acc2, v);
+  return tier_requant<N, INT8, MODE>(v, c, amax, finite_in);
+}
+template <int N, bool INT8, int MODE, bool EXACT>
+__device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, float x, const f32x4* bdt4,
+                                           const f32x4* cw4, float& acc, bool finite_in) {
+  return tier_step<N, INT8, MODE, EXACT, N>(c, sc, decay, x, bdt4, cw4, acc, acc, finite_in);
+}
+
 // One workgroup = WPB waves, each owning HPW head slots of 64 rows (the same
 // P block of NH = WPB * HPW consecutive heads of one B/C group and batch
 // row).  The packed rows of every slot stay in LDS, in the reference's SoA
@@ -647,6 +686,8 @@ struct StepSmem {
   alignas(16) uint32_t pred32[PRED_WORDS];
   alignas(16) std::conditional_t<STAGED, TokenStage, NoStage> stage;
   alignas(16) float pacc[PAIR ? 2 : 1][PAIR ? NH : 1][PAIR ? 64 : 1];
+  // PAIR: the two waves' maxima of their INT4 coordinates (per token parity)
+  alignas(16) float pmax[PAIR ? 2 : 1][PAIR ? NH : 1][2][64];
   alignas(16) uint8_t tile[NH][TILE];
 };
 
@@ -1054,6 +1095,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     rls1 = recip_half(ls1);
   }
 
+  float sc4_carry = 0.f;   // PAIR: the INT8 wave's copy of the slot's INT4 scale
   for (int t = 0; t < L; ++t) {
     const int bt = b * L + t;
     const WaveRaw<HPW> cur = raw;
@@ -1081,15 +1123,26 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
       asm volatile("" : "+s"(hh));
       const int h = h0 + hh;
       wave_priority_by_slots_left(HPW - k);
-      if (t == 0) slot_wait(k);
+      if (t == 0) {
+        slot_wait(k);
+        // a two-wave slot whose INT8 wave also steps INT4 coordinates: the
+        // odd wave's transfers (q4, s4) are visible to it after the barrier
+        if constexpr (PAIR && pair_split(N8, N4) > 0) __syncthreads();
+      }
       uint8_t* tile = s_tile[hh];
       uint16_t* t16 = (uint16_t*)tile;
 
       if constexpr (PAIR) {
-        // ---- one tier per wave (PAIR): the even wave updates and requantizes
-        // the INT8 tier, the odd wave the INT4 tier and the latent
-        // coefficients, then reads out the row with the INT8 wave's partial
-        // sum (published through LDS behind the workgroup barrier) -----------
+        // ---- one slot on two waves (PAIR): the even wave steps the INT8 tier
+        // and the INT4 coordinates [0, SA), the odd wave the INT4 coordinates
+        // [SA, N4) and the latent coefficients.  Each wave first updates its
+        // coordinates (dequantization, readout, update, maximum) and
+        // publishes through LDS what the other needs: the even wave its
+        // readout partial sum, both their INT4 part's maximum.  After the
+        // workgroup barrier both requantize their coordinates (the INT4
+        // scale from the whole tier's maximum, the same on both waves) and
+        // the odd wave reads the row out. --------------------------------------
+        constexpr int SA = pair_split(N8, N4), SB = N4 - SA;
         const float x = h2f(wt.x[0][lane]);
         const float decay = wt.decay[0];
         const float dtv = wt.dtv[0];
@@ -1097,6 +1150,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
         const f32x4* bdt4 = (const f32x4*)wt.bdt[0];
         const f32x4* cw4 = (const f32x4*)cwt;
         float(&pacc)[64] = sm.pacc[t & 1][hh];
+        float(&pmax)[2][64] = sm.pmax[t & 1][hh];
         float acc = 0.f, z0 = 0.f, z1 = 0.f;
         if (role == 0) {
           uint32_t c8[C8];
@@ -1113,11 +1167,41 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
             sc8 = 0.f;
           }
           const bool fin8 = __builtin_fabsf(sc8) <= 65504.f;
+          float v8[N8];
+          float amax8;
           if (__builtin_amdgcn_ballot_w64(!fin8) == 0)
-            sc8 = tier_step<N8, true, MODE, false>(c8, sc8, decay, x, bdt4, cw4, acc, base_ok);
+            amax8 = tier_update<N8, true, false>(c8, sc8, decay, x, bdt4, cw4, acc, acc, v8);
           else
-            sc8 = tier_step<N8, true, MODE, true>(c8, sc8, decay, x, bdt4, cw4, acc, base_ok && fin8);
+            amax8 = tier_update<N8, true, true>(c8, sc8, decay, x, bdt4, cw4, acc, acc, v8);
+          // INT4 coordinates [0, SA): the scale is the tile's at the first
+          // token, then the one this wave requantized with (the odd wave
+          // stores the same value)
+          uint32_t c4[SA > 0 ? SA / 4 : 1];
+          float v4[SA > 0 ? SA : 1];
+          float amax4a = 0.f, s4 = 0.f;
+          bool fin4 = true;
+          if constexpr (SA > 0) {
+            {
+              uint32_t wq[SA / 8];
+              lds_read_row<SA / 2>(tile + O_Q4, lane * W4, wq);
+              plane_to_bytes4<SA>(wq, c4);
+            }
+            s4 = t == 0 ? h2f(t16[O_S4 / 2 + lane]) : sc4_carry;
+            if (PLACEHOLDERS && !valid) {
+#pragma unroll
+              for (int i = 0; i < SA / 4; ++i) c4[i] = 0x08080808u;
+              s4 = 0.f;
+            }
+            fin4 = __builtin_fabsf(s4) <= 65504.f;
+            if (__builtin_amdgcn_ballot_w64(!fin4) == 0)
+              amax4a = tier_update<SA, false, false>(c4, s4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc, acc, v4);
+            else
+              amax4a = tier_update<SA, false, true>(c4, s4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc, acc, v4);
+            pmax[0][lane] = amax4a;
+          }
           pacc[lane] = acc;
+          __syncthreads();   // partial readouts and INT4 maxima are published
+          sc8 = tier_requant<N8, true, MODE>(v8, c8, amax8, base_ok && fin8);
           if (valid) {
             uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4];
             bytes_to_planes8<N8>(c8, wl, wh);
@@ -1125,12 +1209,21 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
             lds_write_row<W8>(tile + O_HI, lane * W8, wh);
             t16[O_S8 / 2 + lane] = f2h(sc8);
           }
+          if constexpr (SA > 0) {
+            const float amax4 = max3_abs(amax4a, pmax[1][lane], 0.f);
+            sc4_carry = tier_requant<SA, false, MODE>(v4, c4, amax4, base_ok && fin4);
+            if (valid) {
+              uint32_t wq[SA / 8];
+              bytes_to_plane4<SA>(c4, wq);
+              lds_write_row<SA / 2>(tile + O_Q4, lane * W4, wq);
+            }
+          }
         } else {
-          uint32_t c4[C4];
+          uint32_t c4[SB / 4];
           {
-            uint32_t wq[(W4 + 3) / 4];
-            lds_read_row<W4>(tile + O_Q4, lane * W4, wq);
-            plane_to_bytes4<N4>(wq, c4);
+            uint32_t wq[(SB / 2 + 3) / 4];
+            lds_read_row<SB / 2>(tile + O_Q4, lane * W4 + SA / 2, wq);
+            plane_to_bytes4<SB>(wq, c4);
           }
           float sc4 = h2f(t16[O_S4 / 2 + lane]);
           if constexpr (RIDGE) {
@@ -1140,15 +1233,19 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           }
           if (PLACEHOLDERS && !valid) {
 #pragma unroll
-            for (int i = 0; i < C4; ++i) c4[i] = 0x08080808u;
+            for (int i = 0; i < SB / 4; ++i) c4[i] = 0x08080808u;
             sc4 = z0 = z1 = 0.f;
           }
           const bool fin4 = __builtin_fabsf(sc4) <= 65504.f;
+          float v4[SB];
+          float amax4;
           if (__builtin_amdgcn_ballot_w64(!fin4) == 0)
-            sc4 = tier_step<N4, false, MODE, false>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc, base_ok);
+            amax4 = tier_update<SB, false, false>(c4, sc4, decay, x, bdt4 + (N8 + SA) / 4, cw4 + (N8 + SA) / 4, acc,
+                                                  acc, v4);
           else
-            sc4 = tier_step<N4, false, MODE, true>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc,
-                                                   base_ok && fin4);
+            amax4 = tier_update<SB, false, true>(c4, sc4, decay, x, bdt4 + (N8 + SA) / 4, cw4 + (N8 + SA) / 4, acc,
+                                                 acc, v4);
+          if constexpr (SA > 0) pmax[1][lane] = amax4;
           uint32_t qz = 0;
           if constexpr (RIDGE) {   // latent step (bit-exact), as in the one-wave slot below
             const float xdt = x * dtv;
@@ -1158,22 +1255,24 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
             const float q1 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn1, ls1, rls1), -448.f), 448.f);
             qz = f32x2_to_e4m3(q0, q1);
           }
+          __syncthreads();   // partial readouts and INT4 maxima are published
+          {
+            const float acc8 = pacc[lane];
+            float out;
+            if constexpr (RIDGE) out = decay * ((acc8 + acc) + z0 * dot1 + z1 * dot2) + x * (dtv * wt.dots[0] + wt.D[0]);
+            else out = decay * (acc8 + acc) + x * (dtv * wt.dots[0] + wt.D[0]);
+            const __amdgpu_buffer_rsrc_t ry = raw_buffer(a.y + ((size_t)bt * H + h) * P + pbase, 2 * nvalid);
+            __builtin_amdgcn_raw_buffer_store_b16(f2h(out), ry, 2 * lane, 0, STORE_THROUGH);
+          }
+          if constexpr (SA > 0) amax4 = max3_abs(pmax[0][lane], amax4, 0.f);
+          sc4 = tier_requant<SB, false, MODE>(v4, c4, amax4, base_ok && fin4);
           if (valid) {
-            uint32_t wq[(W4 + 3) / 4];
-            bytes_to_plane4<N4>(c4, wq);
-            lds_write_row<W4>(tile + O_Q4, lane * W4, wq);
+            uint32_t wq[(SB / 2 + 3) / 4];
+            bytes_to_plane4<SB>(c4, wq);
+            lds_write_row<SB / 2>(tile + O_Q4, lane * W4 + SA / 2, wq);
             t16[O_S4 / 2 + lane] = f2h(sc4);
             if constexpr (RIDGE) t16[O_LAT / 2 + lane] = (uint16_t)qz;
           }
-        }
-        __syncthreads();   // the INT8 waves' partial readouts are published
-        if (role == 1) {
-          const float acc8 = pacc[lane];
-          float out;
-          if constexpr (RIDGE) out = decay * ((acc8 + acc) + z0 * dot1 + z1 * dot2) + x * (dtv * wt.dots[0] + wt.D[0]);
-          else out = decay * (acc8 + acc) + x * (dtv * wt.dots[0] + wt.D[0]);
-          const __amdgpu_buffer_rsrc_t ry = raw_buffer(a.y + ((size_t)bt * H + h) * P + pbase, 2 * nvalid);
-          __builtin_amdgcn_raw_buffer_store_b16(f2h(out), ry, 2 * lane, 0, STORE_THROUGH);
         }
       } else {
         const float x = h2f(wt.x[k][lane]);
@@ -1253,11 +1352,15 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           sc4 = z0 = z1 = 0.f;
         }
         const bool fin4 = __builtin_fabsf(sc4) <= 65504.f;
+        // the readout of the INT4 coordinates [0, SA) continues the INT8
+        // tier's sum, as on the two-wave slot
+        constexpr int SA = pair_split(N8, N4);
         if (__builtin_amdgcn_ballot_w64(!fin4) == 0)
-          sc4 = tier_step<N4, false, MODE, false>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc4, base_ok);
+          sc4 = tier_step<N4, false, MODE, false, SA>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc8, acc4,
+                                                      base_ok);
         else
-          sc4 = tier_step<N4, false, MODE, true>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc4,
-                                                 base_ok && fin4);
+          sc4 = tier_step<N4, false, MODE, true, SA>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc8, acc4,
+                                                     base_ok && fin4);
         __builtin_amdgcn_sched_barrier(0);
         if (t == L - 1 && k > 0) slot_copy_out(hh - 1);   // the previous slot's state (head_slot(k - 1))
         __builtin_amdgcn_sched_barrier(0);
@@ -1294,7 +1397,11 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
       }
       wave_sync();
     }
-    if (t == L - 1) slot_copy_out(head_slot(HPW - 1));
+    if (t == L - 1) {
+      // a two-wave slot's q4 rows hold both waves' last writes after the barrier
+      if constexpr (PAIR && pair_split(N8, N4) > 0) __syncthreads();
+      slot_copy_out(head_slot(HPW - 1));
+    }
     if (t + 1 < L) {
       if (((t + 1) & 63) == 0) batch_activation(t + 1);
       act = token_act(t + 1);
