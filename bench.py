@@ -769,7 +769,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--step-shape", default=None, metavar="WAVES,HEADS",
-                    help="with --only step: force the step kernel's workgroup shape (m2r_set_step_shape), "
+                    help="with --only step or prefill: force the step kernel's workgroup shape (m2r_set_step_shape), "
                          "for counter runs that compare shapes")
     ap.add_argument("--skip-fp4", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
@@ -797,8 +797,12 @@ def main():
                               bytes_written=a.numel(), launches=args.steps)))
         return
 
+    if args.step_shape:
+        if args.only not in ("step", "prefill"):
+            raise SystemExit("--step-shape applies to --only step and --only prefill")
+        _native.call("m2r_set_step_shape", *(int(v) for v in args.step_shape.split(",")))
     if args.only == "prefill":
-        print(json.dumps(dict(only="prefill", prefill_b1_2048=prefill_timing(device))))
+        print(json.dumps(dict(only="prefill", step_shape=args.step_shape, prefill_b1_2048=prefill_timing(device))))
         return
     if args.only == "ceiling":
         print(json.dumps(dict(only="ceiling", ceiling=stream_ceiling(device))))
@@ -823,11 +827,6 @@ def main():
         print(json.dumps(dict(only="layers", batch=args.batch, ms_per_step=round(ms, 5))))
         return
     stack = RidgeStack(args.batch, device)
-    if args.step_shape:
-        if args.only != "step":
-            raise SystemExit("--step-shape applies to --only step")
-        from mamba2_recall import _native
-        _native.call("m2r_set_step_shape", *(int(v) for v in args.step_shape.split(",")))
     g = stack.graph()
     ms, wall_ms = time_graph(g, args.steps, args.warmup)
     nbytes = step_bytes(args.batch, PUBLISHED_LAYOUTS)

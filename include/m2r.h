@@ -75,9 +75,10 @@ int m2r_state_step_legacy(const void* x, const void* dt, const float* A, const v
 /*
  * Test and tuning hook for the three steps above: force the workgroup shape
  * (waves per workgroup, 64-row head slots per wave) to one of (1,1), (4,1),
- * (4,2), (4,4), (8,2), or (4,0): four waves, two per head slot (one per
- * tier; the automatic choice at small batches); (0,0) restores the automatic
- * choice.  A forced shape whose head count does not divide the heads per group
+ * (4,2), (4,4), (8,2), (4,0) = (4,-2): four waves, two per head slot (the
+ * automatic choice at small batches), or (4,-4): four waves, all on one head
+ * slot (each wave steps a quarter of the carried coordinates); (0,0) restores
+ * the automatic choice.  A forced shape whose head count does not divide the heads per group
  * falls back to the automatic choice.  Process-wide; results do not depend on the shape.  No counterpart
  * in the reference (its Triton launch grid is fixed per call).
  */

@@ -14,25 +14,28 @@ namespace m2r {
 // amortized while the grid still spans every CU; small grids keep four waves
 // per workgroup, which splits the per-token shared work four ways.
 // Workgroup shape forced through m2r_set_step_shape (0 = automatic), encoded
-// as waves_per_block * 16 + heads_per_wave.
+// as waves_per_block * 16 + heads_per_wave; (4, 0) = 2 waves per head slot and
+// FOUR_PER_SLOT = 4 waves per head slot, one head per workgroup.
 static std::atomic<int> g_forced_shape{0};
+static constexpr int FOUR_PER_SLOT = 256 + 4 * 16;
 
 // a.dma_tiles: bit 0 = 16-byte LDS transfers of the state rows; bit 1 = the
 // one-token inputs may be staged by dword transfers (the staged prologue of
 // the one-token instances with an even number of heads per workgroup).
-// PAIR: two waves per head slot (one per tier), 4 waves and 2 heads per
-// workgroup: the small-batch shape (one wave per SIMD on twice the CUs).
-template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool PAIR = false>
+// WPS > 1: WPS waves per head slot (each steps a quarter or half of the
+// carried coordinates), 4 waves per workgroup: the small-batch shapes (one
+// wave per SIMD, the slots' work on two or four times the SIMDs).
+template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, int WPS = 1>
 static void launch_shape(const StepArgs& a, dim3 grid, hipStream_t stream) {
-  constexpr bool staged = StepSmem<N8, N4, NZ, MODE, WPB, HPW, true, true, PAIR>::STAGED;
+  constexpr bool staged = StepSmem<N8, N4, NZ, MODE, WPB, HPW, true, true, WPS>::STAGED;
   if ((a.dma_tiles & 1) && a.L == 1 && (!staged || (a.dma_tiles & 2))) {
-    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, WPB, HPW, true, true, PAIR>), grid, dim3(64 * WPB), 0, stream,
+    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, WPB, HPW, true, true, WPS>), grid, dim3(64 * WPB), 0, stream,
                        a);
   } else if (a.dma_tiles & 1) {
-    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, WPB, HPW, true, false, PAIR>), grid, dim3(64 * WPB), 0, stream,
+    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, WPB, HPW, true, false, WPS>), grid, dim3(64 * WPB), 0, stream,
                        a);
   } else {
-    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, WPB, HPW, false, false, PAIR>), grid, dim3(64 * WPB), 0,
+    hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, WPB, HPW, false, false, WPS>), grid, dim3(64 * WPB), 0,
                        stream, a);
   }
 }
@@ -46,7 +49,11 @@ static hipError_t launch_layout(const StepArgs& args, hipStream_t stream) {
   const long long slots = (long long)a.B * a.H * pblocks;
   const int forced = g_forced_shape.load(std::memory_order_relaxed);
   if (forced == 4 * 16 && hpg % 2 == 0) {   // (4, 0): two waves per head slot
-    launch_shape<N8, N4, NZ, MODE, 4, 1, true>(a, dim3(pblocks, a.H / 2, a.B), stream);
+    launch_shape<N8, N4, NZ, MODE, 4, 1, 2>(a, dim3(pblocks, a.H / 2, a.B), stream);
+    return hipGetLastError();
+  }
+  if (forced == FOUR_PER_SLOT) {   // (4, -4): four waves per head slot
+    launch_shape<N8, N4, NZ, MODE, 4, 1, 4>(a, dim3(pblocks, a.H, a.B), stream);
     return hipGetLastError();
   }
   if (forced && (forced & 15) && hpg % ((forced >> 4) * (forced & 15)) == 0) {
@@ -61,8 +68,10 @@ static hipError_t launch_layout(const StepArgs& args, hipStream_t stream) {
   }
   if (hpg % 16 == 0 && slots >= 16LL * 512) {
     launch_shape<N8, N4, NZ, MODE, 4, 4>(a, dim3(pblocks, a.H / 16, a.B), stream);
+  } else if (a.L > 1 && slots <= 256) {   // multi-token, one wave per SIMD with four per slot
+    launch_shape<N8, N4, NZ, MODE, 4, 1, 4>(a, dim3(pblocks, a.H, a.B), stream);
   } else if (hpg % 2 == 0 && slots <= 512) {   // at most one wave per SIMD even with two per slot
-    launch_shape<N8, N4, NZ, MODE, 4, 1, true>(a, dim3(pblocks, a.H / 2, a.B), stream);
+    launch_shape<N8, N4, NZ, MODE, 4, 1, 2>(a, dim3(pblocks, a.H / 2, a.B), stream);
   } else if (hpg % 8 == 0 && slots >= 8LL * 512) {
     launch_shape<N8, N4, NZ, MODE, 4, 2>(a, dim3(pblocks, a.H / 8, a.B), stream);
   } else if (hpg % 4 == 0) {
@@ -181,12 +190,12 @@ int m2r_forced_step_shape() { return g_forced_shape.load(std::memory_order_relax
 
 extern "C" int m2r_set_step_shape(int waves_per_block, int heads_per_wave) {
   const int w = waves_per_block, k = heads_per_wave;
-  const bool ok = (w == 0 && k == 0) || (w == 1 && k == 1) || (w == 4 && (k == 0 || k == 1 || k == 2 || k == 4)) ||
-                  (w == 8 && k == 2);
+  const bool ok = (w == 0 && k == 0) || (w == 1 && k == 1) ||
+                  (w == 4 && (k == 0 || k == 1 || k == 2 || k == 4 || k == -2 || k == -4)) || (w == 8 && k == 2);
   if (!ok)
     return m2r_fail("step shape: supported (waves, heads per wave) are (1,1), (4,1), (4,2), (4,4), (8,2), "
-                    "(4,0) = two waves per head, or (0,0)");
-  g_forced_shape.store(w * 16 + k, std::memory_order_relaxed);
+                    "(4,0) = (4,-2) = two waves per head, (4,-4) = four waves per head, or (0,0)");
+  g_forced_shape.store(k == -4 ? FOUR_PER_SLOT : w * 16 + (k < 0 ? 0 : k), std::memory_order_relaxed);
   return 0;
 }
 

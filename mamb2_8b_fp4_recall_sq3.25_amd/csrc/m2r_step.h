@@ -115,14 +115,79 @@ constexpr int tier_packed_of(int j, int T) {
   if (g * 8 + 8 <= T) return g * 8 + (k < 4 ? 2 * k : 2 * (k - 4) + 1);
   return g * 8 + (k < 2 ? 2 * k : 2 * (k - 2) + 1);
 }
-// A two-wave slot steps the INT4 coordinates [0, pair_split(n8, n4)) on the
-// INT8 tier's wave: whole nibble-plane words (a multiple of 8), the split
-// that brings the two waves' coordinate counts closest (none when the INT8
-// tier is the wider one).
-constexpr int pair_split(int n8, int n4) { return n4 > n8 ? 8 * ((n4 - n8 + 7) / 16) : 0; }
-static_assert(pair_split(8, 76) == 32 && pair_split(16, 60) == 24 && pair_split(24, 44) == 8 &&
-                  pair_split(32, 28) == 0 && pair_split(8, 80) == 32,
-              "two-wave INT4 split");
+// Readout segments.  The carried coordinates, the INT8 tier then the INT4
+// tier in one index space [0, NL), are cut into four segments.  A cut is a
+// whole nibble-plane word into its tier (a multiple of 8 from the tier's
+// start) or the tier boundary n8.  One cut is the two-wave split: the tier
+// boundary, moved into the INT4 tier by the multiple of 8 that brings the two
+// halves' coordinate counts closest when the INT4 tier is the wider one (the
+// INT8 tier is never split between two waves); the other two are the valid
+// cuts that make the largest segment smallest, then the sum of the segments'
+// squares (the lowest cuts on a further tie).  Each
+// segment's readout is one fma chain, and the row's readout their left fold
+// ((s0 + s1) + s2) + s3 on every workgroup shape.  A slot stepped by four
+// waves gives wave r segment r; by two waves, wave 0 the segments before the
+// two-wave split and wave 1 the others.
+constexpr bool seg_cut_ok(int n8, int p) { return p <= n8 ? (p % 8 == 0 || p == n8) : (p - n8) % 8 == 0; }
+constexpr int pair_cut(int n8, int n4) { return n8 + (n4 > n8 ? 8 * ((n4 - n8 + 7) / 16) : 0); }
+struct SegCuts { int c[3]; int j; };   // cuts c[0] < c[1] < c[2]; c[j] is the two-wave split
+constexpr SegCuts seg_cuts(int n8, int n4) {
+  const int nl = n8 + n4, c2 = pair_cut(n8, n4);
+  int v[40] = {};   // the valid cut positions (at most 16 per tier and the boundary)
+  int nv = 0;
+  for (int p = 1; p < nl; ++p)
+    if (seg_cut_ok(n8, p)) v[nv++] = p;
+  SegCuts best{{0, 0, 0}, -1};
+  int best_max = 1 << 30, best_sq = 1 << 30;
+  for (int i = 0; i < nv; ++i)
+    for (int j = i + 1; j < nv; ++j)
+      for (int k = j + 1; k < nv; ++k) {
+        const int a = v[i], b = v[j], c = v[k];
+        if (a != c2 && b != c2 && c != c2) continue;
+        int m = a;
+        if (b - a > m) m = b - a;
+        if (c - b > m) m = c - b;
+        if (nl - c > m) m = nl - c;
+        const int sq = a * a + (b - a) * (b - a) + (c - b) * (c - b) + (nl - c) * (nl - c);
+        if (m < best_max || (m == best_max && sq < best_sq)) {
+          best_max = m;
+          best_sq = sq;
+          best = SegCuts{{a, b, c}, a == c2 ? 0 : b == c2 ? 1 : 2};
+        }
+      }
+  return best;
+}
+constexpr int seg_pos(int n8, int n4, int k) {
+  return k <= 0 ? 0 : k >= 4 ? n8 + n4 : seg_cuts(n8, n4).c[k - 1];
+}
+// first segment of wave r of a WPS-wave slot (r = WPS: 4)
+constexpr int role_seg(int n8, int n4, int wps, int r) {
+  return wps == 4 ? r : wps == 2 ? (r == 0 ? 0 : r == 1 ? seg_cuts(n8, n4).j + 1 : 4) : (r == 0 ? 0 : 4);
+}
+constexpr bool seg_layout_ok(int n8, int n4) { return seg_cuts(n8, n4).j >= 0; }
+static_assert(seg_pos(8, 76, 1) == 16 && seg_pos(8, 76, 2) == 40 && seg_pos(8, 76, 3) == 64 &&
+                  seg_cuts(8, 76).j == 1 && seg_pos(32, 28, 1) == 16 && seg_pos(32, 28, 2) == 32 &&
+                  seg_pos(32, 28, 3) == 48 && seg_pos(36, 20, 1) == 8 && seg_pos(36, 20, 2) == 24 &&
+                  seg_pos(36, 20, 3) == 36 && seg_cuts(36, 20).j == 2 && seg_pos(44, 4, 3) == 44 &&
+                  seg_cuts(44, 4).j == 2 && seg_pos(24, 44, 2) == 32 && seg_pos(16, 60, 3) == 56,
+              "readout segments");
+// segment of carried coordinate p (the cuts as template-level constants, so
+// that a call with an unrolled loop index folds)
+template <int N8, int N4>
+__host__ __device__ __forceinline__ constexpr int seg_of(int p) {
+  constexpr int S1 = seg_pos(N8, N4, 1), S2 = seg_pos(N8, N4, 2), S3 = seg_pos(N8, N4, 3);
+  return p < S1 ? 0 : p < S2 ? 1 : p < S3 ? 2 : 3;
+}
+// bit r: wave r of a WPS-wave slot steps INT8 (TIER4 false) or INT4 coordinates
+template <int N8, int N4, int WPS, bool TIER4>
+constexpr unsigned tier_waves() {
+  unsigned m = 0;
+  for (int r = 0; r < WPS; ++r) {
+    const int lo = seg_pos(N8, N4, role_seg(N8, N4, WPS, r)), hi = seg_pos(N8, N4, role_seg(N8, N4, WPS, r + 1));
+    if (TIER4 ? hi > N8 : lo < N8) m |= 1u << r;
+  }
+  return m;
+}
 
 template <int N8, int N4>
 __device__ __forceinline__ int packed_lane(int j) {
@@ -238,20 +303,20 @@ struct WaveRaw {
 // Every load here is unconditional, with clamped indices (a conditional load
 // makes the compiler wait for it at the end of its branch).
 // A wave's head slots are HPW consecutive heads (slot k of wave w is
-// workgroup head w * HPW + k); PAIR: two waves per head (one per tier), a
-// wave's only slot is head wave / 2.
-template <int WPB, int HPW, bool PAIR = false>
+// workgroup head w * HPW + k); WPS > 1: WPS waves per head, a wave's only
+// slot is head wave / WPS.
+template <int WPB, int HPW, int WPS = 1>
 __device__ __forceinline__ void wave_load_dt(const StepArgs& a, WaveRaw<HPW>& r, int bt, int h0, int lane,
                                              int wave) {
   // lanes >= HPW repeat the last slot
-  const int h = h0 + (PAIR ? (wave >> 1) : wave * HPW + min(lane, HPW - 1));
+  const int h = h0 + (WPS > 1 ? wave / WPS : wave * HPW + min(lane, HPW - 1));
   const uint16_t* db = (const uint16_t*)a.dt_bias;
   r.dt = a.dt[(size_t)bt * a.H + h];
   r.db_lo = db[a.db_f32 ? 2 * h : h];
   r.db_hi = db[a.db_f32 ? 2 * h + 1 : h];
 }
 // ALIGNED: B and C are 4-byte aligned, so a lane's pair is one load each.
-template <int WPB, int HPW, bool ALIGNED, bool PAIR = false>
+template <int WPB, int HPW, bool ALIGNED, int WPS = 1>
 __device__ __forceinline__ void wave_load_rest(const StepArgs& a, WaveRaw<HPW>& r, int bt, int g, int h0,
                                                int pbase, int lane, int wave) {
   const size_t row = ((size_t)bt * a.G + g) * 128 + 2 * lane;
@@ -270,7 +335,7 @@ __device__ __forceinline__ void wave_load_rest(const StepArgs& a, WaveRaw<HPW>& 
   const int p = min(pbase + lane, a.P - 1);   // rows past P read row P-1 (never stored)
 #pragma unroll
   for (int k = 0; k < HPW; ++k) {
-    const int h = h0 + (PAIR ? (wave >> 1) : wave * HPW + k);
+    const int h = h0 + (WPS > 1 ? wave / WPS : wave * HPW + k);
     r.xv[k] = a.x[((size_t)bt * a.H + h) * a.P + p];
   }
 }
@@ -498,13 +563,13 @@ __device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, Gro
 // inf - inf).
 //
 // tier_update is the first half (dequantization, readout, update and the
-// maximum of |update|; coordinates [0, SA) accumulate the readout into acc,
-// [SA, N) into acc2), tier_requant the second (the new scale and codes from
-// the maximum over the whole tier): a tier split between two waves runs the
-// halves on its parts with the two parts' maxima combined in between.
-template <int N, bool INT8, bool EXACT, int SA = N>
+// maximum of |update|; the readout of carried coordinate P0 + i accumulates
+// into acc[seg_of(P0 + i)]), tier_requant the second (the new scale and codes
+// from the maximum over the whole tier): a tier split between waves runs the
+// halves on its parts with the parts' maxima combined in between.
+template <int N, bool INT8, bool EXACT, int N8, int N4, int P0>
 __device__ __forceinline__ float tier_update(const uint32_t* c, float sc, float decay, float x, const f32x4* bdt4,
-                                             const f32x4* cw4, float& acc, float& acc2, float (&v)[N]) {
+                                             const f32x4* cw4, float (&acc)[4], float (&v)[N]) {
   constexpr float BIAS = INT8 ? 128.0f : 8.0f;
   const float nb = -(1024.0f + BIAS) * sc;
   const f16x2 nbias = {(_Float16)(-(1024.0f + BIAS)), (_Float16)(-(1024.0f + BIAS))};
@@ -535,8 +600,8 @@ __device__ __forceinline__ float tier_update(const uint32_t* c, float sc, float 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float prior = pr[j];
-      if (i0 < SA) acc = __builtin_fmaf(prior, cw[j], acc);
-      else acc2 = __builtin_fmaf(prior, cw[j], acc2);
+      const int sg = seg_of<N8, N4>(P0 + i0);   // a whole chunk lies in one segment
+      acc[sg] = __builtin_fmaf(prior, cw[j], acc[sg]);
       float u = state_update(prior, decay, cb[j] * x);
       // ordered pin: chunk by chunk, each prior dies as soon as it is used
       asm volatile("" : "+v"(u));
@@ -549,9 +614,11 @@ __device__ __forceinline__ float tier_update(const uint32_t* c, float sc, float 
   // Materialize the accumulator and the maximum here: otherwise the compiler
   // sinks their chains (and every update behind the maximum) into the
   // requantization, which keeps every prior and LDS operand live at once.
-  if constexpr (SA > 0 && SA < N) asm volatile("" : "+v"(acc), "+v"(acc2), "+v"(amax));
-  else if constexpr (SA > 0) asm volatile("" : "+v"(acc), "+v"(amax));
-  else asm volatile("" : "+v"(acc2), "+v"(amax));
+  constexpr int G0 = seg_of<N8, N4>(P0), G1 = seg_of<N8, N4>(P0 + N - 1);
+  if constexpr (G0 == G1) asm volatile("" : "+v"(acc[G0]), "+v"(amax));
+  else if constexpr (G1 == G0 + 1) asm volatile("" : "+v"(acc[G0]), "+v"(acc[G1]), "+v"(amax));
+  else if constexpr (G1 == G0 + 2) asm volatile("" : "+v"(acc[G0]), "+v"(acc[G0 + 1]), "+v"(acc[G1]), "+v"(amax));
+  else asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(amax));
   return amax;
 }
 
@@ -636,20 +703,13 @@ __device__ __forceinline__ float tier_requant(const float (&v)[N], uint32_t* c, 
   return stored;
 }
 
-// The whole tier on one wave; SA < N: the readout of coordinates [SA, N)
-// accumulates into acc2 (the order of the two-wave slot, which splits the
-// INT4 tier there).
-template <int N, bool INT8, int MODE, bool EXACT, int SA = N>
+// The whole tier on one wave (P0: its first carried coordinate, 0 or N8).
+template <int N, bool INT8, int MODE, bool EXACT, int N8, int N4, int P0>
 __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, float x, const f32x4* bdt4,
-                                           const f32x4* cw4, float& acc, float& acc2, bool finite_in) {
+                                           const f32x4* cw4, float (&acc)[4], bool finite_in) {
   float v[N];
-  const float amax = tier_update<N, INT8, EXACT, SA>(c, sc, decay, x, bdt4, cw4, acc, acc2, v);
+  const float amax = tier_update<N, INT8, EXACT, N8, N4, P0>(c, sc, decay, x, bdt4, cw4, acc, v);
   return tier_requant<N, INT8, MODE>(v, c, amax, finite_in);
-}
-template <int N, bool INT8, int MODE, bool EXACT>
-__device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, float x, const f32x4* bdt4,
-                                           const f32x4* cw4, float& acc, bool finite_in) {
-  return tier_step<N, INT8, MODE, EXACT, N>(c, sc, decay, x, bdt4, cw4, acc, acc, finite_in);
 }
 
 // One workgroup = WPB waves, each owning HPW head slots of 64 rows (the same
@@ -667,10 +727,13 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
 // coefficients and the readout, so that each slot's serial chain is about
 // half as long; `pacc` passes the INT8 tier's readout partial sums (one
 // buffer per token parity).
-template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE, bool PAIR = false>
+template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE, int WPS = 1>
 struct StepSmem {
-  static_assert(!PAIR || (HPW == 1 && WPB % 2 == 0), "two waves per head slot, one slot each");
-  static constexpr int NL = N8 + N4, F = NL + 2, NH = PAIR ? WPB / 2 : WPB * HPW;
+  static constexpr bool PAIR = WPS > 1;
+  static_assert(WPS == 1 || ((WPS == 2 || WPS == 4) && HPW == 1 && WPB % WPS == 0),
+                "two or four waves per head slot, one slot each");
+  static_assert(seg_layout_ok(N8, N4), "four non-empty readout segments");
+  static constexpr int NL = N8 + N4, F = NL + 2, NH = PAIR ? WPB / WPS : WPB * HPW;
   static constexpr bool RIDGE = MODE == MODE_RIDGE, SPLIT = RIDGE && WPB >= 4;
   // one-token instances with an even number of heads per workgroup stage
   // their token inputs in LDS by direct transfers
@@ -685,24 +748,26 @@ struct StepSmem {
   alignas(16) GroupToken<NL> gt[SPLIT && !ONE ? 2 : 1];
   alignas(16) uint32_t pred32[PRED_WORDS];
   alignas(16) std::conditional_t<STAGED, TokenStage, NoStage> stage;
-  alignas(16) float pacc[PAIR ? 2 : 1][PAIR ? NH : 1][PAIR ? 64 : 1];
-  // PAIR: the two waves' maxima of their INT4 coordinates (per token parity)
-  alignas(16) float pmax[PAIR ? 2 : 1][PAIR ? NH : 1][2][64];
+  // WPS > 1 (per token parity): the readout partial sums of waves 0 ..
+  // WPS - 2 of a slot, and every wave's maxima of its INT8 and INT4 parts
+  alignas(16) float pacc[PAIR ? 2 : 1][PAIR ? NH : 1][PAIR ? WPS - 1 : 1][PAIR ? 64 : 1];
+  alignas(16) float pmax[PAIR ? 2 : 1][PAIR ? NH : 1][2][PAIR ? WPS : 1][PAIR ? 64 : 1];
   alignas(16) uint8_t tile[NH][TILE];
 };
 
 // The step of one workgroup: block coordinates (bx, by) and batch row b,
 // arguments `a`, LDS `sm`.  k_state_step runs it on its own grid; the
 // multi-layer kernel runs it with arguments read from a table of layers.
-template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE, bool PAIR = false>
+template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE, int WPS = 1>
 __device__ __forceinline__ void state_step_body(const StepArgs& a,
-                                                StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, PAIR>& sm, int bx,
+                                                StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, WPS>& sm, int bx,
                                                 int by, int b) {
+  constexpr bool PAIR = WPS > 1;      // several waves per slot
   constexpr int W8 = N8 / 2;          // bytes per row of lo and of hi
   constexpr int W4 = N4 / 2;          // bytes per row of q4
   constexpr int NL = N8 + N4;         // carried coordinates
   constexpr int F = NL + 2;           // ridge predictor features
-  constexpr int NH = PAIR ? WPB / 2 : WPB * HPW;
+  constexpr int NH = PAIR ? WPB / WPS : WPB * HPW;
   constexpr int RZ = next_pow2(NZ);
   constexpr bool RIDGE = MODE == MODE_RIDGE;
   constexpr int O_LO = 0, O_HI = 64 * W8, O_Q4 = 128 * W8, O_S8 = O_Q4 + 64 * W4, O_S4 = O_S8 + 128;
@@ -718,7 +783,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   static_assert(!RIDGE || (F * NZ) % 2 == 0, "predictor staged as dwords");
   static_assert(TILE % 16 == 0, "tiles stay 16-byte aligned");
 
-  using Smem = StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, PAIR>;
+  using Smem = StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, WPS>;
   static_assert(Smem::TILE == TILE && Smem::PRED_WORDS == (DMA ? PRED_OPS16 * 256 : PRED_OPS * 64), "LDS layout");
   constexpr bool SPLIT = Smem::SPLIT;
   auto& s_wt = sm.wt;
@@ -729,10 +794,12 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: per-wave values in SGPRs
-  // PAIR: tier role of the wave (0: INT8 tier; 1: INT4 tier, latent, readout)
-  const int role = PAIR ? (wave & 1) : 0;
+  // WPS > 1: the wave's role in its slot (0: also moves the INT8 fields;
+  // WPS - 1: also moves the INT4 fields, steps the latent coefficients and
+  // reads the rows out)
+  const int role = PAIR ? (wave & (WPS - 1)) : 0;
   // workgroup-local head of the wave's slot k
-  auto head_slot = [&](int k) { return PAIR ? (wave >> 1) : wave * HPW + k; };
+  auto head_slot = [&](int k) { return PAIR ? wave / WPS : wave * HPW + k; };
   const int h0 = by * NH;
   const int H = a.H, P = a.P;
   // ONE: the one-token (decode) instance, with a compile-time token count:
@@ -763,7 +830,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   constexpr int SLOT_DMA = PAIR ? OPS8 + OPS4 : 2 * C8W + 1 + C4W;
   static_assert(SLOT_DMA <= 63, "a slot's transfers must fit the vmcnt range");
   static_assert(O_S4 == O_S8 + 128 && O_LAT == O_S4 + 128, "two-byte fields back to back in the tile");
-  const bool own8 = !PAIR || role == 0, own4 = !PAIR || role == 1;   // the fields this wave moves
+  const bool own8 = !PAIR || role == 0, own4 = !PAIR || role == WPS - 1;   // the fields this wave moves
   auto slot_row0 = [&](int hh) { return (b * H + h0 + hh) * P + pbase; };
   auto slot_dma = [&](int hh) {   // direct global -> LDS transfers
     const int row0 = slot_row0(hh);
@@ -781,7 +848,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
       field_dma16_tile<W8, O_LO>(tl, a.lo, row0, nvalid, lane);
       field_dma16_tile<W8, O_HI>(tl, a.hi, row0, nvalid, lane);
       scale_fields_dma16_tile<1, O_S8>(tl, s8, s8, s8, row0, nvalid, lane);
-    } else {
+    } else if (own4) {
       field_dma16_tile<W4, O_Q4>(tl, a.q4, row0, nvalid, lane);
       scale_fields_dma16_tile<RIDGE ? 2 : 1, O_S4>(tl, s4, RIDGE ? a.latent : s4, s4, row0, nvalid, lane);
     }
@@ -838,7 +905,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
         field_write16<W8>(a.lo, v, row0, nvalid, lane);
         field_write16<W8>(a.hi, v + C8W, row0, nvalid, lane);
         field_write16<2>((uint8_t*)a.s8, v + 2 * C8W, row0, nvalid, lane);
-      } else {
+      } else if (own4) {
         field_read16<W4>(t + O_Q4, lane, v);
         field_read16<2>(t + O_S4, lane, v + C4W);
         if constexpr (RIDGE) field_read16<2>(t + O_LAT, lane, v + C4W + C2);
@@ -1004,8 +1071,9 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     act = wave_dt_activation<HPW, !PAIR>(raw, Ah, a.db_f32);
     // this wave's token, statics and predictor transfers have landed
     if (!PAIR) wait_vmcnt<SLOT_DMA>();
-    else if (role == 0) wait_vmcnt<OPS8>();
-    else wait_vmcnt<OPS4>();
+    else if (own8) wait_vmcnt<OPS8>();
+    else if (own4) wait_vmcnt<OPS4>();
+    else wait_vmcnt<0>();
     __syncthreads();          // ... and every other wave's
     const uint32_t bw = st.b[lane], cw = st.c[lane];
     raw.bc[0] = (uint16_t)bw;
@@ -1029,7 +1097,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     // token is built; each later slot is fetched while the previous computes --
     // (order: the dt inputs, the predictor transfer, then the rest; the dt
     // activation's wait for its inputs thus covers only the first two)
-    wave_load_dt<WPB, HPW, PAIR>(a, raw, b * L, h0, lane, wave);
+    wave_load_dt<WPB, HPW, WPS>(a, raw, b * L, h0, lane, wave);
     const int hl = h0 + head_slot(min(lane, HPW - 1));   // head of slot `lane` (lanes < HPW)
     Ah = a.A[hl];
     if constexpr (RIDGE) {
@@ -1042,7 +1110,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           lds_dma_b32(pg + 4 * min(j * 64 + lane, PRED_DW - 1), lds_address(s_pred32 + 64 * j));
       }
     }
-    wave_load_rest<WPB, HPW, DMA, PAIR>(a, raw, b * L, g, h0, pbase, lane, wave);
+    wave_load_rest<WPB, HPW, DMA, WPS>(a, raw, b * L, g, h0, pbase, lane, wave);
     // statics, kept as loaded bits until the first token's full wait (a
     // conversion here would make the compiler wait for them before the dt
     // activation)
@@ -1095,13 +1163,17 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     rls1 = recip_half(ls1);
   }
 
-  float sc4_carry = 0.f;   // PAIR: the INT8 wave's copy of the slot's INT4 scale
+  // WPS > 1: the wave's copies of its slot's INT8 and INT4 scales
+  float sc8_carry = 0.f, sc4_carry = 0.f;
+  // a wave steps coordinates of a field another wave moves (not so only for
+  // two waves split at the tier boundary)
+  constexpr bool CROSS = PAIR && !(WPS == 2 && pair_cut(N8, N4) == N8);
   for (int t = 0; t < L; ++t) {
     const int bt = b * L + t;
     const WaveRaw<HPW> cur = raw;
     if (t + 1 < L) {   // prefetch
-      wave_load_dt<WPB, HPW, PAIR>(a, raw, bt + 1, h0, lane, wave);
-      wave_load_rest<WPB, HPW, DMA, PAIR>(a, raw, bt + 1, g, h0, pbase, lane, wave);
+      wave_load_dt<WPB, HPW, WPS>(a, raw, bt + 1, h0, lane, wave);
+      wave_load_rest<WPB, HPW, DMA, WPS>(a, raw, bt + 1, g, h0, pbase, lane, wave);
     }
     GroupToken<NL>& gt = s_gt[SPLIT && !ONE ? (t & 1) : 0];
     wave_token_build<N8, N4, NZ, MODE, WPB, HPW, Smem::STAGED>(wt, gt, cur, act, pv0, pv1, e0v, e1v, s_pred, t == 0,
@@ -1125,129 +1197,97 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
       wave_priority_by_slots_left(HPW - k);
       if (t == 0) {
         slot_wait(k);
-        // a two-wave slot whose INT8 wave also steps INT4 coordinates: the
-        // odd wave's transfers (q4, s4) are visible to it after the barrier
-        if constexpr (PAIR && pair_split(N8, N4) > 0) __syncthreads();
+        // a slot on several waves where a wave steps fields another one
+        // moved: those transfers are visible to it after the barrier
+        if constexpr (CROSS) __syncthreads();
       }
       uint8_t* tile = s_tile[hh];
       uint16_t* t16 = (uint16_t*)tile;
 
       if constexpr (PAIR) {
-        // ---- one slot on two waves (PAIR): the even wave steps the INT8 tier
-        // and the INT4 coordinates [0, SA), the odd wave the INT4 coordinates
-        // [SA, N4) and the latent coefficients.  Each wave first updates its
-        // coordinates (dequantization, readout, update, maximum) and
-        // publishes through LDS what the other needs: the even wave its
-        // readout partial sum, both their INT4 part's maximum.  After the
-        // workgroup barrier both requantize their coordinates (the INT4
-        // scale from the whole tier's maximum, the same on both waves) and
-        // the odd wave reads the row out. --------------------------------------
-        constexpr int SA = pair_split(N8, N4), SB = N4 - SA;
+        // ---- one slot on WPS waves: wave r updates the coordinates of its
+        // readout segments (dequantization, readout, update, maximum) and
+        // publishes through LDS what the others need (waves 0 .. WPS - 2
+        // their readout partial sum, every wave its INT8 and INT4 parts'
+        // maxima); after the workgroup barrier each requantizes its
+        // coordinates with the whole tiers' maxima (the same values on every
+        // wave, so the same scales and codes as one wave gets) and the last
+        // wave steps the latent coefficients and reads the row out. ---------
         const float x = h2f(wt.x[0][lane]);
         const float decay = wt.decay[0];
         const float dtv = wt.dtv[0];
         const bool base_ok = wt.bounded[0] != 0 && __builtin_fabsf(x) <= 65504.f;
         const f32x4* bdt4 = (const f32x4*)wt.bdt[0];
         const f32x4* cw4 = (const f32x4*)cwt;
-        float(&pacc)[64] = sm.pacc[t & 1][hh];
-        float(&pmax)[2][64] = sm.pmax[t & 1][hh];
-        float acc = 0.f, z0 = 0.f, z1 = 0.f;
-        if (role == 0) {
-          uint32_t c8[C8];
-          {
-            uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4];
-            lds_read_row<W8>(tile + O_LO, lane * W8, wl);
-            lds_read_row<W8>(tile + O_HI, lane * W8, wh);
-            planes_to_bytes8<N8>(wl, wh, c8);
-          }
-          float sc8 = h2f(t16[O_S8 / 2 + lane]);
-          if (PLACEHOLDERS && !valid) {   // rows past P: finite placeholders, never stored
-#pragma unroll
-            for (int i = 0; i < C8; ++i) c8[i] = 0x80808080u;
-            sc8 = 0.f;
-          }
-          const bool fin8 = __builtin_fabsf(sc8) <= 65504.f;
-          float v8[N8];
-          float amax8;
-          if (__builtin_amdgcn_ballot_w64(!fin8) == 0)
-            amax8 = tier_update<N8, true, false>(c8, sc8, decay, x, bdt4, cw4, acc, acc, v8);
-          else
-            amax8 = tier_update<N8, true, true>(c8, sc8, decay, x, bdt4, cw4, acc, acc, v8);
-          // INT4 coordinates [0, SA): the scale is the tile's at the first
-          // token, then the one this wave requantized with (the odd wave
-          // stores the same value)
-          uint32_t c4[SA > 0 ? SA / 4 : 1];
-          float v4[SA > 0 ? SA : 1];
-          float amax4a = 0.f, s4 = 0.f;
-          bool fin4 = true;
-          if constexpr (SA > 0) {
+        auto& pacc = sm.pacc[t & 1][hh];
+        auto& pmax = sm.pmax[t & 1][hh];
+        auto role_body = [&](auto role_c) {
+          constexpr int R = decltype(role_c)::value;
+          constexpr int G0 = role_seg(N8, N4, WPS, R), G1 = role_seg(N8, N4, WPS, R + 1);   // its segments
+          constexpr int PLO = seg_pos(N8, N4, G0), PHI = seg_pos(N8, N4, G1);
+          constexpr int A8 = PLO < N8 ? PLO : N8, E8 = PHI < N8 ? PHI : N8;
+          constexpr int A4 = PLO > N8 ? PLO - N8 : 0, E4 = PHI > N8 ? PHI - N8 : 0;
+          constexpr int M8 = E8 - A8, M4 = E4 - A4;   // this wave's INT8 and INT4 coordinates
+          constexpr bool LAST = R == WPS - 1;
+          constexpr unsigned HAS8 = tier_waves<N8, N4, WPS, false>(), HAS4 = tier_waves<N8, N4, WPS, true>();
+          // a tier's maximum is published only when another wave steps part of it
+          constexpr bool SHARE8 = (HAS8 & (HAS8 - 1)) != 0, SHARE4 = (HAS4 & (HAS4 - 1)) != 0;
+          float accs[4] = {0.f, 0.f, 0.f, 0.f};
+          uint32_t c8[M8 > 0 ? (M8 + 3) / 4 : 1], c4[M4 > 0 ? (M4 + 3) / 4 : 1];
+          float v8[M8 > 0 ? M8 : 1], v4[M4 > 0 ? M4 : 1];
+          float amax8 = 0.f, amax4 = 0.f, s8 = 0.f, s4 = 0.f, z0 = 0.f, z1 = 0.f;
+          bool fin8 = true, fin4 = true;
+          // a tier's scale: the tile's at the first token, then the value this
+          // wave requantized with (every wave of the tier derives the same one)
+          if constexpr (M8 > 0) {
             {
-              uint32_t wq[SA / 8];
-              lds_read_row<SA / 2>(tile + O_Q4, lane * W4, wq);
-              plane_to_bytes4<SA>(wq, c4);
+              uint32_t wl[(M8 / 2 + 3) / 4], wh[(M8 / 2 + 3) / 4];
+              lds_read_row<M8 / 2>(tile + O_LO, lane * W8 + A8 / 2, wl);
+              lds_read_row<M8 / 2>(tile + O_HI, lane * W8 + A8 / 2, wh);
+              planes_to_bytes8<M8>(wl, wh, c8);
+            }
+            s8 = t == 0 ? h2f(t16[O_S8 / 2 + lane]) : sc8_carry;
+            if (PLACEHOLDERS && !valid) {   // rows past P: finite placeholders, never stored
+#pragma unroll
+              for (int i = 0; i < (M8 + 3) / 4; ++i) c8[i] = 0x80808080u;
+              s8 = 0.f;
+            }
+            fin8 = __builtin_fabsf(s8) <= 65504.f;
+            if (__builtin_amdgcn_ballot_w64(!fin8) == 0)
+              amax8 = tier_update<M8, true, false, N8, N4, A8>(c8, s8, decay, x, bdt4 + A8 / 4, cw4 + A8 / 4, accs, v8);
+            else
+              amax8 = tier_update<M8, true, true, N8, N4, A8>(c8, s8, decay, x, bdt4 + A8 / 4, cw4 + A8 / 4, accs, v8);
+            if constexpr (SHARE8) pmax[0][R][lane] = amax8;
+          }
+          if constexpr (LAST && RIDGE) {   // the latent coefficients, read with the rows
+            const uint32_t lat = t16[O_LAT / 2 + lane];
+            z0 = e4m3_byte_to_f32<0>(lat) * ls0;
+            z1 = e4m3_byte_to_f32<1>(lat) * ls1;
+            if (PLACEHOLDERS && !valid) z0 = z1 = 0.f;
+          }
+          if constexpr (M4 > 0) {
+            {
+              uint32_t wq[(M4 / 2 + 3) / 4];
+              lds_read_row<M4 / 2>(tile + O_Q4, lane * W4 + A4 / 2, wq);
+              plane_to_bytes4<M4>(wq, c4);
             }
             s4 = t == 0 ? h2f(t16[O_S4 / 2 + lane]) : sc4_carry;
             if (PLACEHOLDERS && !valid) {
 #pragma unroll
-              for (int i = 0; i < SA / 4; ++i) c4[i] = 0x08080808u;
+              for (int i = 0; i < (M4 + 3) / 4; ++i) c4[i] = 0x08080808u;
               s4 = 0.f;
             }
             fin4 = __builtin_fabsf(s4) <= 65504.f;
             if (__builtin_amdgcn_ballot_w64(!fin4) == 0)
-              amax4a = tier_update<SA, false, false>(c4, s4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc, acc, v4);
+              amax4 = tier_update<M4, false, false, N8, N4, N8 + A4>(c4, s4, decay, x, bdt4 + (N8 + A4) / 4,
+                                                                     cw4 + (N8 + A4) / 4, accs, v4);
             else
-              amax4a = tier_update<SA, false, true>(c4, s4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc, acc, v4);
-            pmax[0][lane] = amax4a;
+              amax4 = tier_update<M4, false, true, N8, N4, N8 + A4>(c4, s4, decay, x, bdt4 + (N8 + A4) / 4,
+                                                                    cw4 + (N8 + A4) / 4, accs, v4);
+            if constexpr (SHARE4) pmax[1][R][lane] = amax4;
           }
-          pacc[lane] = acc;
-          __syncthreads();   // partial readouts and INT4 maxima are published
-          sc8 = tier_requant<N8, true, MODE>(v8, c8, amax8, base_ok && fin8);
-          if (valid) {
-            uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4];
-            bytes_to_planes8<N8>(c8, wl, wh);
-            lds_write_row<W8>(tile + O_LO, lane * W8, wl);
-            lds_write_row<W8>(tile + O_HI, lane * W8, wh);
-            t16[O_S8 / 2 + lane] = f2h(sc8);
-          }
-          if constexpr (SA > 0) {
-            const float amax4 = max3_abs(amax4a, pmax[1][lane], 0.f);
-            sc4_carry = tier_requant<SA, false, MODE>(v4, c4, amax4, base_ok && fin4);
-            if (valid) {
-              uint32_t wq[SA / 8];
-              bytes_to_plane4<SA>(c4, wq);
-              lds_write_row<SA / 2>(tile + O_Q4, lane * W4, wq);
-            }
-          }
-        } else {
-          uint32_t c4[SB / 4];
-          {
-            uint32_t wq[(SB / 2 + 3) / 4];
-            lds_read_row<SB / 2>(tile + O_Q4, lane * W4 + SA / 2, wq);
-            plane_to_bytes4<SB>(wq, c4);
-          }
-          float sc4 = h2f(t16[O_S4 / 2 + lane]);
-          if constexpr (RIDGE) {
-            const uint32_t lat = t16[O_LAT / 2 + lane];
-            z0 = e4m3_byte_to_f32<0>(lat) * ls0;
-            z1 = e4m3_byte_to_f32<1>(lat) * ls1;
-          }
-          if (PLACEHOLDERS && !valid) {
-#pragma unroll
-            for (int i = 0; i < SB / 4; ++i) c4[i] = 0x08080808u;
-            sc4 = z0 = z1 = 0.f;
-          }
-          const bool fin4 = __builtin_fabsf(sc4) <= 65504.f;
-          float v4[SB];
-          float amax4;
-          if (__builtin_amdgcn_ballot_w64(!fin4) == 0)
-            amax4 = tier_update<SB, false, false>(c4, sc4, decay, x, bdt4 + (N8 + SA) / 4, cw4 + (N8 + SA) / 4, acc,
-                                                  acc, v4);
-          else
-            amax4 = tier_update<SB, false, true>(c4, sc4, decay, x, bdt4 + (N8 + SA) / 4, cw4 + (N8 + SA) / 4, acc,
-                                                 acc, v4);
-          if constexpr (SA > 0) pmax[1][lane] = amax4;
           uint32_t qz = 0;
-          if constexpr (RIDGE) {   // latent step (bit-exact), as in the one-wave slot below
+          if constexpr (LAST && RIDGE) {   // latent step (bit-exact), as in the one-wave slot below
             const float xdt = x * dtv;
             const float zn0 = state_update(z0, decay, xdt * dot3);
             const float zn1 = state_update(z1, decay, xdt * dot4);
@@ -1255,24 +1295,69 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
             const float q1 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn1, ls1, rls1), -448.f), 448.f);
             qz = f32x2_to_e4m3(q0, q1);
           }
-          __syncthreads();   // partial readouts and INT4 maxima are published
-          {
-            const float acc8 = pacc[lane];
+          // the left fold of the readout segments: waves before the last
+          // publish the fold of their segments, the last continues it
+          float part = 0.f;
+          if constexpr (!LAST) {
+            part = accs[G0];
+#pragma unroll
+            for (int sg = G0 + 1; sg < G1; ++sg) part = part + accs[sg];
+            pacc[R][lane] = part;
+          }
+          __syncthreads();   // readout partials and tier maxima are published
+          if constexpr (LAST) {
+            float acc = pacc[0][lane];
+#pragma unroll
+            for (int r = 1; r < WPS - 1; ++r) acc = acc + pacc[r][lane];
+#pragma unroll
+            for (int sg = G0; sg < 4; ++sg) acc = acc + accs[sg];
             float out;
-            if constexpr (RIDGE) out = decay * ((acc8 + acc) + z0 * dot1 + z1 * dot2) + x * (dtv * wt.dots[0] + wt.D[0]);
-            else out = decay * (acc8 + acc) + x * (dtv * wt.dots[0] + wt.D[0]);
+            if constexpr (RIDGE) out = decay * (acc + z0 * dot1 + z1 * dot2) + x * (dtv * wt.dots[0] + wt.D[0]);
+            else out = decay * acc + x * (dtv * wt.dots[0] + wt.D[0]);
             const __amdgpu_buffer_rsrc_t ry = raw_buffer(a.y + ((size_t)bt * H + h) * P + pbase, 2 * nvalid);
             __builtin_amdgcn_raw_buffer_store_b16(f2h(out), ry, 2 * lane, 0, STORE_THROUGH);
           }
-          if constexpr (SA > 0) amax4 = max3_abs(pmax[0][lane], amax4, 0.f);
-          sc4 = tier_requant<SB, false, MODE>(v4, c4, amax4, base_ok && fin4);
-          if (valid) {
-            uint32_t wq[(SB / 2 + 3) / 4];
-            bytes_to_plane4<SB>(c4, wq);
-            lds_write_row<SB / 2>(tile + O_Q4, lane * W4 + SA / 2, wq);
-            t16[O_S4 / 2 + lane] = f2h(sc4);
-            if constexpr (RIDGE) t16[O_LAT / 2 + lane] = (uint16_t)qz;
+          // the whole tiers' maxima (maxima are exact: any order)
+          auto tier_max = [&](int tier, float own, unsigned has) {
+            float m = own;
+#pragma unroll
+            for (int r = 0; r < WPS; ++r)
+              if (r != R && ((has >> r) & 1u)) m = max3_abs(m, pmax[tier][r][lane], 0.f);
+            return m;
+          };
+          if constexpr (M8 > 0) {
+            const float m8 = tier_max(0, amax8, HAS8);
+            sc8_carry = tier_requant<M8, true, MODE>(v8, c8, m8, base_ok && fin8);
+            if (valid) {
+              uint32_t wl[(M8 / 2 + 3) / 4], wh[(M8 / 2 + 3) / 4];
+              bytes_to_planes8<M8>(c8, wl, wh);
+              lds_write_row<M8 / 2>(tile + O_LO, lane * W8 + A8 / 2, wl);
+              lds_write_row<M8 / 2>(tile + O_HI, lane * W8 + A8 / 2, wh);
+              if constexpr (R == 0) t16[O_S8 / 2 + lane] = f2h(sc8_carry);
+            }
           }
+          if constexpr (M4 > 0) {
+            const float m4 = tier_max(1, amax4, HAS4);
+            sc4_carry = tier_requant<M4, false, MODE>(v4, c4, m4, base_ok && fin4);
+            if (valid) {
+              uint32_t wq[(M4 / 2 + 3) / 4];
+              bytes_to_plane4<M4>(c4, wq);
+              lds_write_row<M4 / 2>(tile + O_Q4, lane * W4 + A4 / 2, wq);
+              if constexpr (LAST) t16[O_S4 / 2 + lane] = f2h(sc4_carry);
+            }
+          }
+          if constexpr (LAST && RIDGE) {
+            if (valid) t16[O_LAT / 2 + lane] = (uint16_t)qz;
+          }
+        };
+        if constexpr (WPS == 2) {
+          if (role == 0) role_body(std::integral_constant<int, 0>{});
+          else role_body(std::integral_constant<int, 1>{});
+        } else {
+          if (role == 0) role_body(std::integral_constant<int, 0>{});
+          else if (role == 1) role_body(std::integral_constant<int, 1>{});
+          else if (role == 2) role_body(std::integral_constant<int, 2>{});
+          else role_body(std::integral_constant<int, 3>{});
         }
       } else {
         const float x = h2f(wt.x[k][lane]);
@@ -1283,7 +1368,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
         const f32x4* cw4 = (const f32x4*)cwt;
         // the readout's partial sums per tier, added after both (the same order
         // as the two-wave slot, whose tiers run on different waves)
-        float acc8 = 0.f, acc4 = 0.f;
+        float accs[4] = {0.f, 0.f, 0.f, 0.f};
 
         // ---- INT8 tier: unpack (byte k of c8[i] is q8 + 128 of internal
         // coordinate 4i+k), update with readout accumulation, requantize and
@@ -1309,9 +1394,9 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           }
           const bool fin8 = __builtin_fabsf(sc8) <= 65504.f;
           if (__builtin_amdgcn_ballot_w64(!fin8) == 0)
-            sc8 = tier_step<N8, true, MODE, false>(c8, sc8, decay, x, bdt4, cw4, acc8, base_ok);
+            sc8 = tier_step<N8, true, MODE, false, N8, N4, 0>(c8, sc8, decay, x, bdt4, cw4, accs, base_ok);
           else
-            sc8 = tier_step<N8, true, MODE, true>(c8, sc8, decay, x, bdt4, cw4, acc8, base_ok && fin8);
+            sc8 = tier_step<N8, true, MODE, true, N8, N4, 0>(c8, sc8, decay, x, bdt4, cw4, accs, base_ok && fin8);
           if (valid) {
             uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4];
             bytes_to_planes8<N8>(c8, wl, wh);
@@ -1352,19 +1437,16 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           sc4 = z0 = z1 = 0.f;
         }
         const bool fin4 = __builtin_fabsf(sc4) <= 65504.f;
-        // the readout of the INT4 coordinates [0, SA) continues the INT8
-        // tier's sum, as on the two-wave slot
-        constexpr int SA = pair_split(N8, N4);
         if (__builtin_amdgcn_ballot_w64(!fin4) == 0)
-          sc4 = tier_step<N4, false, MODE, false, SA>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc8, acc4,
-                                                      base_ok);
+          sc4 = tier_step<N4, false, MODE, false, N8, N4, N8>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, accs,
+                                                              base_ok);
         else
-          sc4 = tier_step<N4, false, MODE, true, SA>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, acc8, acc4,
-                                                     base_ok && fin4);
+          sc4 = tier_step<N4, false, MODE, true, N8, N4, N8>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, accs,
+                                                             base_ok && fin4);
         __builtin_amdgcn_sched_barrier(0);
         if (t == L - 1 && k > 0) slot_copy_out(hh - 1);   // the previous slot's state (head_slot(k - 1))
         __builtin_amdgcn_sched_barrier(0);
-        const float acc = acc8 + acc4;
+        const float acc = ((accs[0] + accs[1]) + accs[2]) + accs[3];   // the readout segments' left fold
         // readout: sum_i u_i c_i + corrections = decay * (sum_i prior_i (c_i +
         // corr_i) + latent terms) + x * (dt * sum_all b c + D)
         float out;
@@ -1398,8 +1480,8 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
       wave_sync();
     }
     if (t == L - 1) {
-      // a two-wave slot's q4 rows hold both waves' last writes after the barrier
-      if constexpr (PAIR && pair_split(N8, N4) > 0) __syncthreads();
+      // ... and the moving wave writes back every wave's last values
+      if constexpr (CROSS) __syncthreads();
       slot_copy_out(head_slot(HPW - 1));
     }
     if (t + 1 < L) {
@@ -1409,11 +1491,11 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   }
 }
 
-template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE, bool PAIR = false>
-__global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(WPB == 8 && !PAIR ? 4 : 2, 8)))
+template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE, int WPS = 1>
+__global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(WPB == 8 && WPS == 1 ? 4 : 2, 8)))
 void k_state_step(StepArgs a) {
-  __shared__ StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, PAIR> sm;
-  state_step_body<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, PAIR>(a, sm, blockIdx.x, blockIdx.y, blockIdx.z);
+  __shared__ StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, WPS> sm;
+  state_step_body<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, WPS>(a, sm, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 }  // namespace m2r

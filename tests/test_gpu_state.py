@@ -245,7 +245,7 @@ def test_ridge_unvalidated_scan_still_checks_table_shapes(device):
     assert all(torch.equal(before[k], state.tensors[k]) for k in before)
 
 
-SHAPES = [(1, 1), (4, 1), (4, 2), (4, 4), (8, 2), (4, 0)]
+SHAPES = [(1, 1), (4, 1), (4, 2), (4, 4), (8, 2), (4, 0), (4, -4)]
 
 
 @pytest.fixture

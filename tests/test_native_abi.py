@@ -41,14 +41,14 @@ def test_error_reporting_without_device():
 
 def test_step_shape_hook_accepts_documented_shapes_only():
     """m2r_set_step_shape takes the documented shapes, including (4, 0) (two
-    waves per head slot), rejects the others with a message, and (0, 0)
+    waves per head slot) and (4, -4) (four), rejects the others with a message, and (0, 0)
     restores the automatic choice (no launch, no device)."""
     from mamba2_recall import _native
     lib = _native.lib()
     try:
-        for shape in [(1, 1), (4, 1), (4, 2), (4, 4), (8, 2), (4, 0), (0, 0)]:
+        for shape in [(1, 1), (4, 1), (4, 2), (4, 4), (8, 2), (4, 0), (4, -2), (4, -4), (0, 0)]:
             assert lib.m2r_set_step_shape(*shape) == 0, shape
-        for shape in [(8, 0), (2, 2), (8, 4), (1, 0), (16, 1)]:
+        for shape in [(8, 0), (2, 2), (8, 4), (1, 0), (16, 1), (4, -3), (8, -4), (4, -1)]:
             assert lib.m2r_set_step_shape(*shape) != 0, shape
             assert b"step shape" in lib.m2r_last_error()
     finally:
