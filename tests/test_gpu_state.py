@@ -256,6 +256,49 @@ def forced_shape(request):
     _native.call("m2r_set_step_shape", 0, 0)
 
 
+@pytest.mark.parametrize("L", [1, 3])
+def test_ridge_every_shape_same_bits(device, L):
+    """Every workgroup shape of four or eight waves, including the slots on
+    two and four waves (whose waves step parts of a tier and share the tier
+    maxima and the readout partial sums), gives the same codes, scales and y
+    bit for bit: the readout is summed per segment of the carried coordinates
+    in one fixed order, and the ridge correction is split the same way.  (The
+    one-wave workgroups compute the correction of the readout weights in
+    another order: the same codes, y within the oracle tolerance, checked by
+    the per-shape tests.)  Layouts whose INT4 tier is split between waves,
+    whose INT8 tier is, and neither."""
+    from mamba2_recall import _native, ridge_codec
+    for layout in ("8_80_40", "24_48_56", "36_24_68", "44_8_76"):
+        n8, n4, nz = ridge_counts(layout)
+        rng = np.random.default_rng(90 + L)
+        B, H, P, G = 2, 16, 64, 1
+        inp = cases.step_inputs(rng, B, L, H, P, G)
+        sta = cases.ridge_statics(rng, G, n8, n4, nz)
+        st0 = cases.random_packed_state(rng, B, H, P, n8, n4, latent=True)
+        t = device_inputs(inp, device)
+        perm = torch.from_numpy(inp["perm"]).to(device)
+        basis, ls, pred = (dev16(sta[k], device) for k in ("basis", "lscale", "pred"))
+        results = []
+        try:
+            for shape in [sh for sh in SHAPES if sh[0] >= 4]:
+                print(f"[same bits] layout={layout} L={L} shape={shape}", flush=True)
+                _native.call("m2r_set_step_shape", *shape)
+                state = ridge_codec.allocate_state(B, H, P, 128, device, layout=layout)
+                to_state(st0, state, device)
+                y, _ = ridge_codec.scan(t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["dt_bias"], state, perm,
+                                        basis, ls, pred, layout=layout)
+                torch.cuda.synchronize()
+                results.append((shape, y.view(torch.int16).clone(),
+                                {k: v.view(torch.uint8).clone() for k, v in state.tensors.items()}))
+        finally:
+            _native.call("m2r_set_step_shape", 0, 0)
+        shape0, y0, s0 = results[0]
+        for shape, y, st in results[1:]:
+            assert torch.equal(y, y0), (layout, L, shape, shape0)
+            for k in s0:
+                assert torch.equal(st[k], s0[k]), (layout, L, shape, k)
+
+
 @pytest.mark.parametrize("forced_shape", SHAPES, indirect=True, ids=lambda s: f"w{s[0]}h{s[1]}")
 def test_ridge_every_workgroup_shape(oracle, device, forced_shape):
     """Each (waves, head slots per wave) variant: multi-token, ragged P, one
