@@ -750,7 +750,7 @@ struct StepSmem {
   alignas(16) std::conditional_t<STAGED, TokenStage, NoStage> stage;
   // WPS > 1 (per token parity): the readout partial sums of waves 0 ..
   // WPS - 2 of a slot, and every wave's maxima of its INT8 and INT4 parts
-  alignas(16) float pacc[PAIR ? 2 : 1][PAIR ? NH : 1][PAIR ? WPS - 1 : 1][PAIR ? 64 : 1];
+  alignas(16) float pacc[PAIR ? 2 : 1][PAIR ? NH : 1][PAIR ? WPS : 1][PAIR ? 64 : 1];
   alignas(16) float pmax[PAIR ? 2 : 1][PAIR ? NH : 1][2][PAIR ? WPS : 1][PAIR ? 64 : 1];
   alignas(16) uint8_t tile[NH][TILE];
 };
@@ -1229,6 +1229,11 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           constexpr int A4 = PLO > N8 ? PLO - N8 : 0, E4 = PHI > N8 ? PHI - N8 : 0;
           constexpr int M8 = E8 - A8, M4 = E4 - A4;   // this wave's INT8 and INT4 coordinates
           constexpr bool LAST = R == WPS - 1;
+          // the wave that reads the rows out: four waves per slot, wave 0 (the
+          // last one also steps the latent coefficients and stores their and
+          // the INT4 scales); two, the last
+          constexpr int RO = WPS == 4 ? 0 : WPS - 1;
+          constexpr bool READS_OUT = R == RO;
           constexpr unsigned HAS8 = tier_waves<N8, N4, WPS, false>(), HAS4 = tier_waves<N8, N4, WPS, true>();
           // a tier's maximum is published only when another wave steps part of it
           constexpr bool SHARE8 = (HAS8 & (HAS8 - 1)) != 0, SHARE4 = (HAS4 & (HAS4 - 1)) != 0;
@@ -1259,7 +1264,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
               amax8 = tier_update<M8, true, true, N8, N4, A8>(c8, s8, decay, x, bdt4 + A8 / 4, cw4 + A8 / 4, accs, v8);
             if constexpr (SHARE8) pmax[0][R][lane] = amax8;
           }
-          if constexpr (LAST && RIDGE) {   // the latent coefficients, read with the rows
+          if constexpr ((LAST || READS_OUT) && RIDGE) {   // the latent coefficients, read with the rows
             const uint32_t lat = t16[O_LAT / 2 + lane];
             z0 = e4m3_byte_to_f32<0>(lat) * ls0;
             z1 = e4m3_byte_to_f32<1>(lat) * ls1;
@@ -1295,22 +1300,24 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
             const float q1 = __builtin_fminf(__builtin_fmaxf(latent_quotient(zn1, ls1, rls1), -448.f), 448.f);
             qz = f32x2_to_e4m3(q0, q1);
           }
-          // the left fold of the readout segments: waves before the last
-          // publish the fold of their segments, the last continues it
-          float part = 0.f;
-          if constexpr (!LAST) {
-            part = accs[G0];
+          // the left fold of the readout segments: the other waves publish
+          // the fold of their segments, the reading wave folds them in order
+          float part = accs[G0];
 #pragma unroll
-            for (int sg = G0 + 1; sg < G1; ++sg) part = part + accs[sg];
-            pacc[R][lane] = part;
-          }
+          for (int sg = G0 + 1; sg < G1; ++sg) part = part + accs[sg];
+          if constexpr (!READS_OUT) pacc[R][lane] = part;
           __syncthreads();   // readout partials and tier maxima are published
-          if constexpr (LAST) {
-            float acc = pacc[0][lane];
+          if constexpr (READS_OUT) {
+            float acc = RO == 0 ? part : pacc[0][lane];
 #pragma unroll
-            for (int r = 1; r < WPS - 1; ++r) acc = acc + pacc[r][lane];
+            for (int r = 1; r < WPS; ++r) {
+              if (r < RO) acc = acc + pacc[r][lane];
+              else if (r > RO) acc = acc + pacc[r][lane];
+            }
+            if constexpr (RO > 0) {   // the reading wave's own segments after the others' before it
 #pragma unroll
-            for (int sg = G0; sg < 4; ++sg) acc = acc + accs[sg];
+              for (int sg = G0; sg < G1; ++sg) acc = acc + accs[sg];
+            }
             float out;
             if constexpr (RIDGE) out = decay * (acc + z0 * dot1 + z1 * dot2) + x * (dtv * wt.dots[0] + wt.D[0]);
             else out = decay * acc + x * (dtv * wt.dots[0] + wt.D[0]);
