@@ -395,6 +395,41 @@ def test_sequential_tokens_equal_one_call(oracle, device):
     assert torch.equal(torch.cat(ys, 1), y_all)
 
 
+@pytest.mark.parametrize("layout,L", [("8_80_40", 2048), ("36_24_68", 300), ("44_8_76", 300)])
+def test_prefill_window_equals_token_by_token(device, layout, L):
+    """The reference's prefill shape (batch 1, 128 heads, 8 groups): one
+    multi-token call (four waves per 64-row slot, the dt activation and its
+    batches of 64 tokens) leaves the same packed state and y bits as L
+    one-token calls (two waves per slot), up to a whole 2048-token window."""
+    from mamba2_recall import ridge_codec
+    n8, n4, nz = ridge_counts(layout)
+    rng = np.random.default_rng(L)
+    batch, H, P, G = 1, 128, 64, 8
+    print(f"[prefill window] layout={layout} L={L}", flush=True)
+    inp = cases.step_inputs(rng, batch, L, H, P, G)
+    sta = cases.ridge_statics(rng, G, n8, n4, nz)
+    st0 = cases.random_packed_state(rng, batch, H, P, n8, n4, latent=True)
+    t = {k: devp(v, device) for k, v in inp.items() if k != "perm"}
+    perm = torch.from_numpy(inp["perm"]).to(device)
+    basis, ls, pred = (dev16(sta[k], device) for k in ("basis", "lscale", "pred"))
+    s_all = ridge_codec.allocate_state(batch, H, P, 128, device, layout=layout)
+    s_seq = ridge_codec.allocate_state(batch, H, P, 128, device, layout=layout)
+    to_state(st0, s_all, device)
+    to_state(st0, s_seq, device)
+    y_all, _ = ridge_codec.scan(t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["dt_bias"], s_all, perm, basis,
+                                ls, pred, layout=layout)
+    y_seq = torch.empty_like(y_all)
+    for i in range(L):
+        sl = slice(i, i + 1)
+        y1, _ = ridge_codec.scan(t["x"][:, sl], t["dt"][:, sl], t["A"], t["B"][:, sl], t["C"][:, sl], t["D"],
+                                 t["dt_bias"], s_seq, perm, basis, ls, pred, layout=layout, validate=False)
+        y_seq[:, sl] = y1
+    torch.cuda.synchronize()
+    assert_state_equal(from_state(s_seq), from_state(s_all), f"prefill window {layout} L={L}")
+    assert torch.equal(y_seq.view(torch.int16), y_all.view(torch.int16))
+    assert torch.isfinite(y_all).all()
+
+
 def run_dense3(oracle, device, kind, batch, L, H, P, G, seed, *, random_state=True, x_scale=1.0, scale_mu=-2.0,
                special_scales=None, nonfinite_y=False):
     """`special_scales`: binary16 bit patterns written into the scales of a
