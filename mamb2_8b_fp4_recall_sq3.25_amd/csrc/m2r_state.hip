@@ -70,7 +70,7 @@ static hipError_t launch_layout(const StepArgs& args, hipStream_t stream) {
     launch_shape<N8, N4, NZ, MODE, 4, 4>(a, dim3(pblocks, a.H / 16, a.B), stream);
   } else if (a.L > 1 && slots <= 512) {   // multi-token: four waves per slot up to two per SIMD
     launch_shape<N8, N4, NZ, MODE, 4, 1, 4>(a, dim3(pblocks, a.H, a.B), stream);
-  } else if (hpg % 2 == 0 && (slots <= 512 || (a.L > 1 && slots <= 1024))) {   // two waves per slot
+  } else if (hpg % 2 == 0 && slots <= 1024) {   // two waves per slot, up to two waves per SIMD
     launch_shape<N8, N4, NZ, MODE, 4, 1, 2>(a, dim3(pblocks, a.H / 2, a.B), stream);
   } else if (hpg % 8 == 0 && slots >= 8LL * 512) {
     launch_shape<N8, N4, NZ, MODE, 4, 2>(a, dim3(pblocks, a.H / 8, a.B), stream);
