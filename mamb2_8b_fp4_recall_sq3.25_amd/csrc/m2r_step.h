@@ -722,11 +722,11 @@ __device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, f
 // publishes the ridge predictor (staged once, shared by all waves).
 // LDS of one workgroup: the waves' token records, the shared ridge-correction
 // record(s), the staged predictor and the slot tiles.
-// PAIR: the small-batch layout, two waves per head slot (HPW == 1): the even
-// wave carries the INT8 tier, the odd wave the INT4 tier, the latent
-// coefficients and the readout, so that each slot's serial chain is about
-// half as long; `pacc` passes the INT8 tier's readout partial sums (one
-// buffer per token parity).
+// WPS > 1: the small-batch layouts, two or four waves per head slot (HPW ==
+// 1), each stepping the coordinates of its readout segments, so that each
+// slot's serial chain is about half or a quarter as long; `pacc` and `pmax`
+// pass the waves' readout partial sums and tier maxima (one buffer per token
+// parity).
 template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE, int WPS = 1>
 struct StepSmem {
   static constexpr bool PAIR = WPS > 1;
@@ -818,12 +818,12 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   const uint16_t* s_pred = (const uint16_t*)s_pred32;
   WaveToken<N8, N4, HPW>& wt = s_wt[wave];
 
-  // vector memory operations per slot transfer (and per state copy-out); in
-  // PAIR mode a wave transfers its tier's fields only: the INT8 wave lo, hi
-  // and s8 (OPS8), the INT4 wave q4, s4 and the latent bytes (OPS4)
-  // (the two-byte fields of a transfer go in one operation: s8, s4 and the
-  // latent bytes of a one-wave slot; s8, or s4 and the latent bytes, in
-  // PAIR mode)
+  // vector memory operations per slot transfer (and per state copy-out); on
+  // a slot of several waves wave 0 transfers the INT8 tier's fields (lo, hi
+  // and s8: OPS8), the last wave the INT4 tier's (q4, s4 and the latent
+  // bytes: OPS4), the others none (the two-byte fields of a transfer go in
+  // one operation: s8, s4 and the latent bytes of a one-wave slot; s8, or s4
+  // and the latent bytes, on a slot of several waves)
   constexpr int C8W = chunk_ops(W8), C4W = chunk_ops(W4);
   constexpr int OPS8 = 2 * C8W + 1;
   constexpr int OPS4 = C4W + 1;
@@ -1067,7 +1067,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     d_bits = vD;
     // (with two waves per SIMD the prologue's scalar issue is its
     // bottleneck: the binary64 constants go in vector registers; the
-    // two-wave slots, one wave per SIMD, keep them in scalar ones)
+    // multi-wave slots, one wave per SIMD, keep them in scalar ones)
     act = wave_dt_activation<HPW, !PAIR>(raw, Ah, a.db_f32);
     // this wave's token, statics and predictor transfers have landed
     if (!PAIR) wait_vmcnt<SLOT_DMA>();
@@ -1373,8 +1373,9 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
         const bool base_ok = wt.bounded[k] != 0 && __builtin_fabsf(x) <= 65504.f;
         const f32x4* bdt4 = (const f32x4*)wt.bdt[k];
         const f32x4* cw4 = (const f32x4*)cwt;
-        // the readout's partial sums per tier, added after both (the same order
-        // as the two-wave slot, whose tiers run on different waves)
+        // the readout's partial sums per readout segment, folded after both
+        // tiers (the order of the multi-wave slots, whose segments run on
+        // different waves)
         float accs[4] = {0.f, 0.f, 0.f, 0.f};
 
         // ---- INT8 tier: unpack (byte k of c8[i] is q8 + 128 of internal
