@@ -21,7 +21,7 @@ static constexpr int FOUR_PER_SLOT = 256 + 4 * 16;
 
 // a.dma_tiles: bit 0 = 16-byte LDS transfers of the state rows; bit 1 = the
 // one-token inputs may be staged by dword transfers (the staged prologue of
-// the one-token instances with an even number of heads per workgroup).
+// the one-token instances of four or more waves).
 // WPS > 1: WPS waves per head slot (each steps a quarter or half of the
 // carried coordinates), 4 waves per workgroup: the small-batch shapes (one
 // wave per SIMD, the slots' work on two or four times the SIMDs).
@@ -68,7 +68,7 @@ static hipError_t launch_layout(const StepArgs& args, hipStream_t stream) {
   }
   if (hpg % 16 == 0 && slots >= 16LL * 512) {
     launch_shape<N8, N4, NZ, MODE, 4, 4>(a, dim3(pblocks, a.H / 16, a.B), stream);
-  } else if (a.L > 1 && slots <= 512) {   // multi-token: four waves per slot up to two per SIMD
+  } else if (slots <= 512) {   // four waves per slot, up to two waves per SIMD
     launch_shape<N8, N4, NZ, MODE, 4, 1, 4>(a, dim3(pblocks, a.H, a.B), stream);
   } else if (hpg % 2 == 0 && slots <= 1024) {   // two waves per slot, up to two waves per SIMD
     launch_shape<N8, N4, NZ, MODE, 4, 1, 2>(a, dim3(pblocks, a.H / 2, a.B), stream);

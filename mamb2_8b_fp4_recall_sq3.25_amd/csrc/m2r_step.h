@@ -735,9 +735,9 @@ struct StepSmem {
   static_assert(seg_layout_ok(N8, N4), "four non-empty readout segments");
   static constexpr int NL = N8 + N4, F = NL + 2, NH = PAIR ? WPB / WPS : WPB * HPW;
   static constexpr bool RIDGE = MODE == MODE_RIDGE, SPLIT = RIDGE && WPB >= 4;
-  // one-token instances with an even number of heads per workgroup stage
-  // their token inputs in LDS by direct transfers
-  static constexpr bool STAGED = DMA && ONE && NH % 2 == 0 && NH <= 16;
+  // one-token instances of four or more waves stage their token inputs in
+  // LDS by direct transfers (one shared transfer per wave)
+  static constexpr bool STAGED = DMA && ONE && WPB >= 4 && NH <= 16;
   // slot tile: lo, hi, q4, s8, s4 (and latent) fields of 64 rows, 16 bytes of slack
   static constexpr int TILE = 128 * (N8 / 2) + 64 * (N4 / 2) + 256 + (RIDGE ? 128 : 0) + 16;
   static constexpr int PRED_DW = RIDGE ? F * NZ / 2 : 1;
