@@ -159,9 +159,9 @@ def prefill_timing(device, tokens=2048, steps=5, warmup=2):
 def layers_one_launch(stack, steps, warmup):
     """The same 56-layer one-token step as one launch of the multi-layer
     kernel (m2r_state_step_ridge_layers: every workgroup reads its layer's
-    arguments from a table in device memory), captured as a one-node graph
-    after the table's first copy (replays reuse the staged table).  Returns ms
-    per 56-layer step."""
+    arguments from a table in device memory), timed as eager calls, each of
+    which copies the table from the host before its launch.  Returns ms per
+    56-layer step."""
     import ctypes
     from mamba2_recall import ridge_codec
     steps_ = [dict(x=d["x"], dt=d["dt"], A=d["A"], B=d["B"], C=d["C"], D=d["D"], dt_bias=d["dt_bias"],
@@ -174,7 +174,6 @@ def layers_one_launch(stack, steps, warmup):
     args = (ctypes.byref(table), n, x.shape[0], H, P, G, stack.native.ptr(ws), ws.numel())
     stack.native.call("m2r_state_step_ridge_layers", *args, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     torch.cuda.synchronize()
-    import time as _t
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for _ in range(warmup):
         stack.native.call("m2r_state_step_ridge_layers", *args, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
@@ -697,8 +696,8 @@ def cpu_baseline(budget_s=12.0, fp4_budget_s=3.0):
                 sample=f"C oracle (OpenMP over rows), {layers} published ridge layer steps in order at batch "
                        f"{batch}, 1 token each, {elapsed:.1f} s",
                 fp4_g16_decode=dict(value=round(fp4_bytes / fp4_s / 1e9, 3), unit="GB/s", cores=cores, kind="port",
-                                    sample=f"C oracle, {rounds} x (in_proj [18560,4096] + out_proj [4096,8192]), "
-                                           f"{fp4_s:.1f} s"),
+                                    sample=f"C oracle, {rounds} x (in_proj rows [4096,4096] + out_proj rows "
+                                           f"[1024,8192]), {fp4_s:.1f} s"),
                 pytorch_cpu=torch_leg)
 
 

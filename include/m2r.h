@@ -235,11 +235,14 @@ int m2r_state_step_ridge_layers(const m2r_ridge_layer* layers, int nlayers, int6
  * of the layer table goes to a static device array of the library, at most
  * M2R_LAYERS_NOALLOC_MAX layers per call (larger calls are rejected).  No
  * counterpart in the reference; it is for callers that cannot allocate
- * (code under HIP graph capture, tight serving loops, harnesses that forbid
- * allocation).  Every call on one GPU shares that GPU's array (and the
- * library's host staging buffer, under a lock): calls that overlap on one
- * GPU, from other streams or host threads, race; calls on one stream are
- * ordered.  Results equal m2r_state_step_ridge_layers'.
+ * (tight serving loops, harnesses that forbid allocation).  Every call on
+ * one GPU shares that GPU's array (and the library's host staging buffer,
+ * under a lock): calls that overlap on one GPU, from other streams or host
+ * threads, race; calls on one stream are ordered.  Results equal
+ * m2r_state_step_ridge_layers'.  Neither multi-layer entry point can be
+ * captured into a HIP graph: each copies the table from host memory that
+ * later calls overwrite, so on a capturing stream both return an error
+ * before enqueueing anything.
  */
 #define M2R_LAYERS_NOALLOC_MAX 256
 int m2r_state_step_ridge_layers_noalloc(const m2r_ridge_layer* layers, int nlayers, int64_t batch, int64_t H,

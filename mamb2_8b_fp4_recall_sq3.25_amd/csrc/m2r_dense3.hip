@@ -598,7 +598,12 @@ void k_dense3_slots(Dense3Args a) {
 // ---------------------------------------------------------------------------
 // FP16-carry control: state = half(fma(state, decay, (B*dt) * x)) after the
 // readout y = sum(state * C) + x * D.  Optional statistics: sum over tokens
-// and the rows of each 16-row P tile of |FP16 carry| per coordinate.
+// and the rows of each 16-row P tile of |FP16 carry| per coordinate, in one
+// fixed order (so they are the same on every run): each row's sum over the
+// tokens in token order (state_codec.py:100-101), the rows of each 4-row
+// sub-tile as (r0 + r1) + (r2 + r3) (the per-program tl.sum of :102), and
+// the four sub-tiles of a 16-row tile in order, ((T0 + T1) + T2) + T3 (the
+// host-side sum of state_codec.py:255-261).
 struct S16Args {
   const uint16_t* x; const uint16_t* dt; const float* A; const uint16_t* Bm; const uint16_t* Cm;
   const void* D; const void* dt_bias;
@@ -613,13 +618,16 @@ struct S16Args {
 // 16 bytes of its own row covers the 64 banks once.  Otherwise every lane
 // reads its row directly.
 constexpr int S16_PITCH = 68;   // dwords per staged row (64 + 4 padding)
+constexpr int S16_SUM_PITCH = 132;   // dwords per row of the statistics' per-row sums
 typedef uint32_t s16x4 __attribute__((ext_vector_type(4)));
 
-template <bool STAGED>
+// STATS: each lane keeps its row's sums over the tokens in LDS (its own row:
+// no other lane adds to it), reduced in the fixed order above at the end.
+template <bool STAGED, bool STATS>
 __global__ __launch_bounds__(64) void k_s16_step(S16Args a) {
   __shared__ __align__(16) float s_b[128];
   __shared__ __align__(16) float s_c[128];
-  __shared__ float s_acc[4][128];
+  __shared__ __align__(16) float s_sum[STATS ? 64 * S16_SUM_PITCH : 4];
   __shared__ __align__(16) uint32_t s_rows[STAGED ? 64 * S16_PITCH : 4];
   const int lane = threadIdx.x;
   const int b = blockIdx.z, h = blockIdx.y;
@@ -650,7 +658,10 @@ __global__ __launch_bounds__(64) void k_s16_step(S16Args a) {
 #pragma unroll
     for (int n = 0; n < 128; ++n) st[n] = valid ? h2f(a.state[row * 128 + n]) : 0.f;
   }
-  for (int n = lane; n < 512; n += 64) (&s_acc[0][0])[n] = 0.f;
+  if constexpr (STATS) {   // the lane's own row of sums (rows past P stay zero)
+#pragma unroll
+    for (int q = 0; q < 32; ++q) *(f32x4*)(s_sum + lane * S16_SUM_PITCH + 4 * q) = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
   const float av = a.A[h], Dh = load_param(a.D, a.d_f32, h), bias = load_param(a.dt_bias, a.db_f32, h);
   for (int t = 0; t < L; ++t) {
     const int bt = b * L + t;
@@ -673,10 +684,19 @@ __global__ __launch_bounds__(64) void k_s16_step(S16Args a) {
     if (valid) a.y[((size_t)bt * H + h) * P + pbase + lane] = f2h(acc + x * Dh);
 #pragma unroll
     for (int n = 0; n < 128; ++n) st[n] = round_to_half(st[n]);
-    if (a.stats && valid) {
-      const int tile = lane >> 4;
+    if constexpr (STATS) {
+      if (valid) {   // the row's sums over the tokens, in token order
+        float* row_sum = s_sum + lane * S16_SUM_PITCH;
 #pragma unroll
-      for (int n = 0; n < 128; ++n) atomicAdd(&s_acc[tile][n], __builtin_fabsf(st[n]));
+        for (int q = 0; q < 32; ++q) {
+          f32x4 v = *(const f32x4*)(row_sum + 4 * q);
+          v.x = v.x + __builtin_fabsf(st[4 * q]);
+          v.y = v.y + __builtin_fabsf(st[4 * q + 1]);
+          v.z = v.z + __builtin_fabsf(st[4 * q + 2]);
+          v.w = v.w + __builtin_fabsf(st[4 * q + 3]);
+          *(f32x4*)(row_sum + 4 * q) = v;
+        }
+      }
     }
     __syncthreads();
   }
@@ -701,13 +721,20 @@ __global__ __launch_bounds__(64) void k_s16_step(S16Args a) {
 #pragma unroll
     for (int n = 0; n < 128; ++n) a.state[row * 128 + n] = f2h(st[n]);
   }
-  if (a.stats) {
+  if constexpr (STATS) {
+    __syncthreads();   // every row's sums are complete
     const int tiles = (P + 15) / 16;
     for (int i = lane; i < 512; i += 64) {
-      int tl = i >> 7, n = i & 127;
-      int tile = pbase / 16 + tl;
+      const int tl = i >> 7, n = i & 127;
+      const int tile = pbase / 16 + tl;
+      float sub[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {   // 4-row sub-tile j of the 16-row tile
+        const float* r = s_sum + (16 * tl + 4 * j) * S16_SUM_PITCH + n;
+        sub[j] = (r[0] + r[S16_SUM_PITCH]) + (r[2 * S16_SUM_PITCH] + r[3 * S16_SUM_PITCH]);
+      }
       if (tile < tiles && pbase + 16 * tl < P)
-        a.stats[(((size_t)b * H + h) * tiles + tile) * 128 + n] = s_acc[tl][n];
+        a.stats[(((size_t)b * H + h) * tiles + tile) * 128 + n] = ((sub[0] + sub[1]) + sub[2]) + sub[3];
     }
   }
 }
@@ -841,10 +868,11 @@ extern "C" int m2r_state_step_s16(const void* x, const void* dt, const float* A,
                (uint16_t*)state, (uint16_t*)y, stats, (int)batch, (int)L, (int)H, (int)P, (int)G, d_is_f32,
                db_is_f32};
   const dim3 grid((unsigned)((P + 63) / 64), (unsigned)H, (unsigned)batch);
-  if (((uintptr_t)state & 15) == 0)
-    hipLaunchKernelGGL(k_s16_step<true>, grid, dim3(64), 0, stream, args);
-  else
-    hipLaunchKernelGGL(k_s16_step<false>, grid, dim3(64), 0, stream, args);
+  const bool staged = ((uintptr_t)state & 15) == 0;
+  if (staged && stats) hipLaunchKernelGGL((k_s16_step<true, true>), grid, dim3(64), 0, stream, args);
+  else if (staged) hipLaunchKernelGGL((k_s16_step<true, false>), grid, dim3(64), 0, stream, args);
+  else if (stats) hipLaunchKernelGGL((k_s16_step<false, true>), grid, dim3(64), 0, stream, args);
+  else hipLaunchKernelGGL((k_s16_step<false, false>), grid, dim3(64), 0, stream, args);
   return m2r_check(hipGetLastError(), "s16 step launch");
 }
 

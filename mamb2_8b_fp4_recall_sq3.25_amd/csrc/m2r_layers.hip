@@ -177,6 +177,20 @@ static int launch_layers(const LayerEntry* dev_table, int nlayers, int64_t batch
 // staged before hipMemcpyAsync returns, so the buffer is reusable at once).
 static thread_local std::vector<LayerEntry> t_table;
 
+// Both entry points copy the table from host memory that the next call
+// overwrites.  Captured into a graph, that copy would read the host buffer at
+// replay time, when it holds whatever table the latest call built: the
+// replay would step another call's layers with the captured grid.  So a
+// capturing stream is rejected before anything is enqueued.
+static int reject_capture(hipStream_t stream, const char* what) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (int e = m2r_check(hipStreamIsCapturing(stream, &st), what)) return e;
+  if (st != hipStreamCaptureStatusNone)
+    return m2r_fail("layers step: the stream is capturing a graph; the layer table is copied from host memory "
+                    "that later calls overwrite, so this entry point cannot be captured (launch it eagerly)");
+  return 0;
+}
+
 }  // namespace m2r
 
 using namespace m2r;
@@ -195,6 +209,7 @@ extern "C" int m2r_state_step_ridge_layers(const m2r_ridge_layer* layers, int nl
   const int64_t need = m2r_state_step_ridge_layers_workspace(nlayers);
   if (!workspace || !aligned(workspace, 16) || workspace_bytes < need)
     return m2r_fail("layers step: workspace must be 16-byte aligned and hold m2r_state_step_ridge_layers_workspace(nlayers) bytes");
+  if (int e = reject_capture(stream, "layers step: capture query")) return e;
   if (int e = m2r_check(hipMemcpyAsync(workspace, t_table.data(), (size_t)need, hipMemcpyHostToDevice, stream),
                         "layers step table copy"))
     return e;
@@ -205,11 +220,12 @@ extern "C" int m2r_state_step_ridge_layers_noalloc(const m2r_ridge_layer* layers
                                                    int64_t H, int64_t P, int64_t G, hipStream_t stream) {
   if (nlayers > M2R_LAYERS_NOALLOC_MAX)
     return m2r_fail("layers step (no-alloc): more than M2R_LAYERS_NOALLOC_MAX (256) layers in one call");
-  void* dev_table = nullptr;
-  if (int e = scratch_address(&dev_table)) return e;
   std::lock_guard<std::mutex> lock(g_noalloc_mu);
   int wpb = 0, hpw = 0;
   if (int e = build_table(layers, nlayers, batch, H, P, G, g_noalloc_table, wpb, hpw)) return e;
+  if (int e = reject_capture(stream, "layers step (no-alloc): capture query")) return e;
+  void* dev_table = nullptr;
+  if (int e = scratch_address(&dev_table)) return e;
   const size_t bytes = (size_t)m2r_state_step_ridge_layers_workspace(nlayers);
   if (int e = m2r_check(hipMemcpyAsync(dev_table, g_noalloc_table, bytes, hipMemcpyHostToDevice, stream),
                         "layers step (no-alloc) table copy"))

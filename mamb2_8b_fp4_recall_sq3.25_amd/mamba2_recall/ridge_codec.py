@@ -162,6 +162,12 @@ def layer_table(steps):
     if not steps:
         raise ValueError("At least one layer required")
     x0 = steps[0]["x"]
+    # the launch takes one group count for every layer (the kernel indexes
+    # each layer's B, C and statics with it): a layer with fewer groups would
+    # be read past its tensors' ends
+    group_counts = {tuple(st["B"].shape[2:3]) if st["B"].ndim == 4 else None for st in steps}
+    if len(group_counts) != 1 or None in group_counts:
+        raise ValueError("Every layer needs the same number of B/C groups")
     table = (_native.RidgeLayer * len(steps))()
     for i, st in enumerate(steps):
         x, state, layout = st["x"], st["state"], st["layout"]

@@ -147,11 +147,19 @@ class _NormHook:
     def __call__(self, x, z=None):
         m = self.module
         if (z is not None and x.dtype == torch.float16 and z.dtype == torch.float16 and x.shape == z.shape
-                and _row_view(x, x.shape[-1]) is not None and _row_view(z, z.shape[-1]) is not None
-                and x.data_ptr() % 8 == 0 and z.data_ptr() % 8 == 0 and all(
-                    v[1] % 4 == 0 for v in (_row_view(x, x.shape[-1]), _row_view(z, z.shape[-1])))):
+                and x.data_ptr() % 8 == 0 and z.data_ptr() % 8 == 0
+                and _kernel_rows(x) and _kernel_rows(z)):
             return gated_rmsnorm(x, z, m.weight, m.eps, m.group_size)
         return self.fallback(x, z)
+
+
+def _kernel_rows(t):
+    """True when `t` is rows the gated-norm kernel reads: one row stride, a
+    multiple of 4 elements, and rows that do not overlap (stride at least the
+    channel count, or a single row); a broadcast or overlapping view goes to
+    the module's own forward instead."""
+    v = _row_view(t, t.shape[-1])
+    return v is not None and v[1] % 4 == 0 and (v[0] == 1 or v[1] >= t.shape[-1])
 
 
 def native_norm_compatible(norm, channels, group_size):
@@ -184,7 +192,12 @@ class _MixerController:
 
     LAYERS, D_MODEL, HEADS, HEADDIM, D_STATE, GROUPS, D_CONV, D_INNER = 56, 4096, 128, 64, 128, 8, 4, 8192
     # the mixers' gated norms run on the native kernel while installed (their
-    # module hooks still run); False keeps the model's own norm computation
+    # module hooks still run); False keeps the model's own norm computation.
+    # The native kernel sums the squares in a fixed tree of its own and agrees
+    # with a binary64 restatement of the formula to one binary16 rounding; the
+    # reference's norm (mamba_ssm's RMSNormGated, a Triton kernel) reduces in
+    # another order, so outputs can differ from it in the last bit of some
+    # channels (that kernel's arithmetic is not available here to pin).
     native_norm = True
     PARAMETER_TENSORS, PARAMETER_COUNT = 507, 8_236_999_680
     TABLE_SHAPE = (56, 8, 128)

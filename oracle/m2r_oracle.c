@@ -194,8 +194,13 @@ static float load_param(const void* p, int f32, int64_t i) {
  * orc_update), read out against C with D*x,
  * then rounded to FP16.  Statistics (optional, may be NULL): for every
  * (b, h, 16-row tile of P, coordinate) the sum over tokens and tile rows of
- * |FP16 carry|, accumulated in double and rounded once.  state is
- * [B,H,P,128] f16 bits, stats [B,H,ceil(P/16),128] f32.
+ * |FP16 carry| in binary32, in this order: each row's sum over the tokens in
+ * token order (the per-program accumulator of state_codec.py:100-101), the
+ * rows of each 4-row sub-tile as (r0 + r1) + (r2 + r3) (the tl.sum of :102;
+ * rows past P add zero), then the four sub-tiles of the 16-row tile in order,
+ * ((T0 + T1) + T2) + T3 (the host sum over sub-tiles, state_codec.py:255-261,
+ * missing sub-tiles zero).  state is [B,H,P,128] f16 bits, stats
+ * [B,H,ceil(P/16),128] f32.
  */
 int orc_s16_step(const uint16_t* X, const uint16_t* DT, const float* A, const uint16_t* Bm, const uint16_t* Cm,
                  const void* D, int d_f32, const void* DB, int db_f32, uint16_t* S, uint16_t* Y, float* stats,
@@ -208,7 +213,8 @@ int orc_s16_step(const uint16_t* X, const uint16_t* DT, const float* A, const ui
     for (int64_t h = 0; h < H; ++h) {
       const int64_t g = h / hpg;
       const float av = A[h], dv = load_param(D, d_f32, h), bias = load_param(DB, db_f32, h);
-      double* acc = stats ? (double*)calloc((size_t)tiles * 128, sizeof(double)) : NULL;
+      /* per-row sums over the tokens, rows padded to whole 16-row tiles */
+      float* acc = stats ? (float*)calloc((size_t)tiles * 16 * 128, sizeof(float)) : NULL;
       for (int64_t p = 0; p < P; ++p) {
         uint16_t* st = S + ((b * H + h) * P + p) * 128;
         float v[128];
@@ -229,13 +235,21 @@ int orc_s16_step(const uint16_t* X, const uint16_t* DT, const float* A, const ui
           Y[(bt * H + h) * P + p] = orc_f32_to_f16((float)out + x * dv);
           for (int n = 0; n < 128; ++n) {
             v[n] = orc_f16_to_f32(orc_f32_to_f16(v[n]));
-            if (acc) acc[(p / 16) * 128 + n] += fabs((double)v[n]);
+            if (acc) acc[p * 128 + n] = acc[p * 128 + n] + fabsf(v[n]);
           }
         }
         for (int n = 0; n < 128; ++n) st[n] = orc_f32_to_f16(v[n]);
       }
       if (acc) {
-        for (int64_t i = 0; i < tiles * 128; ++i) stats[(b * H + h) * tiles * 128 + i] = (float)acc[i];
+        for (int64_t tile = 0; tile < tiles; ++tile)
+          for (int n = 0; n < 128; ++n) {
+            float sub[4];
+            for (int j = 0; j < 4; ++j) {
+              const float* r = acc + (tile * 16 + 4 * j) * 128 + n;
+              sub[j] = (r[0] + r[128]) + (r[256] + r[384]);
+            }
+            stats[((b * H + h) * tiles + tile) * 128 + n] = ((sub[0] + sub[1]) + sub[2]) + sub[3];
+          }
         free(acc);
       }
     }

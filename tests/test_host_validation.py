@@ -214,3 +214,31 @@ def test_layers_step_rejects_bad_calls_before_any_launch():
     arr[0].lo = 0x10000
     assert "multiple of 8" in err(ctypes.byref(arr), 1, 1, 128, 60, 8, 0x900000, 1 << 20, None)
     assert lib.m2r_state_step_ridge_layers_workspace(56) == 56 * lib.m2r_state_step_ridge_layers_workspace(1)
+
+
+def test_layer_table_rejects_mixed_group_counts():
+    """The multi-layer launch takes one group count for all layers and the
+    kernel indexes every layer's B, C and statics with it: a table whose
+    layers disagree is rejected on the host, before any device check."""
+    def step(groups):
+        return {"x": torch.zeros(1, 1, 128, 64, dtype=torch.float16),
+                "B": torch.zeros(1, 1, groups, 128, dtype=torch.float16)}
+    with pytest.raises(ValueError, match="same number of B/C groups"):
+        ridge_codec.layer_table([step(8), step(8), step(4)])
+    with pytest.raises(ValueError, match="same number of B/C groups"):
+        ridge_codec.layer_table([step(8), {"x": step(8)["x"], "B": torch.zeros(8, 128)}])
+
+
+def test_norm_hook_takes_only_non_overlapping_rows():
+    """The gated-norm hook calls the kernel only for operands it reads as
+    separate rows; a broadcast gate (row stride 0) or overlapping rows go to
+    the module's own forward instead of failing in the kernel's checks."""
+    from mamba2_recall import state_quant
+    base = torch.zeros(4, 96, dtype=torch.float16)
+    assert state_quant._kernel_rows(base)
+    assert state_quant._kernel_rows(torch.zeros(4, 128, dtype=torch.float16)[:, :96])   # projection split
+    assert state_quant._kernel_rows(torch.zeros(1, 1, 96, dtype=torch.float16))
+    assert not state_quant._kernel_rows(torch.zeros(1, 96, dtype=torch.float16).expand(4, 96))
+    overlap = torch.zeros(400, dtype=torch.float16).as_strided((4, 96), (8, 1))
+    assert not state_quant._kernel_rows(overlap)
+    assert not state_quant._kernel_rows(torch.zeros(4, 97, dtype=torch.float16)[:, :96])   # stride not % 4

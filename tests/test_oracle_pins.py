@@ -978,3 +978,58 @@ def test_torch_cpu_fp4_decode_matches_c_oracle(oracle):
         assert err == 0
         got = torch_cpu.fp4_g16_decode(torch.from_numpy(packed), torch.from_numpy(sb), float(g))
         assert np.array_equal(got.numpy().view(np.uint16), want)
+
+
+def test_s16_statistics_fixed_summation_order(oracle):
+    """The s16 calibration statistics are binary32 sums in one fixed order:
+    each row over the tokens in order, a 4-row sub-tile as (r0 + r1) + (r2 +
+    r3), the four sub-tiles of a 16-row tile as ((T0 + T1) + T2) + T3
+    (state_codec.py:100-102 per program, :255-261 on the host).  With x = 0
+    and decay exactly 1 (A = -1e-30) the FP16 carry is the state itself, so
+    the rows can be chosen where the plausible other orders round
+    differently: 131008 + 2^-8 is a tie that rounds back to 131008 (even
+    significand), while 131008 + 2^-7 is exact.  Sequential row sums, or a
+    pairwise fold of the sub-tiles, give 131008 where the fixed order gives
+    131008 + 2^-7; a float64 accumulation gives 131008 + 2^-7 + 2^-8 in the
+    second case."""
+    H, P, G, L = 1, 32, 1, 2
+    big, small = 65504.0, 2.0 ** -8
+    state = np.zeros((1, H, P, 128), np.float32)
+    # tile 0 (rows 0-15): sub-tile 0 holds big, big, small, small -> (2 big) + 2^-7
+    state[0, 0, 0:2, 0] = big
+    state[0, 0, 2:4, 0] = small
+    # tile 1 (rows 16-31): sub-tiles 2^-8... T0 = 2 big, T1 = 0, T2 = T3 = small
+    state[0, 0, 16:18, 1] = big
+    state[0, 0, 24, 1] = small
+    state[0, 0, 28, 1] = small
+    # coordinate 2: two tokens of the same rows sum per row first (token order)
+    state[0, 0, 5, 2] = 3.0
+    st = cases.f16(state)
+    x = np.zeros((1, L, H, P), np.uint16)
+    dt = cases.f16(np.zeros((1, L, H)))
+    A = np.full(H, -1e-30, np.float32)
+    B = cases.f16(np.ones((1, L, G, 128)))
+    C = cases.f16(np.ones((1, L, G, 128)))
+    D = cases.f16(np.zeros(H))
+    db = cases.f16(np.zeros(H))
+    carry = st.copy()
+    _, stats = oracle.s16_step(x, dt, A, B, C, D, db, carry, collect_stats=True)
+    assert np.array_equal(carry, st), "decay 1 and x = 0 must leave the carry unchanged"
+    f = np.float32
+    two_big = f(big) + f(big)
+    # per token: tile 0 coordinate 0 is 2 big + 2^-7 exactly; over two tokens
+    # each row is summed first, so the tile is (2 (2 big)) + 2 (2^-7)
+    want0 = (f(2 * big) + f(2 * big)) + (f(2 * small) + f(2 * small))
+    assert stats[0, 0, 0, 0] == want0 == f(4 * big + 4 * small)
+    # tile 1, coordinate 1: T0 = 2 big (per token) and T2 = T3 = 2^-8 per token
+    t0 = f(2 * big) + f(2 * big)
+    want1 = ((t0 + f(0)) + f(2 * small)) + f(2 * small)
+    assert stats[0, 0, 1, 1] == want1
+    assert stats[0, 0, 0, 2] == f(6.0)
+    # the orders this rules out round differently on the single-token case
+    _, one = oracle.s16_step(x[:, :1], dt[:, :1], A, B[:, :1], C[:, :1], D, db, st.copy(), collect_stats=True)
+    assert one[0, 0, 0, 0] == two_big + f(2 * small)          # (big + big) + (small + small): exact
+    assert ((two_big + f(small)) + f(small)) == two_big        # sequential rows: the ties lose both
+    assert one[0, 0, 1, 1] == two_big                          # ((T0 + 0) + small) + small ties back
+    assert (two_big + f(0)) + (f(small) + f(small)) != two_big  # a pairwise fold would keep 2^-7
+    assert float(one[0, 0, 1, 1]) != 2 * big + 2 * small       # nor is it the float64 sum

@@ -67,3 +67,36 @@ def test_noalloc_layers_step_rejects_oversized_table():
     arr = (_native.RidgeLayer * 257)()
     rc = lib.m2r_state_step_ridge_layers_noalloc(ctypes.byref(arr), 257, 1, 128, 64, 8, None)
     assert rc != 0 and b"M2R_LAYERS_NOALLOC_MAX" in lib.m2r_last_error()
+
+
+def test_layers_entry_points_reject_graph_capture(device):
+    """Both multi-layer entry points copy their layer table from host memory
+    that the next call overwrites, so a captured copy would replay with
+    another call's table: on a capturing stream they return an error before
+    anything is enqueued, and eager calls still match afterwards."""
+    from mamba2_recall import _native, ridge_codec
+    rng = np.random.default_rng(11)
+    steps, _ = make_layers(rng, 1, RIDGE_LAYOUTS[:2], device)
+    table = ridge_codec.layer_table(steps)
+    ws = torch.empty(ridge_codec.layers_workspace_bytes(len(steps)), dtype=torch.uint8, device=device)
+    lib = _native.lib()
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    print("[no-alloc] capture: both entry points on a capturing stream", flush=True)
+    with torch.cuda.stream(side):
+        graph.capture_begin()
+        try:
+            st = ctypes.c_void_p(side.cuda_stream)
+            rc_noalloc = lib.m2r_state_step_ridge_layers_noalloc(ctypes.byref(table), len(steps), 1, H, P, G, st)
+            err_noalloc = lib.m2r_last_error()
+            rc_ws = lib.m2r_state_step_ridge_layers(ctypes.byref(table), len(steps), 1, H, P, G,
+                                                    ctypes.c_void_p(ws.data_ptr()), ws.numel(), st)
+            err_ws = lib.m2r_last_error()
+        finally:
+            graph.capture_end()
+    assert rc_noalloc != 0 and b"capturing" in err_noalloc, err_noalloc
+    assert rc_ws != 0 and b"capturing" in err_ws, err_ws
+    torch.cuda.synchronize()
+    print("[no-alloc] eager calls after the rejected capture", flush=True)
+    call_both(steps)
