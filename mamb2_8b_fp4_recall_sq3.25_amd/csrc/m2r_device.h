@@ -180,6 +180,29 @@ __device__ __forceinline__ uint32_t round_residual_code(float v, float y, float 
   return __builtin_bit_cast(uint32_t, t);
 }
 
+// Two-sided form of the same quantizer: with y = RN(1/d) for a positive
+// normal binary32 d, yh = RN(y + y 2^-22) and yl = RN(y - y 2^-22), the
+// biased codes th = RN(v yh + magic) and tl = RN(v yl + magic) (each one
+// rounding of an exact product plus magic, as above) bracket roundf(RN(v/d)):
+//   v yh >= (v/d) (1 - 2^-24)^2 (1 + 2^-22) > (v/d)(1 + 2^-24) >= RN(v/d)
+// for v > 0 (mirrored for v < 0, and v yl below RN(v/d) alike), so RN(v/d)
+// lies strictly between v yl and v yh.  When th == tl == magic + k, both
+// products lie within 1/2 of k, hence |RN(v/d) - k| < 1/2 and roundf gives
+// k: the code is kept.  Otherwise a half-integer lies between them (or on an
+// end) and the tier is requantized with the exact quotients.  Per coordinate
+// two fmas and one bitwise accumulation of th ^ tl, against three
+// instructions and half a maximum for the residual form.  The CPU checks
+// verify it on random quotients and every half-integer boundary, and that an
+// offset of 0 or 2^-25 is not enough.
+constexpr float TWO_SIDED_REL = 0x1p-22f;
+__device__ __forceinline__ uint32_t two_sided_code(float v, float yh, float yl, float bias, uint32_t& diff) {
+  const float magic = 0x1.8p23f + bias;
+  const uint32_t th = __builtin_bit_cast(uint32_t, __builtin_fmaf(v, yh, magic));
+  const uint32_t tl = __builtin_bit_cast(uint32_t, __builtin_fmaf(v, yl, magic));
+  diff |= th ^ tl;
+  return th;
+}
+
 // q * s exactly, for a code q held as binary16 (an integer of at most 11
 // bits) and any binary32 s: one mixed-precision fma with a -0 addend (x + -0
 // is x, also for signed zeros), so infinite and NaN scales give the IEEE

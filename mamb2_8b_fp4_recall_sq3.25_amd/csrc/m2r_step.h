@@ -33,6 +33,37 @@ namespace m2r {
 
 enum { MODE_LEGACY = 0, MODE_STORED = 1, MODE_RIDGE = 2 };
 
+// Phase timeline of one launch, compiled only into the instrumented build
+// (M2R_PHASE_TIMELINE; the library proper has none of it).  Lane 0 of every
+// wave stamps the shader clock (s_memtime) at the phase boundaries below into
+// LDS and, at the end, writes its 32 stamps to g_phase_stamps[(block * WPB +
+// wave) * 32 + i], block = (z * gridDim.y + y) * gridDim.x + x.  Stamps 30 and
+// 31 read the constant 100 MHz clock (s_memrealtime) at the start and the end,
+// which gives the shader clock's rate.  Phases of slot k (k < 4) are stamps
+// ST_SLOT + 4 k + {0: its data landed, 1: update (one wave per slot: INT8
+// tier) done, 2: barrier passed (one wave per slot: INT4 tier done), 3: slot
+// done}.
+enum {
+  ST_START = 0, ST_ARGS = 1, ST_ISSUED = 2, ST_SLOT0_ISSUED = 3, ST_ACT = 4, ST_TOKEN = 5, ST_BARRIER = 6,
+  ST_BUILD = 7, ST_SLOT = 8, ST_COPYOUT = 24, ST_END = 25, ST_REAL0 = 30, ST_REAL1 = 31
+};
+#ifdef M2R_PHASE_TIMELINE
+__device__ unsigned long long* g_phase_stamps;
+#define M2R_STAMP(i)                                                                     \
+  do {                                                                                   \
+    const unsigned long long t_ = __builtin_amdgcn_s_memtime();                          \
+    if (lane == 0) sm.stamps[wave][(i)] = t_;                                            \
+  } while (0)
+#define M2R_STAMP_REAL(i)                                                                \
+  do {                                                                                   \
+    const unsigned long long t_ = __builtin_amdgcn_s_memrealtime();                      \
+    if (lane == 0) sm.stamps[wave][(i)] = t_;                                            \
+  } while (0)
+#else
+#define M2R_STAMP(i) do {} while (0)
+#define M2R_STAMP_REAL(i) do {} while (0)
+#endif
+
 struct StepArgs {
   const uint16_t* x;       // f16 [B, L, H, P]
   const uint16_t* dt;      // f16 [B, L, H]
@@ -541,11 +572,10 @@ __device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, Gro
 }
 
 // One tier of a row: update its N carried coordinates (biased code bytes in
-// c[0 .. N/4)), accumulate the readout (prior * readout weight), then
-// requantize with den = max(RN(amax / lim), 1e-8) and the stored (binary16)
-// scale, writing the new codes back into c.  Returns the new stored scale.
-// INT8: byte = q + 128, lim 127; INT4: byte = q + 8, lim 7.  Legacy mode
-// quantizes with the binary32 denominator.
+// c[0 .. N/4)), accumulate the readout, then requantize with den =
+// max(RN(amax / lim), 1e-8) and the stored (binary16) scale, writing the new
+// codes back into c.  INT8: byte = q + 128, lim 127; INT4: byte = q + 8,
+// lim 7.  Legacy mode quantizes with the binary32 denominator.
 //
 // Clamping the rounded quotient to +-lim only matters when the divisor is
 // below den (a binary16-subnormal stored scale) or when an update is not
@@ -562,31 +592,45 @@ __device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, Gro
 // IEEE product for infinite and NaN scales (where the fused form gives
 // inf - inf).
 //
+// Readout: rs[sg] is set, for each readout segment sg the tier's
+// coordinates reach, to the binary32 chain of prior * w over them (w the
+// readout weights; one segment's chain is live at a time, segments being
+// contiguous runs of chunks).  `bdt4` and `cw4` are the head's B*dt and the
+// readout weights of the carried coordinates, as four-value chunks.
+//
 // tier_update is the first half (dequantization, readout, update and the
-// maximum of |update|; the readout of carried coordinate P0 + i accumulates
-// into acc[seg_of(P0 + i)]), tier_requant the second (the new scale and codes
+// maximum of |update|), tier_requant the second (the new scale and codes
 // from the maximum over the whole tier): a tier split between waves runs the
 // halves on its parts with the parts' maxima combined in between.
 template <int N, bool INT8, bool EXACT, int N8, int N4, int P0>
 __device__ __forceinline__ float tier_update(const uint32_t* c, float sc, float decay, float x, const f32x4* bdt4,
-                                             const f32x4* cw4, float (&acc)[4], float (&v)[N]) {
+                                             const f32x4* cw4, float (&rs)[4], float (&v)[N]) {
   constexpr float BIAS = INT8 ? 128.0f : 8.0f;
+  static_assert(P0 % 4 == 0 && N % 4 == 0, "whole chunks");
   const float nb = -(1024.0f + BIAS) * sc;
   const f16x2 nbias = {(_Float16)(-(1024.0f + BIAS)), (_Float16)(-(1024.0f + BIAS))};
   const float mz = EXACT ? opaque_neg_zero() : 0.f;
   float amax = 0.f;
+  float racc = 0.f;   // the current segment's readout chain
   // the shared operands of chunk i+1 are read while chunk i computes
-  f32x4 cb_next = bdt4[0], cw_next = cw4[0];
+  constexpr int C0 = P0 / 4;
+  f32x4 cb_next = bdt4[C0], cw_next = cw4[C0];
 #pragma unroll
   for (int i0 = 0; i0 < N; i0 += 4) {
+    const int ci = C0 + i0 / 4;   // chunk index among the carried coordinates
     const f32x4 cb = cb_next, cw = cw_next;
     if (i0 + 4 < N) {
-      cb_next = bdt4[i0 / 4 + 1];
-      cw_next = cw4[i0 / 4 + 1];
+      cb_next = bdt4[ci + 1];
+      cw_next = cw4[ci + 1];
     }
-    // the chunk's code bytes as binary16 values 1024 + byte (exponent byte 0x64)
-    const uint32_t h01 = __builtin_amdgcn_perm(0x64646464u, c[i0 / 4], 0x04010400u);
-    const uint32_t h23 = __builtin_amdgcn_perm(0x64646464u, c[i0 / 4], 0x04030402u);
+    // the chunk's code bytes as binary16 values 1024 + byte (exponent byte
+    // 0x64), formed here (the empty asm keeps the compiler from forming every
+    // chunk's pairs ahead of the tier, which would hold them all live)
+    uint32_t cc = c[i0 / 4];
+    asm volatile("" : "+v"(cc));
+    const uint32_t h01 = __builtin_amdgcn_perm(0x64646464u, cc, 0x04010400u);
+    const uint32_t h23 = __builtin_amdgcn_perm(0x64646464u, cc, 0x04030402u);
+    const int sg = seg_of<N8, N4>(P0 + i0);   // a whole chunk lies in one segment
     float pr[4];
     if constexpr (EXACT) {
       const f16x2 q01 = pk_add_h(__builtin_bit_cast(f16x2, h01), nbias);
@@ -599,27 +643,35 @@ __device__ __forceinline__ float tier_update(const uint32_t* c, float sc, float 
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float prior = pr[j];
-      const int sg = seg_of<N8, N4>(P0 + i0);   // a whole chunk lies in one segment
-      acc[sg] = __builtin_fmaf(prior, cw[j], acc[sg]);
-      float u = state_update(prior, decay, cb[j] * x);
+      racc = __builtin_fmaf(pr[j], cw[j], racc);
+      float u = state_update(pr[j], decay, cb[j] * x);
       // ordered pin: chunk by chunk, each prior dies as soon as it is used
       asm volatile("" : "+v"(u));
       v[i0 + j] = u;
     }
     amax = max3_abs(amax, v[i0], v[i0 + 1]);
     amax = max3_abs(amax, v[i0 + 2], v[i0 + 3]);
+    if (i0 + 4 == N || seg_of<N8, N4>(P0 + i0 + 4) != sg) {   // the segment's last chunk in this tier
+      rs[sg] = racc;
+      racc = 0.f;
+    }
     __builtin_amdgcn_sched_barrier(0);
   }
-  // Materialize the accumulator and the maximum here: otherwise the compiler
+  // Materialize the readout and the maximum here: otherwise the compiler
   // sinks their chains (and every update behind the maximum) into the
   // requantization, which keeps every prior and LDS operand live at once.
   constexpr int G0 = seg_of<N8, N4>(P0), G1 = seg_of<N8, N4>(P0 + N - 1);
-  if constexpr (G0 == G1) asm volatile("" : "+v"(acc[G0]), "+v"(amax));
-  else if constexpr (G1 == G0 + 1) asm volatile("" : "+v"(acc[G0]), "+v"(acc[G1]), "+v"(amax));
-  else if constexpr (G1 == G0 + 2) asm volatile("" : "+v"(acc[G0]), "+v"(acc[G0 + 1]), "+v"(acc[G1]), "+v"(amax));
-  else asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(amax));
+#pragma unroll
+  for (int sg = G0; sg <= G1; ++sg) asm volatile("" : "+v"(rs[sg]));
+  asm volatile("" : "+v"(amax));
   return amax;
+}
+
+// Readout of segment sg: its INT8 tier contribution, then its INT4 one.
+template <int N8, int N4>
+__device__ __forceinline__ float segment_readout(int sg, float c8, float c4) {
+  const bool h8 = seg_pos(N8, N4, sg) < N8, h4 = seg_pos(N8, N4, sg + 1) > N8;
+  return (h8 && h4) ? c8 + c4 : (h8 ? c8 : c4);
 }
 
 template <int N, bool INT8, int MODE>
@@ -654,27 +706,28 @@ __device__ __forceinline__ float tier_requant(const float (&v)[N], uint32_t* c, 
   // makes the register allocator keep both versions' values apart)
   const bool fast = __builtin_amdgcn_ballot_w64(!unclamped) == 0;
   if (fast) {
-    // the biased code as the low byte of t = RN(u r + 1.5 2^23 + bias) =
-    // 1.5 2^23 + bias + rint(u r), with a running maximum of the rounding
-    // residuals |f| = |RN(u r - rint(u r))| (round_residual_code)
-    float fmax_res = 0.f;
+    // the biased code as the low byte of t = RN(u yh + 1.5 2^23 + bias) =
+    // 1.5 2^23 + bias + rint(u yh), kept where the code of the other side,
+    // RN(u yl + ...), agrees (two_sided_code)
+    const float yh = __builtin_fmaf(r, TWO_SIDED_REL, r), yl = __builtin_fmaf(r, -TWO_SIDED_REL, r);
+    uint32_t diff = 0u;
 #pragma unroll
     for (int i = 0; i < N / 4; ++i) {
-      float f[4];
       uint32_t tb[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) tb[j] = round_residual_code(v[4 * i + j], r, BIAS, f[j]);
-      fmax_res = max3_abs(fmax_res, f[0], f[1]);
-      fmax_res = max3_abs(fmax_res, f[2], f[3]);
+      for (int j = 0; j < 4; ++j) {
+        tb[j] = two_sided_code(v[4 * i + j], yh, yl, BIAS, diff);
+        asm volatile("" : "+v"(diff));   // one three-input bitwise operation per coordinate
+      }
       uint32_t packed = pack4((int)tb[0], (int)tb[1], (int)tb[2], (int)tb[3]);
       asm volatile("" : "+v"(packed));
       c[i] = packed;
       __builtin_amdgcn_sched_barrier(0);
     }
-    // A lane whose u r lies within the residual margin of a half-integer may
-    // round differently from roundf(RN(u / d)): the wave then requantizes the
-    // tier with the exact quotients (rare: about 2 N margin per lane).
-    if (__builtin_amdgcn_ballot_w64(fmax_res > (INT8 ? RESIDUAL_OK8 : RESIDUAL_OK4)) != 0) {
+    // A lane whose two codes differ has a half-integer between u yl and u
+    // yh: the wave then requantizes the tier with the exact quotients (rare:
+    // the window is 2^-21 of the quotient wide).
+    if (__builtin_amdgcn_ballot_w64(diff != 0u) != 0) {
 #pragma unroll
       for (int i = 0; i < N / 4; ++i) {
         const int q0 = quantize_code_unclamped(v[4 * i], d, r);
@@ -701,15 +754,6 @@ __device__ __forceinline__ float tier_requant(const float (&v)[N], uint32_t* c, 
     }
   }
   return stored;
-}
-
-// The whole tier on one wave (P0: its first carried coordinate, 0 or N8).
-template <int N, bool INT8, int MODE, bool EXACT, int N8, int N4, int P0>
-__device__ __forceinline__ float tier_step(uint32_t* c, float sc, float decay, float x, const f32x4* bdt4,
-                                           const f32x4* cw4, float (&acc)[4], bool finite_in) {
-  float v[N];
-  const float amax = tier_update<N, INT8, EXACT, N8, N4, P0>(c, sc, decay, x, bdt4, cw4, acc, v);
-  return tier_requant<N, INT8, MODE>(v, c, amax, finite_in);
 }
 
 // One workgroup = WPB waves, each owning HPW head slots of 64 rows (the same
@@ -753,6 +797,9 @@ struct StepSmem {
   alignas(16) float pacc[PAIR ? 2 : 1][PAIR ? NH : 1][PAIR ? WPS : 1][PAIR ? 64 : 1];
   alignas(16) float pmax[PAIR ? 2 : 1][PAIR ? NH : 1][2][PAIR ? WPS : 1][PAIR ? 64 : 1];
   alignas(16) uint8_t tile[NH][TILE];
+#ifdef M2R_PHASE_TIMELINE
+  unsigned long long stamps[WPB][32];
+#endif
 };
 
 // The step of one workgroup: block coordinates (bx, by) and batch row b,
@@ -794,6 +841,8 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: per-wave values in SGPRs
+  M2R_STAMP_REAL(ST_REAL0);
+  M2R_STAMP(ST_START);
   // WPS > 1: the wave's role in its slot (0: also moves the INT8 fields;
   // WPS - 1: also moves the INT4 fields, steps the latent coefficients and
   // reads the rows out)
@@ -990,6 +1039,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     TokenStage& st = sm.stage;
     const int bt = b;   // b * L with L == 1
     load_args(a);
+    M2R_STAMP(ST_ARGS);
     // shared transfer j by wave j, branch-free: the B row (0), the C row (1),
     // the permutation bytes and the first 32 basis pairs (2), basis pairs
     // 32 .. NZ - 1 (3)
@@ -1039,7 +1089,9 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
       const uint16_t* src = a.x + ((size_t)bt * H + hk) * P + pbase + 2 * min(lane & 31, nvalid / 2 - 1);
       if (HPW % 2 == 0 || k < HPW) lds_dma_b32(src, lds_address(&wt.x[2 * j][0]));
     }
+    M2R_STAMP(ST_ISSUED);
     slot_dma(head_slot(0));
+    M2R_STAMP(ST_SLOT0_ISSUED);
     // head slot k's values (binary16 bits, or binary32 bits of D and
     // dt_bias), then head slot `lane`'s in lanes < HPW (the others take the
     // last slot's)
@@ -1069,12 +1121,18 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     // bottleneck: the binary64 constants go in vector registers; the
     // multi-wave slots, one wave per SIMD, keep them in scalar ones)
     act = wave_dt_activation<HPW, !PAIR>(raw, Ah, a.db_f32);
+#ifdef M2R_PHASE_TIMELINE
+    asm volatile("" ::"v"(act.x), "v"(act.y));   // the activation is complete at its stamp
+#endif
+    M2R_STAMP(ST_ACT);
     // this wave's token, statics and predictor transfers have landed
     if (!PAIR) wait_vmcnt<SLOT_DMA>();
     else if (own8) wait_vmcnt<OPS8>();
     else if (own4) wait_vmcnt<OPS4>();
     else wait_vmcnt<0>();
+    M2R_STAMP(ST_TOKEN);
     __syncthreads();          // ... and every other wave's
+    M2R_STAMP(ST_BARRIER);
     const uint32_t bw = st.b[lane], cw = st.c[lane];
     raw.bc[0] = (uint16_t)bw;
     raw.bc[1] = (uint16_t)(bw >> 16);
@@ -1178,6 +1236,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     GroupToken<NL>& gt = s_gt[SPLIT && !ONE ? (t & 1) : 0];
     wave_token_build<N8, N4, NZ, MODE, WPB, HPW, Smem::STAGED>(wt, gt, cur, act, pv0, pv1, e0v, e1v, s_pred, t == 0,
                                                               lane, wave);
+    if (t == 0) M2R_STAMP(ST_BUILD);
     // readout weights and dead-tier dot products of this token
     const float* cwt = SPLIT ? gt.cw : wt.cw;
     const float dot1 = SPLIT ? gt.tree[0] + gt.cw[NL] : wt.dots[1];
@@ -1200,6 +1259,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
         // a slot on several waves where a wave steps fields another one
         // moved: those transfers are visible to it after the barrier
         if constexpr (CROSS) __syncthreads();
+        if (k < 4) M2R_STAMP(ST_SLOT + 4 * k);
       }
       uint8_t* tile = s_tile[hh];
       uint16_t* t16 = (uint16_t*)tile;
@@ -1237,7 +1297,8 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           constexpr unsigned HAS8 = tier_waves<N8, N4, WPS, false>(), HAS4 = tier_waves<N8, N4, WPS, true>();
           // a tier's maximum is published only when another wave steps part of it
           constexpr bool SHARE8 = (HAS8 & (HAS8 - 1)) != 0, SHARE4 = (HAS4 & (HAS4 - 1)) != 0;
-          float accs[4] = {0.f, 0.f, 0.f, 0.f};
+          // per segment: the tiers' readout chains, then the segment's readout
+          float c8s[4] = {0.f, 0.f, 0.f, 0.f}, c4s[4] = {0.f, 0.f, 0.f, 0.f}, accs[4];
           uint32_t c8[M8 > 0 ? (M8 + 3) / 4 : 1], c4[M4 > 0 ? (M4 + 3) / 4 : 1];
           float v8[M8 > 0 ? M8 : 1], v4[M4 > 0 ? M4 : 1];
           float amax8 = 0.f, amax4 = 0.f, s8 = 0.f, s4 = 0.f, z0 = 0.f, z1 = 0.f;
@@ -1259,9 +1320,9 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
             }
             fin8 = __builtin_fabsf(s8) <= 65504.f;
             if (__builtin_amdgcn_ballot_w64(!fin8) == 0)
-              amax8 = tier_update<M8, true, false, N8, N4, A8>(c8, s8, decay, x, bdt4 + A8 / 4, cw4 + A8 / 4, accs, v8);
+              amax8 = tier_update<M8, true, false, N8, N4, A8>(c8, s8, decay, x, bdt4, cw4, c8s, v8);
             else
-              amax8 = tier_update<M8, true, true, N8, N4, A8>(c8, s8, decay, x, bdt4 + A8 / 4, cw4 + A8 / 4, accs, v8);
+              amax8 = tier_update<M8, true, true, N8, N4, A8>(c8, s8, decay, x, bdt4, cw4, c8s, v8);
             if constexpr (SHARE8) pmax[0][R][lane] = amax8;
           }
           if constexpr ((LAST || READS_OUT) && RIDGE) {   // the latent coefficients, read with the rows
@@ -1284,11 +1345,9 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
             }
             fin4 = __builtin_fabsf(s4) <= 65504.f;
             if (__builtin_amdgcn_ballot_w64(!fin4) == 0)
-              amax4 = tier_update<M4, false, false, N8, N4, N8 + A4>(c4, s4, decay, x, bdt4 + (N8 + A4) / 4,
-                                                                     cw4 + (N8 + A4) / 4, accs, v4);
+              amax4 = tier_update<M4, false, false, N8, N4, N8 + A4>(c4, s4, decay, x, bdt4, cw4, c4s, v4);
             else
-              amax4 = tier_update<M4, false, true, N8, N4, N8 + A4>(c4, s4, decay, x, bdt4 + (N8 + A4) / 4,
-                                                                    cw4 + (N8 + A4) / 4, accs, v4);
+              amax4 = tier_update<M4, false, true, N8, N4, N8 + A4>(c4, s4, decay, x, bdt4, cw4, c4s, v4);
             if constexpr (SHARE4) pmax[1][R][lane] = amax4;
           }
           uint32_t qz = 0;
@@ -1302,11 +1361,15 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           }
           // the left fold of the readout segments: the other waves publish
           // the fold of their segments, the reading wave folds them in order
+#pragma unroll
+          for (int sg = G0; sg < G1; ++sg) accs[sg] = segment_readout<N8, N4>(sg, c8s[sg], c4s[sg]);
           float part = accs[G0];
 #pragma unroll
           for (int sg = G0 + 1; sg < G1; ++sg) part = part + accs[sg];
           if constexpr (!READS_OUT) pacc[R][lane] = part;
+          if (t == 0) M2R_STAMP(ST_SLOT + 1);
           __syncthreads();   // readout partials and tier maxima are published
+          if (t == 0) M2R_STAMP(ST_SLOT + 2);
           if constexpr (READS_OUT) {
             float acc = RO == 0 ? part : pacc[0][lane];
 #pragma unroll
@@ -1373,10 +1436,10 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
         const bool base_ok = wt.bounded[k] != 0 && __builtin_fabsf(x) <= 65504.f;
         const f32x4* bdt4 = (const f32x4*)wt.bdt[k];
         const f32x4* cw4 = (const f32x4*)cwt;
-        // the readout's partial sums per readout segment, folded after both
-        // tiers (the order of the multi-wave slots, whose segments run on
-        // different waves)
-        float accs[4] = {0.f, 0.f, 0.f, 0.f};
+        // the readout per readout segment: each tier's contribution, then the
+        // segment's sum, folded after both tiers (the order of the multi-wave
+        // slots, whose segments run on different waves)
+        float c8s[4] = {0.f, 0.f, 0.f, 0.f}, c4s[4] = {0.f, 0.f, 0.f, 0.f};
 
         // ---- INT8 tier: unpack (byte k of c8[i] is q8 + 128 of internal
         // coordinate 4i+k), update with readout accumulation, requantize and
@@ -1401,10 +1464,16 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
             sc8 = 0.f;
           }
           const bool fin8 = __builtin_fabsf(sc8) <= 65504.f;
-          if (__builtin_amdgcn_ballot_w64(!fin8) == 0)
-            sc8 = tier_step<N8, true, MODE, false, N8, N4, 0>(c8, sc8, decay, x, bdt4, cw4, accs, base_ok);
-          else
-            sc8 = tier_step<N8, true, MODE, true, N8, N4, 0>(c8, sc8, decay, x, bdt4, cw4, accs, base_ok && fin8);
+          {
+            float v8[N8];
+            if (__builtin_amdgcn_ballot_w64(!fin8) == 0) {
+              const float m8 = tier_update<N8, true, false, N8, N4, 0>(c8, sc8, decay, x, bdt4, cw4, c8s, v8);
+              sc8 = tier_requant<N8, true, MODE>(v8, c8, m8, base_ok);
+            } else {
+              const float m8 = tier_update<N8, true, true, N8, N4, 0>(c8, sc8, decay, x, bdt4, cw4, c8s, v8);
+              sc8 = tier_requant<N8, true, MODE>(v8, c8, m8, base_ok && fin8);
+            }
+          }
           if (valid) {
             uint32_t wl[(W8 + 3) / 4], wh[(W8 + 3) / 4];
             bytes_to_planes8<N8>(c8, wl, wh);
@@ -1413,6 +1482,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
             t16[O_S8 / 2 + lane] = f2h(sc8);
           }
         }
+        if (t == 0 && k < 4) M2R_STAMP(ST_SLOT + 4 * k + 1);
         __builtin_amdgcn_sched_barrier(0);
         // the next slot's transfers are issued between the tiers, where the
         // other waves' arithmetic covers their issue time
@@ -1445,15 +1515,23 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           sc4 = z0 = z1 = 0.f;
         }
         const bool fin4 = __builtin_fabsf(sc4) <= 65504.f;
-        if (__builtin_amdgcn_ballot_w64(!fin4) == 0)
-          sc4 = tier_step<N4, false, MODE, false, N8, N4, N8>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, accs,
-                                                              base_ok);
-        else
-          sc4 = tier_step<N4, false, MODE, true, N8, N4, N8>(c4, sc4, decay, x, bdt4 + N8 / 4, cw4 + N8 / 4, accs,
-                                                             base_ok && fin4);
+        {
+          float v4[N4];
+          if (__builtin_amdgcn_ballot_w64(!fin4) == 0) {
+            const float m4 = tier_update<N4, false, false, N8, N4, N8>(c4, sc4, decay, x, bdt4, cw4, c4s, v4);
+            sc4 = tier_requant<N4, false, MODE>(v4, c4, m4, base_ok);
+          } else {
+            const float m4 = tier_update<N4, false, true, N8, N4, N8>(c4, sc4, decay, x, bdt4, cw4, c4s, v4);
+            sc4 = tier_requant<N4, false, MODE>(v4, c4, m4, base_ok && fin4);
+          }
+        }
         __builtin_amdgcn_sched_barrier(0);
+        if (t == 0 && k < 4) M2R_STAMP(ST_SLOT + 4 * k + 2);
         if (t == L - 1 && k > 0) slot_copy_out(hh - 1);   // the previous slot's state (head_slot(k - 1))
         __builtin_amdgcn_sched_barrier(0);
+        float accs[4];
+#pragma unroll
+        for (int sg = 0; sg < 4; ++sg) accs[sg] = segment_readout<N8, N4>(sg, c8s[sg], c4s[sg]);
         const float acc = ((accs[0] + accs[1]) + accs[2]) + accs[3];   // the readout segments' left fold
         // readout: sum_i u_i c_i + corrections = decay * (sum_i prior_i (c_i +
         // corr_i) + latent terms) + x * (dt * sum_all b c + D)
@@ -1486,17 +1564,29 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
         }
       }
       wave_sync();
+      if (t == 0 && k < 4) M2R_STAMP(ST_SLOT + 4 * k + 3);
     }
     if (t == L - 1) {
       // ... and the moving wave writes back every wave's last values
       if constexpr (CROSS) __syncthreads();
       slot_copy_out(head_slot(HPW - 1));
+      M2R_STAMP(ST_COPYOUT);
     }
     if (t + 1 < L) {
       if (((t + 1) & 63) == 0) batch_activation(t + 1);
       act = token_act(t + 1);
     }
   }
+#ifdef M2R_PHASE_TIMELINE
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): every store of the wave has completed
+  M2R_STAMP(ST_END);
+  M2R_STAMP_REAL(ST_REAL1);
+  wave_sync();
+  if (g_phase_stamps && lane < 32) {
+    const size_t blk = ((size_t)b * gridDim.y + by) * gridDim.x + bx;
+    g_phase_stamps[(blk * WPB + wave) * 32 + lane] = sm.stamps[wave][lane];
+  }
+#endif
 }
 
 template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE, int WPS = 1>

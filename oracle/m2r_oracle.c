@@ -792,3 +792,58 @@ int64_t orc_check_residual_round(uint64_t seed, int64_t n_random, int n_boundary
   if (flagged) *flagged = flg;
   return bad;
 }
+
+/* The device's two-sided magic-number quantizer (m2r_device.h,
+ * two_sided_code): with y = RN(1/d), y_hi = RN(y + y rel), y_lo = RN(y - y rel)
+ * and magic = 1.5 2^23 + bias, the codes t_hi = RN(v y_hi + magic) and
+ * t_lo = RN(v y_lo + magic) are kept when equal; then t - magic must equal
+ * roundf(v / d) with IEEE division, and the low byte of t the biased code.
+ * Same case mix as orc_check_residual_round: random quotients in
+ * (-lim - 1/2, lim + 1/2) over binary16 and binary32 divisors, and for every
+ * boundary scale the values k + 1/2 (times d, exact) and +-40 ulps around
+ * them.  Returns the number of kept codes that differ; *flagged counts the
+ * cases sent to the exact path. */
+int64_t orc_check_two_sided_round(uint64_t seed, int64_t n_random, int n_boundary_scales, float rel,
+                                  int64_t* flagged) {
+  int64_t bad = 0, flg = 0;
+#pragma omp parallel for reduction(+ : bad, flg) schedule(static)
+  for (int64_t i = 0; i < n_random + (int64_t)n_boundary_scales; ++i) {
+    uint64_t z = seed + (uint64_t)i * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    const int li = (int)((z >> 3) % 3);
+    const float lim = li == 0 ? 127.0f : (li == 1 ? 7.0f : 3.0f);
+    const float bias = li == 0 ? 128.0f : (li == 1 ? 8.0f : 4.0f);
+    float d;
+    if (z & 1) d = orc_f16_to_f32((uint16_t)(0x0400 + (uint16_t)((z >> 8) % (0x7BFF - 0x0400 + 1))));
+    else d = bits_f((uint32_t)(0x32800000u + ((z >> 8) % (0x7F000000u - 0x32800000u))));
+    const float y = 1.0f / d;
+    const float yh = fmaf(y, rel, y), yl = fmaf(y, -rel, y);
+    const float magic = 0x1.8p23f + bias;
+    float vs[2 * 81 * 2 + 1];
+    int nv = 0;
+    if (i < n_random) {
+      const float u = (bits_f((uint32_t)(0x3F800000u | ((z >> 20) & 0x7FFFFFu))) - 1.5f) * 2.0f * (lim + 0.49f);
+      vs[nv++] = u * d;
+    } else {
+      const int k = (int)((z >> 40) % (uint64_t)lim);     /* boundary k + 1/2 for k < lim */
+      const uint32_t mb = f_bits(((float)k + 0.5f) * d);  /* exact */
+      for (int du = -40; du <= 40; ++du) {
+        vs[nv++] = bits_f(mb + du);
+        vs[nv++] = -bits_f(mb + du);
+      }
+    }
+    for (int j = 0; j < nv; ++j) {
+      const float v = vs[j];
+      if (!isfinite(v) || fabsf(v / d) > lim + 0.49f) continue;
+      const float th = fmaf(v, yh, magic), tl = fmaf(v, yl, magic);
+      if (th != tl) { ++flg; continue; }
+      const int fast = (int)(th - magic);
+      const int exact = (int)roundf(v / d);
+      if (fast != exact || ((f_bits(th) - (uint32_t)(exact + (int)bias)) & 0xFFu) != 0u) ++bad;
+    }
+  }
+  if (flagged) *flagged = flg;
+  return bad;
+}

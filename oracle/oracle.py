@@ -53,6 +53,8 @@ def lib():
         _lib.orc_encode_legacy.argtypes = [P] * 6 + [I64]
         _lib.orc_check_residual_round.argtypes = [ctypes.c_uint64, I64, I, ctypes.c_float, ctypes.c_float, P]
         _lib.orc_check_residual_round.restype = I64
+        _lib.orc_check_two_sided_round.argtypes = [ctypes.c_uint64, I64, I, ctypes.c_float, P]
+        _lib.orc_check_two_sided_round.restype = I64
         _lib.orc_check_latent_division.argtypes = [ctypes.c_uint64, I]
         _lib.orc_check_latent_division.restype = I64
     return _lib
@@ -157,6 +159,14 @@ def check_residual_round(seed: int, n_random: int, n_boundary_scales: int, thr8:
     exact path)."""
     flagged = ctypes.c_int64(0)
     bad = lib().orc_check_residual_round(seed, n_random, n_boundary_scales, thr8, thr4, ctypes.byref(flagged))
+    return int(bad), int(flagged.value)
+
+
+def check_two_sided_round(seed: int, n_random: int, n_boundary_scales: int, rel: float):
+    """Returns (kept two-sided codes that differ from roundf(v / d), cases sent
+    to the exact path)."""
+    flagged = ctypes.c_int64(0)
+    bad = lib().orc_check_two_sided_round(seed, n_random, n_boundary_scales, rel, ctypes.byref(flagged))
     return int(bad), int(flagged.value)
 
 

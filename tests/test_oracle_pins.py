@@ -117,6 +117,32 @@ def test_residual_rounding_without_margin_is_caught(oracle):
     assert bad > 0
 
 
+# relative offset of the two-sided quantizer's reciprocals (m2r_device.h)
+TWO_SIDED_REL = 2.0 ** -22
+
+
+def test_two_sided_rounding_quantizer_equals_roundf_of_ieee_division(oracle):
+    """The device's unclamped quantizer in its two-sided form: the codes of
+    fma(v, y_hi, magic) and fma(v, y_lo, magic), with y = RN(1/d) and y_hi/lo
+    = RN(y (1 +- 2^-22)), are kept when they agree, and every kept code must
+    equal roundf(v / d) with its byte code + bias (lim 127, 7 and 3, random
+    quotients and every half-integer boundary +-40 ulps).  Near-ties reach
+    the exact path; so do fewer random cases than with a residual bound of
+    the same width would reach by chance."""
+    bad, flagged = oracle.check_two_sided_round(20261203, 20_000_000, 400_000, TWO_SIDED_REL)
+    assert bad == 0
+    assert flagged > 400_000   # boundary cases within the window went to the exact path
+
+
+@pytest.mark.parametrize("rel", [0.0, 2.0 ** -25])
+def test_two_sided_rounding_without_enough_margin_is_caught(oracle, rel):
+    """Planted mistakes: no offset (one code kept always, ties to even) and
+    an offset below the reciprocal's own rounding error both keep codes that
+    disagree with roundf(v / d) on the boundary cases."""
+    bad, _ = oracle.check_two_sided_round(20261203, 0, 20_000, rel)
+    assert bad > 0
+
+
 def test_latent_reciprocal_division_gives_ieee_e4m3_bytes(oracle):
     """Every binary16 latent scale: copysign(reciprocal-form quotient, z)
     yields the same E4M3 byte as IEEE z / ls, signed zeros and subnormals
