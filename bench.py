@@ -311,6 +311,56 @@ def stream_ceiling(device, reps=10):
                      "256-thread workgroups; GB/s of bytes read + written")
 
 
+PHASED_MIXES = {"read_100": (1, 0), "read_0": (0, 1), "read_10": (1, 9), "read_20": (1, 4),
+                "read_20_block16k": (4, 16), "read_30": (3, 7), "read_50": (1, 1)}
+
+
+def stream_sweep(device, reps=10):
+    """Read-fraction sweep and time-phased variants of the streaming probe
+    (m2r_stream_probe_phased): per 256-thread workgroup step, r 16-byte loads
+    then w 16-byte stores per thread (every instruction a contiguous 1 KiB per
+    wave), 0/10/20/30/50/100% of the bytes read (20% also with 16 KiB read and
+    64 KiB written per workgroup step); phase 0 (a thread stores once its own
+    loads land), 1 (a workgroup barrier between the step's loads and stores),
+    2 (the stores also complete before the next step's loads); one step per
+    workgroup or a grid of 2048 / 8192 workgroups; default or non-temporal
+    cache policy.  About 1 GiB moved per launch.  Returns GB/s per variant and
+    the best per mix."""
+    import ctypes
+    from mamba2_recall import _native
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=device)
+    dst = torch.empty(2 << 30, dtype=torch.uint8, device=device)
+    src.fill_(3)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    h = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out, best = {}, {}
+    for name, (r, w) in PHASED_MIXES.items():
+        per_step = 256 * 16 * (r + w)
+        steps = min((1 << 30) // per_step, (src.numel() // (256 * 16 * r)) if r else 1 << 62,
+                    (dst.numel() // (256 * 16 * max(w, 1))))
+        for phase in (0, 1, 2):
+            for blocks in (0, 2048, 8192):
+                for nt in (0, 1):
+                    def run():
+                        _native.call("m2r_stream_probe_phased", _native.ptr(src), _native.ptr(dst), steps, r, w,
+                                     phase, blocks, nt, h)
+                    run()
+                    torch.cuda.synchronize()
+                    ev0.record()
+                    for _ in range(reps):
+                        run()
+                    ev1.record()
+                    torch.cuda.synchronize()
+                    gbs = steps * per_step * reps / (ev0.elapsed_time(ev1) * 1e-3) / 1e9
+                    key = f"{name}/phase{phase}/{'blocks' + str(blocks) if blocks else 'onestep'}/{'nt' if nt else 'default'}"
+                    out[key] = round(gbs, 1)
+                    best[name] = max(best.get(name, 0.0), round(gbs, 1))
+    del src, dst
+    torch.cuda.empty_cache()
+    return dict(best_gbs=best, variants_gbs=out,
+                note="m2r_stream_probe_phased: GB/s of bytes read + written; read_N = N% of the bytes read")
+
+
 def fp4_full_decode(device, steps=10):
     """56 x in_proj [18560,4096] + 56 x out_proj [4096,8192]
     + embedding and lm_head [256000,4096]; random nibbles, lognormal(-3,0.5)
@@ -804,7 +854,7 @@ def main():
         print(json.dumps(dict(only="prefill", step_shape=args.step_shape, prefill_b1_2048=prefill_timing(device))))
         return
     if args.only == "ceiling":
-        print(json.dumps(dict(only="ceiling", ceiling=stream_ceiling(device))))
+        print(json.dumps(dict(only="ceiling", ceiling=stream_ceiling(device), sweep=stream_sweep(device))))
         return
     if args.only == "loader":
         print(json.dumps(dict(only="loader", loader=loader_bench(device))))

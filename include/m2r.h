@@ -189,6 +189,23 @@ int m2r_stream_probe(const void* src, void* dst, int64_t units, int read_bytes, 
                      int nontemporal, hipStream_t stream);
 
 /*
+ * Read-fraction sweep and time-phased variants of the streaming probe (no
+ * counterpart in the reference; a measurement aid).  Each of `steps`
+ * workgroup steps (256 threads) loads read_vectors 16-byte vectors per thread
+ * from a contiguous source block and stores write_vectors per thread to a
+ * contiguous destination block (src: steps*256*read_vectors*16 bytes, dst:
+ * steps*256*max(write_vectors,1)*16 bytes, 16-byte aligned), grid-stride over
+ * `blocks` workgroups (0: one step each).  phase 0: a thread stores as soon as
+ * its own loads land; 1: a workgroup barrier separates the step's loads from
+ * its stores; 2: the step's stores also complete, behind a barrier, before
+ * the next step's loads.  (read_vectors, write_vectors) in {(1,0), (0,1),
+ * (1,9), (1,4), (4,16), (3,7), (1,1)}: 100, 0, 10, 20, 20, 30 and 50% of
+ * the bytes read.
+ */
+int m2r_stream_probe_phased(const void* src, void* dst, int64_t steps, int read_vectors, int write_vectors,
+                            int phase, int blocks, int nontemporal, hipStream_t stream);
+
+/*
  * One launch of the one-token ridge-latent step over many layers whose inputs
  * are all resident: every workgroup reads its layer's arguments from a table
  * and runs the per-layer step on them (results identical to one

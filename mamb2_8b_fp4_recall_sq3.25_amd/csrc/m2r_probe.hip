@@ -161,9 +161,86 @@ __global__ __launch_bounds__(256) void k_stream_probe(const void* src, u32x4* ds
   }
 }
 
+// Read-fraction and time-phased streaming probe.  A workgroup step moves
+// RV 16-byte vectors per thread from a contiguous source block (every load
+// instruction a contiguous 1 KiB per wave) and then stores WV 16-byte vectors
+// per thread to a contiguous destination block (1 KiB per store instruction),
+// grid-stride over `steps` steps.  PHASE 0: each thread stores as soon as its
+// own loads have landed (the waves of a workgroup interleave loads and
+// stores); 1: a workgroup barrier between the step's loads and its stores
+// (every load of the workgroup has landed before any of its stores issue);
+// 2: also waits for the step's stores to complete, with a barrier, before the
+// next step's loads (the workgroup alternates whole read and write phases).
+// Stores write the XOR of the thread's loads (the step index when RV = 0).
+template <int RV, int WV, int PHASE, bool NT>
+__global__ __launch_bounds__(256) void k_phase_probe(const u32x4* src, u32x4* dst, int64_t steps) {
+  const int tid = threadIdx.x;
+  for (int64_t st = blockIdx.x; st < steps; st += gridDim.x) {
+    u32x4 x = u32x4{(uint32_t)st, (uint32_t)tid, 0u, 0u};
+    if constexpr (RV > 0) {
+      const u32x4* s = src + st * (256 * RV);
+      u32x4 v[RV];
+#pragma unroll
+      for (int i = 0; i < RV; ++i) v[i] = NT ? __builtin_nontemporal_load(s + 256 * i + tid) : s[256 * i + tid];
+#pragma unroll
+      for (int i = 0; i < RV; ++i) x ^= v[i];
+    }
+    if constexpr (PHASE >= 1) __syncthreads();
+    if constexpr (WV > 0) {
+      u32x4* d = dst + st * (256 * WV);
+#pragma unroll
+      for (int i = 0; i < WV; ++i) {
+        const u32x4 val = x + (uint32_t)i;
+        if constexpr (NT) __builtin_nontemporal_store(val, d + 256 * i + tid);
+        else d[256 * i + tid] = val;
+      }
+    } else {
+      if (x.x == 0x9E3779B9u && x.y == 0x7F4A7C15u) dst[tid] = x;   // keeps the loads live
+    }
+    if constexpr (PHASE == 2) {
+      __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this thread's stores have completed
+      __syncthreads();
+    }
+  }
+}
+
 }  // namespace m2r
 
 using namespace m2r;
+
+// Read-fraction sweep and time-phased variants (k_phase_probe): (read
+// vectors, write vectors) per thread and step in {(1,0), (0,1), (1,9), (1,4),
+// (4,16), (3,7), (1,1)} = 100, 0, 10, 20, 20, 30 and 50% of the bytes read,
+// phase 0, 1 or 2, default or non-temporal cache policy; `blocks` 0 = one step
+// per workgroup.
+extern "C" int m2r_stream_probe_phased(const void* src, void* dst, int64_t steps, int read_vectors,
+                                       int write_vectors, int phase, int blocks, int nontemporal,
+                                       hipStream_t stream) {
+  if (steps <= 0 || blocks < 0 || phase < 0 || phase > 2) return m2r_fail("phased probe: bad geometry");
+  if ((read_vectors > 0 && !src) || !dst || (((uintptr_t)src | (uintptr_t)dst) & 15))
+    return m2r_fail("phased probe: bad buffers");
+  if (blocks == 0) {
+    if (steps > 0x7FFFFFFF) return m2r_fail("phased probe: grid too large");
+    blocks = (int)steps;
+  }
+  const dim3 grid((unsigned)blocks), block(256);
+  const u32x4* s = (const u32x4*)src;
+  u32x4* d = (u32x4*)dst;
+#define M2R_PHASED(r, w)                                                                                    \
+  if (read_vectors == r && write_vectors == w) {                                                            \
+    if (phase == 0 && nontemporal) hipLaunchKernelGGL((k_phase_probe<r, w, 0, true>), grid, block, 0, stream, s, d, steps); \
+    if (phase == 0 && !nontemporal) hipLaunchKernelGGL((k_phase_probe<r, w, 0, false>), grid, block, 0, stream, s, d, steps); \
+    if (phase == 1 && nontemporal) hipLaunchKernelGGL((k_phase_probe<r, w, 1, true>), grid, block, 0, stream, s, d, steps); \
+    if (phase == 1 && !nontemporal) hipLaunchKernelGGL((k_phase_probe<r, w, 1, false>), grid, block, 0, stream, s, d, steps); \
+    if (phase == 2 && nontemporal) hipLaunchKernelGGL((k_phase_probe<r, w, 2, true>), grid, block, 0, stream, s, d, steps); \
+    if (phase == 2 && !nontemporal) hipLaunchKernelGGL((k_phase_probe<r, w, 2, false>), grid, block, 0, stream, s, d, steps); \
+    return m2r_check(hipGetLastError(), "phased probe");                                                    \
+  }
+  M2R_PHASED(1, 0) M2R_PHASED(0, 1) M2R_PHASED(1, 9) M2R_PHASED(1, 4) M2R_PHASED(4, 16) M2R_PHASED(3, 7)
+  M2R_PHASED(1, 1)
+#undef M2R_PHASED
+  return m2r_fail("phased probe: (read, write) vectors per thread must be (1,0), (0,1), (1,9), (1,4), (4,16), (3,7) or (1,1)");
+}
 
 // (RB, W, BURST, NT) instances: read-only, write-only, 1:1 copy, 2:7 vectors
 // (22:78, the FP4 G16 decode's byte mix), and a dword read per 16-byte write

@@ -36,6 +36,7 @@ _SIGNATURES = {
     "m2r_probe_div": ([P, P, P, I64, P], I),
     "m2r_set_fp4_decode_shape": ([I, I, I], I),
     "m2r_stream_probe": ([P, P, I64, I, I, I, I, I, P], I),
+    "m2r_stream_probe_phased": ([P, P, I64, I, I, I, I, I, P], I),
     "m2r_probe_butterfly": ([P, P, P], I),
     "m2r_set_step_shape": ([I, I], I),
     "m2r_causal_conv_update": ([P, I64, I64, I64, P, I64, P, P, P, I64, I64, I, I, P], I),
