@@ -244,116 +244,165 @@ __device__ __forceinline__ float state_update(float state, float decay, float in
 // m in [sqrt(1/2), sqrt(2)), log(m) = 2*atanh(s), s = (m-1)/(m+1), series to
 // s^23.  Constants are the binary64 roundings of the named values.
 //
-// A binary64 constant passed through an empty volatile asm: the value is
-// unchanged, but the compiler can no longer hoist its materialization out of
-// loops (keeping ~20 such constants in registers for a whole kernel).  VREG
-// materializes it in vector registers instead of scalar ones (for code whose
-// scalar issue is the bottleneck).
+// The binary64 constants of both recipes, by index (name, value).
+#define M2R_TRANS_CONSTS(X)                                                    \
+  X(KC_EXP_BIG, 100.0)                                                         \
+  X(KC_EXP_TINY, 110.0)                                                        \
+  X(KC_INV_LN2, 1.4426950408889634)              /* 1/ln2 */                   \
+  X(KC_LN2_HI, 6.93147180369123816490e-01)       /* high 32 bits of ln2 */     \
+  X(KC_LN2_LO, 1.90821492927058770002e-10)       /* ln2 - ln2_hi */            \
+  X(KC_MAGIC, 6755399441055744.0)                /* 1.5 * 2^52 */              \
+  X(KC_E13, 1.0 / 6227020800.0)                                                \
+  X(KC_E12, 1.0 / 479001600.0)                                                 \
+  X(KC_E11, 1.0 / 39916800.0)                                                  \
+  X(KC_E10, 1.0 / 3628800.0)                                                   \
+  X(KC_E9, 1.0 / 362880.0)                                                     \
+  X(KC_E8, 1.0 / 40320.0)                                                      \
+  X(KC_E7, 1.0 / 5040.0)                                                       \
+  X(KC_E6, 1.0 / 720.0)                                                        \
+  X(KC_E5, 1.0 / 120.0)                                                        \
+  X(KC_E4, 1.0 / 24.0)                                                         \
+  X(KC_E3, 1.0 / 6.0)                                                          \
+  X(KC_SQRT2, 1.4142135623730951)                                              \
+  X(KC_L23, 1.0 / 23.0)                                                        \
+  X(KC_L21, 1.0 / 21.0)                                                        \
+  X(KC_L19, 1.0 / 19.0)                                                        \
+  X(KC_L17, 1.0 / 17.0)                                                        \
+  X(KC_L15, 1.0 / 15.0)                                                        \
+  X(KC_L13, 1.0 / 13.0)                                                        \
+  X(KC_L11, 1.0 / 11.0)                                                        \
+  X(KC_L9, 1.0 / 9.0)                                                          \
+  X(KC_L7, 1.0 / 7.0)                                                          \
+  X(KC_L5, 1.0 / 5.0)                                                          \
+  X(KC_L3, 1.0 / 3.0)
+#define M2R_KC_NAME(n, v) n,
+#define M2R_KC_VALUE(n, v) v,
+enum TransConst { M2R_TRANS_CONSTS(M2R_KC_NAME) KC_COUNT };
+constexpr double kTransValue[KC_COUNT] = {M2R_TRANS_CONSTS(M2R_KC_VALUE)};
+#undef M2R_KC_NAME
+#undef M2R_KC_VALUE
+
+// How a recipe's binary64 constant is materialized (the value is the same):
+//  - KM_ASM: an immediate passed through an empty volatile asm, so the
+//    compiler can no longer hoist its materialization out of loops (keeping
+//    ~20 such constants in registers for a whole kernel); VREG materializes
+//    it in vector registers instead of scalar ones (for code whose scalar
+//    issue is the bottleneck);
+//  - KM_PLAIN: a plain immediate, for code that evaluates the recipes once
+//    (one token per launch): the compiler then materializes each constant
+//    once, shares it between the two exponentials and needs no copies.
 template <bool VREG = false>
 __device__ __forceinline__ double kconst(double v) {
   if constexpr (VREG) asm volatile("" : "+v"(v));
   else asm volatile("" : "+s"(v));
   return v;
 }
+enum { KM_ASM = 0, KM_PLAIN = 1 };
+template <bool VREG, int KM>
+__device__ __forceinline__ double kc(TransConst i) {
+  if constexpr (KM == KM_PLAIN) return kTransValue[i];
+  else return kconst<VREG>(kTransValue[i]);
+}
 
 // VREG: branch-free, the out-of-range cases selected at the end (the
 // polynomial then runs on an in-range stand-in argument); otherwise early
 // returns.  Both give the same bits.
-template <bool VREG = false>
+template <bool VREG = false, int KM = 0>
 __device__ __forceinline__ double xexp_d(double x) {
   if constexpr (!VREG) {
-    if (x > kconst(100.0)) return __builtin_inf();
-    if (x < -kconst(110.0)) return kconst(0.0);
+    if (x > kc<VREG, KM>(KC_EXP_BIG)) return __builtin_inf();
+    if (x < -kc<VREG, KM>(KC_EXP_TINY)) return 0.0;
   }
-  const bool big = VREG && x > kconst<VREG>(100.0), tiny = VREG && x < -kconst<VREG>(110.0);
+  const bool big = VREG && x > kc<VREG, KM>(KC_EXP_BIG), tiny = VREG && x < -kc<VREG, KM>(KC_EXP_TINY);
   const double xr = (big || tiny) ? 0.0 : x;
-  const double inv_ln2 = kconst<VREG>(1.4426950408889634);           // 1/ln2
-  const double ln2_hi = kconst<VREG>(6.93147180369123816490e-01);    // high 32 bits of ln2
-  const double ln2_lo = kconst<VREG>(1.90821492927058770002e-10);    // ln2 - ln2_hi
-  const double magic = kconst<VREG>(6755399441055744.0);             // 1.5 * 2^52
-  double kd = (xr * inv_ln2 + magic) - magic;           // rint(x/ln2)
-  double r = (xr - kd * ln2_hi) - kd * ln2_lo;
-  double p = kconst<VREG>(1.0 / 6227020800.0);                       // 1/13!
-  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 479001600.0));
-  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 39916800.0));
-  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 3628800.0));
-  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 362880.0));
-  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 40320.0));
-  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 5040.0));
-  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 720.0));
-  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 120.0));
-  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 24.0));
-  p = __builtin_fma(p, r, kconst<VREG>(1.0 / 6.0));
-  p = __builtin_fma(p, r, kconst<VREG>(0.5));
-  p = __builtin_fma(p, r, kconst<VREG>(1.0));
-  p = __builtin_fma(p, r, kconst<VREG>(1.0));
+  const double magic = kc<VREG, KM>(KC_MAGIC);
+  double kd = (xr * kc<VREG, KM>(KC_INV_LN2) + magic) - magic;   // rint(x/ln2)
+  double r = (xr - kd * kc<VREG, KM>(KC_LN2_HI)) - kd * kc<VREG, KM>(KC_LN2_LO);
+  double p = kc<VREG, KM>(KC_E13);                                 // 1/13!
+  p = __builtin_fma(p, r, kc<VREG, KM>(KC_E12));
+  p = __builtin_fma(p, r, kc<VREG, KM>(KC_E11));
+  p = __builtin_fma(p, r, kc<VREG, KM>(KC_E10));
+  p = __builtin_fma(p, r, kc<VREG, KM>(KC_E9));
+  p = __builtin_fma(p, r, kc<VREG, KM>(KC_E8));
+  p = __builtin_fma(p, r, kc<VREG, KM>(KC_E7));
+  p = __builtin_fma(p, r, kc<VREG, KM>(KC_E6));
+  p = __builtin_fma(p, r, kc<VREG, KM>(KC_E5));
+  p = __builtin_fma(p, r, kc<VREG, KM>(KC_E4));
+  p = __builtin_fma(p, r, kc<VREG, KM>(KC_E3));
+  p = __builtin_fma(p, r, 0.5);
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
   int64_t k = (int64_t)kd;
   double scale = __builtin_bit_cast(double, (uint64_t)(k + 1023) << 52);
   const double y = p * scale;
   return big ? __builtin_inf() : (tiny ? 0.0 : y);
 }
 
-template <bool VREG = false>
+template <bool VREG = false, int KM = 0>
 __device__ __forceinline__ double xlog_d(double x) {
   // Domain used by the codec: finite x >= 1 (softplus argument exp(d)+1).
   uint64_t u = __builtin_bit_cast(uint64_t, x);
   int64_t e = (int64_t)((u >> 52) & 0x7FF) - 1023;
   double m = __builtin_bit_cast(double, (u & 0x000FFFFFFFFFFFFFull) | 0x3FF0000000000000ull);
   if constexpr (VREG) {
-    const bool upper = m > kconst<VREG>(1.4142135623730951);
-    m = upper ? m * kconst<VREG>(0.5) : m;
+    const bool upper = m > kc<VREG, KM>(KC_SQRT2);
+    m = upper ? m * 0.5 : m;
     e += upper ? 1 : 0;
-  } else if (m > kconst(1.4142135623730951)) {
-    m = m * kconst(0.5);
+  } else if (m > kc<VREG, KM>(KC_SQRT2)) {
+    m = m * 0.5;
     e += 1;
   }
-  double s = (m - kconst<VREG>(1.0)) / (m + kconst<VREG>(1.0));
+  double s = (m - 1.0) / (m + 1.0);
   double s2 = s * s;
-  double p = kconst<VREG>(1.0 / 23.0);
-  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 21.0));
-  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 19.0));
-  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 17.0));
-  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 15.0));
-  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 13.0));
-  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 11.0));
-  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 9.0));
-  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 7.0));
-  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 5.0));
-  p = __builtin_fma(p, s2, kconst<VREG>(1.0 / 3.0));
-  p = __builtin_fma(p, s2, kconst<VREG>(1.0));
-  double logm = kconst<VREG>(2.0) * s * p;
+  double p = kc<VREG, KM>(KC_L23);
+  p = __builtin_fma(p, s2, kc<VREG, KM>(KC_L21));
+  p = __builtin_fma(p, s2, kc<VREG, KM>(KC_L19));
+  p = __builtin_fma(p, s2, kc<VREG, KM>(KC_L17));
+  p = __builtin_fma(p, s2, kc<VREG, KM>(KC_L15));
+  p = __builtin_fma(p, s2, kc<VREG, KM>(KC_L13));
+  p = __builtin_fma(p, s2, kc<VREG, KM>(KC_L11));
+  p = __builtin_fma(p, s2, kc<VREG, KM>(KC_L9));
+  p = __builtin_fma(p, s2, kc<VREG, KM>(KC_L7));
+  p = __builtin_fma(p, s2, kc<VREG, KM>(KC_L5));
+  p = __builtin_fma(p, s2, kc<VREG, KM>(KC_L3));
+  p = __builtin_fma(p, s2, 1.0);
+  double logm = 2.0 * s * p;
   double ed = (double)e;
-  const double ln2_hi = kconst<VREG>(6.93147180369123816490e-01);
-  const double ln2_lo = kconst<VREG>(1.90821492927058770002e-10);
+  const double ln2_hi = kc<VREG, KM>(KC_LN2_HI);
+  const double ln2_lo = kc<VREG, KM>(KC_LN2_LO);
   return (ed * ln2_hi + logm) + ed * ln2_lo;
 }
 
-template <bool VREG = false>
-__device__ __forceinline__ float xexpf(float x) { return (float)xexp_d<VREG>((double)x); }
-template <bool VREG = false>
-__device__ __forceinline__ float xlogf(float x) { return (float)xlog_d<VREG>((double)x); }
+template <bool VREG = false, int KM = 0>
+__device__ __forceinline__ float xexpf(float x) {
+  return (float)xexp_d<VREG, KM>((double)x);
+}
+template <bool VREG = false, int KM = 0>
+__device__ __forceinline__ float xlogf(float x) {
+  return (float)xlog_d<VREG, KM>((double)x);
+}
 
 // Mamba-2 dt activation of the codec kernels: v = dt + dt_bias;
 // v <= 20 ? log(exp(v) + 1) : v, with the inner +1 rounded in binary32
 // (VREG: branch-free, arguments above 20, and NaN, select v itself).
-template <bool VREG = false>
+template <bool VREG = false, int KM = 0>
 __device__ __forceinline__ float softplus_dt(float v) {
   if constexpr (!VREG) {
-    if (v <= 20.0f) return xlogf(xexpf(v) + 1.0f);
+    if (v <= 20.0f) return xlogf<VREG, KM>(xexpf<VREG, KM>(v) + 1.0f);
     return v;
   }
   const bool soft = v <= 20.0f;
-  const float e = xexpf<VREG>(soft ? v : 0.0f);
-  const float l = xlogf<VREG>(e + 1.0f);
+  const float e = xexpf<VREG, KM>(soft ? v : 0.0f);
+  const float l = xlogf<VREG, KM>(e + 1.0f);
   return soft ? l : v;
 }
 
 // dt activation and decay for one head (inline; its binary64 constants are
 // rematerialized at each use, see kconst).
-template <bool VREG = false>
+template <bool VREG = false, int KM = 0>
 __device__ __forceinline__ float2 dt_activation(float dt_plus_bias, float A) {
-  const float dtv = softplus_dt<VREG>(dt_plus_bias);
-  return make_float2(dtv, xexpf<VREG>(A * dtv));
+  const float dtv = softplus_dt<VREG, KM>(dt_plus_bias);
+  return make_float2(dtv, xexpf<VREG, KM>(A * dtv));
 }
 
 }  // namespace m2r

@@ -373,10 +373,10 @@ __device__ __forceinline__ void wave_load_rest(const StepArgs& a, WaveRaw<HPW>& 
 
 // dt activation of head slot `lane` (lanes < HPW; the others compute a copy
 // of the last slot's, unused).
-template <int HPW, bool VREG = false>
+template <int HPW, bool VREG = false, int KM = KM_ASM>
 __device__ __forceinline__ float2 wave_dt_activation(const WaveRaw<HPW>& r, float Ah, int db_f32) {
   const float db = db_f32 ? __builtin_bit_cast(float, (uint32_t)r.db_lo | ((uint32_t)r.db_hi << 16)) : h2f(r.db_lo);
-  return dt_activation<VREG>(h2f(r.dt) + db, Ah);
+  return dt_activation<VREG, KM>(h2f(r.dt) + db, Ah);
 }
 
 // Builds the wave's token values from its landed raw inputs and the dt
@@ -1119,8 +1119,9 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     d_bits = vD;
     // (with two waves per SIMD the prologue's scalar issue is its
     // bottleneck: the binary64 constants go in vector registers; the
-    // multi-wave slots, one wave per SIMD, keep them in scalar ones)
-    act = wave_dt_activation<HPW, !PAIR>(raw, Ah, a.db_f32);
+    // multi-wave slots, one wave per SIMD, keep them in scalar ones; one
+    // evaluation per launch, so plain immediates)
+    act = wave_dt_activation<HPW, !PAIR, KM_PLAIN>(raw, Ah, a.db_f32);
 #ifdef M2R_PHASE_TIMELINE
     asm volatile("" ::"v"(act.x), "v"(act.y));   // the activation is complete at its stamp
 #endif
@@ -1187,7 +1188,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     // dt activation of the first token (multi-token: of the first 64) while
     // the other loads are in flight
     if constexpr (ONE) {
-      act = wave_dt_activation<HPW>(raw, Ah, a.db_f32);
+      act = wave_dt_activation<HPW, false, KM_PLAIN>(raw, Ah, a.db_f32);
     } else {
       batch_activation(0);
       act = token_act(0);
