@@ -75,6 +75,7 @@ class RidgeStack:
         self.batch = batch
         self.tokens = tokens
         self.device = device
+        self.ws = None   # token-record workspace of a multi-token stack (allocated on first launch)
         gen = torch.Generator(device=device).manual_seed(seed)
         f16 = torch.float16
         self.layers = []
@@ -109,14 +110,21 @@ class RidgeStack:
         torch.cuda.synchronize()
 
     def launch_all(self, stream_handle):
+        """The 56 layers in order; a multi-token stack passes its token-record
+        workspace (one buffer: the layers run one after another on one
+        stream), as ridge_codec.scan does for multi-token calls."""
         p = self.native.ptr
+        if self.tokens > 1 and self.ws is None:
+            nbytes = int(self.native.lib().m2r_ridge_records_bytes(self.batch, self.tokens, G))
+            self.ws = torch.empty(nbytes // 4, dtype=torch.float32, device=self.device)
+        ws, ws_bytes = (p(self.ws), self.ws.numel() * 4) if self.ws is not None else (None, 0)
         for d in self.layers:
             t = d["state"].tensors
-            self.native.call("m2r_state_step_ridge", p(d["x"]), p(d["dt"]), p(d["A"]), p(d["B"]), p(d["C"]),
+            self.native.call("m2r_state_step_ridge_ws", p(d["x"]), p(d["dt"]), p(d["A"]), p(d["B"]), p(d["C"]),
                              p(d["D"]), 0, p(d["dt_bias"]), 0, p(d["perm"]), p(d["basis"]), p(d["lscale"]),
                              p(d["pred"]), p(t["lo"]), p(t["hi"]), p(t["q4"]), p(t["latent"]), p(t["s8"]),
                              p(t["s4"]), p(d["y"]), self.batch, self.tokens, H, P, G, d["n8"], d["n4"], d["nz"],
-                             stream_handle)
+                             ws, ws_bytes, stream_handle)
 
     def graph(self):
         import ctypes

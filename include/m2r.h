@@ -52,6 +52,29 @@ int m2r_state_step_ridge(const void* x, const void* dt, const float* A, const vo
                          int64_t H, int64_t P, int64_t G, int n8, int n4, int nz, hipStream_t stream);
 
 /*
+ * The same step with a caller workspace for its token records.  The
+ * reference computes the ridge correction of every token's readout weights
+ * before its scan (scripts/fp4_zero_predictor_codec_v1.py:221-225, the einsum
+ * over all L tokens); here, for L > 1 on the small-batch shapes (at most 1024
+ * 64-row slots) with 16-byte transfers, a first kernel writes one record per
+ * (batch row, token, group) of the state-independent token values (readout
+ * weights with the correction, dead-tier dot products, sum b.c, the carried
+ * b) into `workspace`, and the scan reads them instead of building each token
+ * itself.  Results are identical to m2r_state_step_ridge bit for bit.
+ * workspace: null (then exactly m2r_state_step_ridge), or 16-byte aligned
+ * device memory of at least m2r_ridge_records_bytes(batch, L, G) bytes,
+ * used on `stream` only (calls that overlap on one workspace race).
+ */
+int m2r_state_step_ridge_ws(const void* x, const void* dt, const float* A, const void* B, const void* C,
+                            const void* D, int d_is_f32, const void* dt_bias, int db_is_f32, const uint8_t* perm,
+                            const void* basis, const void* lscale, const void* pred, uint8_t* lo, uint8_t* hi,
+                            uint8_t* q4, uint8_t* latent, void* s8, void* s4, void* y, int64_t batch, int64_t L,
+                            int64_t H, int64_t P, int64_t G, int n8, int n4, int nz, void* workspace,
+                            int64_t workspace_bytes, hipStream_t stream);
+/* Workspace bytes of m2r_state_step_ridge_ws: batch * L * G records of 1 KiB. */
+int64_t m2r_ridge_records_bytes(int64_t batch, int64_t L, int64_t G);
+
+/*
  * Stored-scale tier step (INT8/INT4/zero-carry), same row format without the
  * latent.  Replaces scripts/state_ppl_codec_v10.py:157-192 (scan, _tier_scan
  * :78-154), scripts/w4_state_repair_codec_v2.py:103-137 (scan) and the

@@ -40,6 +40,11 @@ static void launch_shape(const StepArgs& a, dim3 grid, hipStream_t stream) {
   }
 }
 
+// args.rec on entry: a token-record workspace of at least B * L * G records
+// (or null).  The shapes of several waves per slot take it for a
+// multi-token ridge launch with 16-byte transfers: k_token_records fills it
+// and the step's token loop reads the records instead of building each
+// token (the same values); every other launch runs with rec = null.
 template <int N8, int N4, int NZ, int MODE>
 static hipError_t launch_layout(const StepArgs& args, hipStream_t stream) {
   StepArgs a = args;
@@ -48,11 +53,25 @@ static hipError_t launch_layout(const StepArgs& args, hipStream_t stream) {
   const int hpg = a.H / a.G;
   const long long slots = (long long)a.B * a.H * pblocks;
   const int forced = g_forced_shape.load(std::memory_order_relaxed);
+  float* const ws = (float*)args.rec;
+  a.rec = nullptr;
+  // the token records of a shape of several waves per slot
+  auto records = [&]() {
+    if constexpr (MODE == MODE_RIDGE) {
+      if (ws && a.L > 1 && (a.dma_tiles & 1)) {
+        hipLaunchKernelGGL((k_token_records<N8, N4, NZ>), dim3((a.L + REC_TOKENS - 1) / REC_TOKENS, a.G, a.B),
+                           dim3(256), 0, stream, a, ws);
+        a.rec = ws;
+      }
+    }
+  };
   if (forced == 4 * 16 && hpg % 2 == 0) {   // (4, 0): two waves per head slot
+    records();
     launch_shape<N8, N4, NZ, MODE, 4, 1, 2>(a, dim3(pblocks, a.H / 2, a.B), stream);
     return hipGetLastError();
   }
   if (forced == FOUR_PER_SLOT) {   // (4, -4): four waves per head slot
+    records();
     launch_shape<N8, N4, NZ, MODE, 4, 1, 4>(a, dim3(pblocks, a.H, a.B), stream);
     return hipGetLastError();
   }
@@ -69,8 +88,10 @@ static hipError_t launch_layout(const StepArgs& args, hipStream_t stream) {
   if (hpg % 16 == 0 && slots >= 16LL * 512) {
     launch_shape<N8, N4, NZ, MODE, 4, 4>(a, dim3(pblocks, a.H / 16, a.B), stream);
   } else if (slots <= 512) {   // four waves per slot, up to two waves per SIMD
+    records();
     launch_shape<N8, N4, NZ, MODE, 4, 1, 4>(a, dim3(pblocks, a.H, a.B), stream);
   } else if (hpg % 2 == 0 && slots <= 1024) {   // two waves per slot, up to two waves per SIMD
+    records();
     launch_shape<N8, N4, NZ, MODE, 4, 1, 2>(a, dim3(pblocks, a.H / 2, a.B), stream);
   } else if (hpg % 8 == 0 && slots >= 8LL * 512) {
     launch_shape<N8, N4, NZ, MODE, 4, 2>(a, dim3(pblocks, a.H / 8, a.B), stream);
@@ -149,13 +170,24 @@ static int check_geometry(int64_t batch, int64_t L, int64_t H, int64_t P, int64_
   return 0;
 }
 
-extern "C" int m2r_state_step_ridge(const void* x, const void* dt, const float* A, const void* B, const void* C,
-                                    const void* D, int d_is_f32, const void* dt_bias, int db_is_f32,
-                                    const uint8_t* perm, const void* basis, const void* lscale, const void* pred,
-                                    uint8_t* lo, uint8_t* hi, uint8_t* q4, uint8_t* latent, void* s8, void* s4,
-                                    void* y, int64_t batch, int64_t L, int64_t H, int64_t P, int64_t G, int n8,
-                                    int n4, int nz, hipStream_t stream) {
+extern "C" int64_t m2r_ridge_records_bytes(int64_t batch, int64_t L, int64_t G) {
+  if (batch <= 0 || L <= 0 || G <= 0) return 0;
+  return batch * L * G * (int64_t)(REC_FLOATS * sizeof(float));
+}
+
+extern "C" int m2r_state_step_ridge_ws(const void* x, const void* dt, const float* A, const void* B, const void* C,
+                                       const void* D, int d_is_f32, const void* dt_bias, int db_is_f32,
+                                       const uint8_t* perm, const void* basis, const void* lscale, const void* pred,
+                                       uint8_t* lo, uint8_t* hi, uint8_t* q4, uint8_t* latent, void* s8, void* s4,
+                                       void* y, int64_t batch, int64_t L, int64_t H, int64_t P, int64_t G, int n8,
+                                       int n4, int nz, void* workspace, int64_t workspace_bytes,
+                                       hipStream_t stream) {
   if (int e = check_geometry(batch, L, H, P, G)) return e;
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace))
+    return m2r_fail("ridge step: workspace size without a workspace");
+  if (workspace && ((uintptr_t)workspace & 15)) return m2r_fail("ridge step: workspace must be 16-byte aligned");
+  if (workspace && workspace_bytes < m2r_ridge_records_bytes(batch, L, G))
+    return m2r_fail("ridge step: workspace smaller than m2r_ridge_records_bytes(batch, L, G)");
   Dispatch d{};
   d.args = StepArgs{(const uint16_t*)x, (const uint16_t*)dt, A, (const uint16_t*)B, (const uint16_t*)C, D, dt_bias,
                     perm, (const uint16_t*)basis, (const uint16_t*)lscale, (const uint16_t*)pred, lo, hi, q4, latent,
@@ -163,10 +195,21 @@ extern "C" int m2r_state_step_ridge(const void* x, const void* dt, const float* 
                     d_is_f32, db_is_f32,
                     dma_tiles_ok(P, {lo, hi, q4, latent, s8, s4, pred}, {B, C, lscale}) |
                         staged_ok(H, {x, dt, A, D, dt_bias, perm, basis})};
+  d.args.rec = (const float*)workspace;
   d.n8_ = n8; d.n4_ = n4; d.nz_ = nz;
   hipError_t e = dispatch_ridge(d, stream);
   if (e == hipErrorInvalidValue) return m2r_fail("ridge step: unsupported tier layout");
   return m2r_check(e, "ridge step launch");
+}
+
+extern "C" int m2r_state_step_ridge(const void* x, const void* dt, const float* A, const void* B, const void* C,
+                                    const void* D, int d_is_f32, const void* dt_bias, int db_is_f32,
+                                    const uint8_t* perm, const void* basis, const void* lscale, const void* pred,
+                                    uint8_t* lo, uint8_t* hi, uint8_t* q4, uint8_t* latent, void* s8, void* s4,
+                                    void* y, int64_t batch, int64_t L, int64_t H, int64_t P, int64_t G, int n8,
+                                    int n4, int nz, hipStream_t stream) {
+  return m2r_state_step_ridge_ws(x, dt, A, B, C, D, d_is_f32, dt_bias, db_is_f32, perm, basis, lscale, pred, lo, hi,
+                                 q4, latent, s8, s4, y, batch, L, H, P, G, n8, n4, nz, nullptr, 0, stream);
 }
 
 extern "C" int m2r_state_step_tier(const void* x, const void* dt, const float* A, const void* B, const void* C,

@@ -90,6 +90,10 @@ struct StepArgs {
                            // even and 4-byte aligned x, dt, A, D, dt_bias, perm (and basis): the
                            // one-token instances may stage their inputs by dword transfers
   float rhpg;              // 1 / (H / G) rounded to binary32: group of head h = (int)((h + 0.5) * rhpg)
+  // multi-token ridge launches of several waves per slot: the token records
+  // k_token_records wrote ([B, L, G] records of REC_FLOATS), or null (each
+  // workgroup builds its tokens itself)
+  const float* rec;
 };
 
 // Loads every field of the arguments into scalar registers at once (one
@@ -306,6 +310,18 @@ struct GroupToken {
   float tree[4];                  // e0.c, e1.c, e0.b, e1.b
 };
 
+// Token record of the ridge codec: the per-token values of one (batch row,
+// group, token) that do not depend on the state, as the split token build
+// (wave_token_build, four waves) computes them: [REC_CW, REC_CW + NL + 2)
+// the readout weights and the latent coefficients' corrections (GroupToken
+// cw), [REC_TREE, REC_TREE + 4) the dead-tier dot products, REC_SBC the sum
+// of b.c, REC_BOK 1.0 when every carried b is finite (else 0.0), and
+// [REC_B, REC_B + NL) the carried b in internal order.  1 KiB: one 16-byte
+// load per lane of one wave.
+constexpr int REC_FLOATS = 256, REC_CW = 0, REC_TREE = 88, REC_SBC = 92, REC_BOK = 93, REC_B = 96;
+static_assert(REC_CW + 84 + 2 <= REC_TREE && REC_B + 84 <= REC_FLOATS, "every published layout fits (NL <= 84)");
+
+
 // Token inputs of a one-token workgroup staged in LDS by direct transfers
 // (the staged prologue): the group's B and C rows (f16 pairs) and statics,
 // `stat`: [0, 32) the permutation bytes, [32, 32 + NZ) the dead-tier basis
@@ -346,6 +362,18 @@ __device__ __forceinline__ void wave_load_dt(const StepArgs& a, WaveRaw<HPW>& r,
   r.db_lo = db[a.db_f32 ? 2 * h : h];
   r.db_hi = db[a.db_f32 ? 2 * h + 1 : h];
 }
+// x of the wave's rows in each head slot (a record-fed token loop loads
+// only these: dt comes 64 tokens at a time, B and C with the records).
+template <int WPB, int HPW, int WPS = 1>
+__device__ __forceinline__ void wave_load_x(const StepArgs& a, WaveRaw<HPW>& r, int bt, int h0, int pbase, int lane,
+                                            int wave) {
+  const int p = min(pbase + lane, a.P - 1);   // rows past P read row P-1 (never stored)
+#pragma unroll
+  for (int k = 0; k < HPW; ++k) {
+    const int h = h0 + (WPS > 1 ? wave / WPS : wave * HPW + k);
+    r.xv[k] = a.x[((size_t)bt * a.H + h) * a.P + p];
+  }
+}
 // ALIGNED: B and C are 4-byte aligned, so a lane's pair is one load each.
 template <int WPB, int HPW, bool ALIGNED, int WPS = 1>
 __device__ __forceinline__ void wave_load_rest(const StepArgs& a, WaveRaw<HPW>& r, int bt, int g, int h0,
@@ -363,12 +391,33 @@ __device__ __forceinline__ void wave_load_rest(const StepArgs& a, WaveRaw<HPW>& 
     r.bc[2] = a.Cm[row];
     r.bc[3] = a.Cm[row + 1];
   }
-  const int p = min(pbase + lane, a.P - 1);   // rows past P read row P-1 (never stored)
+  wave_load_x<WPB, HPW, WPS>(a, r, bt, h0, pbase, lane, wave);
+}
+
+// The wave's token values of a record-fed launch: x of its rows, per head
+// slot dt, the decay and the bound flag, B*dt of every carried coordinate
+// and sum b.c, with the same arithmetic as wave_token_build.
+template <int N8, int N4, int HPW>
+__device__ __forceinline__ void wave_token_from_record(WaveToken<N8, N4, HPW>& wt, const float* rec,
+                                                       const WaveRaw<HPW>& r, float2 act, int lane) {
+  constexpr int NL = N8 + N4;
+  static_assert(NL <= 84, "record layout");
+#pragma unroll
+  for (int k = 0; k < HPW; ++k) wt.x[k][lane] = r.xv[k];
+  const float b0 = rec[REC_B + min(lane, NL - 1)], b1 = rec[REC_B + min(64 + lane, NL - 1)];
+  const bool b_ok = rec[REC_BOK] != 0.f;
+  if (lane < HPW) {
+    wt.dtv[lane] = act.x;
+    wt.decay[lane] = act.y;
+    wt.bounded[lane] = (b_ok && 65504.f * __builtin_fabsf(act.x) < 0x1p100f && __builtin_fabsf(act.y) < 0x1p100f);
+  }
 #pragma unroll
   for (int k = 0; k < HPW; ++k) {
-    const int h = h0 + (WPS > 1 ? wave / WPS : wave * HPW + k);
-    r.xv[k] = a.x[((size_t)bt * a.H + h) * a.P + p];
+    const float dk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, act.x), k));
+    if (lane < NL) wt.bdt[k][lane] = b0 * dk;
+    if (64 + lane < NL) wt.bdt[k][64 + lane] = b1 * dk;
   }
+  if (lane == 0) wt.dots[0] = rec[REC_SBC];
 }
 
 // dt activation of head slot `lane` (lanes < HPW; the others compute a copy
@@ -782,6 +831,9 @@ struct StepSmem {
   // one-token instances of four or more waves stage their token inputs in
   // LDS by direct transfers (one shared transfer per wave)
   static constexpr bool STAGED = DMA && ONE && WPB >= 4 && NH <= 16;
+  // multi-token ridge instances of several waves per slot may be fed token
+  // records (StepArgs::rec): two buffers, by token parity
+  static constexpr bool RECS = RIDGE && PAIR && SPLIT && !ONE;
   // slot tile: lo, hi, q4, s8, s4 (and latent) fields of 64 rows, 16 bytes of slack
   static constexpr int TILE = 128 * (N8 / 2) + 64 * (N4 / 2) + 256 + (RIDGE ? 128 : 0) + 16;
   static constexpr int PRED_DW = RIDGE ? F * NZ / 2 : 1;
@@ -792,6 +844,7 @@ struct StepSmem {
   alignas(16) GroupToken<NL> gt[SPLIT && !ONE ? 2 : 1];
   alignas(16) uint32_t pred32[PRED_WORDS];
   alignas(16) std::conditional_t<STAGED, TokenStage, NoStage> stage;
+  alignas(16) float rec[RECS ? 2 : 1][RECS ? REC_FLOATS : 4];
   // WPS > 1 (per token parity): the readout partial sums of waves 0 ..
   // WPS - 2 of a slot, and every wave's maxima of its INT8 and INT4 parts
   alignas(16) float pacc[PAIR ? 2 : 1][PAIR ? NH : 1][PAIR ? WPS : 1][PAIR ? 64 : 1];
@@ -833,6 +886,12 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   using Smem = StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, WPS>;
   static_assert(Smem::TILE == TILE && Smem::PRED_WORDS == (DMA ? PRED_OPS16 * 256 : PRED_OPS * 64), "LDS layout");
   constexpr bool SPLIT = Smem::SPLIT;
+  // record-fed token loop (StepArgs::rec): every token's state-independent
+  // values come from its record; wave REC_LOADER loads record t + 1 while
+  // token t steps and puts it in LDS at the token's end
+  constexpr bool RECS = Smem::RECS;
+  const bool use_rec = RECS && a.rec != nullptr;
+  constexpr int REC_LOADER = 1;
   auto& s_wt = sm.wt;
   auto& s_gt = sm.gt;
   auto& s_pred32 = sm.pred32;
@@ -1025,6 +1084,12 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   uint32_t basis_w[2] = {0u, 0u};
   uint32_t ls_w = 0u;
   float2 act;
+  // record-fed loop: the loader's copy of the next token's record (16 bytes
+  // per lane), and the record of token t of this workgroup's batch row and group
+  uint4 rnext = make_uint4(0u, 0u, 0u, 0u);
+  auto rec_load = [&](int t) {
+    return ((const uint4*)(a.rec + ((size_t)(b * L + t) * a.G + g) * REC_FLOATS))[lane];
+  };
   if constexpr (Smem::STAGED) {
     // ---- staged prologue (one token, LDS transfers): the vector inputs of
     // the token and the statics travel by direct transfers into LDS together
@@ -1159,7 +1224,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     wave_load_dt<WPB, HPW, WPS>(a, raw, b * L, h0, lane, wave);
     const int hl = h0 + head_slot(min(lane, HPW - 1));   // head of slot `lane` (lanes < HPW)
     Ah = a.A[hl];
-    if constexpr (RIDGE) {
+    if (RIDGE && !use_rec) {   // (a record-fed loop never reads the predictor)
       const uint8_t* pg = (const uint8_t*)(a.pred + (size_t)g * F * NZ);
       if constexpr (DMA) {   // 16-byte chunks; lanes past the end re-read the last one
         for (int j = wave; j < PRED_OPS16; j += WPB)
@@ -1168,6 +1233,9 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
         for (int j = wave; j < PRED_OPS; j += WPB)
           lds_dma_b32(pg + 4 * min(j * 64 + lane, PRED_DW - 1), lds_address(s_pred32 + 64 * j));
       }
+    }
+    if constexpr (RECS) {
+      if (use_rec && wave == REC_LOADER) rnext = rec_load(0);
     }
     wave_load_rest<WPB, HPW, DMA, WPS>(a, raw, b * L, g, h0, pbase, lane, wave);
     // statics, kept as loaded bits until the first token's full wait (a
@@ -1203,6 +1271,9 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     else {
       for (int k = 0; k < HPW; ++k) slot_copy_in(head_slot(k));
     }
+    if constexpr (RECS) {   // record 0, published by the first token's barrier
+      if (use_rec && wave == REC_LOADER) ((uint4*)sm.rec[0])[lane] = rnext;
+    }
   }
   if (lane < HPW) wt.D[lane] = a.d_f32 ? __builtin_bit_cast(float, d_bits) : h2f((uint16_t)d_bits);
   const int pv0 = perm0 & 127, pv1 = perm1 & 127;   // raw B/C index of internal positions lane, lane + 64
@@ -1231,19 +1302,46 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     const int bt = b * L + t;
     const WaveRaw<HPW> cur = raw;
     if (t + 1 < L) {   // prefetch
-      wave_load_dt<WPB, HPW, WPS>(a, raw, bt + 1, h0, lane, wave);
-      wave_load_rest<WPB, HPW, DMA, WPS>(a, raw, bt + 1, g, h0, pbase, lane, wave);
+      if (use_rec) {
+        wave_load_x<WPB, HPW, WPS>(a, raw, bt + 1, h0, pbase, lane, wave);
+      } else {
+        wave_load_dt<WPB, HPW, WPS>(a, raw, bt + 1, h0, lane, wave);
+        wave_load_rest<WPB, HPW, DMA, WPS>(a, raw, bt + 1, g, h0, pbase, lane, wave);
+      }
     }
-    GroupToken<NL>& gt = s_gt[SPLIT && !ONE ? (t & 1) : 0];
-    wave_token_build<N8, N4, NZ, MODE, WPB, HPW, Smem::STAGED>(wt, gt, cur, act, pv0, pv1, e0v, e1v, s_pred, t == 0,
-                                                              lane, wave);
-    if (t == 0) M2R_STAMP(ST_BUILD);
     // readout weights and dead-tier dot products of this token
-    const float* cwt = SPLIT ? gt.cw : wt.cw;
-    const float dot1 = SPLIT ? gt.tree[0] + gt.cw[NL] : wt.dots[1];
-    const float dot2 = SPLIT ? gt.tree[1] + gt.cw[NL + 1] : wt.dots[2];
-    const float dot3 = SPLIT ? gt.tree[2] : wt.dots[3];
-    const float dot4 = SPLIT ? gt.tree[3] : wt.dots[4];
+    const float* cwt;
+    float dot1, dot2, dot3, dot4;
+    auto build_token = [&]() {
+      GroupToken<NL>& gt = s_gt[SPLIT && !ONE ? (t & 1) : 0];
+      wave_token_build<N8, N4, NZ, MODE, WPB, HPW, Smem::STAGED>(wt, gt, cur, act, pv0, pv1, e0v, e1v, s_pred,
+                                                                t == 0, lane, wave);
+      cwt = SPLIT ? gt.cw : wt.cw;
+      dot1 = SPLIT ? gt.tree[0] + gt.cw[NL] : wt.dots[1];
+      dot2 = SPLIT ? gt.tree[1] + gt.cw[NL + 1] : wt.dots[2];
+      dot3 = SPLIT ? gt.tree[2] : wt.dots[3];
+      dot4 = SPLIT ? gt.tree[3] : wt.dots[4];
+    };
+    if constexpr (RECS) {
+      if (use_rec) {
+        if (t + 1 < L && wave == REC_LOADER) rnext = rec_load(t + 1);
+        // record t is in LDS (put there during token t - 1, or before the
+        // first token), and every wave is done with token t - 1
+        __syncthreads();
+        const float* rv = sm.rec[t & 1];
+        wave_token_from_record<N8, N4, HPW>(wt, rv, cur, act, lane);
+        cwt = rv + REC_CW;
+        dot1 = rv[REC_TREE] + rv[REC_CW + NL];
+        dot2 = rv[REC_TREE + 1] + rv[REC_CW + NL + 1];
+        dot3 = rv[REC_TREE + 2];
+        dot4 = rv[REC_TREE + 3];
+      } else {
+        build_token();
+      }
+    } else {
+      build_token();
+    }
+    if (t == 0) M2R_STAMP(ST_BUILD);
 
     for (int k = 0; k < HPW; ++k) {
       // The slot's head index, opaque to the optimizer: every address and
@@ -1567,6 +1665,9 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
       wave_sync();
       if (t == 0 && k < 4) M2R_STAMP(ST_SLOT + 4 * k + 3);
     }
+    if constexpr (RECS) {   // record t + 1 into the buffer token t - 1 used (every wave is past it)
+      if (use_rec && wave == REC_LOADER && t + 1 < L) ((uint4*)sm.rec[(t + 1) & 1])[lane] = rnext;
+    }
     if (t == L - 1) {
       // ... and the moving wave writes back every wave's last values
       if constexpr (CROSS) __syncthreads();
@@ -1595,6 +1696,87 @@ __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(WPB ==
 void k_state_step(StepArgs a) {
   __shared__ StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, WPS> sm;
   state_step_body<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, WPS>(a, sm, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+// ---------------------------------------------------------------------------
+// Token records of a multi-token ridge launch (the record-fed token loop of
+// k_state_step): one four-wave workgroup per (REC_TOKENS tokens, group,
+// batch row) runs the split token build of every token (wave_token_build with
+// four waves: the same gathers, sums, ridge correction and dead-tier trees,
+// so the same bits) and wave 0 stores the state-independent values as the
+// token's record at rec[((b L + t) G + g) REC_FLOATS].  Needs 16-byte
+// aligned predictor and 4-byte aligned B and C (StepArgs::dma_tiles bit 0).
+constexpr int REC_TOKENS = 16;
+
+template <int N8, int N4, int NZ>
+struct RecordSmem {
+  static constexpr int NL = N8 + N4, F = NL + 2;
+  static constexpr int PRED_DW = F * NZ / 2, PRED_WORDS = (PRED_DW + 255) / 256 * 256;
+  alignas(16) WaveToken<N8, N4, 1> wt[4];
+  alignas(16) GroupToken<NL> gt[2];   // by token parity: wave 0 reads token t's while the others build t + 1
+  alignas(16) uint32_t pred32[PRED_WORDS];
+};
+
+template <int N8, int N4, int NZ>
+__global__ __launch_bounds__(256) void k_token_records(StepArgs a, float* rec) {
+  constexpr int NL = N8 + N4, F = NL + 2, RZ = next_pow2(NZ);
+  using Smem = RecordSmem<N8, N4, NZ>;
+  constexpr int PRED_OPS16 = (Smem::PRED_DW + 255) / 256;
+  static_assert(NL <= 84, "record layout");
+  __shared__ Smem sm;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = blockIdx.y, b = blockIdx.z;
+  const int L = a.L, t0 = blockIdx.x * REC_TOKENS, t1 = min(t0 + REC_TOKENS, L);
+  const int h0 = g * (a.H / a.G);   // a head of the group (the build also copies x of its rows: unused)
+  // the group's predictor (16-byte chunks; lanes past the end re-read the
+  // last one), permutation and dead-tier basis, as the step kernel loads them
+  const uint8_t* pg = (const uint8_t*)(a.pred + (size_t)g * F * NZ);
+  for (int j = wave; j < PRED_OPS16; j += 4)
+    lds_dma_b128(pg + 16 * min(j * 64 + lane, Smem::PRED_DW / 4 - 1), lds_address(sm.pred32 + 256 * j));
+  const uint32_t perm0 = a.perm[g * 128 + packed_lane<N8, N4>(lane)];
+  const uint32_t perm1 = a.perm[g * 128 + packed_lane<N8, N4>(64 + lane)];
+  float e0v[2], e1v[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int d0 = (RZ == 128) ? 2 * lane + j : lane;
+    const uint32_t w = ((const uint32_t*)a.basis)[g * NZ + min(d0, NZ - 1)];   // unused past NZ
+    e0v[j] = h2f((uint16_t)(w & 0xFFFFu));
+    e1v[j] = h2f((uint16_t)(w >> 16));
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the predictor transfer has landed
+  __syncthreads();                      // ... every wave's share
+  const int pv0 = perm0 & 127, pv1 = perm1 & 127;
+  const uint16_t* s_pred = (const uint16_t*)sm.pred32;
+  for (int t = t0; t < t1; ++t) {
+    WaveRaw<1> r;
+    wave_load_rest<4, 1, true, 4>(a, r, b * L + t, g, h0, 0, lane, wave);
+    GroupToken<NL>& gt = sm.gt[t & 1];
+    // dt 0, decay 0: the bound flag is then that of b alone
+    wave_token_build<N8, N4, NZ, MODE_RIDGE, 4, 1, false>(sm.wt[wave], gt, r, make_float2(0.f, 0.f), pv0, pv1, e0v,
+                                                         e1v, s_pred, false, lane, wave);
+    // (the split build ends with a workgroup barrier: gt is complete)
+    if (wave == 0) {
+      const WaveToken<N8, N4, 1>& wt = sm.wt[0];
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int idx = 4 * lane + i;
+        const float cw = gt.cw[min(idx, NL + 1)];
+        const float tr = gt.tree[min(max(idx - REC_TREE, 0), 3)];
+        const float bv = wt.b[min(max(idx - REC_B, 0), NL - 1)];
+        float x = 0.f;
+        if (idx < NL + 2) x = cw;
+        else if (idx >= REC_TREE && idx < REC_TREE + 4) x = tr;
+        else if (idx == REC_SBC) x = wt.dots[0];
+        else if (idx == REC_BOK) x = wt.bounded[0] ? 1.f : 0.f;
+        else if (idx >= REC_B && idx < REC_B + NL) x = bv;
+        v[i] = x;
+      }
+      float4* dst = (float4*)(rec + ((size_t)(b * L + t) * a.G + g) * REC_FLOATS);
+      dst[lane] = make_float4(v[0], v[1], v[2], v[3]);
+    }
+  }
 }
 
 }  // namespace m2r

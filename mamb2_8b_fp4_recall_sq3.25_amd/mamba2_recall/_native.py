@@ -23,6 +23,8 @@ _SIGNATURES = {
     "m2r_abi_version": ([], I),
     "m2r_last_error": ([], ctypes.c_char_p),
     "m2r_state_step_ridge": ([P] * 5 + [P, I, P, I] + [P] * 4 + [P] * 7 + [I64] * 5 + [I] * 3 + [P], I),
+    "m2r_state_step_ridge_ws": ([P] * 5 + [P, I, P, I] + [P] * 4 + [P] * 7 + [I64] * 5 + [I] * 3 + [P, I64, P], I),
+    "m2r_ridge_records_bytes": ([I64] * 3, I64),
     "m2r_state_step_tier": ([P] * 5 + [P, I, P, I] + [P] + [P] * 6 + [I64] * 5 + [I] * 3 + [P], I),
     "m2r_state_step_legacy": ([P] * 5 + [P, I, P, I] + [P] + [P] * 6 + [I64] * 5 + [P], I),
     "m2r_state_step_dense3": ([P] * 5 + [P, I, P, I] + [P, I] + [P] * 3 + [I64] * 5 + [P], I),

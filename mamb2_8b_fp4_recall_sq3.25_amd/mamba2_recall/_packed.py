@@ -57,10 +57,16 @@ def launch_packed(kind, x, dt, A, B, C, D, dt_bias, perm, tensors, *, n8, n4, nz
         common = (p(x), p(dt), p(A), p(B), p(C), p(D), d_f32, p(dt_bias), db_f32, p(perm))
         geo = (batch, length, heads, dim, groups)
         if kind == "ridge":
-            _native.call("m2r_state_step_ridge", *common, p(basis.contiguous()), p(lscale.contiguous()),
+            # multi-token calls on the small-batch shapes (at most 1024 64-row
+            # slots) take a token-record workspace (results identical without)
+            ws, ws_bytes = None, 0
+            if length > 1 and batch * heads * -(-dim // 64) <= 1024:
+                ws_bytes = int(_native.lib().m2r_ridge_records_bytes(batch, length, groups))
+                ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=x.device)
+            _native.call("m2r_state_step_ridge_ws", *common, p(basis.contiguous()), p(lscale.contiguous()),
                          p(pred.contiguous()), p(tensors["lo"]), p(tensors["hi"]), p(tensors["q4"]),
                          p(tensors["latent"]), p(tensors["s8"]), p(tensors["s4"]), p(y), *geo, n8, n4, nz,
-                         stream)
+                         p(ws) if ws is not None else None, ws_bytes, stream)
         elif kind == "tier":
             _native.call("m2r_state_step_tier", *common, p(tensors["lo"]), p(tensors["hi"]), p(tensors["q4"]),
                          p(tensors["s8"]), p(tensors["s4"]), p(y), *geo, n8, n4, nz, stream)

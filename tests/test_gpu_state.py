@@ -299,6 +299,67 @@ def test_ridge_every_shape_same_bits(device, L):
                 assert torch.equal(st[k], s0[k]), (layout, L, shape, k)
 
 
+def _ridge_step_direct(t, perm, basis, ls, pred, state, layout, ws):
+    """One m2r_state_step_ridge_ws call (ws: a workspace tensor or None)."""
+    from mamba2_recall import _native
+    n8, n4, nz = ridge_counts(layout)
+    p = _native.ptr
+    batch, L, H, P = t["x"].shape
+    G = t["B"].shape[2]
+    y = torch.empty_like(t["x"])
+    st = state.tensors
+    _native.call("m2r_state_step_ridge_ws", p(t["x"]), p(t["dt"]), p(t["A"]), p(t["B"]), p(t["C"]), p(t["D"]),
+                 int(t["D"].dtype == torch.float32), p(t["dt_bias"]), int(t["dt_bias"].dtype == torch.float32),
+                 p(perm), p(basis), p(ls), p(pred), p(st["lo"]), p(st["hi"]), p(st["q4"]), p(st["latent"]),
+                 p(st["s8"]), p(st["s4"]), p(y), batch, L, H, P, G, n8, n4, nz, p(ws),
+                 0 if ws is None else ws.numel() * 4, _native.stream_of(t["x"]))
+    return y
+
+
+@pytest.mark.parametrize("layout", RIDGE_LAYOUTS)
+def test_ridge_token_records_same_bits_as_in_kernel_build(device, layout):
+    """Multi-token launches of the shapes with several waves per slot read
+    their tokens' state-independent values from records a first kernel wrote
+    (the split token build of four waves, run per token): codes, scales,
+    latent bytes and y equal the in-kernel build's bit for bit, with the
+    automatic shape (four waves per slot) and forced two- and four-wave
+    slots, token counts that are and are not multiples of the records
+    kernel's 16 tokens per workgroup, and batch rows 1 and 2."""
+    from mamba2_recall import _native, ridge_codec
+    n8, n4, nz = ridge_counts(layout)
+    H, P, G = 128, 64, 8
+    try:
+        for shape in ((0, 0), (4, 0), (4, -4)):
+            for batch, L in ((1, 37), (2, 16), (1, 2)):
+                print(f"[token records] layout={layout} shape={shape} B={batch} L={L}", flush=True)
+                _native.call("m2r_set_step_shape", *shape)
+                rng = np.random.default_rng(700 + batch * 100 + L)
+                inp = cases.step_inputs(rng, batch, L, H, P, G)
+                sta = cases.ridge_statics(rng, G, n8, n4, nz)
+                st0 = cases.random_packed_state(rng, batch, H, P, n8, n4, latent=True)
+                t = device_inputs(inp, device)
+                perm = torch.from_numpy(inp["perm"]).to(device)
+                basis, ls, pred = (dev16(sta[k], device) for k in ("basis", "lscale", "pred"))
+                ws_bytes = int(_native.lib().m2r_ridge_records_bytes(batch, L, G))
+                assert ws_bytes == batch * L * G * 1024
+                # poison the workspace: every record value must come from the records kernel
+                ws = torch.full((ws_bytes // 4,), float("nan"), dtype=torch.float32, device=device)
+                s_build = ridge_codec.allocate_state(batch, H, P, 128, device, layout=layout)
+                s_rec = ridge_codec.allocate_state(batch, H, P, 128, device, layout=layout)
+                to_state(st0, s_build, device)
+                to_state(st0, s_rec, device)
+                y_build = _ridge_step_direct(t, perm, basis, ls, pred, s_build, layout, None)
+                y_rec = _ridge_step_direct(t, perm, basis, ls, pred, s_rec, layout, ws)
+                torch.cuda.synchronize()
+                assert torch.equal(y_rec.view(torch.int16), y_build.view(torch.int16)), (layout, shape, batch, L)
+                for k in s_build.tensors:
+                    assert torch.equal(s_rec.tensors[k].view(torch.uint8), s_build.tensors[k].view(torch.uint8)), \
+                        (layout, shape, batch, L, k)
+                assert not torch.isnan(ws).all()   # the records path ran
+    finally:
+        _native.call("m2r_set_step_shape", 0, 0)
+
+
 @pytest.mark.parametrize("forced_shape", SHAPES, indirect=True, ids=lambda s: f"w{s[0]}h{s[1]}")
 def test_ridge_every_workgroup_shape(oracle, device, forced_shape):
     """Each (waves, head slots per wave) variant: multi-token, ragged P, one

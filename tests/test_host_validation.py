@@ -216,6 +216,29 @@ def test_layers_step_rejects_bad_calls_before_any_launch():
     assert lib.m2r_state_step_ridge_layers_workspace(56) == 56 * lib.m2r_state_step_ridge_layers_workspace(1)
 
 
+def test_ridge_workspace_step_rejects_bad_workspaces_before_any_launch():
+    """The workspace variant of the ridge step checks its workspace on the
+    host (fake, never dereferenced device addresses): a size without a
+    workspace, a misaligned one and one smaller than the records need are
+    rejected with a message; the size query is batch * L * G KiB."""
+    from mamba2_recall import _native
+    lib = _native.lib()
+    assert lib.m2r_ridge_records_bytes(1, 2048, 8) == 2048 * 8 * 1024
+    assert lib.m2r_ridge_records_bytes(0, 5, 8) == 0
+    fake = [0x10000 * (i + 1) for i in range(20)]
+
+    def err(ws, nbytes):
+        args = fake[:6] + [0, fake[6], 0] + fake[7:11] + fake[11:18] + [1, 37, 128, 64, 8, 32, 28, 68, ws, nbytes,
+                                                                          None]
+        rc = lib.m2r_state_step_ridge_ws(*args)
+        assert rc != 0
+        return lib.m2r_last_error().decode()
+
+    assert "without a workspace" in err(None, 4096)
+    assert "16-byte" in err(0x900008, 1 << 30)
+    assert "smaller" in err(0x900000, 37 * 8 * 1024 - 1)
+
+
 def test_layer_table_rejects_mixed_group_counts():
     """The multi-layer launch takes one group count for all layers and the
     kernel indexes every layer's B, C and statics with it: a table whose
