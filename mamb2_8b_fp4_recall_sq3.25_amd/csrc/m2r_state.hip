@@ -28,6 +28,13 @@ static constexpr int FOUR_PER_SLOT = 256 + 4 * 16;
 template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, int WPS = 1>
 static void launch_shape(const StepArgs& a, dim3 grid, hipStream_t stream) {
   constexpr bool staged = StepSmem<N8, N4, NZ, MODE, WPB, HPW, true, true, WPS>::STAGED;
+  if constexpr (MODE == MODE_RIDGE && WPS > 1) {   // the record-fed instance (a.rec: records written)
+    if (a.rec) {
+      hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, WPB, HPW, true, false, WPS, true>), grid, dim3(64 * WPB), 0,
+                         stream, a);
+      return;
+    }
+  }
   if ((a.dma_tiles & 1) && a.L == 1 && (!staged || (a.dma_tiles & 2))) {
     hipLaunchKernelGGL((k_state_step<N8, N4, NZ, MODE, WPB, HPW, true, true, WPS>), grid, dim3(64 * WPB), 0, stream,
                        a);

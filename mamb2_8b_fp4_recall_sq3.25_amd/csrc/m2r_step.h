@@ -42,11 +42,15 @@ enum { MODE_LEGACY = 0, MODE_STORED = 1, MODE_RIDGE = 2 };
 // which gives the shader clock's rate.  Phases of slot k (k < 4) are stamps
 // ST_SLOT + 4 k + {0: its data landed, 1: update (one wave per slot: INT8
 // tier) done, 2: barrier passed (one wave per slot: INT4 tier done), 3: slot
-// done}.
+// done}.  Multi-token launches of several waves per slot also stamp token
+// ST_TL_TOKEN at ST_TL + {0: token start, 1: token values ready (record read
+// or token built), 2: update half done, 3: maxima barrier passed, 4:
+// requantization half done, 5: token end}.
 enum {
   ST_START = 0, ST_ARGS = 1, ST_ISSUED = 2, ST_SLOT0_ISSUED = 3, ST_ACT = 4, ST_TOKEN = 5, ST_BARRIER = 6,
-  ST_BUILD = 7, ST_SLOT = 8, ST_COPYOUT = 24, ST_END = 25, ST_REAL0 = 30, ST_REAL1 = 31
+  ST_BUILD = 7, ST_SLOT = 8, ST_TL = 12, ST_COPYOUT = 24, ST_END = 25, ST_REAL0 = 30, ST_REAL1 = 31
 };
+constexpr int ST_TL_TOKEN = 100;
 #ifdef M2R_PHASE_TIMELINE
 __device__ unsigned long long* g_phase_stamps;
 #define M2R_STAMP(i)                                                                     \
@@ -321,7 +325,6 @@ struct GroupToken {
 constexpr int REC_FLOATS = 256, REC_CW = 0, REC_TREE = 88, REC_SBC = 92, REC_BOK = 93, REC_B = 96;
 static_assert(REC_CW + 84 + 2 <= REC_TREE && REC_B + 84 <= REC_FLOATS, "every published layout fits (NL <= 84)");
 
-
 // Token inputs of a one-token workgroup staged in LDS by direct transfers
 // (the staged prologue): the group's B and C rows (f16 pairs) and statics,
 // `stat`: [0, 32) the permutation bytes, [32, 32 + NZ) the dead-tier basis
@@ -392,32 +395,6 @@ __device__ __forceinline__ void wave_load_rest(const StepArgs& a, WaveRaw<HPW>& 
     r.bc[3] = a.Cm[row + 1];
   }
   wave_load_x<WPB, HPW, WPS>(a, r, bt, h0, pbase, lane, wave);
-}
-
-// The wave's token values of a record-fed launch: x of its rows, per head
-// slot dt, the decay and the bound flag, B*dt of every carried coordinate
-// and sum b.c, with the same arithmetic as wave_token_build.
-template <int N8, int N4, int HPW>
-__device__ __forceinline__ void wave_token_from_record(WaveToken<N8, N4, HPW>& wt, const float* rec,
-                                                       const WaveRaw<HPW>& r, float2 act, int lane) {
-  constexpr int NL = N8 + N4;
-  static_assert(NL <= 84, "record layout");
-#pragma unroll
-  for (int k = 0; k < HPW; ++k) wt.x[k][lane] = r.xv[k];
-  const float b0 = rec[REC_B + min(lane, NL - 1)], b1 = rec[REC_B + min(64 + lane, NL - 1)];
-  const bool b_ok = rec[REC_BOK] != 0.f;
-  if (lane < HPW) {
-    wt.dtv[lane] = act.x;
-    wt.decay[lane] = act.y;
-    wt.bounded[lane] = (b_ok && 65504.f * __builtin_fabsf(act.x) < 0x1p100f && __builtin_fabsf(act.y) < 0x1p100f);
-  }
-#pragma unroll
-  for (int k = 0; k < HPW; ++k) {
-    const float dk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, act.x), k));
-    if (lane < NL) wt.bdt[k][lane] = b0 * dk;
-    if (64 + lane < NL) wt.bdt[k][64 + lane] = b1 * dk;
-  }
-  if (lane == 0) wt.dots[0] = rec[REC_SBC];
 }
 
 // dt activation of head slot `lane` (lanes < HPW; the others compute a copy
@@ -645,15 +622,16 @@ __device__ __forceinline__ void wave_token_build(WaveToken<N8, N4, HPW>& wt, Gro
 // coordinates reach, to the binary32 chain of prior * w over them (w the
 // readout weights; one segment's chain is live at a time, segments being
 // contiguous runs of chunks).  `bdt4` and `cw4` are the head's B*dt and the
-// readout weights of the carried coordinates, as four-value chunks.
+// readout weights of the carried coordinates, as four-value chunks (BMUL:
+// `bdt4` holds b, and B * dt is formed here with dtk).
 //
 // tier_update is the first half (dequantization, readout, update and the
 // maximum of |update|), tier_requant the second (the new scale and codes
 // from the maximum over the whole tier): a tier split between waves runs the
 // halves on its parts with the parts' maxima combined in between.
-template <int N, bool INT8, bool EXACT, int N8, int N4, int P0>
+template <int N, bool INT8, bool EXACT, int N8, int N4, int P0, bool BMUL = false>
 __device__ __forceinline__ float tier_update(const uint32_t* c, float sc, float decay, float x, const f32x4* bdt4,
-                                             const f32x4* cw4, float (&rs)[4], float (&v)[N]) {
+                                             const f32x4* cw4, float (&rs)[4], float (&v)[N], float dtk = 0.f) {
   constexpr float BIAS = INT8 ? 128.0f : 8.0f;
   static_assert(P0 % 4 == 0 && N % 4 == 0, "whole chunks");
   const float nb = -(1024.0f + BIAS) * sc;
@@ -667,7 +645,8 @@ __device__ __forceinline__ float tier_update(const uint32_t* c, float sc, float 
 #pragma unroll
   for (int i0 = 0; i0 < N; i0 += 4) {
     const int ci = C0 + i0 / 4;   // chunk index among the carried coordinates
-    const f32x4 cb = cb_next, cw = cw_next;
+    // BMUL: bdt4 holds b, and B * dt is formed here (the same RN(b * dt))
+    const f32x4 cb = BMUL ? cb_next * dtk : cb_next, cw = cw_next;
     if (i0 + 4 < N) {
       cb_next = bdt4[ci + 1];
       cw_next = cw4[ci + 1];
@@ -820,7 +799,7 @@ __device__ __forceinline__ float tier_requant(const float (&v)[N], uint32_t* c, 
 // slot's serial chain is about half or a quarter as long; `pacc` and `pmax`
 // pass the waves' readout partial sums and tier maxima (one buffer per token
 // parity).
-template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE, int WPS = 1>
+template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE, int WPS = 1, bool REC = false>
 struct StepSmem {
   static constexpr bool PAIR = WPS > 1;
   static_assert(WPS == 1 || ((WPS == 2 || WPS == 4) && HPW == 1 && WPB % WPS == 0),
@@ -831,9 +810,11 @@ struct StepSmem {
   // one-token instances of four or more waves stage their token inputs in
   // LDS by direct transfers (one shared transfer per wave)
   static constexpr bool STAGED = DMA && ONE && WPB >= 4 && NH <= 16;
-  // multi-token ridge instances of several waves per slot may be fed token
-  // records (StepArgs::rec): two buffers, by token parity
-  static constexpr bool RECS = RIDGE && PAIR && SPLIT && !ONE;
+  // REC: the record-fed instance (multi-token ridge, several waves per slot,
+  // 16-byte transfers): three record buffers (token t mod 3), and the prior
+  // latent coefficients the last wave of a slot passes to its reading wave
+  // (per token parity)
+  static_assert(!REC || (RIDGE && PAIR && SPLIT && !ONE && DMA), "record-fed instances");
   // slot tile: lo, hi, q4, s8, s4 (and latent) fields of 64 rows, 16 bytes of slack
   static constexpr int TILE = 128 * (N8 / 2) + 64 * (N4 / 2) + 256 + (RIDGE ? 128 : 0) + 16;
   static constexpr int PRED_DW = RIDGE ? F * NZ / 2 : 1;
@@ -844,7 +825,8 @@ struct StepSmem {
   alignas(16) GroupToken<NL> gt[SPLIT && !ONE ? 2 : 1];
   alignas(16) uint32_t pred32[PRED_WORDS];
   alignas(16) std::conditional_t<STAGED, TokenStage, NoStage> stage;
-  alignas(16) float rec[RECS ? 2 : 1][RECS ? REC_FLOATS : 4];
+  alignas(16) float rec[REC ? 3 : 1][REC ? REC_FLOATS : 4];
+  alignas(16) float2 pz[REC ? 2 : 1][REC ? NH : 1][REC ? 64 : 1];
   // WPS > 1 (per token parity): the readout partial sums of waves 0 ..
   // WPS - 2 of a slot, and every wave's maxima of its INT8 and INT4 parts
   alignas(16) float pacc[PAIR ? 2 : 1][PAIR ? NH : 1][PAIR ? WPS : 1][PAIR ? 64 : 1];
@@ -858,9 +840,9 @@ struct StepSmem {
 // The step of one workgroup: block coordinates (bx, by) and batch row b,
 // arguments `a`, LDS `sm`.  k_state_step runs it on its own grid; the
 // multi-layer kernel runs it with arguments read from a table of layers.
-template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE, int WPS = 1>
+template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE, int WPS = 1, bool REC = false>
 __device__ __forceinline__ void state_step_body(const StepArgs& a,
-                                                StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, WPS>& sm, int bx,
+                                                StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, WPS, REC>& sm, int bx,
                                                 int by, int b) {
   constexpr bool PAIR = WPS > 1;      // several waves per slot
   constexpr int W8 = N8 / 2;          // bytes per row of lo and of hi
@@ -883,14 +865,14 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   static_assert(!RIDGE || (F * NZ) % 2 == 0, "predictor staged as dwords");
   static_assert(TILE % 16 == 0, "tiles stay 16-byte aligned");
 
-  using Smem = StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, WPS>;
+  using Smem = StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, WPS, REC>;
   static_assert(Smem::TILE == TILE && Smem::PRED_WORDS == (DMA ? PRED_OPS16 * 256 : PRED_OPS * 64), "LDS layout");
   constexpr bool SPLIT = Smem::SPLIT;
-  // record-fed token loop (StepArgs::rec): every token's state-independent
-  // values come from its record; wave REC_LOADER loads record t + 1 while
-  // token t steps and puts it in LDS at the token's end
-  constexpr bool RECS = Smem::RECS;
-  const bool use_rec = RECS && a.rec != nullptr;
+  // REC, the record-fed token loop (StepArgs::rec): every token's
+  // state-independent values come from its record in LDS.  Wave REC_LOADER
+  // loads record t + 2 while token t steps, and puts record t + 1 in LDS
+  // before token t's maxima barrier, so that the maxima barrier is the only
+  // workgroup barrier of a token (after the first).
   constexpr int REC_LOADER = 1;
   auto& s_wt = sm.wt;
   auto& s_gt = sm.gt;
@@ -1084,9 +1066,10 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   uint32_t basis_w[2] = {0u, 0u};
   uint32_t ls_w = 0u;
   float2 act;
-  // record-fed loop: the loader's copy of the next token's record (16 bytes
-  // per lane), and the record of token t of this workgroup's batch row and group
-  uint4 rnext = make_uint4(0u, 0u, 0u, 0u);
+  // record-fed loop: the loader's copies of records t + 1 and t + 2 (16
+  // bytes per lane), and the record of token t of this workgroup's batch row
+  // and group
+  uint4 rnext = make_uint4(0u, 0u, 0u, 0u), rnext2 = make_uint4(0u, 0u, 0u, 0u);
   auto rec_load = [&](int t) {
     return ((const uint4*)(a.rec + ((size_t)(b * L + t) * a.G + g) * REC_FLOATS))[lane];
   };
@@ -1224,7 +1207,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     wave_load_dt<WPB, HPW, WPS>(a, raw, b * L, h0, lane, wave);
     const int hl = h0 + head_slot(min(lane, HPW - 1));   // head of slot `lane` (lanes < HPW)
     Ah = a.A[hl];
-    if (RIDGE && !use_rec) {   // (a record-fed loop never reads the predictor)
+    if (RIDGE && !REC) {   // (a record-fed loop never reads the predictor)
       const uint8_t* pg = (const uint8_t*)(a.pred + (size_t)g * F * NZ);
       if constexpr (DMA) {   // 16-byte chunks; lanes past the end re-read the last one
         for (int j = wave; j < PRED_OPS16; j += WPB)
@@ -1234,8 +1217,11 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           lds_dma_b32(pg + 4 * min(j * 64 + lane, PRED_DW - 1), lds_address(s_pred32 + 64 * j));
       }
     }
-    if constexpr (RECS) {
-      if (use_rec && wave == REC_LOADER) rnext = rec_load(0);
+    if constexpr (REC) {
+      if (wave == REC_LOADER) {
+        rnext2 = rec_load(0);
+        if (L > 1) rnext = rec_load(1);
+      }
     }
     wave_load_rest<WPB, HPW, DMA, WPS>(a, raw, b * L, g, h0, pbase, lane, wave);
     // statics, kept as loaded bits until the first token's full wait (a
@@ -1271,8 +1257,8 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     else {
       for (int k = 0; k < HPW; ++k) slot_copy_in(head_slot(k));
     }
-    if constexpr (RECS) {   // record 0, published by the first token's barrier
-      if (use_rec && wave == REC_LOADER) ((uint4*)sm.rec[0])[lane] = rnext;
+    if constexpr (REC) {   // record 0, published by the first token's barrier
+      if (wave == REC_LOADER) ((uint4*)sm.rec[0])[lane] = rnext2;
     }
   }
   if (lane < HPW) wt.D[lane] = a.d_f32 ? __builtin_bit_cast(float, d_bits) : h2f((uint16_t)d_bits);
@@ -1298,11 +1284,13 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   // a wave steps coordinates of a field another wave moves (not so only for
   // two waves split at the tier boundary)
   constexpr bool CROSS = PAIR && !(WPS == 2 && pair_cut(N8, N4) == N8);
+  int rbuf = 0;   // REC: the buffer of token t's record (t mod 3)
   for (int t = 0; t < L; ++t) {
     const int bt = b * L + t;
     const WaveRaw<HPW> cur = raw;
+    if (PAIR && t == ST_TL_TOKEN) M2R_STAMP(ST_TL);
     if (t + 1 < L) {   // prefetch
-      if (use_rec) {
+      if constexpr (REC) {
         wave_load_x<WPB, HPW, WPS>(a, raw, bt + 1, h0, pbase, lane, wave);
       } else {
         wave_load_dt<WPB, HPW, WPS>(a, raw, bt + 1, h0, lane, wave);
@@ -1322,26 +1310,22 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
       dot3 = SPLIT ? gt.tree[2] : wt.dots[3];
       dot4 = SPLIT ? gt.tree[3] : wt.dots[4];
     };
-    if constexpr (RECS) {
-      if (use_rec) {
-        if (t + 1 < L && wave == REC_LOADER) rnext = rec_load(t + 1);
-        // record t is in LDS (put there during token t - 1, or before the
-        // first token), and every wave is done with token t - 1
-        __syncthreads();
-        const float* rv = sm.rec[t & 1];
-        wave_token_from_record<N8, N4, HPW>(wt, rv, cur, act, lane);
-        cwt = rv + REC_CW;
-        dot1 = rv[REC_TREE] + rv[REC_CW + NL];
-        dot2 = rv[REC_TREE + 1] + rv[REC_CW + NL + 1];
-        dot3 = rv[REC_TREE + 2];
-        dot4 = rv[REC_TREE + 3];
-      } else {
-        build_token();
-      }
+    // REC: record t sits in buffer rbuf (put there before token t - 1's
+    // maxima barrier, or before the first token)
+    const float* rv = sm.rec[REC ? rbuf : 0];
+    if constexpr (REC) {
+      if (t + 2 < L && wave == REC_LOADER) rnext2 = rec_load(t + 2);
+      if (t == 0) __syncthreads();   // record 0 is in LDS
+      cwt = rv + REC_CW;
+      dot1 = rv[REC_TREE] + rv[REC_CW + NL];
+      dot2 = rv[REC_TREE + 1] + rv[REC_CW + NL + 1];
+      dot3 = rv[REC_TREE + 2];
+      dot4 = rv[REC_TREE + 3];
     } else {
       build_token();
     }
     if (t == 0) M2R_STAMP(ST_BUILD);
+    if (PAIR && t == ST_TL_TOKEN) M2R_STAMP(ST_TL + 1);
 
     for (int k = 0; k < HPW; ++k) {
       // The slot's head index, opaque to the optimizer: every address and
@@ -1372,12 +1356,19 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
         // coordinates with the whole tiers' maxima (the same values on every
         // wave, so the same scales and codes as one wave gets) and the last
         // wave steps the latent coefficients and reads the row out. ---------
-        const float x = h2f(wt.x[0][lane]);
-        const float decay = wt.decay[0];
-        const float dtv = wt.dtv[0];
-        const bool base_ok = wt.bounded[0] != 0 && __builtin_fabsf(x) <= 65504.f;
-        const f32x4* bdt4 = (const f32x4*)wt.bdt[0];
+        // (REC: from registers and the record: x of the wave's rows, dt and
+        // the decay, the bound flag with the record's flag for b, B * dt
+        // formed in tier_update from the record's b, and sum b.c)
+        const float x = REC ? h2f(cur.xv[0]) : h2f(wt.x[0][lane]);
+        const float decay = REC ? act.y : wt.decay[0];
+        const float dtv = REC ? act.x : wt.dtv[0];
+        const bool bounded = REC ? (rv[REC_BOK] != 0.f && 65504.f * __builtin_fabsf(act.x) < 0x1p100f &&
+                                    __builtin_fabsf(act.y) < 0x1p100f)
+                                 : wt.bounded[0] != 0;
+        const bool base_ok = bounded && __builtin_fabsf(x) <= 65504.f;
+        const f32x4* bdt4 = (const f32x4*)(REC ? rv + REC_B : wt.bdt[0]);
         const f32x4* cw4 = (const f32x4*)cwt;
+        const float sbc = REC ? rv[REC_SBC] : wt.dots[0];
         auto& pacc = sm.pacc[t & 1][hh];
         auto& pmax = sm.pmax[t & 1][hh];
         auto role_body = [&](auto role_c) {
@@ -1419,16 +1410,22 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
             }
             fin8 = __builtin_fabsf(s8) <= 65504.f;
             if (__builtin_amdgcn_ballot_w64(!fin8) == 0)
-              amax8 = tier_update<M8, true, false, N8, N4, A8>(c8, s8, decay, x, bdt4, cw4, c8s, v8);
+              amax8 = tier_update<M8, true, false, N8, N4, A8, REC>(c8, s8, decay, x, bdt4, cw4, c8s, v8, dtv);
             else
-              amax8 = tier_update<M8, true, true, N8, N4, A8>(c8, s8, decay, x, bdt4, cw4, c8s, v8);
+              amax8 = tier_update<M8, true, true, N8, N4, A8, REC>(c8, s8, decay, x, bdt4, cw4, c8s, v8, dtv);
             if constexpr (SHARE8) pmax[0][R][lane] = amax8;
           }
-          if constexpr ((LAST || READS_OUT) && RIDGE) {   // the latent coefficients, read with the rows
+          // the latent coefficients, read with the rows (REC: by the last
+          // wave only, which passes them to the reading wave through pz: the
+          // tile's latent bytes of token t are rewritten after the barrier
+          // without another barrier before token t + 1)
+          constexpr bool PASS_Z = REC && READS_OUT != LAST;
+          if constexpr ((LAST || (READS_OUT && !PASS_Z)) && RIDGE) {
             const uint32_t lat = t16[O_LAT / 2 + lane];
             z0 = e4m3_byte_to_f32<0>(lat) * ls0;
             z1 = e4m3_byte_to_f32<1>(lat) * ls1;
             if (PLACEHOLDERS && !valid) z0 = z1 = 0.f;
+            if constexpr (PASS_Z && LAST) sm.pz[t & 1][hh][lane] = make_float2(z0, z1);
           }
           if constexpr (M4 > 0) {
             {
@@ -1444,9 +1441,9 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
             }
             fin4 = __builtin_fabsf(s4) <= 65504.f;
             if (__builtin_amdgcn_ballot_w64(!fin4) == 0)
-              amax4 = tier_update<M4, false, false, N8, N4, N8 + A4>(c4, s4, decay, x, bdt4, cw4, c4s, v4);
+              amax4 = tier_update<M4, false, false, N8, N4, N8 + A4, REC>(c4, s4, decay, x, bdt4, cw4, c4s, v4, dtv);
             else
-              amax4 = tier_update<M4, false, true, N8, N4, N8 + A4>(c4, s4, decay, x, bdt4, cw4, c4s, v4);
+              amax4 = tier_update<M4, false, true, N8, N4, N8 + A4, REC>(c4, s4, decay, x, bdt4, cw4, c4s, v4, dtv);
             if constexpr (SHARE4) pmax[1][R][lane] = amax4;
           }
           uint32_t qz = 0;
@@ -1466,10 +1463,20 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
 #pragma unroll
           for (int sg = G0 + 1; sg < G1; ++sg) part = part + accs[sg];
           if constexpr (!READS_OUT) pacc[R][lane] = part;
+          if constexpr (REC) {   // record t + 1 into the buffer token t - 2 used (every wave is past it)
+            if (wave == REC_LOADER && t + 1 < L) ((uint4*)sm.rec[rbuf == 2 ? 0 : rbuf + 1])[lane] = rnext;
+          }
           if (t == 0) M2R_STAMP(ST_SLOT + 1);
+          if (t == ST_TL_TOKEN) M2R_STAMP(ST_TL + 2);
           __syncthreads();   // readout partials and tier maxima are published
           if (t == 0) M2R_STAMP(ST_SLOT + 2);
+          if (t == ST_TL_TOKEN) M2R_STAMP(ST_TL + 3);
           if constexpr (READS_OUT) {
+            if constexpr (PASS_Z && RIDGE) {
+              const float2 zz = sm.pz[t & 1][hh][lane];
+              z0 = zz.x;
+              z1 = zz.y;
+            }
             float acc = RO == 0 ? part : pacc[0][lane];
 #pragma unroll
             for (int r = 1; r < WPS; ++r) {
@@ -1481,8 +1488,8 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
               for (int sg = G0; sg < G1; ++sg) acc = acc + accs[sg];
             }
             float out;
-            if constexpr (RIDGE) out = decay * (acc + z0 * dot1 + z1 * dot2) + x * (dtv * wt.dots[0] + wt.D[0]);
-            else out = decay * acc + x * (dtv * wt.dots[0] + wt.D[0]);
+            if constexpr (RIDGE) out = decay * (acc + z0 * dot1 + z1 * dot2) + x * (dtv * sbc + wt.D[0]);
+            else out = decay * acc + x * (dtv * sbc + wt.D[0]);
             const __amdgpu_buffer_rsrc_t ry = raw_buffer(a.y + ((size_t)bt * H + h) * P + pbase, 2 * nvalid);
             __builtin_amdgcn_raw_buffer_store_b16(f2h(out), ry, 2 * lane, 0, STORE_THROUGH);
           }
@@ -1664,10 +1671,13 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
       }
       wave_sync();
       if (t == 0 && k < 4) M2R_STAMP(ST_SLOT + 4 * k + 3);
+      if (PAIR && t == ST_TL_TOKEN) M2R_STAMP(ST_TL + 4);
     }
-    if constexpr (RECS) {   // record t + 1 into the buffer token t - 1 used (every wave is past it)
-      if (use_rec && wave == REC_LOADER && t + 1 < L) ((uint4*)sm.rec[(t + 1) & 1])[lane] = rnext;
+    if constexpr (REC) {
+      rbuf = rbuf == 2 ? 0 : rbuf + 1;
+      if (wave == REC_LOADER) rnext = rnext2;
     }
+    if (PAIR && t == ST_TL_TOKEN) M2R_STAMP(ST_TL + 5);
     if (t == L - 1) {
       // ... and the moving wave writes back every wave's last values
       if constexpr (CROSS) __syncthreads();
@@ -1691,11 +1701,11 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
 #endif
 }
 
-template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE, int WPS = 1>
+template <int N8, int N4, int NZ, int MODE, int WPB, int HPW, bool DMA, bool ONE, int WPS = 1, bool REC = false>
 __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(WPB == 8 && WPS == 1 ? 4 : 2, 8)))
 void k_state_step(StepArgs a) {
-  __shared__ StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, WPS> sm;
-  state_step_body<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, WPS>(a, sm, blockIdx.x, blockIdx.y, blockIdx.z);
+  __shared__ StepSmem<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, WPS, REC> sm;
+  state_step_body<N8, N4, NZ, MODE, WPB, HPW, DMA, ONE, WPS, REC>(a, sm, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // ---------------------------------------------------------------------------

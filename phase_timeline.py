@@ -9,8 +9,9 @@ boundaries (m2r_step.h: ST_* stamps) and writes them to a device buffer.
                                      links lib/libm2r_timeline.so (CPU, hipcc)
   python phase_timeline.py run [--out FILE]
                                      on the GPU: the 56 published layers at
-                                     batch 1 and 64, each layer launched twice
-                                     in a row with the stamps (the second
+                                     batch 1 and 64 (one token) and the batch-1
+                                     2048-token prefill, each layer launched
+                                     twice in a row with the stamps (the second
                                      launch kept), and prints (or writes) the
                                      per-phase medians
 
@@ -35,7 +36,8 @@ LIB = PKG / "lib" / "libm2r_timeline.so"
 
 # stamp indices (m2r_step.h, enum ST_*)
 ST_START, ST_ARGS, ST_ISSUED, ST_SLOT0_ISSUED, ST_ACT, ST_TOKEN, ST_BARRIER, ST_BUILD, ST_SLOT = range(9)
-ST_COPYOUT, ST_END, ST_REAL0, ST_REAL1 = 24, 25, 30, 31
+ST_TL, ST_COPYOUT, ST_END, ST_REAL0, ST_REAL1 = 12, 24, 25, 30, 31
+ST_TL_TOKEN = 100   # the prefill token whose phases are stamped (m2r_step.h)
 
 
 def build():
@@ -77,6 +79,11 @@ def phase_rows(batch):
     return rows
 
 
+TL_ROWS = [("token values ready (record read, or token built)", ST_TL + 1), ("update half done", ST_TL + 2),
+           ("maxima barrier passed", ST_TL + 3), ("requantization half and y store done", ST_TL + 4),
+           ("token end (next record published)", ST_TL + 5)]
+
+
 def run(out):
     import numpy as np
     import torch
@@ -87,8 +94,9 @@ def run(out):
     if not LIB.exists():
         raise RuntimeError(f"{LIB} is missing: run `python phase_timeline.py build` first")
     lib = ctypes.CDLL(str(LIB))
-    argt, rest = _native._SIGNATURES["m2r_state_step_ridge"]
-    lib.m2r_state_step_ridge.argtypes, lib.m2r_state_step_ridge.restype = argt, rest
+    for name in ("m2r_state_step_ridge_ws", "m2r_ridge_records_bytes"):
+        argt, rest = _native._SIGNATURES[name]
+        getattr(lib, name).argtypes, getattr(lib, name).restype = argt, rest
     lib.m2r_timeline_set.argtypes, lib.m2r_timeline_set.restype = [ctypes.c_void_p], ctypes.c_int
     dev = torch.device("cuda:0")
     lines = [f"# phase timeline of the ridge step (instrumented build, kernel_source_sha16 {source_digest()})",
@@ -97,20 +105,23 @@ def run(out):
              "# layers, each layer launched twice in a row and the second launch kept; each stamp costs a few",
              "# instructions and an LDS write, so the instrumented launch is slightly slower than the library's"]
     p = _native.ptr
-    for batch in (64, 1):
-        print(f"[timeline] batch {batch}", flush=True)
-        st = bench.RidgeStack(batch, dev)
+    for batch, tokens in ((64, 1), (1, 1), (1, 2048)):
+        print(f"[timeline] batch {batch} tokens {tokens}", flush=True)
+        st = bench.RidgeStack(batch, dev, tokens=tokens)
         blocks = batch * 128 // 16 if batch == 64 else batch * 128   # (4,4) or four waves per head slot
         waves = blocks * 4
         buf = torch.zeros((56, waves * 32), dtype=torch.int64, device=dev)
+        ws = None
+        if tokens > 1:   # the token-record workspace, as bench.py's multi-token stack passes it
+            ws = torch.empty(lib.m2r_ridge_records_bytes(batch, tokens, 8) // 4, dtype=torch.float32, device=dev)
 
         def launch(d, stream):
             t = d["state"].tensors
-            rc = lib.m2r_state_step_ridge(p(d["x"]), p(d["dt"]), p(d["A"]), p(d["B"]), p(d["C"]), p(d["D"]), 0,
-                                          p(d["dt_bias"]), 0, p(d["perm"]), p(d["basis"]), p(d["lscale"]),
-                                          p(d["pred"]), p(t["lo"]), p(t["hi"]), p(t["q4"]), p(t["latent"]),
-                                          p(t["s8"]), p(t["s4"]), p(d["y"]), batch, 1, 128, 64, 8, d["n8"],
-                                          d["n4"], d["nz"], stream)
+            rc = lib.m2r_state_step_ridge_ws(p(d["x"]), p(d["dt"]), p(d["A"]), p(d["B"]), p(d["C"]), p(d["D"]), 0,
+                                             p(d["dt_bias"]), 0, p(d["perm"]), p(d["basis"]), p(d["lscale"]),
+                                             p(d["pred"]), p(t["lo"]), p(t["hi"]), p(t["q4"]), p(t["latent"]),
+                                             p(t["s8"]), p(t["s4"]), p(d["y"]), batch, tokens, 128, 64, 8, d["n8"],
+                                             d["n4"], d["nz"], p(ws), 0 if ws is None else ws.numel() * 4, stream)
             assert rc == 0, rc
 
         stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -134,10 +145,31 @@ def run(out):
         ghz = np.median(ticks / np.maximum(real, 1e-3)) / 1e3
         span = [(s[i, :, ST_REAL1].max() - s[i, :, ST_REAL0].min()) / 100.0 for i in range(56)]
         start_spread = [(s[i, :, ST_REAL0].max() - s[i, :, ST_REAL0].min()) / 100.0 for i in range(56)]
-        lines += ["", f"## batch {batch}: {blocks} workgroups x 4 waves per launch; shader clock {ghz:.2f} GHz",
+        what = "one token" if tokens == 1 else f"{tokens}-token prefill"
+        lines += ["", f"## batch {batch}, {what}: {blocks} workgroups x 4 waves per launch; shader clock {ghz:.2f} GHz",
                   f"launch span (first wave start to last wave end), median over layers: {np.median(span):.2f} µs "
-                  f"(min {np.min(span):.2f}, max {np.max(span):.2f}); wave start spread {np.median(start_spread):.2f} µs",
-                  f"{'phase':52s} {'median':>8s}  [p10 - p90] µs"]
+                  f"(min {np.min(span):.2f}, max {np.max(span):.2f}); wave start spread {np.median(start_spread):.2f} µs"]
+        if tokens > 1:
+            lines += [f"per token: {np.median(span) / tokens:.3f} µs (span / tokens); token {ST_TL_TOKEN}, µs from "
+                      "that token's start on each wave:", f"{'phase':52s} {'median':>8s}  [p10 - p90] µs"]
+            for label, idx in TL_ROWS:
+                v = (s[:, :, idx] - s[:, :, ST_TL]) / (ghz * 1e3)
+                v = v[(s[:, :, idx] != 0) & (s[:, :, ST_TL] != 0)]
+                lines.append(f"{label:52s} {np.median(v):8.3f}  [{np.percentile(v, 10):.3f} - "
+                             f"{np.percentile(v, 90):.3f}]")
+            # per wave of the slot (wave w of a four-wave workgroup steps readout segment w)
+            lines.append(f"by wave of the slot, medians (µs from the token's start): " +
+                         ", ".join(label.split(" (")[0] for label, _ in TL_ROWS))
+            for w in range(4):
+                cells = []
+                for _, idx in TL_ROWS:
+                    v = (s[:, w::4, idx] - s[:, w::4, ST_TL]) / (ghz * 1e3)
+                    cells.append(f"{np.median(v[(s[:, w::4, idx] != 0) & (s[:, w::4, ST_TL] != 0)]):.3f}")
+                lines.append(f"  wave {w}: " + "  ".join(cells))
+            del st, buf, ws
+            torch.cuda.empty_cache()
+            continue
+        lines.append(f"{'phase':52s} {'median':>8s}  [p10 - p90] µs")
         for label, idx in phase_rows(batch):
             v = (s[:, :, idx] - s[:, :, ST_START]) / (ghz * 1e3)
             v = v[s[:, :, idx] != 0]
