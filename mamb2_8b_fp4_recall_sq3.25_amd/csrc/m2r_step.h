@@ -228,6 +228,20 @@ constexpr unsigned tier_waves() {
   return m;
 }
 
+// Code words (four coordinates each) of wave r's part of one tier, and the
+// most any wave of a WPS-wave slot has.
+constexpr int role_words(int n8, int n4, int wps, int r, bool tier4) {
+  const int lo = seg_pos(n8, n4, role_seg(n8, n4, wps, r)), hi = seg_pos(n8, n4, role_seg(n8, n4, wps, r + 1));
+  const int a = tier4 ? (lo > n8 ? lo - n8 : 0) : (lo < n8 ? lo : n8);
+  const int e = tier4 ? (hi > n8 ? hi - n8 : 0) : (hi < n8 ? hi : n8);
+  return (e - a + 3) / 4;
+}
+constexpr int max_role_words(int n8, int n4, int wps, bool tier4) {
+  int m = 1;
+  for (int r = 0; r < wps; ++r) m = role_words(n8, n4, wps, r, tier4) > m ? role_words(n8, n4, wps, r, tier4) : m;
+  return m;
+}
+
 template <int N8, int N4>
 __device__ __forceinline__ int packed_lane(int j) {
   return j < N8 ? tier_packed_of(j, N8) : (j < N8 + N4 ? N8 + tier_packed_of(j - N8, N4) : j);
@@ -1285,6 +1299,14 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   // two waves split at the tier boundary)
   constexpr bool CROSS = PAIR && !(WPS == 2 && pair_cut(N8, N4) == N8);
   int rbuf = 0;   // REC: the buffer of token t's record (t mod 3)
+  // KEEP (several waves per slot, several tokens): a wave's code words stay
+  // in registers from token to token, read from the tile at the first token
+  // and written back at the last (no nibble-plane unpacking and repacking
+  // per token); so do the latent bytes where only the last wave reads them
+  constexpr bool KEEP = PAIR && !ONE;
+  uint32_t keep8[max_role_words(N8, N4, PAIR ? WPS : 1, false)];
+  uint32_t keep4[max_role_words(N8, N4, PAIR ? WPS : 1, true)];
+  uint32_t keep_lat = 0u;
   for (int t = 0; t < L; ++t) {
     const int bt = b * L + t;
     const WaveRaw<HPW> cur = raw;
@@ -1395,8 +1417,14 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           bool fin8 = true, fin4 = true;
           // a tier's scale: the tile's at the first token, then the value this
           // wave requantized with (every wave of the tier derives the same one)
+          // (KEEP: the latent bytes stay in a register where only this last
+          // wave reads them, i.e. unless a reading wave reads the tile's)
+          constexpr bool KEEP_LAT = KEEP && (REC || RO == WPS - 1);
           if constexpr (M8 > 0) {
-            {
+            if (KEEP && t > 0) {
+#pragma unroll
+              for (int i = 0; i < (M8 + 3) / 4; ++i) c8[i] = keep8[i];
+            } else {
               uint32_t wl[(M8 / 2 + 3) / 4], wh[(M8 / 2 + 3) / 4];
               lds_read_row<M8 / 2>(tile + O_LO, lane * W8 + A8 / 2, wl);
               lds_read_row<M8 / 2>(tile + O_HI, lane * W8 + A8 / 2, wh);
@@ -1421,14 +1449,17 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           // without another barrier before token t + 1)
           constexpr bool PASS_Z = REC && READS_OUT != LAST;
           if constexpr ((LAST || (READS_OUT && !PASS_Z)) && RIDGE) {
-            const uint32_t lat = t16[O_LAT / 2 + lane];
+            const uint32_t lat = (KEEP_LAT && LAST && t > 0) ? keep_lat : (uint32_t)t16[O_LAT / 2 + lane];
             z0 = e4m3_byte_to_f32<0>(lat) * ls0;
             z1 = e4m3_byte_to_f32<1>(lat) * ls1;
             if (PLACEHOLDERS && !valid) z0 = z1 = 0.f;
             if constexpr (PASS_Z && LAST) sm.pz[t & 1][hh][lane] = make_float2(z0, z1);
           }
           if constexpr (M4 > 0) {
-            {
+            if (KEEP && t > 0) {
+#pragma unroll
+              for (int i = 0; i < (M4 + 3) / 4; ++i) c4[i] = keep4[i];
+            } else {
               uint32_t wq[(M4 / 2 + 3) / 4];
               lds_read_row<M4 / 2>(tile + O_Q4, lane * W4 + A4 / 2, wq);
               plane_to_bytes4<M4>(wq, c4);
@@ -1504,7 +1535,11 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           if constexpr (M8 > 0) {
             const float m8 = tier_max(0, amax8, HAS8);
             sc8_carry = tier_requant<M8, true, MODE>(v8, c8, m8, base_ok && fin8);
-            if (valid) {
+            if constexpr (KEEP) {
+#pragma unroll
+              for (int i = 0; i < (M8 + 3) / 4; ++i) keep8[i] = c8[i];
+            }
+            if (valid && (!KEEP || t == L - 1)) {
               uint32_t wl[(M8 / 2 + 3) / 4], wh[(M8 / 2 + 3) / 4];
               bytes_to_planes8<M8>(c8, wl, wh);
               lds_write_row<M8 / 2>(tile + O_LO, lane * W8 + A8 / 2, wl);
@@ -1515,7 +1550,11 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           if constexpr (M4 > 0) {
             const float m4 = tier_max(1, amax4, HAS4);
             sc4_carry = tier_requant<M4, false, MODE>(v4, c4, m4, base_ok && fin4);
-            if (valid) {
+            if constexpr (KEEP) {
+#pragma unroll
+              for (int i = 0; i < (M4 + 3) / 4; ++i) keep4[i] = c4[i];
+            }
+            if (valid && (!KEEP || t == L - 1)) {
               uint32_t wq[(M4 / 2 + 3) / 4];
               bytes_to_plane4<M4>(c4, wq);
               lds_write_row<M4 / 2>(tile + O_Q4, lane * W4 + A4 / 2, wq);
@@ -1523,7 +1562,8 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
             }
           }
           if constexpr (LAST && RIDGE) {
-            if (valid) t16[O_LAT / 2 + lane] = (uint16_t)qz;
+            if constexpr (KEEP_LAT) keep_lat = qz;
+            if (valid && (!KEEP_LAT || t == L - 1)) t16[O_LAT / 2 + lane] = (uint16_t)qz;
           }
         };
         if constexpr (WPS == 2) {
