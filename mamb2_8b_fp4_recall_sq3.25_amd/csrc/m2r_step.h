@@ -1754,9 +1754,10 @@ void k_state_step(StepArgs a) {
 // batch row) runs the split token build of every token (wave_token_build with
 // four waves: the same gathers, sums, ridge correction and dead-tier trees,
 // so the same bits) and wave 0 stores the state-independent values as the
-// token's record at rec[((b L + t) G + g) REC_FLOATS].  Needs 16-byte
+// token's record at rec[((b L + t) G + g) REC_FLOATS].  Each token's inputs
+// are loaded while the previous token is built.  Needs 16-byte
 // aligned predictor and 4-byte aligned B and C (StepArgs::dma_tiles bit 0).
-constexpr int REC_TOKENS = 16;
+constexpr int REC_TOKENS = 8;
 
 template <int N8, int N4, int NZ>
 struct RecordSmem {
@@ -1794,13 +1795,15 @@ __global__ __launch_bounds__(256) void k_token_records(StepArgs a, float* rec) {
     e0v[j] = h2f((uint16_t)(w & 0xFFFFu));
     e1v[j] = h2f((uint16_t)(w >> 16));
   }
+  WaveRaw<1> raw;   // the first token's inputs, in flight with the predictor
+  wave_load_rest<4, 1, true, 4>(a, raw, b * L + t0, g, h0, 0, lane, wave);
   __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the predictor transfer has landed
   __syncthreads();                      // ... every wave's share
   const int pv0 = perm0 & 127, pv1 = perm1 & 127;
   const uint16_t* s_pred = (const uint16_t*)sm.pred32;
   for (int t = t0; t < t1; ++t) {
-    WaveRaw<1> r;
-    wave_load_rest<4, 1, true, 4>(a, r, b * L + t, g, h0, 0, lane, wave);
+    const WaveRaw<1> r = raw;
+    if (t + 1 < t1) wave_load_rest<4, 1, true, 4>(a, raw, b * L + t + 1, g, h0, 0, lane, wave);
     GroupToken<NL>& gt = sm.gt[t & 1];
     // dt 0, decay 0: the bound flag is then that of b alone
     wave_token_build<N8, N4, NZ, MODE_RIDGE, 4, 1, false>(sm.wt[wave], gt, r, make_float2(0.f, 0.f), pv0, pv1, e0v,
