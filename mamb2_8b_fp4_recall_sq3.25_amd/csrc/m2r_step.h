@@ -1081,8 +1081,8 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   uint32_t ls_w = 0u;
   float2 act;
   // record-fed loop: the loader's copies of records t + 1 and t + 2 (16
-  // bytes per lane), and the record of token t of this workgroup's batch row
-  // and group
+  // bytes per lane), and rec_load(t), this lane's 16 bytes of the record of
+  // token t of the workgroup's batch row and group
   uint4 rnext = make_uint4(0u, 0u, 0u, 0u), rnext2 = make_uint4(0u, 0u, 0u, 0u);
   auto rec_load = [&](int t) {
     return ((const uint4*)(a.rec + ((size_t)(b * L + t) * a.G + g) * REC_FLOATS))[lane];
@@ -1221,7 +1221,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     wave_load_dt<WPB, HPW, WPS>(a, raw, b * L, h0, lane, wave);
     const int hl = h0 + head_slot(min(lane, HPW - 1));   // head of slot `lane` (lanes < HPW)
     Ah = a.A[hl];
-    if (RIDGE && !REC) {   // (a record-fed loop never reads the predictor)
+    if constexpr (RIDGE && !REC) {   // (a record-fed loop never reads the predictor)
       const uint8_t* pg = (const uint8_t*)(a.pred + (size_t)g * F * NZ);
       if constexpr (DMA) {   // 16-byte chunks; lanes past the end re-read the last one
         for (int j = wave; j < PRED_OPS16; j += WPB)
@@ -1231,9 +1231,10 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
           lds_dma_b32(pg + 4 * min(j * 64 + lane, PRED_DW - 1), lds_address(s_pred32 + 64 * j));
       }
     }
+    uint4 rec0 = make_uint4(0u, 0u, 0u, 0u);   // REC: record 0, put in LDS once the loads have landed
     if constexpr (REC) {
       if (wave == REC_LOADER) {
-        rnext2 = rec_load(0);
+        rec0 = rec_load(0);
         if (L > 1) rnext = rec_load(1);
       }
     }
@@ -1272,7 +1273,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
       for (int k = 0; k < HPW; ++k) slot_copy_in(head_slot(k));
     }
     if constexpr (REC) {   // record 0, published by the first token's barrier
-      if (wave == REC_LOADER) ((uint4*)sm.rec[0])[lane] = rnext2;
+      if (wave == REC_LOADER) ((uint4*)sm.rec[0])[lane] = rec0;
     }
   }
   if (lane < HPW) wt.D[lane] = a.d_f32 ? __builtin_bit_cast(float, d_bits) : h2f((uint16_t)d_bits);

@@ -360,6 +360,50 @@ def test_ridge_token_records_same_bits_as_in_kernel_build(device, layout):
         _native.call("m2r_set_step_shape", 0, 0)
 
 
+def test_ridge_token_records_graph_replays_match_eager(device):
+    """The records kernel and the record-fed step captured in a HIP graph
+    (one workspace, static inputs): three replays, each from the same
+    starting state (reset eagerly in between), give the eager call's codes,
+    scales, latent bytes and y bit for bit."""
+    from mamba2_recall import _native, ridge_codec
+    layout = "24_48_56"
+    n8, n4, nz = ridge_counts(layout)
+    batch, L, H, P, G = 1, 37, 128, 64, 8
+    print(f"[token records graph] layout={layout} B={batch} L={L}", flush=True)
+    rng = np.random.default_rng(4242)
+    inp = cases.step_inputs(rng, batch, L, H, P, G)
+    sta = cases.ridge_statics(rng, G, n8, n4, nz)
+    st0 = cases.random_packed_state(rng, batch, H, P, n8, n4, latent=True)
+    t = device_inputs(inp, device)
+    perm = torch.from_numpy(inp["perm"]).to(device)
+    basis, ls, pred = (dev16(sta[k], device) for k in ("basis", "lscale", "pred"))
+    ws = torch.empty(int(_native.lib().m2r_ridge_records_bytes(batch, L, G)) // 4, dtype=torch.float32, device=device)
+    s_eager = ridge_codec.allocate_state(batch, H, P, 128, device, layout=layout)
+    to_state(st0, s_eager, device)
+    y_eager = _ridge_step_direct(t, perm, basis, ls, pred, s_eager, layout, ws)
+    torch.cuda.synchronize()
+    s_graph = ridge_codec.allocate_state(batch, H, P, 128, device, layout=layout)
+    to_state(st0, s_graph, device)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):   # warm-up outside the capture
+        _ridge_step_direct(t, perm, basis, ls, pred, s_graph, layout, ws)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y_graph = _ridge_step_direct(t, perm, basis, ls, pred, s_graph, layout, ws)
+    for rep in range(3):
+        to_state(st0, s_graph, device)
+        ws.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_graph.view(torch.int16), y_eager.view(torch.int16)), rep
+        for k in s_eager.tensors:
+            assert torch.equal(s_graph.tensors[k].view(torch.uint8), s_eager.tensors[k].view(torch.uint8)), (rep, k)
+
+
 @pytest.mark.parametrize("forced_shape", SHAPES, indirect=True, ids=lambda s: f"w{s[0]}h{s[1]}")
 def test_ridge_every_workgroup_shape(oracle, device, forced_shape):
     """Each (waves, head slots per wave) variant: multi-token, ragged P, one
