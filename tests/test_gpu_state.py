@@ -322,16 +322,17 @@ def test_ridge_token_records_same_bits_as_in_kernel_build(device, layout):
     their tokens' state-independent values from records a first kernel wrote
     (the split token build of four waves, run per token): codes, scales,
     latent bytes and y equal the in-kernel build's bit for bit, with the
-    automatic shape (four waves per slot) and forced two- and four-wave
+    automatic shape (four or two waves per slot) and forced two- and four-wave
     slots, token counts that are and are not multiples of the records
-    kernel's 16 tokens per workgroup, and batch rows 1 and 2."""
+    kernel's 8 tokens per workgroup, batch rows 1 to 3, and a ragged head
+    dimension (P = 72: a second, partly filled 64-row block per head)."""
     from mamba2_recall import _native, ridge_codec
     n8, n4, nz = ridge_counts(layout)
-    H, P, G = 128, 64, 8
+    H, G = 128, 8
     try:
         for shape in ((0, 0), (4, 0), (4, -4)):
-            for batch, L in ((1, 37), (2, 16), (1, 2)):
-                print(f"[token records] layout={layout} shape={shape} B={batch} L={L}", flush=True)
+            for batch, L, P in ((1, 37, 64), (2, 16, 64), (1, 2, 64), (3, 19, 72)):
+                print(f"[token records] layout={layout} shape={shape} B={batch} L={L} P={P}", flush=True)
                 _native.call("m2r_set_step_shape", *shape)
                 rng = np.random.default_rng(700 + batch * 100 + L)
                 inp = cases.step_inputs(rng, batch, L, H, P, G)
@@ -351,10 +352,10 @@ def test_ridge_token_records_same_bits_as_in_kernel_build(device, layout):
                 y_build = _ridge_step_direct(t, perm, basis, ls, pred, s_build, layout, None)
                 y_rec = _ridge_step_direct(t, perm, basis, ls, pred, s_rec, layout, ws)
                 torch.cuda.synchronize()
-                assert torch.equal(y_rec.view(torch.int16), y_build.view(torch.int16)), (layout, shape, batch, L)
+                assert torch.equal(y_rec.view(torch.int16), y_build.view(torch.int16)), (layout, shape, batch, L, P)
                 for k in s_build.tensors:
                     assert torch.equal(s_rec.tensors[k].view(torch.uint8), s_build.tensors[k].view(torch.uint8)), \
-                        (layout, shape, batch, L, k)
+                        (layout, shape, batch, L, P, k)
                 assert not torch.isnan(ws).all()   # the records path ran
     finally:
         _native.call("m2r_set_step_shape", 0, 0)
