@@ -417,20 +417,22 @@ __device__ __forceinline__ float d3_half(const uint32_t (&w)[12], uint32_t (&nw)
     }
   };
   if (fast) {
-    // the code as the low bits of t = RN(v r + 1.5 2^23) = 1.5 2^23 + rint(v r),
-    // with a running maximum of the rounding residuals (round_residual_code)
-    float fmax_res = 0.f;
+    // the code as the low bits of th = RN(v yh + 1.5 2^23) = 1.5 2^23 +
+    // rint(v yh), kept where the code of the other side, RN(v yl + ...),
+    // agrees (two_sided_code; r = RN(1/den) of a positive normal den here)
+    const float yh = __builtin_fmaf(r, TWO_SIDED_REL, r), yl = __builtin_fmaf(r, -TWO_SIDED_REL, r);
+    uint32_t diff = 0u;
     to_planes([&](int i0) {
-      float f[4];
       uint32_t tb[4];
 #pragma unroll
-      for (int m = 0; m < 4; ++m) tb[m] = round_residual_code(v[i0 + m], r, 0.0f, f[m]);
-      fmax_res = max3_abs(fmax_res, f[0], f[1]);
-      fmax_res = max3_abs(fmax_res, f[2], f[3]);
+      for (int m = 0; m < 4; ++m) {
+        tb[m] = two_sided_code(v[i0 + m], yh, yl, 0.0f, diff);
+        asm volatile("" : "+v"(diff));   // one three-input bitwise operation per coordinate
+      }
       return pack4((int)tb[0], (int)tb[1], (int)tb[2], (int)tb[3]);
     });
     // a lane near a rounding boundary: the half row again with exact quotients
-    if (__builtin_amdgcn_ballot_w64(fmax_res > RESIDUAL_OK4) != 0)
+    if (__builtin_amdgcn_ballot_w64(diff != 0u) != 0)
       to_planes([&](int i0) {
         return pack4(quantize_code_unclamped(v[i0], d, r), quantize_code_unclamped(v[i0 + 1], d, r),
                      quantize_code_unclamped(v[i0 + 2], d, r), quantize_code_unclamped(v[i0 + 3], d, r));

@@ -161,27 +161,11 @@ constexpr float QTOP3 = 0x1.fffffep+1f;     // below 4
 // Biased code by the magic-number rounding, for a quotient that needs no
 // clamping: t = RN(v y + 1.5 2^23 + bias) lies in [2^23, 2^24), where the
 // spacing is 1, so t = 1.5 2^23 + bias + rint(v y) (one rounding of the exact
-// product) and the low bits of t are the code plus its bias.  f = RN(v y -
-// rint(v y)) is the rounding residual.  rint(v y) is roundf(RN(v / d)) unless
-// v / d lies near a half-integer:
-//   |v y - v / d| <= |v / d| 2^-24 (y = RN(1 / d), a normal binary32 value),
-//   |RN(v / d) - v / d| <= ulp(v / d) / 2, and |f| is exact to 2^-25.
-// With |v / d| < lim + 1/2 (the unclamped case), |f| <= RESIDUAL_OK puts
-// RN(v / d) strictly within 1/2 of rint(v y), where roundf and rint agree:
-//   lim 127: 2^-17 + 2^-18 + 2^-25 < 2^-16, so RESIDUAL_OK8 = 1/2 - 2^-16;
-//   lim 7 (and 3): 2^-21 + 2^-22 + 2^-25 < 2^-20; RESIDUAL_OK4 = 1/2 - 2^-19.
-// Exact half-integer products give |f| = 1/2 and always take the exact path.
-constexpr float RESIDUAL_OK8 = 0.5f - 0x1p-16f;
-constexpr float RESIDUAL_OK4 = 0.5f - 0x1p-19f;
-__device__ __forceinline__ uint32_t round_residual_code(float v, float y, float bias, float& f) {
-  const float magic = 0x1.8p23f + bias;
-  const float t = __builtin_fmaf(v, y, magic);
-  f = __builtin_fmaf(v, y, -(t - magic));
-  return __builtin_bit_cast(uint32_t, t);
-}
-
-// Two-sided form of the same quantizer: with y = RN(1/d) for a positive
-// normal binary32 d, yh = RN(y + y 2^-22) and yl = RN(y - y 2^-22), the
+// product) and the low bits of t are the code plus its bias.  rint(v y) is
+// roundf(RN(v / d)) unless v / d lies near a half-integer.
+//
+// Two-sided form: with y = RN(1/d) for a positive normal binary32 d,
+// yh = RN(y + y 2^-22) and yl = RN(y - y 2^-22), the
 // biased codes th = RN(v yh + magic) and tl = RN(v yl + magic) (each one
 // rounding of an exact product plus magic, as above) bracket roundf(RN(v/d)):
 //   v yh >= (v/d) (1 - 2^-24)^2 (1 + 2^-22) > (v/d)(1 + 2^-24) >= RN(v/d)
@@ -191,9 +175,10 @@ __device__ __forceinline__ uint32_t round_residual_code(float v, float y, float 
 // k: the code is kept.  Otherwise a half-integer lies between them (or on an
 // end) and the tier is requantized with the exact quotients.  Per coordinate
 // two fmas and one bitwise accumulation of th ^ tl, against three
-// instructions and half a maximum for the residual form.  The CPU checks
-// verify it on random quotients and every half-integer boundary, and that an
-// offset of 0 or 2^-25 is not enough.
+// instructions and half a maximum for a residual test (f = RN(v y - (t -
+// magic)) against a bound).  The CPU checks verify it on random quotients and
+// every half-integer boundary, and that an offset of 0 or 2^-25 is not
+// enough.
 constexpr float TWO_SIDED_REL = 0x1p-22f;
 __device__ __forceinline__ uint32_t two_sided_code(float v, float yh, float yl, float bias, uint32_t& diff) {
   const float magic = 0x1.8p23f + bias;

@@ -92,18 +92,19 @@ def test_reciprocal_quantizer_equals_ieee_division(oracle):
     assert codes_bad == 0 and div_bad == 0
 
 
-# residual bounds of the device's magic-number quantizer (m2r_device.h)
+# residual bounds of the magic-number quantizer's residual form (the form
+# the device used before its two-sided form, below; the identity both rest on)
 RESIDUAL_OK8 = 0.5 - 2.0 ** -16
 RESIDUAL_OK4 = 0.5 - 2.0 ** -19
 
 
 def test_residual_rounding_quantizer_equals_roundf_of_ieee_division(oracle):
-    """The device's unclamped quantizer keeps rint(v * RN(1/d)) (the low byte
-    of fma(v, y, 1.5 2^23 + bias)) whenever the rounding residual |f| is within
-    the bound, and recomputes the rest exactly: every kept code equals
-    roundf(v / d) and its byte is code + bias, for lim 127, 7 and 3, random
-    quotients and every half-integer boundary +-40 ulps.  The near-tie cases
-    do reach the exact path."""
+    """The magic-number quantizer in its residual form keeps rint(v * RN(1/d))
+    (the low byte of fma(v, y, 1.5 2^23 + bias)) whenever the rounding residual
+    |f| is within the bound, and recomputes the rest exactly: every kept code
+    equals roundf(v / d) and its byte is code + bias, for lim 127, 7 and 3,
+    random quotients and every half-integer boundary +-40 ulps.  The near-tie
+    cases do reach the exact path."""
     bad, flagged = oracle.check_residual_round(20261202, 20_000_000, 400_000, RESIDUAL_OK8, RESIDUAL_OK4)
     assert bad == 0
     assert flagged > 400_000   # boundary cases within the margin went to the exact path
