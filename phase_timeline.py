@@ -57,7 +57,8 @@ def build():
 
 def source_digest():
     h = hashlib.sha256()
-    for name in ("m2r_step.h", "m2r_state.hip", "m2r_device.h", "m2r_tile.h"):
+    # the same files, in the same order, as the other step profiles' digest
+    for name in ("m2r_state.hip", "m2r_step.h", "m2r_device.h", "m2r_tile.h"):
         h.update((PKG / "csrc" / name).read_bytes())
     return h.hexdigest()[:16]
 
@@ -99,7 +100,8 @@ def run(out):
         getattr(lib, name).argtypes, getattr(lib, name).restype = argt, rest
     lib.m2r_timeline_set.argtypes, lib.m2r_timeline_set.restype = [ctypes.c_void_p], ctypes.c_int
     dev = torch.device("cuda:0")
-    lines = [f"# phase timeline of the ridge step (instrumented build, kernel_source_sha16 {source_digest()})",
+    lines = [f"# phase timeline of the ridge step (instrumented build, kernel_source_sha16 {source_digest()} "
+             "of csrc/{m2r_state.hip, m2r_step.h, m2r_device.h, m2r_tile.h})",
              "# command: python phase_timeline.py run --out <this file> (after `python phase_timeline.py build`)",
              "# µs from each wave's start, median [10th-90th percentile] over every wave of the 56 published",
              "# layers, each layer launched twice in a row and the second launch kept; each stamp costs a few",
