@@ -919,6 +919,16 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
   // stored), the register copies leave them as they were.
   constexpr bool PLACEHOLDERS = !DMA;
   constexpr bool dma_tiles = DMA;   // a.dma_tiles: 16-byte LDS transfers, else staging through VGPRs
+  // Cache policies.  The shapes of one slot per wave (HPW == 1, which the
+  // launch picks below 4,096 slots when the heads per group allow wider
+  // ones) read the state and the predictor as ordinary lines: at small
+  // batches the next launch of the same layer finds them in the L2.  The
+  // shapes of several slots per wave (large batches, whose states exceed
+  // the L2s) read them non-temporal.  The multi-wave slots (at most 1,024)
+  // also keep their stored lines in the L2 (written through at device
+  // scope); the others store non-temporal.
+  constexpr bool NT_LOAD = HPW > 1;
+  constexpr int STORE_CP = PAIR ? STORE_DEVICE : STORE_THROUGH;
   const uint16_t* s_pred = (const uint16_t*)s_pred32;
   WaveToken<N8, N4, HPW>& wt = s_wt[wave];
 
@@ -944,17 +954,17 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     const uint32_t tl = lds_address(t);
     const uint8_t *s8 = (const uint8_t*)a.s8, *s4 = (const uint8_t*)a.s4;
     if constexpr (!PAIR) {
-      field_dma16_tile<W8, O_LO>(tl, a.lo, row0, nvalid, lane);
-      field_dma16_tile<W8, O_HI>(tl, a.hi, row0, nvalid, lane);
-      scale_fields_dma16_tile<RIDGE ? 3 : 2, O_S8>(tl, s8, s4, RIDGE ? a.latent : s4, row0, nvalid, lane);
-      field_dma16_tile<W4, O_Q4>(tl, a.q4, row0, nvalid, lane);
+      field_dma16_tile<W8, O_LO, NT_LOAD>(tl, a.lo, row0, nvalid, lane);
+      field_dma16_tile<W8, O_HI, NT_LOAD>(tl, a.hi, row0, nvalid, lane);
+      scale_fields_dma16_tile<RIDGE ? 3 : 2, O_S8, NT_LOAD>(tl, s8, s4, RIDGE ? a.latent : s4, row0, nvalid, lane);
+      field_dma16_tile<W4, O_Q4, NT_LOAD>(tl, a.q4, row0, nvalid, lane);
     } else if (own8) {
-      field_dma16_tile<W8, O_LO>(tl, a.lo, row0, nvalid, lane);
-      field_dma16_tile<W8, O_HI>(tl, a.hi, row0, nvalid, lane);
-      scale_fields_dma16_tile<1, O_S8>(tl, s8, s8, s8, row0, nvalid, lane);
+      field_dma16_tile<W8, O_LO, NT_LOAD>(tl, a.lo, row0, nvalid, lane);
+      field_dma16_tile<W8, O_HI, NT_LOAD>(tl, a.hi, row0, nvalid, lane);
+      scale_fields_dma16_tile<1, O_S8, NT_LOAD>(tl, s8, s8, s8, row0, nvalid, lane);
     } else if (own4) {
-      field_dma16_tile<W4, O_Q4>(tl, a.q4, row0, nvalid, lane);
-      scale_fields_dma16_tile<RIDGE ? 2 : 1, O_S4>(tl, s4, RIDGE ? a.latent : s4, s4, row0, nvalid, lane);
+      field_dma16_tile<W4, O_Q4, NT_LOAD>(tl, a.q4, row0, nvalid, lane);
+      scale_fields_dma16_tile<RIDGE ? 2 : 1, O_S4, NT_LOAD>(tl, s4, RIDGE ? a.latent : s4, s4, row0, nvalid, lane);
     }
   };
   // store instructions of a slot's copy-out (one per 1 KiB chunk of a field)
@@ -1006,16 +1016,16 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
         field_read16<W8>(t + O_LO, lane, v);
         field_read16<W8>(t + O_HI, lane, v + C8W);
         field_read16<2>(t + O_S8, lane, v + 2 * C8W);
-        field_write16<W8>(a.lo, v, row0, nvalid, lane);
-        field_write16<W8>(a.hi, v + C8W, row0, nvalid, lane);
-        field_write16<2>((uint8_t*)a.s8, v + 2 * C8W, row0, nvalid, lane);
+        field_write16<W8, STORE_CP>(a.lo, v, row0, nvalid, lane);
+        field_write16<W8, STORE_CP>(a.hi, v + C8W, row0, nvalid, lane);
+        field_write16<2, STORE_CP>((uint8_t*)a.s8, v + 2 * C8W, row0, nvalid, lane);
       } else if (own4) {
         field_read16<W4>(t + O_Q4, lane, v);
         field_read16<2>(t + O_S4, lane, v + C4W);
         if constexpr (RIDGE) field_read16<2>(t + O_LAT, lane, v + C4W + C2);
-        field_write16<W4>(a.q4, v, row0, nvalid, lane);
-        field_write16<2>((uint8_t*)a.s4, v + C4W, row0, nvalid, lane);
-        if constexpr (RIDGE) field_write16<2>(a.latent, v + C4W + C2, row0, nvalid, lane);
+        field_write16<W4, STORE_CP>(a.q4, v, row0, nvalid, lane);
+        field_write16<2, STORE_CP>((uint8_t*)a.s4, v + C4W, row0, nvalid, lane);
+        if constexpr (RIDGE) field_write16<2, STORE_CP>(a.latent, v + C4W + C2, row0, nvalid, lane);
       }
       return;
     } else if constexpr (dma_tiles) {   // every LDS read of the slot, then its stores
@@ -1142,7 +1152,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
     if constexpr (RIDGE) {   // the predictor: 16-byte chunks; lanes past the end re-read the last one
       const uint8_t* pg = (const uint8_t*)(a.pred + (size_t)g * F * NZ);
       for (int j = wave; j < PRED_OPS16; j += WPB)
-        lds_dma_b128(pg + 16 * min(j * 64 + lane, PRED_DW / 4 - 1), lds_address(s_pred32 + 256 * j));
+        lds_dma_b128<NT_LOAD>(pg + 16 * min(j * 64 + lane, PRED_DW / 4 - 1), lds_address(s_pred32 + 256 * j));
     }
 #pragma unroll
     for (int j = 0; j < (HPW + 1) / 2; ++j) {   // x of head slots 2j (lanes < 32) and 2j + 1
@@ -1225,7 +1235,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
       const uint8_t* pg = (const uint8_t*)(a.pred + (size_t)g * F * NZ);
       if constexpr (DMA) {   // 16-byte chunks; lanes past the end re-read the last one
         for (int j = wave; j < PRED_OPS16; j += WPB)
-          lds_dma_b128(pg + 16 * min(j * 64 + lane, PRED_DW / 4 - 1), lds_address(s_pred32 + 256 * j));
+          lds_dma_b128<NT_LOAD>(pg + 16 * min(j * 64 + lane, PRED_DW / 4 - 1), lds_address(s_pred32 + 256 * j));
       } else {
         for (int j = wave; j < PRED_OPS; j += WPB)
           lds_dma_b32(pg + 4 * min(j * 64 + lane, PRED_DW - 1), lds_address(s_pred32 + 64 * j));
@@ -1523,7 +1533,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
             if constexpr (RIDGE) out = decay * (acc + z0 * dot1 + z1 * dot2) + x * (dtv * sbc + wt.D[0]);
             else out = decay * acc + x * (dtv * sbc + wt.D[0]);
             const __amdgpu_buffer_rsrc_t ry = raw_buffer(a.y + ((size_t)bt * H + h) * P + pbase, 2 * nvalid);
-            __builtin_amdgcn_raw_buffer_store_b16(f2h(out), ry, 2 * lane, 0, STORE_THROUGH);
+            __builtin_amdgcn_raw_buffer_store_b16(f2h(out), ry, 2 * lane, 0, STORE_CP);
           }
           // the whole tiers' maxima (maxima are exact: any order)
           auto tier_max = [&](int tier, float own, unsigned has) {
@@ -1698,7 +1708,7 @@ __device__ __forceinline__ void state_step_body(const StepArgs& a,
         }
         {   // one unguarded store instruction: the range check drops rows past P
           const __amdgpu_buffer_rsrc_t ry = raw_buffer(a.y + ((size_t)bt * H + h) * P + pbase, 2 * nvalid);
-          __builtin_amdgcn_raw_buffer_store_b16(f2h(out), ry, 2 * lane, 0, STORE_THROUGH);
+          __builtin_amdgcn_raw_buffer_store_b16(f2h(out), ry, 2 * lane, 0, STORE_CP);
         }
 
         // ---- repack the INT4 tier and the latent bytes into the tile ------------------

@@ -120,21 +120,33 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_buffer(const void* base, i
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
 }
 
-// The 16-byte form: lane l's 16 bytes at g land at M0 + 16 l.  Marked
-// non-temporal: every state byte is read once per launch.
+// The 16-byte form: lane l's 16 bytes at g land at M0 + 16 l.  NT: marked
+// non-temporal (a launch whose state is too large for the L2 reads every
+// state byte once); without it the lines stay in the L2 for the next launch
+// of the same layer, which hits there when the state of every layer fits.
+template <bool NT = true>
 __device__ __forceinline__ void lds_dma_b128(const void* g, uint32_t lds) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
-               : "memory");
+  if constexpr (NT)
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
+  else
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
 }
 // The same with an instruction offset, which moves the global and the LDS
 // address alike: lane l's 16 bytes at g + IMM land at lds + IMM + 16 l, so
 // transfers into one tile share M0.
-template <int IMM>
+template <int IMM, bool NT = true>
 __device__ __forceinline__ void lds_dma_b128_imm(const void* g, uint32_t lds) {
   static_assert(IMM >= 0 && IMM < 4096, "instruction offset range");
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off offset:%2 nt" ::"v"(g),
-               "{m0}"(__builtin_amdgcn_readfirstlane(lds)), "n"(IMM)
-               : "memory");
+  if constexpr (NT)
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off offset:%2 nt" ::"v"(g),
+                 "{m0}"(__builtin_amdgcn_readfirstlane(lds)), "n"(IMM)
+                 : "memory");
+  else
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off offset:%2" ::"v"(g),
+                 "{m0}"(__builtin_amdgcn_readfirstlane(lds)), "n"(IMM)
+                 : "memory");
 }
 
 // 16-byte transfers of one SoA field of a 64-row slot (64 * W bytes at
@@ -174,15 +186,15 @@ __device__ __forceinline__ void field_dma16(uint8_t* lds, const uint8_t* g, int 
 // The same transfers into a slot tile whose LDS base `tile` is M0 for every
 // field of the slot: the field sits at tile byte offset O and chunk k goes
 // by instruction offset O + 1024 k.
-template <int W, int O, int K = 0>
+template <int W, int O, bool NT = true, int K = 0>
 __device__ __forceinline__ void field_dma16_tile(uint32_t tile, const uint8_t* g, int row0, int nvalid, int lane) {
   static_assert(chunk_ops(W) <= 4, "fields of at most 4 KiB per slot");
   if constexpr (K < chunk_ops(W)) {
     constexpr int FB = 64 * W, IMM = O + 1024 * K;
     const uint8_t* base = g + (size_t)row0 * W;
     const int o = K * 1024 + 16 * lane;
-    if (K * 1024 + 1024 <= FB || o < FB) lds_dma_b128_imm<IMM>(base + (min(o, nvalid * W - 16) - IMM), tile);
-    field_dma16_tile<W, O, K + 1>(tile, g, row0, nvalid, lane);
+    if (K * 1024 + 1024 <= FB || o < FB) lds_dma_b128_imm<IMM, NT>(base + (min(o, nvalid * W - 16) - IMM), tile);
+    field_dma16_tile<W, O, NT, K + 1>(tile, g, row0, nvalid, lane);
   }
 }
 // NF two-byte fields of a slot (128 bytes each: f0, f1, f2), which sit back
@@ -190,19 +202,22 @@ __device__ __forceinline__ void field_dma16_tile(uint32_t tile, const uint8_t* g
 // 16 bytes of field l / 8 (lanes past the nvalid valid rows re-read the
 // field's last valid chunk, which lands in rows nobody reads).  Requires
 // nvalid % 8 == 0.
-template <int NF, int O>
+template <int NF, int O, bool NT = true>
 __device__ __forceinline__ void scale_fields_dma16_tile(uint32_t tile, const uint8_t* f0, const uint8_t* f1,
                                                         const uint8_t* f2, int row0, int nvalid, int lane) {
   static_assert(NF >= 1 && NF <= 3, "one to three fields");
   const int f = lane >> 3, c = min(lane & 7, nvalid / 8 - 1);
   const uint8_t* fb = f == 0 ? f0 : (f == 1 ? f1 : f2);
-  if (lane < 8 * NF) lds_dma_b128_imm<O>(fb + (size_t)row0 * 2 + (16 * c - O), tile);
+  if (lane < 8 * NF) lds_dma_b128_imm<O, NT>(fb + (size_t)row0 * 2 + (16 * c - O), tile);
 }
 
-// Cache policy of the state and output stores: device scope (sc1) and
-// non-temporal, so they are written through during the launch instead of
-// staying dirty in the issuing XCD's L2 until the end-of-kernel writeback.
-constexpr int STORE_THROUGH = 16 | 2;
+// Cache policies of the state and output stores.  STORE_THROUGH: device
+// scope (sc1) and non-temporal, so they are written through during the
+// launch instead of staying dirty in the issuing XCD's L2 until the
+// end-of-kernel writeback.  STORE_DEVICE: device scope only (written
+// through, the lines kept in the L2), for launches whose state of every
+// layer fits the L2s.
+constexpr int STORE_THROUGH = 16 | 2, STORE_DEVICE = 16;
 
 // LDS -> global in two halves, so that a caller reads every field of a slot
 // before its first store (the compiler does not move LDS reads above a
@@ -219,12 +234,12 @@ __device__ __forceinline__ void field_read16(const uint8_t* lds, int lane, u32x4
 #pragma unroll
   for (int k = 0; k < chunk_ops(W); ++k) v[k] = *(const u32x4*)(lds + min(k * 1024 + 16 * lane, FB - 16));
 }
-template <int W>
+template <int W, int CP = STORE_THROUGH>
 __device__ __forceinline__ void field_write16(uint8_t* g, const u32x4* v, int row0, int nvalid, int lane) {
   const __amdgpu_buffer_rsrc_t rsrc = raw_buffer(g + (size_t)row0 * W, nvalid * W);
 #pragma unroll
   for (int k = 0; k < chunk_ops(W); ++k)
-    __builtin_amdgcn_raw_buffer_store_b128(v[k], rsrc, k * 1024 + 16 * lane, 0, STORE_THROUGH);
+    __builtin_amdgcn_raw_buffer_store_b128(v[k], rsrc, k * 1024 + 16 * lane, 0, CP);
 }
 
 // LDS DMA of one SoA field of a 64-row slot: 64 * W bytes at g + row0 * W
