@@ -25,7 +25,9 @@
 // resident round of workgroups.  The activations of the
 // lane's k range stay in registers, reordered once into the weight pairs'
 // order.  A wave sum per chunk, then the chunks' partial sums in a fixed
-// order through LDS, finish each output.
+// order through LDS, finish each output.  One activation row (the batch-1
+// decode) takes k_fp4_gemv_rows instead where it fills the chip in one
+// resident round: whole rows per wave, no barrier per row, the same sums.
 #include "m2r_device.h"
 #include "m2r_abi_util.h"
 #include "m2r_tile.h"
@@ -158,9 +160,156 @@ __global__ __launch_bounds__(256) void k_fp4_gemv(const uint8_t* __restrict__ co
   }
 }
 
+// One activation row (M == 1): each wave takes D whole rows (rows strided
+// over every wave of the grid, W waves: rows w, w + W, ..., w + (D - 1) W),
+// lane l the same k ranges as above in each of the row's KCH chunks, so a row
+// needs no workgroup barrier: the KCH chunk sums are wave sums added in chunk
+// order, the same bits as k_fp4_gemv<1, KCH>.  The host sizes the grid so
+// that D W >= N with every workgroup resident at once: all of a wave's loads
+// are issued first (rows past N re-read row N - 1, which is never stored),
+// then the table is built, and each row is computed as soon as its loads
+// have landed, while the later rows' loads are still in flight.
+template <int KCH, int D, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_fp4_gemv_rows(const uint8_t* __restrict__ codes,
+                                                           const uint8_t* __restrict__ scales,
+                                                           const float* __restrict__ gscale,
+                                                           const uint16_t* __restrict__ u,
+                                                           uint16_t* __restrict__ y, int N) {
+  static_assert(KCH == 1 || KCH == 2 || KCH == 4, "K of 2048, 4096 or 8192");
+  constexpr int K = KCH * 2048;
+  __shared__ __align__(16) uint32_t s_tab[128][4];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int W = (int)gridDim.x * WPB;
+  const int n0 = (int)blockIdx.x * WPB + wave;
+  // the activations first (shared by every wave, cache hits), so that
+  // waiting for them does not wait for the rows
+  u32x4 uv[KCH][4];
+#pragma unroll
+  for (int cc = 0; cc < KCH; ++cc)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) uv[cc][q] = ((const u32x4*)(u + cc * 2048 + 32 * lane))[q];
+  u32x4 cv[D][KCH];
+  uint32_t sb[D][KCH];
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    const int row = min(n0 + j * W, N - 1);
+#pragma unroll
+    for (int cc = 0; cc < KCH; ++cc) {
+      cv[j][cc] = __builtin_nontemporal_load((const u32x4*)(codes + (size_t)row * (K / 2) + cc * 1024) + lane);
+      sb[j][cc] = *(const uint16_t*)(scales + (size_t)row * (K / 16) + cc * 128 + 2 * lane);
+    }
+  }
+  const float gl = *gscale;
+  for (int e = threadIdx.x; e < 128 * 8; e += 64 * WPB) {
+    const int blk = e >> 3, i = e & 7;
+    const float lev2 = (float)((i < 4) ? i : (i == 4 ? 4 : (i == 5 ? 6 : (i == 6 ? 8 : 12))));
+    const float hb = e4m3_byte_to_f32<0>((uint32_t)blk) * 0.5f;
+    const uint16_t h = f2h((lev2 * hb) * gl);
+    uint8_t* row = (uint8_t*)s_tab[blk];
+    row[i] = (uint8_t)(h & 0xFFu);
+    row[8 + i] = (uint8_t)(h >> 8);
+  }
+  // activation pairs in the weights' order: per 8 positions (u0,u2), (u4,u6)
+  // | (u1,u3), (u5,u7)
+  uint32_t ue[KCH][8], uo[KCH][8];
+#pragma unroll
+  for (int cc = 0; cc < KCH; ++cc) {
+    uint32_t p[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      p[4 * q] = uv[cc][q].x; p[4 * q + 1] = uv[cc][q].y; p[4 * q + 2] = uv[cc][q].z; p[4 * q + 3] = uv[cc][q].w;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      ue[cc][2 * q] = __builtin_amdgcn_perm(p[4 * q + 1], p[4 * q], 0x05040100u);
+      ue[cc][2 * q + 1] = __builtin_amdgcn_perm(p[4 * q + 3], p[4 * q + 2], 0x05040100u);
+      uo[cc][2 * q] = __builtin_amdgcn_perm(p[4 * q + 1], p[4 * q], 0x07060302u);
+      uo[cc][2 * q + 1] = __builtin_amdgcn_perm(p[4 * q + 3], p[4 * q + 2], 0x07060302u);
+    }
+  }
+  __syncthreads();   // the table is complete
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    float tot = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < KCH; ++cc) {
+      const u32x4 cur = cv[j][cc];
+      const uint32_t scur = sb[j][cc];
+      float acc = 0.f;
+#pragma unroll
+      for (int gidx = 0; gidx < 2; ++gidx) {
+        const u32x4 tv = *(const u32x4*)s_tab[(scur >> (8 * gidx)) & 0x7Fu];
+        const uint32_t t[4] = {tv.x, tv.y, tv.z, tv.w};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int q = 2 * gidx + h;
+          const uint32_t cw = q == 0 ? cur.x : q == 1 ? cur.y : q == 2 ? cur.z : cur.w;
+          fp4_dot8(cw, t, &ue[cc][2 * q], &uo[cc][2 * q], acc);
+        }
+      }
+      const float sum = wave_sum(acc);
+      tot = cc == 0 ? sum : tot + sum;
+    }
+    const int n = n0 + j * W;
+    if (lane == 0 && n < N) y[n] = f2h(tot);
+  }
+}
+
 }  // namespace m2r
 
 using namespace m2r;
+
+// The whole-row kernel for one activation row: the smallest rows-per-wave D
+// for which one resident round of eight-wave workgroups covers N rows, if
+// that round has a workgroup for every CU (D <= 6; D <= 2 for K = 8192,
+// whose larger D leave two waves per SIMD, slower than the general kernel).
+// Returns 1 when launched, 0 when the general kernel is to be used, or a
+// negative error.
+template <int KCH, int D>
+static int launch_rows_d(const uint8_t* packed, const uint8_t* sc, const float* gs, const uint16_t* u, uint16_t* y,
+                         int64_t N, int cus, hipStream_t stream) {
+  constexpr int WPB = 8;
+  static int per_cu = -1;   // resident workgroups per CU of this instance (same on every MI355X)
+  if (per_cu < 0) {
+    int b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, (const void*)k_fp4_gemv_rows<KCH, D, WPB>, 64 * WPB, 0) !=
+        hipSuccess)
+      return -m2r_fail("fp4 gemv: occupancy query failed");
+    per_cu = b;
+  }
+  const int64_t waves = (N + D - 1) / D, blocks = (waves + WPB - 1) / WPB;
+  if (per_cu <= 0 || blocks > (int64_t)per_cu * cus || blocks < cus) return 0;
+  hipLaunchKernelGGL((k_fp4_gemv_rows<KCH, D, WPB>), dim3((unsigned)blocks), dim3(64 * WPB), 0, stream, packed, sc,
+                     gs, u, y, (int)N);
+  return 1;
+}
+
+template <int KCH>
+static int launch_rows_k(const uint8_t* packed, const uint8_t* sc, const float* gs, const uint16_t* u, uint16_t* y,
+                         int64_t N, int cus, hipStream_t stream) {
+  int r = 0;
+  if (!r) r = launch_rows_d<KCH, 1>(packed, sc, gs, u, y, N, cus, stream);
+  if (!r) r = launch_rows_d<KCH, 2>(packed, sc, gs, u, y, N, cus, stream);
+  if constexpr (KCH < 4) {
+    if (!r) r = launch_rows_d<KCH, 3>(packed, sc, gs, u, y, N, cus, stream);
+    if (!r) r = launch_rows_d<KCH, 4>(packed, sc, gs, u, y, N, cus, stream);
+    if (!r) r = launch_rows_d<KCH, 5>(packed, sc, gs, u, y, N, cus, stream);
+    if (!r) r = launch_rows_d<KCH, 6>(packed, sc, gs, u, y, N, cus, stream);
+  }
+  return r;
+}
+
+static int launch_rows(int kch, const uint8_t* packed, const uint8_t* sc, const float* gs, const uint16_t* u,
+                       uint16_t* y, int64_t N, hipStream_t stream) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return -m2r_fail("fp4 gemv: device query failed");
+  if (kch == 1) return launch_rows_k<1>(packed, sc, gs, u, y, N, cus, stream);
+  if (kch == 2) return launch_rows_k<2>(packed, sc, gs, u, y, N, cus, stream);
+  return launch_rows_k<4>(packed, sc, gs, u, y, N, cus, stream);
+}
 
 extern "C" int m2r_fp4_gemv_g16(const uint8_t* packed, const uint8_t* e4m3_scales, const float* global_scale,
                                 const void* u, int64_t u_stride, void* y, int64_t y_stride, int64_t M, int64_t N,
@@ -171,6 +320,10 @@ extern "C" int m2r_fp4_gemv_g16(const uint8_t* packed, const uint8_t* e4m3_scale
   if ((((uintptr_t)packed | (uintptr_t)u) & 15) || (u_stride % 8) || ((uintptr_t)e4m3_scales & 1))
     return m2r_fail("fp4 gemv: codes and activation rows must be 16-byte aligned, scales 2-byte aligned");
   const int kch = (int)(K / 2048);
+  if (M == 1) {
+    if (int e = launch_rows(kch, packed, e4m3_scales, global_scale, (const uint16_t*)u, (uint16_t*)y, N, stream))
+      return e > 0 ? m2r_check(hipGetLastError(), "fp4 gemv launch") : 1;
+  }
   const int rpi = 4 / kch > 0 ? 4 / kch : 1;
   // one resident round: eight four-wave workgroups per CU
   const int blocks = (int)std::min<int64_t>((N + rpi - 1) / rpi, 2048);
