@@ -33,6 +33,7 @@
 #include "m2r_tile.h"
 
 #include <algorithm>
+#include <atomic>
 
 namespace m2r {
 
@@ -270,13 +271,17 @@ template <int KCH, int D>
 static int launch_rows_d(const uint8_t* packed, const uint8_t* sc, const float* gs, const uint16_t* u, uint16_t* y,
                          int64_t N, int cus, hipStream_t stream) {
   constexpr int WPB = 8;
-  static int per_cu = -1;   // resident workgroups per CU of this instance (same on every MI355X)
+  // resident workgroups per CU of this instance (a property of the code
+  // object, the same on every gfx950 device), queried once
+  static std::atomic<int> per_cu_cache{-1};
+  int per_cu = per_cu_cache.load(std::memory_order_relaxed);
   if (per_cu < 0) {
     int b = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, (const void*)k_fp4_gemv_rows<KCH, D, WPB>, 64 * WPB, 0) !=
         hipSuccess)
       return -m2r_fail("fp4 gemv: occupancy query failed");
     per_cu = b;
+    per_cu_cache.store(b, std::memory_order_relaxed);
   }
   const int64_t waves = (N + D - 1) / D, blocks = (waves + WPB - 1) / WPB;
   if (per_cu <= 0 || blocks > (int64_t)per_cu * cus || blocks < cus) return 0;
