@@ -230,3 +230,25 @@ def test_fp4_gemv_matches_decoded_weights(device, M, N, K):
     assert float(err) <= 1e-3, float(err)
     bound = (ref.abs() * 2.0 ** -11 + (u.double().abs() @ w.double().abs().T) * K * 2.0 ** -22 + 2.0 ** -24)
     assert bool(((y.double() - ref).abs() <= bound).all())
+
+
+@pytest.mark.parametrize("N,K", [(18560, 4096), (4640, 4096), (4096, 8192), (2048, 8192), (100, 2048)])
+def test_fp4_gemv_one_row_same_bits_as_two_rows(device, N, K):
+    """One activation row runs the whole-row kernel where it fills the chip in
+    one resident round (in_proj and out_proj shapes of the 8B model), several
+    rows the general kernel; both add each row's 2048-wide chunk sums (wave
+    sums) in chunk order, so y of one row equals row 0 of the same row passed
+    twice, bit for bit."""
+    from mamba2_recall import fp4
+    gen = torch.Generator(device=device).manual_seed(N + K)
+    print(f"[fp4 gemv one row] N={N} K={K}", flush=True)
+    codes = torch.randint(0, 256, (N, K // 2), generator=gen, device=device, dtype=torch.uint8)
+    s = torch.exp(torch.randn((N, K // 16), generator=gen, device=device) * 0.5 - 3.0)
+    g = (s.max() / 448.0).float().reshape(1)
+    sb = (s / g).clamp(0, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+    u = torch.randn((1, K), generator=gen, device=device).half()
+    y1 = fp4.gemv_g16(codes, sb, g, u)
+    y2 = fp4.gemv_g16(codes, sb, g, torch.cat((u, u)))
+    torch.cuda.synchronize()
+    assert torch.equal(y1[0].view(torch.int16), y2[0].view(torch.int16))
+    assert torch.equal(y2[0].view(torch.int16), y2[1].view(torch.int16))
