@@ -1,5 +1,6 @@
-"""Seeded parity sweep of the packed-row steps against the C oracle: every
-published layout at batch 1 to 64 (every workgroup shape the launch picks:
+"""Seeded parity sweep of the packed-row steps (ridge, tier, legacy, dense3)
+against the C oracle: every published layout at batch 1 to 64 (every
+workgroup shape the launch picks:
 four and two waves per slot, one slot per wave, four slots per wave), one and
 three tokens, head dimensions 48, 64 and 80, D / dt_bias in binary16 and
 binary32, and inputs and stored scales over several decades.  Packed codes,
@@ -39,3 +40,16 @@ def test_tier_and_legacy_sweep(oracle, device, batch):
         kind = "legacy" if k == 0 else "tier"
         run_tier(oracle, device, kind, "16_64_48" if kind == "legacy" else layout, batch, 1 + (seed % 3), 128, P, 8,
                  seed, x_scale=xs, scale_mu=mu, d_f32=bool(seed % 2))
+
+
+@pytest.mark.parametrize("batch", BATCHES)
+@pytest.mark.parametrize("kind", ("permutation", "equalizer"))
+def test_dense3_sweep(oracle, device, batch, kind):
+    from test_gpu_state import run_dense3
+    for L in (1, 2):
+        seed = 9500 + 100 * batch + 10 * L + (kind == "equalizer")
+        xs, _, P = _case(seed)
+        mu = (-2.0, -6.0, 1.0)[(seed // 3) % 3]
+        # inputs 30x the unit scale can overflow y (binary16) on both sides:
+        # then finite rows and the NaN / infinite pattern are compared
+        run_dense3(oracle, device, kind, batch, L, 128, P, 8, seed, x_scale=xs, scale_mu=mu, nonfinite_y=xs > 1)
