@@ -213,17 +213,20 @@ def time_graph(g, steps, warmup):
 TRAFFIC_PROFILE = ROOT / "profiles" / "state_step_b64_pmc_traffic.txt"
 
 
-STEP_KERNEL_SOURCES = ("m2r_state.hip", "m2r_step.h", "m2r_device.h", "m2r_tile.h")
+# the step kernel's sources and the build script (its compiler flags), in the
+# package directory
+STEP_KERNEL_SOURCES = ("csrc/m2r_state.hip", "csrc/m2r_step.h", "csrc/m2r_device.h", "csrc/m2r_tile.h",
+                       "build_lib.py")
 
 
 def step_kernel_digest():
-    """First 16 hex digits of the SHA-256 of the step kernel's sources (in
-    STEP_KERNEL_SOURCES order): the key under which a traffic profile of that
-    kernel is valid."""
+    """First 16 hex digits of the SHA-256 of the step kernel's sources and
+    build script (in STEP_KERNEL_SOURCES order): the key under which a
+    traffic profile of that kernel is valid."""
     import hashlib
     h = hashlib.sha256()
     for name in STEP_KERNEL_SOURCES:
-        h.update((ROOT / "mamb2_8b_fp4_recall_sq3.25_amd" / "csrc" / name).read_bytes())
+        h.update((ROOT / "mamb2_8b_fp4_recall_sq3.25_amd" / name).read_bytes())
     return h.hexdigest()[:16]
 
 

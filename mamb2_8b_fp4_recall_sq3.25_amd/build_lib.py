@@ -3,7 +3,9 @@
 Every translation unit is compiled with binary32 contraction disabled
 (-ffp-contract=off: the codec's bit-exactness relies on separately rounded
 products and sums), IEEE denormals kept, and packed-FP32 instruction
-selection disabled.  Objects are compiled in parallel, then linked.
+selection disabled.  The state-step kernels (m2r_state.hip, and the
+instrumented copy that includes it) are scheduled for instruction-level
+parallelism (SOURCE_FLAGS).  Objects are compiled in parallel, then linked.
 """
 from __future__ import annotations
 
@@ -28,12 +30,21 @@ FLAGS = [
 ]
 
 
+# Per-source additions.  The state-step kernels are VALU-bound or latency-bound
+# chains with the instruction order pinned where it matters; the max-ILP
+# machine scheduler measured 1.3-1.8% faster per launch at batch 4 to 64 and
+# 3% on the 2048-token prefill (batch 16 within 0.2%), while the FP4 decode,
+# the GEMV, the s16 step and the multi-layer kernel were 4-19% slower with it.
+STATE_STEP_FLAGS = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
+SOURCE_FLAGS = {"m2r_state.hip": STATE_STEP_FLAGS, "m2r_timeline.hip": STATE_STEP_FLAGS}
+
+
 def sources():
     return sorted(CSRC.glob("*.hip"))
 
 
 def _compile(src: Path, obj: Path):
-    cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "packed-fp32-ops"
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)

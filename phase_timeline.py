@@ -58,8 +58,8 @@ def build():
 def source_digest():
     h = hashlib.sha256()
     # the same files, in the same order, as the other step profiles' digest
-    for name in ("m2r_state.hip", "m2r_step.h", "m2r_device.h", "m2r_tile.h"):
-        h.update((PKG / "csrc" / name).read_bytes())
+    for name in ("csrc/m2r_state.hip", "csrc/m2r_step.h", "csrc/m2r_device.h", "csrc/m2r_tile.h", "build_lib.py"):
+        h.update((PKG / name).read_bytes())
     return h.hexdigest()[:16]
 
 
@@ -101,7 +101,7 @@ def run(out):
     lib.m2r_timeline_set.argtypes, lib.m2r_timeline_set.restype = [ctypes.c_void_p], ctypes.c_int
     dev = torch.device("cuda:0")
     lines = [f"# phase timeline of the ridge step (instrumented build, kernel_source_sha16 {source_digest()} "
-             "of csrc/{m2r_state.hip, m2r_step.h, m2r_device.h, m2r_tile.h})",
+             "of csrc/{m2r_state.hip, m2r_step.h, m2r_device.h, m2r_tile.h} and build_lib.py)",
              "# command: python phase_timeline.py run --out <this file> (after `python phase_timeline.py build`)",
              "# µs from each wave's start, median [10th-90th percentile] over every wave of the 56 published",
              "# layers, each layer launched twice in a row and the second launch kept; each stamp costs a few",
