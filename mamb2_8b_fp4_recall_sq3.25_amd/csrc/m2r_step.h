@@ -697,7 +697,6 @@ __device__ __forceinline__ float tier_update(const uint32_t* c, float sc, float 
       rs[sg] = racc;
       racc = 0.f;
     }
-    __builtin_amdgcn_sched_barrier(0);
   }
   // Materialize the readout and the maximum here: otherwise the compiler
   // sinks their chains (and every update behind the maximum) into the
@@ -764,7 +763,6 @@ __device__ __forceinline__ float tier_requant(const float (&v)[N], uint32_t* c, 
       uint32_t packed = pack4((int)tb[0], (int)tb[1], (int)tb[2], (int)tb[3]);
       asm volatile("" : "+v"(packed));
       c[i] = packed;
-      __builtin_amdgcn_sched_barrier(0);
     }
     // A lane whose two codes differ has a half-integer between u yl and u
     // yh: the wave then requantizes the tier with the exact quotients (rare:
@@ -792,7 +790,6 @@ __device__ __forceinline__ float tier_requant(const float (&v)[N], uint32_t* c, 
       packed = INT8 ? (packed ^ 0x80808080u) : ((packed & 0x0F0F0F0Fu) ^ 0x08080808u);
       asm volatile("" : "+v"(packed));
       c[i] = packed;
-      __builtin_amdgcn_sched_barrier(0);
     }
   }
   return stored;
