@@ -3,9 +3,10 @@
 Every translation unit is compiled with binary32 contraction disabled
 (-ffp-contract=off: the codec's bit-exactness relies on separately rounded
 products and sums), IEEE denormals kept, and packed-FP32 instruction
-selection disabled.  The state-step kernels (m2r_state.hip, and the
-instrumented copy that includes it) are scheduled for instruction-level
-parallelism (SOURCE_FLAGS).  Objects are compiled in parallel, then linked.
+selection disabled.  The packed-row and dense3 step kernels (m2r_state.hip,
+the instrumented copy that includes it, m2r_dense3.hip) are scheduled for
+instruction-level parallelism (SOURCE_FLAGS).  Objects are compiled in
+parallel, then linked.
 """
 from __future__ import annotations
 
@@ -30,13 +31,17 @@ FLAGS = [
 ]
 
 
-# Per-source additions.  The state-step kernels are VALU-bound or latency-bound
-# chains with the instruction order pinned where it matters; the max-ILP
-# machine scheduler measured 1.3-1.8% faster per launch at batch 4 to 64 and
-# 3% on the 2048-token prefill (batch 16 within 0.2%), while the FP4 decode,
-# the GEMV, the s16 step and the multi-layer kernel were 4-19% slower with it.
-STATE_STEP_FLAGS = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
-SOURCE_FLAGS = {"m2r_state.hip": STATE_STEP_FLAGS, "m2r_timeline.hip": STATE_STEP_FLAGS}
+# Per-source additions.  The packed-row and dense3 step kernels are VALU-bound
+# or latency-bound chains with the instruction order pinned where it matters;
+# the max-ILP machine scheduler measured 1.3-1.8% faster per launch at batch 4
+# to 64, 3% on the 2048-token prefill (batch 16 within 0.2%) and, with the
+# tier loops' scheduling barriers dropped, a further 1.3% at batch 64 and
+# 2.4% for dense3, while the FP4 decode, the GEMV, the s16 step (its own
+# translation unit for that reason) and the multi-layer kernel were 4-19%
+# slower with it.
+SCHED_ILP_FLAGS = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
+SOURCE_FLAGS = {"m2r_state.hip": SCHED_ILP_FLAGS, "m2r_timeline.hip": SCHED_ILP_FLAGS,
+                "m2r_dense3.hip": SCHED_ILP_FLAGS}
 
 
 def sources():
