@@ -29,11 +29,13 @@ struct S16Args {
 };
 
 // STAGED (state 16-byte aligned): the slot's 64 rows of 256 B move between
-// HBM and registers through LDS, as 1 KiB wave-wide transfers (16 per slot);
-// rows sit in LDS at a 272-byte pitch, so each group of 16 lanes reading
-// 16 bytes of its own row covers the 64 banks once.  Otherwise every lane
-// reads its row directly.
-constexpr int S16_PITCH = 68;   // dwords per staged row (64 + 4 padding)
+// HBM and registers through LDS, one half-row (128 B) of every row at a
+// time, as 1 KiB wave-wide transfers (8 per half, each 8 rows x 128 B);
+// half-rows sit in LDS at a 144-byte pitch, so each group of 16 lanes
+// reading 16 bytes of its own row covers the 64 banks once.  The half-size
+// buffer (9 KiB) leaves room for more workgroups per CU.  Otherwise every
+// lane reads its row directly.
+constexpr int S16_PITCH = 36;   // dwords per staged half-row (32 + 4 padding)
 constexpr int S16_SUM_PITCH = 132;   // dwords per row of the statistics' per-row sums
 typedef uint32_t s16x4 __attribute__((ext_vector_type(4)));
 
@@ -44,7 +46,7 @@ __global__ __launch_bounds__(64) void k_s16_step(S16Args a) {
   __shared__ __align__(16) float s_b[128];
   __shared__ __align__(16) float s_c[128];
   __shared__ __align__(16) float s_sum[STATS ? 64 * S16_SUM_PITCH : 4];
-  __shared__ __align__(16) uint32_t s_rows[STAGED ? 64 * S16_PITCH : 4];
+  __shared__ __align__(16) uint32_t s_rows[STAGED ? 64 * S16_PITCH : 4];   // one half-row per row
   const int lane = threadIdx.x;
   const int b = blockIdx.z, h = blockIdx.y;
   const int H = a.H, P = a.P, G = a.G, L = a.L;
@@ -58,17 +60,21 @@ __global__ __launch_bounds__(64) void k_s16_step(S16Args a) {
   if constexpr (STAGED) {
     const s16x4* src = (const s16x4*)(a.state + row0 * 128);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {   // chunk q = 64k + lane: row q / 16, 16-byte part q % 16
-      const int r = 4 * k + (lane >> 4), part = lane & 15;
-      const s16x4 v = r < nvalid ? src[64 * k + lane] : s16x4{0u, 0u, 0u, 0u};
-      *(s16x4*)(s_rows + r * S16_PITCH + 4 * part) = v;
-    }
-    __syncthreads();
+    for (int hf = 0; hf < 2; ++hf) {
+      if (hf) __syncthreads();   // every lane has read the first half-rows
 #pragma unroll
-    for (int part = 0; part < 16; ++part) {
-      const s16x4 v = *(const s16x4*)(s_rows + lane * S16_PITCH + 4 * part);
+      for (int k = 0; k < 8; ++k) {   // row 8k + lane / 8, 16-byte part 8 hf + lane % 8
+        const int r = 8 * k + (lane >> 3), part = 8 * hf + (lane & 7);
+        const s16x4 v = r < nvalid ? src[16 * r + part] : s16x4{0u, 0u, 0u, 0u};
+        *(s16x4*)(s_rows + r * S16_PITCH + 4 * (lane & 7)) = v;
+      }
+      __syncthreads();
 #pragma unroll
-      for (int e = 0; e < 8; ++e) st[8 * part + e] = h2f((uint16_t)(v[e >> 1] >> (16 * (e & 1))));
+      for (int p = 0; p < 8; ++p) {
+        const s16x4 v = *(const s16x4*)(s_rows + lane * S16_PITCH + 4 * p);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) st[8 * (8 * hf + p) + e] = h2f((uint16_t)(v[e >> 1] >> (16 * (e & 1))));
+      }
     }
   } else {
 #pragma unroll
@@ -117,21 +123,25 @@ __global__ __launch_bounds__(64) void k_s16_step(S16Args a) {
     __syncthreads();
   }
   if constexpr (STAGED) {
-    __syncthreads();   // every lane has read its row before the buffer is reused
-#pragma unroll
-    for (int part = 0; part < 16; ++part) {
-      s16x4 v;
-#pragma unroll
-      for (int w = 0; w < 4; ++w)
-        v[w] = (uint32_t)f2h(st[8 * part + 2 * w]) | ((uint32_t)f2h(st[8 * part + 2 * w + 1]) << 16);
-      *(s16x4*)(s_rows + lane * S16_PITCH + 4 * part) = v;
-    }
-    __syncthreads();
     s16x4* dst = (s16x4*)(a.state + row0 * 128);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int r = 4 * k + (lane >> 4), part = lane & 15;
-      if (r < nvalid) dst[64 * k + lane] = *(const s16x4*)(s_rows + r * S16_PITCH + 4 * part);
+    for (int hf = 0; hf < 2; ++hf) {
+      __syncthreads();   // every lane has read (or stored) the buffer's previous contents
+#pragma unroll
+      for (int p = 0; p < 8; ++p) {
+        s16x4 v;
+        const int part = 8 * hf + p;
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+          v[w] = (uint32_t)f2h(st[8 * part + 2 * w]) | ((uint32_t)f2h(st[8 * part + 2 * w + 1]) << 16);
+        *(s16x4*)(s_rows + lane * S16_PITCH + 4 * p) = v;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int r = 8 * k + (lane >> 3), part = 8 * hf + (lane & 7);
+        if (r < nvalid) dst[16 * r + part] = *(const s16x4*)(s_rows + r * S16_PITCH + 4 * (lane & 7));
+      }
     }
   } else if (valid) {
 #pragma unroll
