@@ -1,5 +1,5 @@
-"""Seeded parity sweep of the packed-row steps (ridge, tier, legacy, dense3)
-against the C oracle: every published layout at batch 1 to 64 (every
+"""Seeded parity sweep of the state steps (ridge, tier, legacy, dense3 and
+the FP16-carry control) against the C oracle: every published layout at batch 1 to 64 (every
 workgroup shape the launch picks:
 four and two waves per slot, one slot per wave, four slots per wave), one and
 three tokens, head dimensions 48, 64 and 80, D / dt_bias in binary16 and
@@ -53,3 +53,14 @@ def test_dense3_sweep(oracle, device, batch, kind):
         # inputs 30x the unit scale can overflow y (binary16) on both sides:
         # then finite rows and the NaN / infinite pattern are compared
         run_dense3(oracle, device, kind, batch, L, 128, P, 8, seed, x_scale=xs, scale_mu=mu, nonfinite_y=xs > 1)
+
+
+@pytest.mark.parametrize("batch", BATCHES)
+def test_s16_sweep(oracle, device, batch):
+    """FP16-carry step: carry and statistics bit-exact (one fixed summation
+    order), y within tolerance; ragged P included."""
+    from test_gpu_state import run_s16
+    for L in (1, 3):
+        seed = 9800 + 100 * batch + L
+        P = HEAD_DIMS[seed % 4] - (8 if seed % 3 == 0 else 0)
+        run_s16(oracle, device, batch, L, 128, P, 8, seed, collect=bool(seed % 2))
