@@ -940,6 +940,7 @@ def main():
                      fp4_g16_frac_of_mix_ceiling=round(fp4_gbs / fp4_ceiling, 4))
     extra["other_codecs_b64"] = other_codecs(device)
     extra["prefill_b1_2048"] = prefill_timing(device)
+    extra["checkpoint_loader"] = loader_bench(device)
     if not args.skip_e2e:
         extra["e2e_decode"] = e2e_decode(device, batches=(1, 16))
     line = dict(
