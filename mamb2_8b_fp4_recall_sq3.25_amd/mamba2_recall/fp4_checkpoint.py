@@ -23,6 +23,7 @@ from __future__ import annotations
 import hashlib
 import json
 import math
+import os
 import struct
 from pathlib import Path
 
@@ -274,12 +275,47 @@ def export_checkpoint(*args, **kwargs):
 
 class _PinnedReader:
     """Reads file regions into pinned host buffers, reusing a buffer only
-    after the host-to-device copy that read it has completed."""
+    after the host-to-device copy that read it has completed.  A region of
+    at least two CHUNK-sized pieces is read by a few threads at once, each
+    with positioned reads into its own piece of the buffer (the reads
+    release the interpreter lock)."""
+
+    CHUNK = 8 << 20
+    WORKERS = 8
 
     def __init__(self, torch, device, slots=2):
         self.torch, self.device = torch, device
         self.slots = [[None, None] for _ in range(slots)]   # [pinned buffer, copy-done event]
         self.turn = 0
+        self.pool = None
+
+    def _read(self, path, position, buf):
+        """Reads len(buf) bytes at `position` of `path` into the writable
+        memoryview `buf`; returns the number of bytes read (short only at
+        the end of the file)."""
+        count = len(buf)
+        fd = os.open(path, os.O_RDONLY)
+        try:
+            def piece(span):
+                begin, end = span
+                at = begin
+                while at < end:
+                    got = os.preadv(fd, [buf[at:end]], position + at)
+                    if got <= 0:
+                        break
+                    at += got
+                return at - begin
+
+            if count < 2 * self.CHUNK:
+                return piece((0, count))
+            step = max(self.CHUNK, -(-count // self.WORKERS))
+            spans = [(a, min(a + step, count)) for a in range(0, count, step)]
+            if self.pool is None:
+                from concurrent.futures import ThreadPoolExecutor
+                self.pool = ThreadPoolExecutor(max_workers=self.WORKERS)
+            return sum(self.pool.map(piece, spans))
+        finally:
+            os.close(fd)
 
     def to_device(self, path, position, count, dest):
         """Copies `count` file bytes at `position` into the uint8 device tensor
@@ -292,9 +328,7 @@ class _PinnedReader:
         if slot[0] is None or slot[0].numel() < count:
             slot[0] = torch.empty(max(count, 1 << 20), dtype=torch.uint8, pin_memory=True)
         view = slot[0][:count]
-        with Path(path).open("rb") as f:
-            f.seek(position)
-            got = f.readinto(memoryview(view.numpy()))
+        got = self._read(Path(path), position, memoryview(view.numpy()))
         need(got == count, "Truncated checkpoint data")
         dest.copy_(view, non_blocking=True)
         slot[1] = torch.cuda.Event()

@@ -111,3 +111,22 @@ def test_verify_requires_pinned_ledger(tmp_path):
 def test_export_is_not_part_of_this_package():
     with pytest.raises(NotImplementedError):
         ck.export_checkpoint()
+
+
+def test_threaded_region_reads_match_the_file(tmp_path):
+    """The loader's region reads: pieces read by several threads land in
+    their places of the buffer, and a region past the end of the file comes
+    back short (the loader then reports truncated data)."""
+    import numpy as np
+    data = np.random.default_rng(3).integers(0, 256, (1 << 20) + 77, dtype=np.uint8).tobytes()
+    path = tmp_path / "region.bin"
+    path.write_bytes(data)
+    reader = ck._PinnedReader(None, None)
+    reader.CHUNK = 1 << 14   # small pieces: every region below of 32 KiB or more is read by the pool
+    for position, count in [(0, 0), (5, 100), (0, len(data)), (12345, (1 << 19) + 3), (len(data) - 40, 40)]:
+        buf = bytearray(count)
+        assert reader._read(path, position, memoryview(buf)) == count
+        assert bytes(buf) == data[position:position + count]
+    buf = bytearray(1 << 16)
+    assert reader._read(path, len(data) - 1000, memoryview(buf)) == 1000
+    assert bytes(buf[:1000]) == data[-1000:]
