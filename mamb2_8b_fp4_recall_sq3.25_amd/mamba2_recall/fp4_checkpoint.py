@@ -275,18 +275,23 @@ def export_checkpoint(*args, **kwargs):
 
 class _PinnedReader:
     """Reads file regions into pinned host buffers, reusing a buffer only
-    after the host-to-device copy that read it has completed.  A region of
-    at least two CHUNK-sized pieces is read by a few threads at once, each
-    with positioned reads into its own piece of the buffer (the reads
-    release the interpreter lock)."""
+    after the host-to-device copy that read it has completed.  Regions of at
+    least SMALL bytes (the code bytes of a part) and smaller ones (its block
+    scales, the global scales) take turns in separate pairs of buffers, so
+    the read of the next part's codes overlaps the copy of this part's.  A
+    region of at least two CHUNK-sized pieces is read by a few threads at
+    once, each with positioned reads into its own piece of the buffer (the
+    reads release the interpreter lock)."""
 
-    CHUNK = 8 << 20
+    CHUNK = 1 << 20
     WORKERS = 8
+    SMALL = 1 << 20
 
     def __init__(self, torch, device, slots=2):
         self.torch, self.device = torch, device
-        self.slots = [[None, None] for _ in range(slots)]   # [pinned buffer, copy-done event]
-        self.turn = 0
+        # per size class: [pinned buffer, copy-done event] slots and the next turn
+        self.slots = {big: [[None, None] for _ in range(slots)] for big in (False, True)}
+        self.turn = {False: 0, True: 0}
         self.pool = None
 
     def _read(self, path, position, buf):
@@ -321,8 +326,10 @@ class _PinnedReader:
         """Copies `count` file bytes at `position` into the uint8 device tensor
         `dest` (asynchronously, on the current stream)."""
         torch = self.torch
-        slot = self.slots[self.turn]
-        self.turn = (self.turn + 1) % len(self.slots)
+        big = count >= self.SMALL
+        slots = self.slots[big]
+        slot = slots[self.turn[big]]
+        self.turn[big] = (self.turn[big] + 1) % len(slots)
         if slot[1] is not None:
             slot[1].synchronize()
         if slot[0] is None or slot[0].numel() < count:
@@ -339,7 +346,11 @@ def load_packed_tensors(directory, plan, *, device="cuda", hash_decoded=False, p
     """Decodes every tensor of `plan` from the shards in `directory` into
     resident FP16 device tensors.  Returns {name: tensor} and, if
     `hash_decoded`, {name: sha256 hex of the decoded FP16 bytes}.  Shard
-    headers are checked against the plan (inspect_shard) before any read."""
+    headers are checked against the plan (inspect_shard) before any read.
+    The decode's error words are read once, after every matrix is queued
+    (a read per matrix would drain the copy pipeline each time); the error
+    raised is that of the first failing matrix in plan order, as a check
+    after each matrix would raise it."""
     import torch
 
     from . import fp4
@@ -349,6 +360,7 @@ def load_packed_tensors(directory, plan, *, device="cuda", hash_decoded=False, p
     reader = _PinnedReader(torch, device)
     tensors, hashes = {}, {}
     with torch.cuda.device(device):
+        flags = torch.zeros(max(len(plan), 1), dtype=torch.int32, device=device)   # per matrix, plan order
         for ordinal, name in enumerate(sorted(plan), 1):
             item = plan[name]
             shape = item["shape"]
@@ -364,7 +376,7 @@ def load_packed_tensors(directory, plan, *, device="cuda", hash_decoded=False, p
                 global_scale = torch.empty(1, dtype=torch.float32, device=device)
                 reader.to_device(directory / item["global_scale_file"],
                                  base + header["global_scale"]["data_offsets"][0], 4, global_scale.view(torch.uint8))
-                flag = torch.zeros(1, dtype=torch.int32, device=device)
+                flag = flags[ordinal - 1:ordinal]
                 for part in item["parts"]:
                     base, header = headers[part["file"]]
                     r0, r1 = part["row_start"], part["row_stop"]
@@ -377,7 +389,6 @@ def load_packed_tensors(directory, plan, *, device="cuda", hash_decoded=False, p
                                      scales.numel(), scales.view(-1))
                     fp4.decode_into(codes, scales, global_scale, out[r0:r1], rows=n, columns=columns, group=16,
                                     err_flag=flag)
-                fp4.raise_decode_errors(int(flag.item()))
             if hash_decoded:
                 h = hashlib.sha256()
                 flat = out.view(-1)
@@ -388,6 +399,8 @@ def load_packed_tensors(directory, plan, *, device="cuda", hash_decoded=False, p
             tensors[name] = out
             if progress:
                 progress({"tensor": name, "index": ordinal, "total": len(plan)})
+        for err in flags.cpu().tolist():   # synchronizes with every decode
+            fp4.raise_decode_errors(err)
     torch.cuda.synchronize(device)
     return (tensors, hashes) if hash_decoded else tensors
 

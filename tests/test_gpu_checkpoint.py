@@ -74,3 +74,29 @@ def test_loader_raises_reference_error_for_bad_scale(oracle, device, tmp_path):
     write_region(tmp_path / part["file"], base, header, "block_scale_bytes", bytes(scales))
     with pytest.raises(ValueError, match="Invalid stored scale"):
         ck.load_packed_tensors(tmp_path, plan, device=device)
+
+
+@pytest.mark.parametrize("first_bad", ["scale", "global"])
+def test_loader_raises_first_failing_matrix_in_plan_order(device, tmp_path, first_bad):
+    """Two failing matrices with different errors: the error raised is the
+    first one's in plan order (the error words are read after every
+    matrix is queued, not after each)."""
+    from mamba2_recall import fp4_checkpoint as ck
+    plan = ck.make_plan({"tensors": {name: {"kind": "fp4_g16_e4m3", "shape": [8, 32]} for name in ("w0", "w1")}},
+                        1 << 20)
+    specs = ck._file_specs(plan)
+    headers = {f: ck._create_shard(tmp_path / f, s) for f, s in specs.items()}
+    kinds = {"w0": first_bad, "w1": "global" if first_bad == "scale" else "scale"}
+    for name, kind in kinds.items():
+        part = plan[name]["parts"][0]
+        base, header = headers[part["file"]]
+        scales = bytearray([0x38] * 16)
+        if kind == "scale":
+            scales[3] = 0x7F                   # E4M3 NaN block scale
+        write_region(tmp_path / part["file"], base, header, "global_scale",
+                     np.float32(-1.0 if kind == "global" else 0.5).tobytes())
+        write_region(tmp_path / part["file"], base, header, "codes", bytes([0x11] * 128))
+        write_region(tmp_path / part["file"], base, header, "block_scale_bytes", bytes(scales))
+    want = "Invalid stored scale" if first_bad == "scale" else "Global scale must be finite and positive"
+    with pytest.raises(ValueError, match=want):
+        ck.load_packed_tensors(tmp_path, plan, device=device)
