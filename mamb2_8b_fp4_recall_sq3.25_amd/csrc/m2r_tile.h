@@ -20,13 +20,18 @@ __device__ __forceinline__ float load_param(const void* p, int f32, int i) {
 // aligned half-block (equal to the xor partner's value once every lane of a
 // block holds the block sum); levels 4-5 use the row-swap permutes.
 // IEEE addition is commutative, so all lanes of a pair obtain identical bits.
+// Levels 0-3 are written as DPP updates of a zero with every row and bank
+// enabled and out-of-range sources reading zero: every source lane of these
+// patterns lies in its own row, so the value is the moved one, and the form
+// lets the compiler fold the move into the add (one v_add_f32 with a DPP
+// operand per level instead of a move and an add).
 template <int LEVEL>
 __device__ __forceinline__ float butterfly_add(float v) {
   const int iv = __builtin_bit_cast(int, v);
-  if constexpr (LEVEL == 0) return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, false));
-  if constexpr (LEVEL == 1) return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, false));
-  if constexpr (LEVEL == 2) return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x141, 0xF, 0xF, false));
-  if constexpr (LEVEL == 3) return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x140, 0xF, 0xF, false));
+  if constexpr (LEVEL == 0) return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, true));
+  if constexpr (LEVEL == 1) return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, true));
+  if constexpr (LEVEL == 2) return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x141, 0xF, 0xF, true));
+  if constexpr (LEVEL == 3) return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x140, 0xF, 0xF, true));
   // levels 4-5: v_permlane16_swap / v_permlane32_swap of two copies of v
   // leave, in every lane, the values of the lower and the upper half-block
   // of its aligned 32- / 64-lane block; their sum is v + v[lane ^ 16 (32)]
